@@ -1,0 +1,188 @@
+/*
+ * turboquant_hip.h — C ABI of libturboquant_hip.so, the MI355X (gfx950) kernels
+ * behind the TurboQuant packed-KV hot path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, sizes and byte strides (no framework types);
+ *   - launches asynchronously on the given stream and never allocates device memory
+ *     (outputs and workspaces are caller-owned);
+ *   - returns TQ_OK, a negative TQ_ERR_* code for an argument rejected on the host
+ *     before any launch, or a positive hipError_t reported by the launch.
+ *
+ * Head dimension is fixed at 128 (the only size the reference's kernels support,
+ * turboquant/kernels/packed_compress.py:244, packed_attention.py:348, sparse_v.py:19).
+ *
+ * Bit formats (per token, little-endian bit streams; identical to the reference):
+ *   indices, b bits each : index of dim d in bits [b*d, b*d+b) of a 16*b-byte row
+ *                          (2-bit: packed_compress.py:79-90; 3-bit: sparse_v.py:57-60,82-98;
+ *                           4-bit nibble order: docs/design/AITER_TURBO4_DESIGN.md:57-76)
+ *   QJL signs            : bit d of a 16-byte row is 1 when the residual projection is >= 0
+ *                          (packed_compress.py:77,92-106); "permuted" rows hold bit 32c+k = dim 4k+c
+ *                          (packed_compress.py:180-216)
+ *   norms, residual norms: IEEE fp16.
+ */
+#ifndef TURBOQUANT_HIP_H
+#define TURBOQUANT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tq_stream_t; /* == hipStream_t */
+
+/* ---- status codes ------------------------------------------------------------ */
+#define TQ_OK                   0
+#define TQ_ERR_INVALID_ARGUMENT (-1)
+#define TQ_ERR_HEAD_DIM         (-2)  /* head_dim != 128 */
+#define TQ_ERR_BITS             (-3)  /* bits outside the supported set */
+#define TQ_ERR_ALIGNMENT        (-4)  /* pointer or stride not aligned as documented */
+#define TQ_ERR_WORKSPACE        (-5)  /* workspace smaller than tq_decode_workspace_bytes() */
+#define TQ_ERR_GQA              (-6)  /* num_q_heads / num_kv_heads not an integer in [1,16] */
+#define TQ_ERR_DTYPE            (-7)
+#define TQ_ERR_BLOCK_SIZE       (-8)  /* block_size not a positive multiple of 16 */
+#define TQ_ERR_CHUNK            (-9)  /* tokens_per_chunk not a positive multiple of 16 */
+
+/* ---- dtype codes ------------------------------------------------------------- */
+#define TQ_F32  0
+#define TQ_F16  1
+#define TQ_BF16 2
+#define TQ_I32  3
+#define TQ_I64  4
+
+/* Version of this ABI (bumped on any signature or layout change). */
+int tq_abi_version(void);
+
+/* Human-readable text for a status code returned by any tq_* function. */
+const char* tq_status_string(int status);
+
+/* ---- compression ------------------------------------------------------------- */
+
+/*
+ * PolarQuant compression of n_rows vectors of 128 dims, unpacked outputs.
+ * Replaces turboquant/core/quantizer.py:111-183 (polarquant_compress).
+ *   rotate = 1: x_rot = x @ H with H the normalized Walsh-Hadamard matrix
+ *               (core/rotation.py:28-44), H[i][j] = (-1)^popcount(i&j) * wht_scale;
+ *   rotate = 0: x is already rotated (rotation_matrix=None).
+ *   norms = |x_rot|; x_n = x_rot / (norms + 1e-8); idx = #{boundaries < x_n} (searchsorted,
+ *   left), NaN -> 2^bits-1; k_mse = centroids[idx] * norms.
+ *   use_qjl: r = (x_n - centroids[idx]) * norms; rnorm = |r|; sign = (r >= 0) ? +1 : -1.
+ * x: [n_rows, 128] rows at x_row_stride elements. centroids [2^bits], boundaries [2^bits-1]: f32.
+ * Outputs (contiguous): indices int64 [n_rows,128]; norms f32 [n_rows]; k_mse f32 [n_rows,128];
+ * signs f32 [n_rows,128] and rnorm f32 [n_rows] (only read when use_qjl; may be NULL otherwise).
+ * bits: 1..4.
+ */
+int tq_polarquant_compress(const void* x, int x_dtype, int64_t x_row_stride, int64_t n_rows,
+                           int head_dim, int rotate, float wht_scale,
+                           const float* centroids, const float* boundaries, int bits, int use_qjl,
+                           int64_t* indices, float* norms, float* k_mse, float* signs, float* rnorm,
+                           tq_stream_t stream);
+
+/*
+ * Fused paged compression: x [num_tokens, num_heads, 128] -> packed rows written into the
+ * paged cache at slot_mapping[t] (block = slot / block_size, row = slot % block_size).
+ * Negative slots are skipped (the reference clamps them to 0, integration/vllm_backend.py:223-230).
+ * Math as tq_polarquant_compress; stored: index bits, fp16 norm and, with use_qjl, sign bits
+ * and fp16 residual norm.
+ * Cache: one tile per (physical block, KV head) at cache + block*stride_block + head*stride_head;
+ * a tile is the SoA layout returned by tq_tile_bytes()/tq_tile_offsets():
+ *   [block_size rows x 16*bits idx bytes][block_size x 16 sign bytes, QJL only]
+ *   [block_size fp16 norms][block_size fp16 residual norms, QJL only].
+ * Requirements: cache, strides 16-byte aligned; block_size multiple of 16; bits 2..4.
+ * Slots >= num_blocks*block_size are skipped.
+ * Replaces turbo4_fp8_compress_and_scatter (integration/vllm_backend.py:179-230) and the
+ * per-head _fully_packed_k/_v launches of benchmarks/bench_kernels.py:464-470.
+ */
+int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_stride_head,
+                      int64_t num_tokens, int num_heads, int head_dim,
+                      const void* slot_mapping, int slot_dtype,
+                      void* cache, int64_t cache_stride_block, int64_t cache_stride_head,
+                      int64_t num_blocks, int block_size,
+                      int bits, int use_qjl, int rotate, float wht_scale,
+                      const float* centroids, const float* boundaries,
+                      tq_stream_t stream);
+
+/* Bytes of one (block, KV head) tile and the byte offsets of its regions. */
+int64_t tq_tile_bytes(int block_size, int bits, int use_qjl);
+int tq_tile_offsets(int block_size, int bits, int use_qjl,
+                    int64_t* off_idx, int64_t* off_signs, int64_t* off_norm, int64_t* off_rnorm);
+
+/* ---- decode attention --------------------------------------------------------- */
+
+/* Where one stream of per-token data lives. Address of token row r of block blk, KV head h:
+ *   ptr + blk*stride_block + h*stride_head + r*stride_row            (block_tables != NULL)
+ *   ptr + s*stride_seq + lb*stride_block + h*stride_head + r*stride_row (block_tables == NULL,
+ *                                                                        lb = logical block) */
+typedef struct tq_region {
+    const void* ptr;
+    int64_t stride_block;
+    int64_t stride_head;
+    int64_t stride_seq;
+    int64_t stride_row;
+} tq_region;
+
+typedef struct tq_kv_view {
+    tq_region idx;           /* 16*bits bytes per token; ptr and strides 4-byte aligned */
+    tq_region signs;         /* 16 bytes per token (qjl only); 4-byte aligned */
+    tq_region norm;          /* fp16 per token; 2-byte aligned */
+    tq_region rnorm;         /* fp16 per token (qjl only); 2-byte aligned */
+    const float* centroids;  /* device, 2^bits fp32 */
+    int32_t bits;            /* 2, 3 or 4 */
+    int32_t qjl;             /* 1: score adds the QJL term (K only) */
+    int32_t signs_permuted;  /* 1: sign rows in the stride-4 permuted order */
+    int32_t reserved;
+} tq_kv_view;
+
+/*
+ * Packed asymmetric split-K decode attention (one query token per sequence), GQA-shared KV.
+ * For sequence s, query head h, KV head kh = h / (num_q_heads/num_kv_heads), token t < seq_lens[s]:
+ *   score = sm_scale * ( q.(k_cb[idx_t] * norm_t) + corr_scale * rnorm_t * (qp.sign_t) )
+ *   out   = sum_t softmax(score)_t * v_cb[vidx_t] * vnorm_t          (fp32 accumulation)
+ * with qp = q_proj (or q when q_proj == NULL). Follows attention_unpacked_ref
+ * (kernels/packed_attention.py:273-284) with the correct split combine of kernels/attention.py:121-140.
+ * Sparse-V (sparse_threshold > 0, kernels/sparse_v.py:108-149): within each chunk of
+ * tokens_per_chunk tokens, processed in tiles of 16 tokens with a running max m, token t's V is
+ * skipped when max over the GQA group of exp(score - m) <= sparse_threshold; skipped tokens
+ * still count in the softmax denominator.
+ * q, q_proj: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
+ * out: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
+ * block_tables: int32 [num_seqs, block_table_stride]; entries outside [0, num_blocks) are skipped.
+ * max_seq_len: an upper bound of seq_lens (sizes the grid); longer sequences are truncated.
+ * workspace: >= tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk).
+ * skip_stats: NULL or device uint64[2], incremented by (skipped, total) (token, KV head) pairs.
+ * Replaces packed_attention (kernels/packed_attention.py:290-344) and the paged
+ * _tq_v12_sparse_v_kernel / _tq_v11_single_kernel (kernels/sparse_v.py:25-261).
+ */
+int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+              const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+              int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+              const tq_kv_view* k, const tq_kv_view* v,
+              int block_size, int64_t num_blocks,
+              const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+              const int32_t* seq_lens, int max_seq_len,
+              float sm_scale, float corr_scale, float sparse_threshold,
+              int tokens_per_chunk,
+              void* workspace, size_t workspace_bytes,
+              void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+              unsigned long long* skip_stats,
+              tq_stream_t stream);
+
+size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk);
+
+/* ---- packing helpers ----------------------------------------------------------- */
+
+/* Reorder sign rows [n_rows, 16] natural -> stride-4 permuted (out bit 32c+k = in bit 4k+c).
+ * Replaces permute_signs_for_chunked (kernels/packed_compress.py:180-216). */
+int tq_permute_signs(const uint8_t* in, uint8_t* out, int64_t n_rows, int head_dim, tq_stream_t stream);
+
+/* Unpack rows of b-bit fields [n_rows, 16*b bytes] -> int8 [n_rows, 128] (b in 1..4).
+ * Replaces unpack_2bit / unpack_1bit (kernels/packed_compress.py:145-154). */
+int tq_unpack_bits(const uint8_t* in, int8_t* out, int64_t n_rows, int head_dim, int bits, tq_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOQUANT_HIP_H */

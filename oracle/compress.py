@@ -1,0 +1,121 @@
+"""PolarQuant compression oracle (test infrastructure only).
+
+wht_matrix restates core/rotation.py:28-44; polarquant_compress restates
+core/quantizer.py:135-183 with the same torch CPU operations in the same order, so on one
+torch build its outputs equal the reference's bit for bit.
+
+polarquant_compress_fp64 is the pinning shadow: the same math in float64 (rotation by the
+exact +-h entries, no fp32 rounding), which any slip in the restated op sequence (order of
+rotate / normalize, the 1e-8, tie side, clamp, sign of the residual) would contradict beyond
+a few fp32 ulps.  boundary_band classifies index mismatches between two fp32 computations by
+how far the value sits from the nearest boundary, in units of fp32 ulp at the coordinate
+scale 1/sqrt(128) (ulp(2^-4) = 2^-27): the rotation's rounding is of that order.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+ULP_SIGMA = 2.0 ** -27  # fp32 ulp of values in [2^-4, 2^-3), the scale of N(0, 1/128) coordinates
+
+
+def wht_matrix(d: int) -> torch.Tensor:
+    H = torch.tensor([[1.0]])
+    while H.shape[0] < d:
+        H = torch.cat([torch.cat([H, H], dim=1), torch.cat([H, -H], dim=1)], dim=0) / math.sqrt(2)
+    return H[:d, :d]
+
+
+def wht_closed_form(d: int, h: float) -> np.ndarray:
+    i = np.arange(d)[:, None]
+    j = np.arange(d)[None, :]
+    pc = np.vectorize(lambda v: bin(int(v)).count("1"))(i & j)
+    return np.where(pc % 2 == 0, 1.0, -1.0) * h
+
+
+def polarquant_compress(x: torch.Tensor, centroids: torch.Tensor, boundaries: torch.Tensor,
+                        n_centroids: int, use_qjl: bool, rotation_matrix: torch.Tensor | None):
+    """Reference op sequence on CPU tensors; returns the reference's dict."""
+    x = x.cpu()
+    orig_shape = x.shape
+    if x.dim() == 3:
+        x = x.reshape(-1, orig_shape[-1])
+    N, D = x.shape
+    if rotation_matrix is not None:
+        x_rot = x.float() @ rotation_matrix.float().cpu()
+    else:
+        x_rot = x.float()
+    norms = x_rot.norm(dim=-1)
+    x_normalized = x_rot / (norms.unsqueeze(-1) + 1e-8)
+    indices = torch.searchsorted(boundaries.float().cpu(), x_normalized.reshape(-1))
+    indices = indices.clamp(0, n_centroids - 1).reshape(N, D)
+    recon_normalized = centroids.cpu()[indices]
+    k_mse_rot = recon_normalized * norms.unsqueeze(-1)
+    result = {"indices": indices, "norms": norms, "k_mse_rot": k_mse_rot, "x_normalized": x_normalized}
+    if use_qjl:
+        rot_residual = (x_normalized - recon_normalized) * norms.unsqueeze(-1)
+        result["rot_residual_norm"] = rot_residual.norm(dim=-1)
+        signs = torch.sign(rot_residual)
+        signs[signs == 0] = 1.0
+        result["signs"] = signs
+    if len(orig_shape) == 3:
+        for k in ("k_mse_rot", "indices", "signs", "x_normalized"):
+            if k in result:
+                result[k] = result[k].reshape(orig_shape)
+    return result
+
+
+def polarquant_compress_fp64(x: torch.Tensor, centroids: torch.Tensor, boundaries: torch.Tensor,
+                             use_qjl: bool, rotate: bool):
+    """float64 shadow: x_n = (x @ H) / (|x @ H| + 1e-8) with H = +-h exactly; idx = #{b < x_n}."""
+    x64 = x.detach().cpu().double().reshape(-1, x.shape[-1])
+    D = x64.shape[1]
+    if rotate:
+        h = float(wht_matrix(D)[0, 0])
+        H = torch.from_numpy(wht_closed_form(D, h))
+        x_rot = x64 @ H
+    else:
+        x_rot = x64
+    norms = x_rot.norm(dim=-1)
+    xn = x_rot / (norms.unsqueeze(-1) + 1e-8)
+    b = boundaries.double().cpu()
+    idx = (xn.unsqueeze(-1) > b).sum(-1)
+    c = centroids.double().cpu()
+    out = {"indices": idx, "norms": norms, "x_normalized": xn}
+    if use_qjl:
+        r = (xn - c[idx]) * norms.unsqueeze(-1)
+        out["rot_residual_norm"] = r.norm(dim=-1)
+        out["signs"] = torch.where(r >= 0, 1.0, -1.0).double()
+    return out
+
+
+def boundary_band(xn: torch.Tensor, boundaries: torch.Tensor) -> torch.Tensor:
+    """Distance of each value to its nearest boundary, in units of ULP_SIGMA."""
+    d = (xn.double().unsqueeze(-1) - boundaries.double().cpu()).abs().min(dim=-1).values
+    return d / ULP_SIGMA
+
+
+def centroid_band(xn: torch.Tensor, centroids: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """Distance of each value to its own centroid (where QJL signs flip), in ULP_SIGMA units."""
+    c = centroids.double().cpu()[idx.long().cpu()]
+    return (xn.double().cpu() - c).abs() / ULP_SIGMA
+
+
+def classify_index_mismatch(idx_test: torch.Tensor, idx_ref: torch.Tensor, xn_ref: torch.Tensor,
+                            boundaries: torch.Tensor, band_ulps: float):
+    """(n_mismatch, n_in_band, n_out_of_band, max_band) of index differences: a mismatch is
+    'in band' when the reference value lies within band_ulps ULP_SIGMA of a boundary and the
+    two indices are adjacent."""
+    t = idx_test.long().cpu().reshape(-1)
+    r = idx_ref.long().cpu().reshape(-1)
+    mism = t != r
+    n = int(mism.sum())
+    if n == 0:
+        return 0, 0, 0, 0.0
+    band = boundary_band(xn_ref.reshape(-1)[mism], boundaries)
+    adjacent = (t[mism] - r[mism]).abs() == 1
+    ok = (band <= band_ulps) & adjacent
+    return n, int(ok.sum()), int((~ok).sum()), float(band.max())

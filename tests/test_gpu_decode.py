@@ -1,0 +1,289 @@
+"""GPU parity: decode attention kernels vs the float64 CPU oracle.
+
+Bar: attention outputs within rtol 1e-2 / atol 1e-3 of the reference
+path (attention_unpacked_ref semantics with the correct split combine).  The kernel computes
+Q and the dequantized K/V in fp16 with fp32 accumulation.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as odec
+from oracle import packing as opack
+from oracle import paged as opaged
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-2, 1e-3
+
+
+def _cb(bits):
+    from turboquant.core import make_codebook
+    return make_codebook(128, bits)[0]
+
+
+def random_payload(rng, n, bits, qjl, norm_scale=10.0):
+    pl = {"idx": rng.integers(0, 256, size=(n, 16 * bits), dtype=np.uint8),
+          "norm": (rng.uniform(0.5, 1.5, size=n) * norm_scale).astype(np.float16).view(np.uint16)}
+    if qjl:
+        pl["signs"] = rng.integers(0, 256, size=(n, 16), dtype=np.uint8)
+        pl["rnorm"] = (rng.uniform(0.0, 0.3, size=n) * norm_scale).astype(np.float16).view(np.uint16)
+    return pl
+
+
+def build_case(seed, S, Hq, Hkv, seq_lens, kb, kq, vb, bs, extra_blocks=3):
+    rng = np.random.default_rng(seed)
+    maxb = max(1, max(math.ceil(L / bs) for L in seq_lens))
+    nb = S * maxb + extra_blocks
+    perm = rng.permutation(nb)
+    bt = np.full((S, maxb), -1, dtype=np.int32)
+    k_cache = np.zeros((nb, Hkv, opaged.tile_offsets(bs, kb, kq)[4]), np.uint8)
+    v_cache = np.zeros((nb, Hkv, opaged.tile_offsets(bs, vb, False)[4]), np.uint8)
+    k_tok, v_tok = {}, {}
+    nxt = 0
+    for s, L in enumerate(seq_lens):
+        nbl = math.ceil(L / bs)
+        bt[s, :nbl] = perm[nxt:nxt + nbl]
+        nxt += nbl
+        slots = np.array([bt[s, t // bs] * bs + t % bs for t in range(L)], dtype=np.int64)
+        kp = random_payload(rng, L * Hkv, kb, kq)
+        vp = random_payload(rng, L * Hkv, vb, False)
+        kp3 = {k: v.reshape(L, Hkv, *v.shape[1:]) for k, v in kp.items()}
+        vp3 = {k: v.reshape(L, Hkv, *v.shape[1:]) for k, v in vp.items()}
+        opaged.scatter_tokens(kp3, slots, nb, Hkv, bs, kb, kq, k_cache)
+        opaged.scatter_tokens(vp3, slots, nb, Hkv, bs, vb, False, v_cache)
+        k_tok[s], v_tok[s] = kp3, vp3
+    q = rng.standard_normal((S, Hq, 128)).astype(np.float32)
+    return dict(q=q, bt=bt, nb=nb, k_cache=k_cache, v_cache=v_cache, k_tok=k_tok, v_tok=v_tok,
+                seq_lens=np.array(seq_lens, np.int32))
+
+
+def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.0, q_round=None):
+    G = Hq // Hkv
+    kc, vc = _cb(kb).double().numpy(), _cb(vb).double().numpy()
+    S = len(case["seq_lens"])
+    out = np.zeros((S, Hq, 128))
+    skipped = total = 0
+    q = case["q"].astype(np.float64) if q_round is None else q_round
+    qpv = q if qp is None else qp
+    for s in range(S):
+        L = int(case["seq_lens"][s])
+        for kh in range(Hkv):
+            kp = {k: v[:, kh] for k, v in case["k_tok"][s].items()} if L else None
+            vp = {k: v[:, kh] for k, v in case["v_tok"][s].items()} if L else None
+            hs = slice(kh * G, (kh + 1) * G)
+            if L == 0:
+                continue
+            k, sg, rn = odec.dequant_keys(kp, kc, kb, kq)
+            v = odec.dequant_values(vp, vc, vb)
+            if chunk is None:
+                out[s, hs] = odec.decode_dense(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs)
+            else:
+                o, sk, tt = odec.decode_chunked(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs, chunk, thresh)
+                out[s, hs] = o
+                skipped += sk
+                total += tt
+    return out, skipped, total
+
+
+def run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, dtype=torch.bfloat16, chunk=None, thresh=0.0, stats=False):
+    from turboquant.kernels.paged import PagedKVFormat, decode_paged
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    q = torch.from_numpy(case["q"]).to(dtype).to(dev)
+    st = torch.zeros(2, dtype=torch.int64, device=dev) if stats else None
+    out = decode_paged(q, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
+                       torch.from_numpy(case["v_cache"]).to(dev), vf, _cb(vb).to(dev),
+                       torch.from_numpy(case["bt"]).to(dev), torch.from_numpy(case["seq_lens"]).to(dev),
+                       sm_scale=sm, corr_scale=cs, sparse_threshold=thresh, tokens_per_chunk=chunk, skip_stats=st)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), (st.cpu().numpy() if stats else None), q.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize("kb,kq,vb", [(4, False, 4), (3, True, 3), (2, True, 2), (3, False, 3),
+                                      (4, True, 2), (2, False, 4), (3, True, 4), (4, False, 3)])
+def test_decode_bit_widths(dev, kb, kq, vb):
+    S, Hq, Hkv, bs = 3, 8, 2, 16
+    lens = [37, 1, 300]
+    case = build_case(11 + kb * 7 + vb, S, Hq, Hkv, lens, kb, kq, vb, bs)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk=64)
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=qr)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("G", [1, 4, 6, 8, 16])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_decode_gqa_and_block_size(dev, G, bs):
+    Hkv = 2
+    Hq = G * Hkv
+    lens = [15, 16, 17, 129, 513]
+    case = build_case(100 + G * 3 + bs, len(lens), Hq, Hkv, lens, 3, True, 3, bs)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / math.sqrt(128)
+    for chunk in (16, 48, None):
+        got, _, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=chunk)
+        want, _, _ = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, q_round=qr)
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+def test_decode_empty_and_fp32_out(dev):
+    from turboquant.kernels.paged import PagedKVFormat, decode_paged
+    lens = [0, 5]
+    case = build_case(5, 2, 4, 1, lens, 4, False, 4, 16)
+    case["bt"][0, :] = -1
+    got, _, qr = run_gpu(dev, case, 4, 1, 4, False, 4, 16, 0.1, 0.0, dtype=torch.float32)
+    assert np.all(got[0] == 0.0)
+    want, _, _ = oracle_out(case, 4, 1, 4, False, 4, 0.1, 0.0, q_round=qr)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+def test_decode_sparse_v_matches_chunked_oracle(dev):
+    S, Hq, Hkv, bs = 2, 12, 2, 16
+    lens = [700, 1500]
+    case = build_case(77, S, Hq, Hkv, lens, 3, True, 3, bs)
+    case["q"] *= 4.0                            # sharper softmax -> many skips
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    for thresh in (1e-4, 1e-2):
+        got, st, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=256, thresh=thresh, stats=True)
+        want, sk, tot = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, chunk=256, thresh=thresh, q_round=qr)
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+        assert int(st[1]) == tot
+        print(f"thresh {thresh}: skipped gpu {int(st[0])} oracle {sk} of {tot}")
+        assert abs(int(st[0]) - sk) <= max(3, tot // 200)
+        assert sk > 0
+    dense, _, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=256, thresh=0.0)
+    want_dense, _, _ = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, q_round=qr)
+    np.testing.assert_allclose(dense, want_dense, rtol=RTOL, atol=ATOL)
+
+
+def test_decode_bad_block_entries_are_skipped(dev):
+    """Block-table entries outside [0, num_blocks) are ignored instead of read."""
+    lens = [40]
+    case = build_case(9, 1, 2, 1, lens, 4, False, 4, 16)
+    bt = case["bt"].copy()
+    bt[0, 1] = case["nb"] + 100            # second block (tokens 16..31) unreadable
+    case2 = dict(case, bt=bt)
+    got, _, qr = run_gpu(dev, case2, 2, 1, 4, False, 4, 16, 0.1, 0.0, chunk=16)
+    keep = {k: np.concatenate([v[:16], v[32:40]]) for k, v in case["k_tok"][0].items()}
+    keepv = {k: np.concatenate([v[:16], v[32:40]]) for k, v in case["v_tok"][0].items()}
+    k, _, _ = odec.dequant_keys({k: v[:, 0] for k, v in keep.items()}, _cb(4).double().numpy(), 4, False)
+    v = odec.dequant_values({k: v[:, 0] for k, v in keepv.items()}, _cb(4).double().numpy(), 4)
+    want = odec.decode_dense(qr[0], None, k, None, None, v, 0.1, 0.0)
+    np.testing.assert_allclose(got[0], want, rtol=RTOL, atol=ATOL)
+
+
+def test_packed_attention_v7_api(dev):
+    from turboquant.kernels.packed_attention import packed_attention
+    from turboquant.kernels.packed_compress import permute_signs_for_chunked
+    rng = np.random.default_rng(3)
+    cb = _cb(2)
+    cs = math.sqrt(math.pi / 2) / math.sqrt(128)
+    for BH, Sk in [(8, 1), (4, 100), (3, 4097)]:
+        ki = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
+        ks = rng.integers(0, 256, (BH, Sk, 16), dtype=np.uint8)
+        vi = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
+        kr = (rng.random((BH, Sk)) * 0.1).astype(np.float16)
+        kn = (rng.random((BH, Sk)) + 0.5).astype(np.float16)
+        vn = (rng.random((BH, Sk)) + 0.5).astype(np.float16)
+        Q = (rng.standard_normal((BH, 128)) * 0.1).astype(np.float16)
+        Qp = (rng.standard_normal((BH, 128)) * 0.1).astype(np.float16)
+        t = lambda a: torch.from_numpy(a).to(dev)
+        ks_perm = permute_signs_for_chunked(t(ks), 128)
+        out = packed_attention(t(Q), t(Qp), t(ki), ks_perm, t(kr), t(kn), t(vi), t(vn), cb.to(dev), cs)
+        assert out.dtype == torch.float16 and out.shape == (BH, 128)
+        got = out.float().cpu().numpy()
+        for h in range(BH):
+            k, sg, rn = odec.dequant_keys({"idx": ki[h], "norm": kn[h].view(np.uint16), "signs": ks[h],
+                                           "rnorm": kr[h].view(np.uint16)}, cb.double().numpy(), 2, True)
+            v = odec.dequant_values({"idx": vi[h], "norm": vn[h].view(np.uint16)}, cb.double().numpy(), 2)
+            want = odec.decode_dense(Q[h:h + 1].astype(np.float64), Qp[h:h + 1].astype(np.float64), k, sg, rn, v, 1.0, cs)
+            np.testing.assert_allclose(got[h], want[0], rtol=RTOL, atol=ATOL)
+
+
+def test_sparse_v_reference_slot_layout(dev):
+    """tq_v11 / tq_v12_sparse_v read the reference's [NB, 2, BS, Hkv, 128] slot cache in place."""
+    from turboquant.kernels.sparse_v import tq_v11, tq_v12_sparse_v
+    rng = np.random.default_rng(8)
+    Hkv, G, bs, S = 4, 6, 32, 3
+    Hq = Hkv * G
+    lens = [100, 1024, 33]
+    maxb = max(math.ceil(L / bs) for L in lens)
+    nb = S * maxb + 2
+    cache = rng.integers(0, 256, (nb, 2, bs, Hkv, 128), dtype=np.uint8)
+    norms = (rng.uniform(5, 15, (nb, 2, bs, Hkv))).astype(np.float16)
+    cache[..., 48:50] = norms.view(np.uint8).reshape(nb, 2, bs, Hkv, 2)
+    bt = rng.permutation(nb)[: S * maxb].reshape(S, maxb).astype(np.int32)
+    q = rng.standard_normal((S, Hq, 128)).astype(np.float16)
+    cent = _cb(3)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    sm = 1 / math.sqrt(128)
+    out11 = torch.empty((S, Hq, 128), dtype=torch.float16, device=dev)
+    out12 = torch.empty_like(out11)
+    tq_v11(out11, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm)
+    tq_v12_sparse_v(out12, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm)
+    torch.cuda.synchronize()
+    for s, L in enumerate(lens):
+        for kh in range(Hkv):
+            blks = bt[s, np.arange(L) // bs]
+            rows = np.arange(L) % bs
+            ksl = cache[blks, 0, rows, kh]
+            vsl = cache[blks, 1, rows, kh]
+            kp = {"idx": ksl[:, :48], "norm": ksl[:, 48:50].copy().view(np.uint16).reshape(-1)}
+            vp = {"idx": vsl[:, :48], "norm": vsl[:, 48:50].copy().view(np.uint16).reshape(-1)}
+            k, _, _ = odec.dequant_keys(kp, cent.double().numpy(), 3, False)
+            v = odec.dequant_values(vp, cent.double().numpy(), 3)
+            hs = slice(kh * G, (kh + 1) * G)
+            want = odec.decode_dense(q[s, hs].astype(np.float64), None, k, None, None, v, sm, 0.0)
+            np.testing.assert_allclose(out11[s, hs].float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+            np.testing.assert_allclose(out12[s, hs].float().cpu().numpy(), want, rtol=RTOL, atol=5 * ATOL)
+
+
+def test_decode_constant_values_full_size(dev):
+    """BASELINE config 4 shape (B=64, ctx 32768, Hq 48 / Hkv 8): with every V token equal,
+    the output equals that vector whatever the scores (size-independent property), dense and
+    Sparse-V; plus one sequence checked against the oracle in full."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged
+    B, Hq, Hkv, ctx, bs = 64, 48, 8, 32768, 16
+    kf = PagedKVFormat(bits=3, qjl=True, block_size=bs)
+    vf = PagedKVFormat(bits=3, qjl=False, block_size=bs)
+    nb = B * ctx // bs
+    g = torch.Generator(device=dev).manual_seed(4)
+    k_cache = torch.randint(0, 256, (nb, Hkv, kf.tile_bytes), dtype=torch.uint8, device=dev, generator=g)
+    nrm = (torch.rand((nb, Hkv, bs), device=dev, generator=g) * 10 + 5).half()
+    k_cache[:, :, kf.off_norm:kf.off_norm + 2 * bs] = nrm.view(torch.uint8).reshape(nb, Hkv, 2 * bs)
+    k_cache[:, :, kf.off_rnorm:kf.off_rnorm + 2 * bs] = (nrm * 0.1).view(torch.uint8).reshape(nb, Hkv, 2 * bs)
+    v_cache = allocate_cache(nb, Hkv, vf, device=dev)
+    # 3-bit fields all equal to 2 (bits 010): the little-endian stream repeats every 3 bytes
+    pattern = torch.tensor([0x92, 0x24, 0x49], dtype=torch.uint8, device=dev)
+    v_cache[:, :, : bs * 48] = pattern.repeat(bs * 16)
+    v_cache[:, :, vf.off_norm:] = torch.tensor([2.0], dtype=torch.float16).view(torch.uint8).to(dev).repeat(bs)
+    bt = torch.randperm(nb, device=dev, generator=g).to(torch.int32).reshape(B, ctx // bs)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    q = torch.randn((B, Hq, 128), device=dev, generator=g).to(torch.bfloat16)
+    cb = _cb(3)
+    want_val = float(cb[2]) * 2.0
+    for thr in (0.0, 1e-4):
+        out = decode_paged(q, k_cache, kf, cb.to(dev), v_cache, vf, cb.to(dev), bt, lens,
+                           sparse_threshold=thr)
+        torch.cuda.synchronize()
+        err = (out.float() - want_val).abs().max().item()
+        assert err <= ATOL + RTOL * abs(want_val), err
+    # sequence 0 in full against the oracle, with random V
+    v_cache[:, :, : bs * 48] = torch.randint(0, 256, (nb, Hkv, bs * 48), dtype=torch.uint8, device=dev, generator=g)
+    out = decode_paged(q, k_cache, kf, cb.to(dev), v_cache, vf, cb.to(dev), bt, lens)
+    torch.cuda.synchronize()
+    kc_np, vc_np = k_cache.cpu().numpy(), v_cache.cpu().numpy()
+    bt0 = bt[0].cpu().numpy()
+    qr = q[0].float().cpu().numpy().astype(np.float64)
+    G = Hq // Hkv
+    for kh in range(Hkv):
+        kp = opaged.gather_sequence(kc_np, bt0, ctx, kh, bs, 3, True)
+        vp = opaged.gather_sequence(vc_np, bt0, ctx, kh, bs, 3, False)
+        k, sg, rn = odec.dequant_keys(kp, cb.double().numpy(), 3, True)
+        v = odec.dequant_values(vp, cb.double().numpy(), 3)
+        hs = slice(kh * G, (kh + 1) * G)
+        want = odec.decode_dense(qr[hs], qr[hs], k, sg, rn, v, 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128)
+        np.testing.assert_allclose(out[0, hs].float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)

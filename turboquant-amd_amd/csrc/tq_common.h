@@ -1,0 +1,115 @@
+// Shared device helpers for the TurboQuant gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "turboquant_hip.h"
+
+#define TQ_ABI_VERSION 1
+#define TQ_HEAD_DIM 128
+#define TQ_WAVE 64
+
+typedef _Float16 tq_half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 tq_half4 __attribute__((ext_vector_type(4)));
+typedef float tq_floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t tq_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t tq_u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- scalar conversions ---------------------------------------------------------
+
+__device__ __forceinline__ float tq_bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ float tq_f16_to_f32(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)bits16);
+    return (float)h;
+}
+
+// fp32 -> fp16 bits, round to nearest even (hardware v_cvt_f16_f32).
+__device__ __forceinline__ uint32_t tq_f32_to_f16_bits(float f) {
+    _Float16 h = (_Float16)f;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+}
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint32_t tq_f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t tq_pack_half2(float lo, float hi) {
+    return tq_f32_to_f16_bits(lo) | (tq_f32_to_f16_bits(hi) << 16);
+}
+
+// Load 8 consecutive elements of dtype `dt` starting at element `off` of `base` as fp32.
+// The address of element `off` must be 16-byte aligned for f16/bf16 and 32-byte for f32.
+__device__ __forceinline__ void tq_load8(const void* base, int64_t off, int dt, float v[8]) {
+    if (dt == TQ_F32) {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        tq_u32x4 w = *reinterpret_cast<const tq_u32x4*>(static_cast<const uint16_t*>(base) + off);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
+            if (dt == TQ_BF16) {
+                v[2 * k] = tq_bf16_to_f32(lo);
+                v[2 * k + 1] = tq_bf16_to_f32(hi);
+            } else {
+                v[2 * k] = tq_f16_to_f32(lo);
+                v[2 * k + 1] = tq_f16_to_f32(hi);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float tq_load1(const void* base, int64_t off, int dt) {
+    if (dt == TQ_F32) return static_cast<const float*>(base)[off];
+    uint32_t b = static_cast<const uint16_t*>(base)[off];
+    return dt == TQ_BF16 ? tq_bf16_to_f32(b) : tq_f16_to_f32(b);
+}
+
+__device__ __forceinline__ void tq_store1(void* base, int64_t off, int dt, float v) {
+    if (dt == TQ_F32) {
+        static_cast<float*>(base)[off] = v;
+    } else {
+        uint32_t b = dt == TQ_BF16 ? tq_f32_to_bf16_bits(v) : tq_f32_to_f16_bits(v);
+        static_cast<uint16_t*>(base)[off] = (uint16_t)b;
+    }
+}
+
+// ---- bit-field extraction from a little-endian array of 32-bit words -----------------
+// Returns bits [pos, pos+width) of the stream w[]; pos/width are compile-time after unrolling.
+template <int N>
+__device__ __forceinline__ uint32_t tq_field(const uint32_t (&w)[N], int pos, int width) {
+    const int wi = pos >> 5, sh = pos & 31;
+    const uint32_t mask = (width >= 32) ? 0xffffffffu : ((1u << width) - 1u);
+    if (sh + width <= 32 || wi + 1 >= N) return (w[wi] >> sh) & mask;
+    return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & mask;
+}
+
+// ---- correctly rounded quotient by a per-row divisor ------------------------------
+// q = RN(x / d) given rcp = RN(1/d): one residual correction of the product (Markstein).
+__device__ __forceinline__ float tq_div_rn(float x, float d, float rcp) {
+    float q0 = x * rcp;
+    float e = __builtin_fmaf(-q0, d, x);
+    return __builtin_fmaf(e, rcp, q0);
+}
+
+// Paged tile geometry (must match tq_tile_bytes / tq_tile_offsets on the host).
+struct tq_tile_geom {
+    int64_t off_signs, off_norm, off_rnorm, bytes;
+};
+__host__ __device__ inline tq_tile_geom tq_make_tile_geom(int block_size, int bits, int qjl) {
+    tq_tile_geom g;
+    const int64_t idx_bytes = (int64_t)block_size * 16 * bits;
+    g.off_signs = idx_bytes;
+    g.off_norm = idx_bytes + (qjl ? (int64_t)block_size * 16 : 0);
+    g.off_rnorm = g.off_norm + (int64_t)block_size * 2;
+    g.bytes = g.off_norm + (int64_t)block_size * 2 + (qjl ? (int64_t)block_size * 2 : 0);
+    return g;
+}

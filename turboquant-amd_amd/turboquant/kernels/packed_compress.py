@@ -1,0 +1,93 @@
+"""Packed compression helpers (drop-in names of the reference's kernels/packed_compress.py).
+
+Bit-level helpers run as HIP kernels: permute_signs_for_chunked (tq_permute_signs) and
+unpack_2bit / unpack_1bit (tq_unpack_bits).  solve_codebook here is the kernel files' own
+codebook recipe (kernels/packed_compress.py:21-41), which differs from
+turboquant.core.make_codebook (fact documented by the reference: two codebooks exist).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from turboquant import _lib
+
+
+def solve_codebook(d: int, bits: int) -> torch.Tensor:
+    """Kernel-file Lloyd-Max variant: centroids start uniform on +-3.5 sigma (cell midpoints),
+    cells extend to +-10.5 sigma, up to 200 rounds until the centroid change is < 1e-10.
+    Returns fp32 centroids [2^bits] (kernels/packed_compress.py:21-41)."""
+    from scipy import integrate
+
+    n_levels = 2 ** bits
+    sigma = 1.0 / math.sqrt(d)
+
+    def pdf(x):
+        return (1.0 / math.sqrt(2 * math.pi * sigma**2)) * math.exp(-x * x / (2 * sigma**2))
+
+    def first_moment(x):
+        return x * pdf(x)
+
+    lo, hi = -3.5 * sigma, 3.5 * sigma
+    centroids = [lo + (hi - lo) * (i + 0.5) / n_levels for i in range(n_levels)]
+    for _ in range(200):
+        boundaries = [(centroids[i] + centroids[i + 1]) / 2.0 for i in range(n_levels - 1)]
+        edges = [lo * 3] + boundaries + [hi * 3]
+        new_c = []
+        for i in range(n_levels):
+            a, b = edges[i], edges[i + 1]
+            num, _ = integrate.quad(first_moment, a, b)
+            den, _ = integrate.quad(pdf, a, b)
+            new_c.append(num / den if den > 1e-15 else centroids[i])
+        if max(abs(new_c[i] - centroids[i]) for i in range(n_levels)) < 1e-10:
+            break
+        centroids = new_c
+    return torch.tensor(centroids, dtype=torch.float32)
+
+
+def _rows(packed: torch.Tensor, row_bytes: int, what: str) -> torch.Tensor:
+    if packed.dtype == torch.int8:
+        packed = packed.view(torch.uint8)
+    if packed.dtype != torch.uint8 or packed.shape[-1] != row_bytes:
+        raise ValueError(f"{what}: expected uint8 rows of {row_bytes} bytes, got {packed.dtype} {tuple(packed.shape)}")
+    return packed.contiguous()
+
+
+def unpack_bits(packed: torch.Tensor, bits: int, D: int = 128) -> torch.Tensor:
+    """[..., D*bits/8] uint8 rows of little-endian b-bit fields -> int8 [N, D] (N = rows)."""
+    _lib.require_gpu("unpack_bits", packed)
+    if D != 128:
+        raise ValueError("D must be 128")
+    rows = _rows(packed, D * bits // 8, "unpack_bits")
+    n = rows.numel() // (D * bits // 8)
+    out = torch.empty((n, D), dtype=torch.int8, device=rows.device)
+    rc = _lib.lib().tq_unpack_bits(rows.data_ptr(), out.data_ptr(), n, D, bits, _lib.stream_handle(rows.device))
+    _lib.check(rc, "tq_unpack_bits")
+    return out
+
+
+def unpack_2bit(packed: torch.Tensor, D: int) -> torch.Tensor:
+    """[N, D/4] -> int8 [N, D] with values 0..3 (kernels/packed_compress.py:145-148)."""
+    return unpack_bits(packed, 2, D)
+
+
+def unpack_1bit(packed: torch.Tensor, D: int) -> torch.Tensor:
+    """[N, D/8] -> int8 [N, D] with values 0/1 (kernels/packed_compress.py:150-154)."""
+    return unpack_bits(packed, 1, D)
+
+
+def permute_signs_for_chunked(signs_packed: torch.Tensor, D: int = 128) -> torch.Tensor:
+    """Reorder sign rows so chunk c (dims c, c+4, ..., c+124) fills bytes 4c..4c+3:
+    output bit 32c+k = input bit 4k+c.  Same shape as the input (packed_compress.py:180-216)."""
+    _lib.require_gpu("permute_signs_for_chunked", signs_packed)
+    if D != 128:
+        raise ValueError("D must be 128")
+    shape = signs_packed.shape
+    rows = _rows(signs_packed, D // 8, "permute_signs_for_chunked")
+    n = rows.numel() // (D // 8)
+    out = torch.empty_like(rows)
+    rc = _lib.lib().tq_permute_signs(rows.data_ptr(), out.data_ptr(), n, D, _lib.stream_handle(rows.device))
+    _lib.check(rc, "tq_permute_signs")
+    return out.reshape(shape)

@@ -1,0 +1,342 @@
+"""Paged packed-KV cache: format, fused compression, split-K decode attention.
+
+Cache layout.  One tensor per K or V cache, uint8 [num_blocks, num_kv_heads, tile_bytes];
+the tile of (physical block, KV head) stores its block_size tokens structure-of-arrays:
+
+    [block_size x 16*bits index bytes][block_size x 16 sign bytes]  (signs: QJL keys only)
+    [block_size x fp16 norm]          [block_size x fp16 residual norm] (QJL keys only)
+
+Per token this is exactly the reference's payload (index bits as a little-endian bit stream,
+sign bits, fp16 norms: kernels/packed_compress.py:79-106, kernels/sparse_v.py:57-98,
+docs/design/AITER_TURBO4_DESIGN.md:57-76), regrouped so that the 16 tokens a wave reads
+are contiguous (one 128-bit load per lane).  to_reference_slots / from_reference_slots convert
+to and from the reference's array-of-slots layout [num_blocks, block_size, Hkv, slot_bytes]
+(kernels/sparse_v.py:293-304, integration/vllm/compact_kv_allocator.py:36-75).
+
+Slot addressing follows vLLM: token t goes to slot_mapping[t] = block * block_size + row
+(integration/vllm_backend.py:223-230); negative slots are skipped.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from turboquant import _lib
+from turboquant.core.rotation import wht_scale
+
+MI355X_CUS = 256
+
+
+@dataclass(frozen=True)
+class PagedKVFormat:
+    """Geometry of one paged cache (K or V)."""
+
+    bits: int = 4
+    qjl: bool = False
+    block_size: int = 16
+    head_dim: int = 128
+
+    def __post_init__(self):
+        if self.bits not in (2, 3, 4):
+            raise ValueError(f"bits must be 2, 3 or 4, got {self.bits}")
+        if self.block_size <= 0 or self.block_size % 16:
+            raise ValueError(f"block_size must be a positive multiple of 16, got {self.block_size}")
+        if self.head_dim != 128:
+            raise ValueError("head_dim must be 128")
+
+    @property
+    def idx_bytes(self) -> int:
+        return self.head_dim * self.bits // 8
+
+    @property
+    def off_signs(self) -> int:
+        return self.block_size * self.idx_bytes
+
+    @property
+    def off_norm(self) -> int:
+        return self.block_size * (self.idx_bytes + (16 if self.qjl else 0))
+
+    @property
+    def off_rnorm(self) -> int:
+        return self.off_norm + 2 * self.block_size
+
+    @property
+    def tile_bytes(self) -> int:
+        return self.off_norm + 2 * self.block_size * (2 if self.qjl else 1)
+
+    @property
+    def token_bytes(self) -> int:
+        """Payload bytes per (token, KV head)."""
+        return self.tile_bytes // self.block_size
+
+    @property
+    def slot_bytes(self) -> int:
+        """Size of the reference-layout slot (payload, no padding)."""
+        return self.token_bytes
+
+
+def allocate_cache(num_blocks: int, num_kv_heads: int, fmt: PagedKVFormat, device=None) -> torch.Tensor:
+    """Zeroed uint8 cache [num_blocks, num_kv_heads, fmt.tile_bytes]."""
+    return torch.zeros((num_blocks, num_kv_heads, fmt.tile_bytes), dtype=torch.uint8, device=device)
+
+
+def _check_cache(cache: torch.Tensor, fmt: PagedKVFormat, what: str) -> None:
+    if cache.dtype != torch.uint8 or cache.dim() != 3:
+        raise ValueError(f"{what}: cache must be uint8 [num_blocks, num_kv_heads, tile_bytes]")
+    if cache.shape[2] < fmt.tile_bytes or cache.stride(2) != 1:
+        raise ValueError(f"{what}: cache tiles must hold {fmt.tile_bytes} contiguous bytes")
+
+
+def compress_paged(
+    x: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    cache: torch.Tensor,
+    fmt: PagedKVFormat,
+    centroids: torch.Tensor,
+    boundaries: torch.Tensor,
+    rotate: bool = True,
+) -> torch.Tensor:
+    """Compress x [T, Hkv, 128] (f32/f16/bf16) into the paged cache at slot_mapping [T].
+
+    With rotate=True the WHT is applied first (the reference's x @ make_wht_matrix(128));
+    rotate=False takes already-rotated input (weights fused with the rotation).
+    """
+    dev = _lib.require_gpu("compress_paged", x, slot_mapping, cache, centroids, boundaries)
+    if x.dim() != 3 or x.shape[2] != fmt.head_dim:
+        raise ValueError(f"x must be [T, H, {fmt.head_dim}], got {tuple(x.shape)}")
+    T, H, _ = x.shape
+    _check_cache(cache, fmt, "compress_paged")
+    if cache.shape[1] != H:
+        raise ValueError(f"cache has {cache.shape[1]} heads, x has {H}")
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != T:
+        raise ValueError("slot_mapping must be [T]")
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise TypeError("slot_mapping must be int32 or int64")
+    if centroids.numel() != 2 ** fmt.bits:
+        raise ValueError(f"need {2 ** fmt.bits} centroids for bits={fmt.bits}")
+    if x.stride(2) != 1 or x.stride(0) % 8 or x.stride(1) % 8 or x.data_ptr() % 32:
+        x = x.contiguous()
+    slot_mapping = slot_mapping.contiguous()
+    cent = centroids.to(device=dev, dtype=torch.float32).contiguous()
+    bnd = boundaries.to(device=dev, dtype=torch.float32).contiguous()
+    rc = _lib.lib().tq_compress_paged(
+        x.data_ptr(), _lib.dtype_code(x), x.stride(0), x.stride(1), T, H, fmt.head_dim,
+        slot_mapping.data_ptr(), _lib.dtype_code(slot_mapping),
+        cache.data_ptr(), cache.stride(0), cache.stride(1), cache.shape[0], fmt.block_size,
+        fmt.bits, int(fmt.qjl), int(bool(rotate)), wht_scale(fmt.head_dim),
+        cent.data_ptr(), bnd.data_ptr(), _lib.stream_handle(dev),
+    )
+    _lib.check(rc, "tq_compress_paged")
+    return cache
+
+
+def choose_tokens_per_chunk(num_seqs: int, num_kv_heads: int, max_seq_len: int,
+                            waves_per_cu: int = 16, min_chunk: int = 64, max_chunk: int = 4096) -> int:
+    """Split-K chunk length (multiple of 16) aiming at ~waves_per_cu work units per CU."""
+    units = max(1, num_seqs * num_kv_heads)
+    target = MI355X_CUS * waves_per_cu
+    per = math.ceil(max(1, max_seq_len) * units / target)
+    chunk = max(min_chunk, min(max_chunk, per))
+    return int(math.ceil(chunk / 16) * 16)
+
+
+def _region(ptr: int, stride_block: int, stride_head: int, stride_row: int, stride_seq: int = 0) -> _lib.TQRegion:
+    return _lib.TQRegion(ptr, stride_block, stride_head, stride_seq, stride_row)
+
+
+def paged_view(cache: torch.Tensor, fmt: PagedKVFormat, centroids: torch.Tensor) -> _lib.TQKVView:
+    """TQKVView over a cache tensor in this module's tile layout."""
+    base = cache.data_ptr()
+    sb, sh = cache.stride(0), cache.stride(1)
+    view = _lib.TQKVView()
+    view.idx = _region(base, sb, sh, fmt.idx_bytes)
+    if fmt.qjl:
+        view.signs = _region(base + fmt.off_signs, sb, sh, 16)
+        view.rnorm = _region(base + fmt.off_rnorm, sb, sh, 2)
+    view.norm = _region(base + fmt.off_norm, sb, sh, 2)
+    view.centroids = centroids.data_ptr()
+    view.bits = fmt.bits
+    view.qjl = int(fmt.qjl)
+    view.signs_permuted = 0
+    return view
+
+
+def run_decode(
+    q: torch.Tensor,
+    k_view: _lib.TQKVView,
+    v_view: _lib.TQKVView,
+    *,
+    num_kv_heads: int,
+    block_size: int,
+    num_blocks: int,
+    block_tables: Optional[torch.Tensor],
+    max_blocks_per_seq: int,
+    seq_lens: torch.Tensor,
+    max_seq_len: int,
+    sm_scale: float,
+    corr_scale: float,
+    q_proj: Optional[torch.Tensor],
+    sparse_threshold: float,
+    tokens_per_chunk: int,
+    out: torch.Tensor,
+    workspace: Optional[torch.Tensor],
+    skip_stats: Optional[torch.Tensor],
+    keep_alive: tuple = (),
+) -> torch.Tensor:
+    """Launch tq_decode for q [S, Hq, 128] given ready KV views (shared by all wrappers)."""
+    dev = q.device
+    S, Hq, D = q.shape
+    L = _lib.lib()
+    need = L.tq_decode_workspace_bytes(S, Hq, max_seq_len, tokens_per_chunk)
+    if workspace is None or workspace.numel() < need or workspace.data_ptr() % 256:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    if skip_stats is not None and (skip_stats.dtype != torch.int64 or skip_stats.numel() < 2 or not skip_stats.is_cuda):
+        raise ValueError("skip_stats must be a device int64 tensor with 2 elements")
+    bt_ptr = block_tables.data_ptr() if block_tables is not None else None
+    bt_stride = block_tables.stride(0) if block_tables is not None else 0
+    rc = L.tq_decode(
+        q.data_ptr(), _lib.dtype_code(q), q.stride(0), q.stride(1),
+        _lib.ptr(q_proj), q_proj.stride(0) if q_proj is not None else 0, q_proj.stride(1) if q_proj is not None else 0,
+        S, Hq, num_kv_heads, D,
+        ctypes.byref(k_view), ctypes.byref(v_view),
+        block_size, num_blocks,
+        bt_ptr, bt_stride, max_blocks_per_seq,
+        seq_lens.data_ptr(), max_seq_len,
+        float(sm_scale), float(corr_scale), float(sparse_threshold),
+        tokens_per_chunk,
+        workspace.data_ptr(), workspace.numel(),
+        out.data_ptr(), _lib.dtype_code(out), out.stride(0), out.stride(1),
+        _lib.ptr(skip_stats),
+        _lib.stream_handle(dev),
+    )
+    _lib.check(rc, "tq_decode")
+    del keep_alive
+    return out
+
+
+def decode_paged(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    k_fmt: PagedKVFormat,
+    k_centroids: torch.Tensor,
+    v_cache: torch.Tensor,
+    v_fmt: PagedKVFormat,
+    v_centroids: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    corr_scale: Optional[float] = None,
+    q_proj: Optional[torch.Tensor] = None,
+    sparse_threshold: float = 0.0,
+    max_seq_len: Optional[int] = None,
+    tokens_per_chunk: Optional[int] = None,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+    skip_stats: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Decode attention of q [S, Hq, 128] (rotated space) over paged packed K/V caches.
+
+    score = sm_scale * (q . k_mse + corr_scale * rnorm * (q_proj . signs)) with q_proj = q by
+    default (QJL in the rotated basis, as polarquant_compress computes the signs);
+    corr_scale defaults to sqrt(pi/2)/128 (reference/pytorch_reference.py:153-154).
+    block_tables: int32 [S, max_blocks]; seq_lens: int32 [S]; max_seq_len: host-side upper
+    bound of seq_lens (default: max_blocks * block_size).  sparse_threshold > 0 enables
+    Sparse-V.  Output dtype = out.dtype or q.dtype.
+    """
+    dev = _lib.require_gpu("decode_paged", q, k_cache, v_cache, block_tables, seq_lens, k_centroids, v_centroids)
+    if q.dim() != 3 or q.shape[2] != 128:
+        raise ValueError("q must be [S, Hq, 128]")
+    if k_fmt.block_size != v_fmt.block_size:
+        raise ValueError("K and V caches must share block_size")
+    if v_fmt.qjl:
+        raise ValueError("the V cache carries no QJL data")
+    _check_cache(k_cache, k_fmt, "decode_paged(k)")
+    _check_cache(v_cache, v_fmt, "decode_paged(v)")
+    if k_cache.shape[0] != v_cache.shape[0] or k_cache.shape[1] != v_cache.shape[1]:
+        raise ValueError("K and V caches must have the same [num_blocks, num_kv_heads]")
+    S, Hq, _ = q.shape
+    Hkv = k_cache.shape[1]
+    if Hq % Hkv or Hq // Hkv > 16:
+        raise ValueError(f"num_q_heads {Hq} must be a multiple of num_kv_heads {Hkv} with group <= 16")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("block_tables and seq_lens must be int32")
+    if block_tables.dim() != 2 or block_tables.shape[0] != S or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be [S, max_blocks] with unit inner stride")
+    seq_lens = seq_lens.contiguous()
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    if q_proj is not None:
+        if q_proj.shape != q.shape:
+            raise ValueError("q_proj must have q's shape")
+        q_proj = q_proj.to(q.dtype)
+        if q_proj.stride(2) != 1:
+            q_proj = q_proj.contiguous()
+    max_blocks = block_tables.shape[1]
+    cap = max_blocks * k_fmt.block_size
+    msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+    chunk = tokens_per_chunk or choose_tokens_per_chunk(S, Hkv, msl)
+    if out is None:
+        out = torch.empty_like(q)
+    kc = k_centroids.to(device=dev, dtype=torch.float32).contiguous()
+    vc = v_centroids.to(device=dev, dtype=torch.float32).contiguous()
+    if kc.numel() != 2 ** k_fmt.bits or vc.numel() != 2 ** v_fmt.bits:
+        raise ValueError("centroid counts must match the formats' bit widths")
+    kv = paged_view(k_cache, k_fmt, kc)
+    vv = paged_view(v_cache, v_fmt, vc)
+    return run_decode(
+        q, kv, vv, num_kv_heads=Hkv, block_size=k_fmt.block_size, num_blocks=k_cache.shape[0],
+        block_tables=block_tables, max_blocks_per_seq=max_blocks, seq_lens=seq_lens, max_seq_len=msl,
+        sm_scale=(1.0 / math.sqrt(128)) if sm_scale is None else sm_scale,
+        corr_scale=(math.sqrt(math.pi / 2) / 128) if corr_scale is None else corr_scale,
+        q_proj=q_proj, sparse_threshold=sparse_threshold, tokens_per_chunk=chunk, out=out,
+        workspace=workspace, skip_stats=skip_stats, keep_alive=(kc, vc),
+    )
+
+
+# ---- conversion to and from the reference's array-of-slots layout ------------------------
+
+def _tile_fields(fmt: PagedKVFormat):
+    """(name, offset in tile, bytes per token) of each per-token field, in slot order."""
+    fields = [("idx", 0, fmt.idx_bytes)]
+    if fmt.qjl:
+        fields.append(("signs", fmt.off_signs, 16))
+    fields.append(("norm", fmt.off_norm, 2))
+    if fmt.qjl:
+        fields.append(("rnorm", fmt.off_rnorm, 2))
+    return fields
+
+
+def to_reference_slots(cache: torch.Tensor, fmt: PagedKVFormat, slot_bytes: Optional[int] = None) -> torch.Tensor:
+    """Tile layout -> [num_blocks, block_size, Hkv, slot_bytes] slots holding, per token,
+    index bytes, [sign bytes], fp16 norm, [fp16 residual norm], then zero padding."""
+    nb, h, _ = cache.shape
+    bs = fmt.block_size
+    sb = slot_bytes or fmt.slot_bytes
+    if sb < fmt.token_bytes:
+        raise ValueError("slot too small")
+    out = torch.zeros((nb, bs, h, sb), dtype=torch.uint8, device=cache.device)
+    pos = 0
+    for _, off, width in _tile_fields(fmt):
+        part = cache[:, :, off: off + bs * width].reshape(nb, h, bs, width).permute(0, 2, 1, 3)
+        out[..., pos: pos + width] = part
+        pos += width
+    return out
+
+
+def from_reference_slots(slots: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
+    """Inverse of to_reference_slots: [num_blocks, block_size, Hkv, slot_bytes] -> tile layout."""
+    nb, bs, h, _ = slots.shape
+    if bs != fmt.block_size:
+        raise ValueError("block_size mismatch")
+    cache = torch.zeros((nb, h, fmt.tile_bytes), dtype=torch.uint8, device=slots.device)
+    pos = 0
+    for _, off, width in _tile_fields(fmt):
+        part = slots[..., pos: pos + width].permute(0, 2, 1, 3).reshape(nb, h, bs * width)
+        cache[:, :, off: off + bs * width] = part
+        pos += width
+    return cache

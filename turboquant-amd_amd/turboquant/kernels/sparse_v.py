@@ -1,0 +1,86 @@
+"""Paged 3-bit decode over the reference's array-of-slots cache, dense (v11) and Sparse-V (v12).
+
+The reference launches Triton kernels directly on a cache [num_blocks, 2 (K/V), block_size,
+num_kv_heads, slot_bytes] uint8 whose slot holds 48 bytes of 3-bit indices (bits 3d..3d+2 =
+dim d) and the fp16 norm at bytes 48-49 (kernels/sparse_v.py:25-159, 163-261, 293-304).
+tq_v12_sparse_v / tq_v11 run tq_decode on that same memory through strided views, so a
+cache written for the reference is read in place.  block_size is taken from the cache's
+shape (docs/MI355X_BLOCKSIZE_FIX.md:18-21).
+
+Sparse-V rule (kernels/sparse_v.py:108-149): with a running max m over the tokens processed
+so far in the work unit (updated per 16-token tile), token t's V is skipped when
+max over the GQA group of exp(score - m) <= threshold; skipped tokens still count in the
+softmax denominator.  The work unit here is a chunk of tokens_per_chunk tokens.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from turboquant import _lib
+from turboquant.kernels.paged import choose_tokens_per_chunk, run_decode
+
+D = 128
+DQ3 = D * 3 // 8  # 48 index bytes per slot
+CD = 32
+SPARSE_V_THRESHOLD = 1e-6
+
+
+def _aos_view(cache: torch.Tensor, kv: int, centroids: torch.Tensor) -> _lib.TQKVView:
+    nb, two, bs, hkv, slot = cache.shape
+    base = cache.data_ptr() + kv * cache.stride(1)
+    sb, sr, sh = cache.stride(0), cache.stride(2), cache.stride(3)
+    view = _lib.TQKVView()
+    view.idx = _lib.TQRegion(base, sb, sh, 0, sr)
+    view.norm = _lib.TQRegion(base + DQ3, sb, sh, 0, sr)
+    view.centroids = centroids.data_ptr()
+    view.bits, view.qjl, view.signs_permuted = 3, 0, 0
+    return view
+
+
+def tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, scale,
+                         threshold: float = 0.0, max_seq_len=None, tokens_per_chunk=None, skip_stats=None):
+    """out[S, Hq, 128] = attention of q over the 3-bit MSE-only K/V slots of tq_cache."""
+    dev = _lib.require_gpu("tq_paged_decode_3bit", out, q, tq_cache, centroids, block_tables, seq_lens)
+    if tq_cache.dtype != torch.uint8 or tq_cache.dim() != 5 or tq_cache.shape[1] != 2:
+        raise ValueError("tq_cache must be uint8 [num_blocks, 2, block_size, num_kv_heads, slot_bytes]")
+    nb, _, bs, hkv, slot = tq_cache.shape
+    if slot < DQ3 + 2 or tq_cache.stride(4) != 1:
+        raise ValueError("slots must hold 48 index bytes and an fp16 norm contiguously")
+    S, Hq, d = q.shape
+    if d != D or out.shape != q.shape:
+        raise ValueError("q and out must be [S, Hq, 128]")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("block_tables and seq_lens must be int32")
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    cb = centroids.to(device=dev, dtype=torch.float32).contiguous()
+    if cb.numel() != 8:
+        raise ValueError("3-bit codebook needs 8 centroids")
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    max_blocks = block_tables.shape[1]
+    cap = max_blocks * bs
+    msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+    chunk = tokens_per_chunk or choose_tokens_per_chunk(S, hkv, msl)
+    kv = _aos_view(tq_cache, 0, cb)
+    vv = _aos_view(tq_cache, 1, cb)
+    target = out if out.stride(2) == 1 else torch.empty_like(out)
+    run_decode(q, kv, vv, num_kv_heads=hkv, block_size=bs, num_blocks=nb, block_tables=block_tables,
+               max_blocks_per_seq=max_blocks, seq_lens=seq_lens.contiguous(), max_seq_len=msl, sm_scale=float(scale),
+               corr_scale=0.0, q_proj=None, sparse_threshold=threshold, tokens_per_chunk=chunk, out=target,
+               workspace=None, skip_stats=skip_stats, keep_alive=(cb,))
+    if target is not out:
+        out.copy_(target)
+    return out
+
+
+def tq_v12_sparse_v(out, q, tq_cache, centroids, block_tables, seq_lens, scale,
+                    threshold: float = SPARSE_V_THRESHOLD, **kw):
+    """Sparse-V decode (the role of _tq_v12_sparse_v_kernel, kernels/sparse_v.py:25-159)."""
+    return tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, scale, threshold, **kw)
+
+
+def tq_v11(out, q, tq_cache, centroids, block_tables, seq_lens, scale, **kw):
+    """Dense decode without skipping (the role of _tq_v11_single_kernel, kernels/sparse_v.py:163-261)."""
+    return tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, scale, 0.0, **kw)
