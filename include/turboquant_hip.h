@@ -132,7 +132,10 @@ typedef struct tq_kv_view {
     int32_t bits;            /* 2, 3 or 4 */
     int32_t qjl;             /* 1: score adds the QJL term (K only) */
     int32_t signs_permuted;  /* 1: sign rows in the stride-4 permuted order */
-    int32_t reserved;
+    float centroid_scale;    /* kernels tabulate fp16(centroid * centroid_scale) and divide the
+                                scale back out in fp32; a scale in [1,2) chosen so every scaled
+                                centroid is nearly exact in fp16 removes the table's rounding.
+                                0 means 1. */
 } tq_kv_view;
 
 /*

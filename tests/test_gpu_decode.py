@@ -146,10 +146,14 @@ def test_decode_sparse_v_matches_chunked_oracle(dev):
     case = build_case(77, S, Hq, Hkv, lens, 3, True, 3, bs)
     case["q"] *= 4.0                            # sharper softmax -> many skips
     sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    vmax = float(_cb(3).abs().max()) * 15.0          # |centroid| * largest payload norm
     for thresh in (1e-4, 1e-2):
         got, st, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=256, thresh=thresh, stats=True)
         want, sk, tot = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, chunk=256, thresh=thresh, q_round=qr)
-        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+        # A token whose p lies within rounding of the threshold may be skipped on one side only;
+        # each such flip moves an output by at most thresh * max|v| (the denominator is >= 1).
+        flip_tol = 0.0 if thresh < 1e-3 else 2 * thresh * vmax
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL + flip_tol)
         assert int(st[1]) == tot
         print(f"thresh {thresh}: skipped gpu {int(st[0])} oracle {sk} of {tot}")
         assert abs(int(st[0]) - sk) <= max(3, tot // 200)

@@ -49,6 +49,7 @@ def test_wht_matrix(d):
     assert (H @ H - I).abs().max() < 1e-5
     assert is_wht_matrix(H)
     assert not is_wht_matrix(H.flip(0))
+    assert not is_wht_matrix(H * 1.0001 + torch.eye(d) * 1e-3)
     assert wht_scale(d) == float(H.abs().max())
 
 

@@ -39,6 +39,8 @@ struct DecodeParams {
     Region v_idx, v_norm;
     const float* k_cent;
     const float* v_cent;
+    float k_cscale, v_cscale;  // tables hold fp16(c * cscale) ...
+    float k_cinv, v_cinv;      // ... and norms carry 1 / cscale
     int k_perm;
     int block_size;
     int64_t num_blocks;
@@ -80,11 +82,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     // Build the pair tables: entry e -> half2(c[e & (2^b - 1)], c[e >> b]).
     for (int i = threadIdx.x; i < KENT * 32; i += 256) {
         int e = i >> 5;
-        s_ktab[i] = tq_pack_half2(p.k_cent[e & ((1 << KB) - 1)], p.k_cent[e >> KB]);
+        s_ktab[i] = tq_pack_half2(p.k_cent[e & ((1 << KB) - 1)] * p.k_cscale, p.k_cent[e >> KB] * p.k_cscale);
     }
     for (int i = threadIdx.x; i < VENT * 32; i += 256) {
         int e = i >> 5;
-        s_vtab[i] = tq_pack_half2(p.v_cent[e & ((1 << VB) - 1)], p.v_cent[e >> VB]);
+        s_vtab[i] = tq_pack_half2(p.v_cent[e & ((1 << VB) - 1)] * p.v_cscale, p.v_cent[e >> VB] * p.v_cscale);
     }
     __syncthreads();
 
@@ -109,9 +111,11 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     const bool paged = p.bt != nullptr;
 
     // ---- query operands (B of the QK products), pre-scaled into the log2 domain ----
+    // q is split into fp16 hi + lo parts so the MSE score keeps ~22 bits of q.
     const int head = kh * p.group + n;
     const bool hvalid = n < p.group;
     tq_half8 qop[4];
+    tq_half8 qlo[4];
     tq_half8 qpop[4];
     {
         const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh;
@@ -121,7 +125,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 float qv = hvalid ? tq_load1(p.q, qoff + 32 * g + 8 * cc + j, p.q_dtype) * p.q_scale : 0.f;
-                qop[cc][j] = (_Float16)qv;
+                const _Float16 qh = (_Float16)qv;
+                qop[cc][j] = qh;
+                qlo[cc][j] = (_Float16)(qv - (float)qh);
                 if (KQJL) {
                     const int bit = 4 * cc + (j >> 1) + 16 * (j & 1);
                     const int dim = p.k_perm ? 4 * bit + g : 32 * g + bit;
@@ -177,8 +183,8 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
         for (int r = 0; r < 4; ++r) {
             const int tok = 4 * g + r;
             tv[r] = t0 + tok < t_end;
-            kn[r] = tv[r] ? load_f16(knb + (int64_t)tok * p.k_norm.stride_row) : 0.f;
-            vn[r] = tv[r] ? load_f16(vnb + (int64_t)tok * p.v_norm.stride_row) : 0.f;
+            kn[r] = tv[r] ? load_f16(knb + (int64_t)tok * p.k_norm.stride_row) * p.k_cinv : 0.f;
+            vn[r] = tv[r] ? load_f16(vnb + (int64_t)tok * p.v_norm.stride_row) * p.v_cinv : 0.f;
             if (KQJL) {
                 const uint8_t* krb = tile_base(p.k_rnorm, blk, s, kh, paged) + (int64_t)st * p.k_rnorm.stride_row;
                 krn[r] = tv[r] ? load_f16(krb + (int64_t)tok * p.k_rnorm.stride_row) * p.corr_scale : 0.f;
@@ -216,7 +222,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             tq_u32x4 a = {kd[4 * cc], kd[4 * cc + 1], kd[4 * cc + 2], kd[4 * cc + 3]};
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), qop[cc], s1, 0, 0, 0);
+            const tq_half8 ah = __builtin_bit_cast(tq_half8, a);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qop[cc], s1, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[cc], s1, 0, 0, 0);
         }
         tq_floatx4 s2 = {0.f, 0.f, 0.f, 0.f};
         if (KQJL) {
@@ -355,7 +363,8 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     const int lane = threadIdx.x;
     int L = p.seq_lens[s];
     L = L < p.cap ? L : p.cap;
-    const int nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
+    int nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
+    nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
     const int64_t base = sh * p.n_chunks;
     float M = kNegInf;
     for (int c = 0; c < nch; ++c) M = fmaxf(M, p.ws_m[base + c]);
@@ -477,6 +486,10 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     p.v_norm = to_region(v->norm);
     p.k_cent = k->centroids;
     p.v_cent = v->centroids;
+    p.k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
+    p.v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
+    p.k_cinv = 1.f / p.k_cscale;
+    p.v_cinv = 1.f / p.v_cscale;
     p.k_perm = k->signs_permuted ? 1 : 0;
     p.block_size = block_size;
     p.num_blocks = block_tables ? num_blocks : (int64_t)1 << 62;

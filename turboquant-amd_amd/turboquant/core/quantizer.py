@@ -13,7 +13,7 @@ from typing import Optional
 import torch
 
 from turboquant import _lib
-from turboquant.core.rotation import is_wht_matrix, wht_scale
+from turboquant.core.rotation import wht_magnitude
 
 
 @dataclass
@@ -91,12 +91,13 @@ def _rotation_mode(rotation_matrix: Optional[torch.Tensor], d: int) -> tuple[int
         return 0, 1.0
     if tuple(rotation_matrix.shape) != (d, d):
         raise ValueError(f"rotation_matrix must be [{d}, {d}], got {tuple(rotation_matrix.shape)}")
-    if not is_wht_matrix(rotation_matrix.float()):
+    h = wht_magnitude(rotation_matrix)
+    if h is None:
         raise NotImplementedError(
-            "polarquant_compress on the GPU supports rotation_matrix=None or make_wht_matrix(d); "
-            "use turboquant.kernels.packed_compress.compress_k for a general rotation"
+            "polarquant_compress on the GPU supports rotation_matrix=None or a Walsh-Hadamard matrix "
+            "(make_wht_matrix); use turboquant.kernels.packed_compress.compress_k for a general rotation"
         )
-    return 1, wht_scale(d)
+    return 1, h
 
 
 def polarquant_compress(

@@ -31,13 +31,38 @@ def wht_scale(d: int = 128) -> float:
     return float(make_wht_matrix(d)[0, 0].item())
 
 
-def is_wht_matrix(rotation_matrix: torch.Tensor) -> bool:
-    """True when rotation_matrix equals make_wht_matrix(d) exactly (any device)."""
+def _sylvester_signs(d: int) -> torch.Tensor:
+    i = torch.arange(d).unsqueeze(1)
+    j = torch.arange(d).unsqueeze(0)
+    x = i & j
+    parity = torch.zeros_like(x)
+    while bool(x.any()):
+        parity ^= x & 1
+        x = x >> 1
+    return 1 - 2 * parity  # (-1)^popcount(i & j)
+
+
+def wht_magnitude(rotation_matrix: torch.Tensor) -> float | None:
+    """h if rotation_matrix == (-1)^popcount(i&j) * h exactly for one float h, else None.
+
+    make_wht_matrix on different devices can round h differently; the kernels take the
+    caller's own h, so any such matrix is accepted."""
     if rotation_matrix.dim() != 2 or rotation_matrix.shape[0] != rotation_matrix.shape[1]:
-        return False
+        return None
     d = rotation_matrix.shape[0]
-    ref = make_wht_matrix(d, device=rotation_matrix.device).to(rotation_matrix.dtype)
-    return bool(torch.equal(rotation_matrix, ref))
+    if d == 0 or d & (d - 1):
+        return None
+    m = rotation_matrix.detach().float().cpu()
+    h = m[0, 0]
+    if not bool(h > 0):
+        return None
+    return float(h) if bool(torch.equal(m, _sylvester_signs(d).float() * h)) else None
+
+
+def is_wht_matrix(rotation_matrix: torch.Tensor) -> bool:
+    """True when rotation_matrix is a normalized Walsh-Hadamard matrix (sign pattern of
+    make_wht_matrix, one magnitude)."""
+    return wht_magnitude(rotation_matrix) is not None
 
 
 def fuse_rotation_into_qkv_proj(

@@ -100,11 +100,13 @@ def packed_attention(Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
     kv.rnorm = _contig_region(ts["k_r_norm"], 2, Sk)
     kv.centroids = cb.data_ptr()
     kv.bits, kv.qjl, kv.signs_permuted = 2, 1, 1
+    kv.centroid_scale = _lib.centroid_scale(cb)
     vv = _lib.TQKVView()
     vv.idx = _contig_region(ts["v_idx_packed"], D // 4, Sk)
     vv.norm = _contig_region(ts["v_norm"], 2, Sk)
     vv.centroids = cb.data_ptr()
     vv.bits, vv.qjl, vv.signs_permuted = 2, 0, 0
+    vv.centroid_scale = kv.centroid_scale
 
     seq_lens = torch.full((BH,), Sk, dtype=torch.int32, device=dev)
     out = torch.empty((BH, 1, D), dtype=torch.float16, device=dev)

@@ -163,6 +163,7 @@ def paged_view(cache: torch.Tensor, fmt: PagedKVFormat, centroids: torch.Tensor)
     view.bits = fmt.bits
     view.qjl = int(fmt.qjl)
     view.signs_permuted = 0
+    view.centroid_scale = _lib.centroid_scale(centroids)
     return view
 
 

@@ -35,6 +35,7 @@ def _aos_view(cache: torch.Tensor, kv: int, centroids: torch.Tensor) -> _lib.TQK
     view.norm = _lib.TQRegion(base + DQ3, sb, sh, 0, sr)
     view.centroids = centroids.data_ptr()
     view.bits, view.qjl, view.signs_permuted = 3, 0, 0
+    view.centroid_scale = _lib.centroid_scale(centroids)
     return view
 
 
