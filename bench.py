@@ -259,6 +259,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["config2", "config3", "config4", "config5"], default=None)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (reference for rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -271,6 +273,13 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     steps, warmup = args.steps, args.warmup
+    if args.copy_calibration:
+        src = torch.ones(1 << 26, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print("# copy calibration: 268435456 bytes read, 268435456 bytes written", file=sys.stderr, flush=True)
+        del src, dst
     extra = {}
     import random
     rng = random.Random(3)

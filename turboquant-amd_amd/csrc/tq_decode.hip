@@ -59,12 +59,12 @@ struct DecodeParams {
     unsigned long long* skip_stats;
 };
 
-__device__ __forceinline__ const uint8_t* tile_base(const Region& r, int64_t blk, int64_t seq, int kh, bool paged) {
-    return r.ptr + blk * r.stride_block + (int64_t)kh * r.stride_head + (paged ? 0 : seq * r.stride_seq);
-}
+// Buffer resource over [base, base + 2 GiB): loads at offsets >= kOOB return zero, which is how
+// rows past the end of a sequence are masked without branches.
+constexpr uint32_t kOOB = 0x80000000u;
 
-__device__ __forceinline__ float load_f16(const uint8_t* p) {
-    return tq_f16_to_f32(*reinterpret_cast<const uint16_t*>(p));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint8_t* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
 
 // Half2 dword from two fp16 lanes of two dwords: selects the low (s=0) or high (s=1) halves.
@@ -72,14 +72,98 @@ __device__ __forceinline__ uint32_t pick_halves(uint32_t hi_src, uint32_t lo_src
     return __builtin_amdgcn_perm(hi_src, lo_src, s ? 0x07060302u : 0x05040100u);
 }
 
+__device__ __forceinline__ float f16lo(uint32_t w) { return tq_f16_to_f32(w & 0xffffu); }
+__device__ __forceinline__ float f16hi(uint32_t w) { return tq_f16_to_f32(w >> 16); }
+
+// Raw per-lane data of one 16-token tile (see the load plan in decode_kernel).
 template <int KB, bool KQJL, int VB>
+struct TileRaw {
+    uint32_t kw[KB];                      // 32 dims of token n: 32*KB bits
+    uint32_t ks;                          // 32 sign bits of token n
+    uint32_t kn[2], krn[2], vn[2];        // fp16 norms of tokens 4g..4g+3
+    uint32_t vw[4][VB == 3 ? 2 : 1];      // dims 8n..8n+7 of tokens 4g..4g+3
+};
+
+struct LaneOffsets {
+    uint32_t kidx, ksig;
+    uint32_t kn[4], krn[4], vn[4];        // per token 4g+r (u16 loads)
+    uint32_t kn8, krn8, vn8;              // 4 consecutive fp16 (b64 load) when rows are 2 bytes apart
+    uint32_t vidx[4];
+    int vshift;                           // VB == 3: bit offset of the 24-bit field in the 8-byte window
+};
+
+struct TileBases {
+    const uint8_t *kidx, *ksig, *kn, *krn, *vidx, *vn;
+};
+
+template <int KB, bool KQJL, int VB>
+__device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const TileBases& b, const LaneOffsets& o,
+                                          int nvalid, int n, int g, bool norm_vec) {
+    const bool krow = n < nvalid;
+    {
+        auto r = make_rsrc(b.kidx);
+        const uint32_t off = krow ? o.kidx : kOOB;
+        if (KB == 2) {
+            tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+            t.kw[0] = v[0]; t.kw[1 % KB] = v[1];
+        } else if (KB == 3) {
+            typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+            u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+            t.kw[0] = v[0]; t.kw[1 % KB] = v[1]; t.kw[2 % KB] = v[2];
+        } else {
+            tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+            t.kw[0] = v[0]; t.kw[1 % KB] = v[1]; t.kw[2 % KB] = v[2]; t.kw[3 % KB] = v[3];
+        }
+    }
+    if (KQJL) t.ks = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(b.ksig), krow ? o.ksig : kOOB, 0, 0);
+    const bool all4 = 4 * g + 3 < nvalid;
+    if (norm_vec && all4) {
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(b.kn), o.kn8, 0, 0);
+        t.kn[0] = a[0]; t.kn[1] = a[1];
+        tq_u32x2 c = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(b.vn), o.vn8, 0, 0);
+        t.vn[0] = c[0]; t.vn[1] = c[1];
+        if (KQJL) {
+            tq_u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(b.krn), o.krn8, 0, 0);
+            t.krn[0] = d[0]; t.krn[1] = d[1];
+        }
+    } else {
+        uint32_t kv[4], vv[4], rv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool ok = 4 * g + r < nvalid;
+            kv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(b.kn), ok ? o.kn[r] : kOOB, 0, 0);
+            vv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(b.vn), ok ? o.vn[r] : kOOB, 0, 0);
+            if (KQJL) rv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(b.krn), ok ? o.krn[r] : kOOB, 0, 0);
+        }
+        t.kn[0] = kv[0] | (kv[1] << 16); t.kn[1] = kv[2] | (kv[3] << 16);
+        t.vn[0] = vv[0] | (vv[1] << 16); t.vn[1] = vv[2] | (vv[3] << 16);
+        if (KQJL) { t.krn[0] = rv[0] | (rv[1] << 16); t.krn[1] = rv[2] | (rv[3] << 16); }
+    }
+    auto rv = make_rsrc(b.vidx);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t off = (4 * g + r < nvalid) ? o.vidx[r] : kOOB;
+        if (VB == 3) {
+            tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
+            t.vw[r][0] = w[0]; t.vw[r][VB == 3 ? 1 : 0] = w[1];
+        } else if (VB == 4) {
+            t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0);
+        } else {
+            t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, 0, 0);
+        }
+    }
+}
+
+// QCOLS: the GQA group fits in 8 heads, so the 16 columns of the QK product carry q (hi part,
+// columns 0..7) and q - hi (lo part, columns 8..15); a lane swizzle merges them.
+template <int KB, bool KQJL, int VB, bool QCOLS>
 __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     constexpr int KENT = 1 << (2 * KB);
     constexpr int VENT = 1 << (2 * VB);
     __shared__ uint32_t s_ktab[KENT * 32];
     __shared__ uint32_t s_vtab[VENT * 32];
 
-    // Build the pair tables: entry e -> half2(c[e & (2^b - 1)], c[e >> b]).
+    // Pair tables: entry e -> half2(c[e & (2^b - 1)], c[e >> b]) * cscale, 32 bank replicas.
     for (int i = threadIdx.x; i < KENT * 32; i += 256) {
         int e = i >> 5;
         s_ktab[i] = tq_pack_half2(p.k_cent[e & ((1 << KB) - 1)] * p.k_cscale, p.k_cent[e >> KB] * p.k_cscale);
@@ -91,9 +175,9 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;   // lane group
+    const int g = lane >> 4;   // lane group: dims 32g.. (K), tokens 4g..4g+3 (scores, V)
     const int n = lane & 15;   // head column (Q/P/out), token row (K loads), dim row (V)
-    const int bank = lane & 31;
+    const uint32_t bank4 = (uint32_t)(lane & 31) << 2;
 
     const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int c = (int)(unit % p.n_chunks);
@@ -111,12 +195,13 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     const bool paged = p.bt != nullptr;
 
     // ---- query operands (B of the QK products), pre-scaled into the log2 domain ----
-    // q is split into fp16 hi + lo parts so the MSE score keeps ~22 bits of q.
-    const int head = kh * p.group + n;
+    const int hq_col = QCOLS ? (n & 7) : n;
+    const int head = kh * p.group + hq_col;
     const bool hvalid = n < p.group;
+    const bool qload = hq_col < p.group;
     tq_half8 qop[4];
-    tq_half8 qlo[4];
-    tq_half8 qpop[4];
+    tq_half8 qlo[QCOLS ? 1 : 4];
+    tq_half8 qpop[KQJL ? 4 : 1];
     {
         const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh;
         const int64_t qpoff = s * p.qp_ss + (int64_t)head * p.qp_sh;
@@ -124,19 +209,87 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
         for (int cc = 0; cc < 4; ++cc) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                float qv = hvalid ? tq_load1(p.q, qoff + 32 * g + 8 * cc + j, p.q_dtype) * p.q_scale : 0.f;
+                const float qv = qload ? tq_load1(p.q, qoff + 32 * g + 8 * cc + j, p.q_dtype) * p.q_scale : 0.f;
                 const _Float16 qh = (_Float16)qv;
-                qop[cc][j] = qh;
-                qlo[cc][j] = (_Float16)(qv - (float)qh);
+                const _Float16 ql = (_Float16)(qv - (float)qh);
+                if (QCOLS) {
+                    qop[cc][j] = n < 8 ? qh : ql;
+                } else {
+                    qop[cc][j] = qh;
+                    qlo[cc % (QCOLS ? 1 : 4)][j] = ql;
+                }
                 if (KQJL) {
                     const int bit = 4 * cc + (j >> 1) + 16 * (j & 1);
                     const int dim = p.k_perm ? 4 * bit + g : 32 * g + bit;
-                    float qpv = hvalid ? -tq_load1(p.qp, qpoff + dim, p.q_dtype) * p.q_scale : 0.f;
-                    qpop[cc][j] = (_Float16)qpv;
+                    const float qpv = hvalid ? -tq_load1(p.qp, qpoff + dim, p.q_dtype) * p.q_scale : 0.f;
+                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)qpv;
                 }
             }
         }
     }
+
+    // ---- loop-invariant per-lane byte offsets inside a tile ----
+    LaneOffsets o;
+    o.kidx = (uint32_t)(n * p.k_idx.stride_row + 4 * KB * g);
+    o.ksig = KQJL ? (uint32_t)(n * p.k_sig.stride_row + 4 * g) : 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int tok = 4 * g + r;
+        o.kn[r] = (uint32_t)(tok * p.k_norm.stride_row);
+        o.vn[r] = (uint32_t)(tok * p.v_norm.stride_row);
+        o.krn[r] = KQJL ? (uint32_t)(tok * p.k_rnorm.stride_row) : 0u;
+        if (VB == 3) {
+            const int byte0 = 3 * n;
+            int start = (byte0 >> 2) << 2;
+            start = start < 40 ? start : 40;      // 8-byte window kept inside the 48-byte row
+            o.vidx[r] = (uint32_t)(tok * p.v_idx.stride_row + start);
+            o.vshift = 8 * (byte0 - start);
+        } else {
+            o.vidx[r] = (uint32_t)(tok * p.v_idx.stride_row + VB * n);
+            o.vshift = 0;
+        }
+    }
+    o.kn8 = o.kn[0];
+    o.vn8 = o.vn[0];
+    o.krn8 = o.krn[0];
+    // Norm rows 2 bytes apart inside allocated blocks: one 8-byte load per region.
+    const bool norm_vec = paged && p.k_norm.stride_row == 2 && p.v_norm.stride_row == 2 &&
+                          (!KQJL || p.k_rnorm.stride_row == 2);
+
+    // Per-unit parts of the tile bases (uniform).
+    const int64_t seq_off_k = paged ? 0 : s * p.k_idx.stride_seq;
+    auto bases_for = [&](int64_t blk, int st) {
+        TileBases b;
+        const int64_t so = paged ? 0 : s;
+        b.kidx = p.k_idx.ptr + blk * p.k_idx.stride_block + kh * p.k_idx.stride_head + so * p.k_idx.stride_seq + st * p.k_idx.stride_row;
+        b.kn = p.k_norm.ptr + blk * p.k_norm.stride_block + kh * p.k_norm.stride_head + so * p.k_norm.stride_seq + st * p.k_norm.stride_row;
+        b.vidx = p.v_idx.ptr + blk * p.v_idx.stride_block + kh * p.v_idx.stride_head + so * p.v_idx.stride_seq + st * p.v_idx.stride_row;
+        b.vn = p.v_norm.ptr + blk * p.v_norm.stride_block + kh * p.v_norm.stride_head + so * p.v_norm.stride_seq + st * p.v_norm.stride_row;
+        if (KQJL) {
+            b.ksig = p.k_sig.ptr + blk * p.k_sig.stride_block + kh * p.k_sig.stride_head + so * p.k_sig.stride_seq + st * p.k_sig.stride_row;
+            b.krn = p.k_rnorm.ptr + blk * p.k_rnorm.stride_block + kh * p.k_rnorm.stride_head + so * p.k_rnorm.stride_seq + st * p.k_rnorm.stride_row;
+        } else {
+            b.ksig = b.kidx;
+            b.krn = b.kn;
+        }
+        return b;
+    };
+    (void)seq_off_k;
+    // Tile t0 -> (bases, rows valid); a block-table entry outside [0, num_blocks) reads nothing.
+    auto locate = [&](int t0, TileBases& b, int& nvalid) {
+        const int lb = t0 / p.block_size;
+        const int st = t0 - lb * p.block_size;
+        int64_t blk = lb;
+        nvalid = (t_end - t0 < 16) ? t_end - t0 : 16;
+        if (paged) {
+            blk = p.bt[s * p.bt_stride + lb];
+            if (blk < 0 || blk >= p.num_blocks) {
+                blk = 0;
+                nvalid = 0;
+            }
+        }
+        b = bases_for(blk, st);
+    };
 
     float m = kNegInf;
     float lsum = 0.f;
@@ -146,85 +299,35 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     unsigned long long n_skip = 0, n_tot = 0;
     const bool sparse = p.thresh > 0.f;
 
+    TileRaw<KB, KQJL, VB> cur = {}, nxt = {};
+    int cur_valid, nxt_valid = 0;
+    {
+        TileBases b;
+        locate(t_begin, b, cur_valid);
+        load_tile<KB, KQJL, VB>(cur, b, o, cur_valid, n, g, norm_vec);
+    }
+
     for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-        const int lb = t0 / p.block_size;
-        const int st = t0 - lb * p.block_size;  // first row of the 16-row sub-tile
-        int64_t blk;
-        if (paged) {
-            blk = p.bt[s * p.bt_stride + lb];
-            if (blk < 0 || blk >= p.num_blocks) continue;
-        } else {
-            blk = lb;
-        }
-
-        // ---------------- loads ----------------
-        const uint8_t* kib = tile_base(p.k_idx, blk, s, kh, paged) + (int64_t)st * p.k_idx.stride_row;
-        const uint8_t* knb = tile_base(p.k_norm, blk, s, kh, paged) + (int64_t)st * p.k_norm.stride_row;
-        const uint8_t* vib = tile_base(p.v_idx, blk, s, kh, paged) + (int64_t)st * p.v_idx.stride_row;
-        const uint8_t* vnb = tile_base(p.v_norm, blk, s, kh, paged) + (int64_t)st * p.v_norm.stride_row;
-
-        const bool kvalid = t0 + n < t_end;
-        uint32_t kw[KB];
-#pragma unroll
-        for (int i = 0; i < KB; ++i) kw[i] = 0;
-        if (kvalid) {
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(kib + (int64_t)n * p.k_idx.stride_row + 4 * KB * g);
-#pragma unroll
-            for (int i = 0; i < KB; ++i) kw[i] = src[i];
-        }
-        uint32_t ksig = 0;
-        if (KQJL && kvalid) {
-            const uint8_t* ksb = tile_base(p.k_sig, blk, s, kh, paged) + (int64_t)st * p.k_sig.stride_row;
-            ksig = *reinterpret_cast<const uint32_t*>(ksb + (int64_t)n * p.k_sig.stride_row + 4 * g);
-        }
-        float kn[4], krn[4], vn[4];
-        bool tv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = 4 * g + r;
-            tv[r] = t0 + tok < t_end;
-            kn[r] = tv[r] ? load_f16(knb + (int64_t)tok * p.k_norm.stride_row) * p.k_cinv : 0.f;
-            vn[r] = tv[r] ? load_f16(vnb + (int64_t)tok * p.v_norm.stride_row) * p.v_cinv : 0.f;
-            if (KQJL) {
-                const uint8_t* krb = tile_base(p.k_rnorm, blk, s, kh, paged) + (int64_t)st * p.k_rnorm.stride_row;
-                krn[r] = tv[r] ? load_f16(krb + (int64_t)tok * p.k_rnorm.stride_row) * p.corr_scale : 0.f;
-            }
-        }
-        // V words: lane n needs dims 8n..8n+7 (VB bytes at byte VB*n) of tokens 4g..4g+3.
-        uint32_t vw[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            vw[r] = 0;
-            if (tv[r]) {
-                const uint8_t* row = vib + (int64_t)(4 * g + r) * p.v_idx.stride_row;
-                if (VB == 4) {
-                    vw[r] = reinterpret_cast<const uint32_t*>(row)[n];
-                } else if (VB == 2) {
-                    vw[r] = reinterpret_cast<const uint16_t*>(row)[n];
-                } else {
-                    const int byte0 = 3 * n;
-                    const int d0 = byte0 >> 2;
-                    const int d1 = (d0 + 1 < 12) ? d0 + 1 : 11;
-                    const uint32_t* rw = reinterpret_cast<const uint32_t*>(row);
-                    vw[r] = __builtin_amdgcn_alignbit(rw[d1], rw[d0], 8 * (byte0 & 3)) & 0xffffffu;
-                }
-            }
+        const bool more = t0 + 16 < t_end;
+        if (more) {  // prefetch the next tile while this one is computed
+            TileBases b;
+            locate(t0 + 16, b, nxt_valid);
+            load_tile<KB, KQJL, VB>(nxt, b, o, nxt_valid, n, g, norm_vec);
         }
 
         // ---------------- QK products ----------------
-        uint32_t kd[16];
-#pragma unroll
-        for (int pp = 0; pp < 16; ++pp) {
-            const uint32_t e = tq_field(kw, 2 * KB * pp, 2 * KB);
-            kd[pp] = s_ktab[(e << 5) | bank];
-        }
         tq_floatx4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
-            tq_u32x4 a = {kd[4 * cc], kd[4 * cc + 1], kd[4 * cc + 2], kd[4 * cc + 3]};
+            tq_u32x4 a;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t e = tq_field(cur.kw, 2 * KB * (4 * cc + j), 2 * KB);
+                a[j] = s_ktab[(e << 5) | (bank4 >> 2)];
+            }
             const tq_half8 ah = __builtin_bit_cast(tq_half8, a);
             s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qop[cc], s1, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[cc], s1, 0, 0, 0);
+            if (!QCOLS) s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[cc % (QCOLS ? 1 : 4)], s1, 0, 0, 0);
         }
         tq_floatx4 s2 = {0.f, 0.f, 0.f, 0.f};
         if (KQJL) {
@@ -234,34 +337,61 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int pp = 4 * cc + j;
-                    a[j] = ((ksig << (15 - pp)) & 0x80008000u) | 0x3C003C00u;
+                    a[j] = ((cur.ks << (15 - pp)) & 0x80008000u) | 0x3C003C00u;
                 }
-                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), qpop[cc], s2, 0, 0, 0);
+                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), qpop[cc % (KQJL ? 4 : 1)], s2, 0, 0, 0);
             }
+        }
+        float s1v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s1v[r] = s1[r];
+        if (QCOLS) {
+            // column n (hi part) + column n ^ 8 (lo part): swizzle xor 8 inside each 16-lane row.
+            // Scalar copies on purpose: shuffling elements of an ext_vector in place miscompiles
+            // (the backend reuses one shuffle result for the other elements).
+            int sw[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sw[r] = __builtin_amdgcn_ds_swizzle(__float_as_int(s1v[r]), 0x201f);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s1v[r] += __int_as_float(sw[r]);
         }
 
         // ---------------- online softmax ----------------
-        float sc[4];
+        float sc[4], kn[4], vn[4];
+        kn[0] = f16lo(cur.kn[0]); kn[1] = f16hi(cur.kn[0]); kn[2] = f16lo(cur.kn[1]); kn[3] = f16hi(cur.kn[1]);
+        vn[0] = f16lo(cur.vn[0]); vn[1] = f16hi(cur.vn[0]); vn[2] = f16lo(cur.vn[1]); vn[3] = f16hi(cur.vn[1]);
         float mt = kNegInf;
+        bool tv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float v = kn[r] * s1[r];
-            if (KQJL) v = __builtin_fmaf(krn[r], s2[r], v);
+            tv[r] = 4 * g + r < cur_valid;
+            float v = kn[r] * p.k_cinv * s1v[r];
+            if (KQJL) {
+                const float rn = (r & 1) ? f16hi(cur.krn[r >> 1]) : f16lo(cur.krn[r >> 1]);
+                v = __builtin_fmaf(rn * p.corr_scale, s2[r], v);
+            }
             sc[r] = tv[r] ? v : kNegInf;
             mt = fmaxf(mt, sc[r]);
         }
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, mt), 0x401f)));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
         const float m_new = fmaxf(m, mt);
-        const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+        const float mref = m_new == kNegInf ? 0.f : m_new;
         float pr[4];
         float psum = 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            pr[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
+            pr[r] = __builtin_amdgcn_exp2f(sc[r] - mref);
             psum += pr[r];
         }
-        lsum = __builtin_fmaf(lsum, alpha, psum);
+        // Rescale only when some head's running max moved (alpha == 1 otherwise).
+        if (__ballot(hvalid && m_new > m) != 0) {
+            const float alpha = __builtin_amdgcn_exp2f(m - mref);
+            lsum *= alpha;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+        }
+        lsum += psum;
         m = m_new;
 
         // Sparse-V: token significant when some head of the group has p > thresh.
@@ -271,12 +401,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
             uint64_t orall = 0;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                uint64_t bal = __ballot(hvalid && pr[r] > p.thresh);
+                const uint64_t bal = __ballot(hvalid && pr[r] > p.thresh);
                 orall |= bal;
                 sig[r] = ((bal >> (16 * g)) & 0xffffull) != 0;
             }
             any = orall != 0;
-            if (n == 0) {
+            if (p.skip_stats && n == 0) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     n_tot += tv[r] ? 1 : 0;
@@ -285,24 +415,27 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
             }
         }
 
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-
         if (any) {
-            // P^T operand: tokens 4g..4g+3 of head n, V norm folded in.
             float pv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pv[r] = (tv[r] && sig[r]) ? pr[r] * vn[r] : 0.f;
+            for (int r = 0; r < 4; ++r) pv[r] = (tv[r] && sig[r]) ? pr[r] * (vn[r] * p.v_cinv) : 0.f;
             tq_u32x2 bw = {tq_pack_half2(pv[0], pv[1]), tq_pack_half2(pv[2], pv[3])};
             const tq_half4 bop = __builtin_bit_cast(tq_half4, bw);
             // V dequant: vp[r][q] = half2(dims 8n+2q, 8n+2q+1) of token 4g+r.
             uint32_t vp[4][4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+                uint32_t w;
+                if (VB == 3) {
+                    const uint32_t hi = cur.vw[r][VB == 3 ? 1 : 0], lo = cur.vw[r][0];
+                    w = o.vshift >= 32 ? (hi >> (o.vshift - 32)) : __builtin_amdgcn_alignbit(hi, lo, o.vshift);
+                } else {
+                    w = cur.vw[r][0];
+                }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const uint32_t e = (vw[r] >> (2 * VB * q)) & (VENT - 1);
-                    vp[r][q] = s_vtab[(e << 5) | bank];
+                    const uint32_t e = (w >> (2 * VB * q)) & (VENT - 1);
+                    vp[r][q] = s_vtab[(e << 5) | (bank4 >> 2)];
                 }
             }
 #pragma unroll
@@ -312,9 +445,13 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
                 acc[nn] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(tq_half4, aw), bop, acc[nn], 0, 0, 0);
             }
         }
+        if (more) {
+            cur = nxt;
+            cur_valid = nxt_valid;
+        }
     }
 
-    lsum += __shfl_xor(lsum, 16);
+    lsum += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, lsum), 0x401f));
     lsum += __shfl_xor(lsum, 32);
 
     if (hvalid) {
@@ -511,8 +648,13 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     const int64_t grid = (units + 3) / 4;
     if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
     hipStream_t st = (hipStream_t)stream;
-#define TQ_DEC(KB, KQ, VB) \
-    hipLaunchKernelGGL((decode_kernel<KB, KQ, VB>), dim3((unsigned)grid), dim3(256), 0, st, p)
+#define TQ_DEC(KB, KQ, VB)                                                                           \
+    do {                                                                                             \
+        if (group <= 8)                                                                              \
+            hipLaunchKernelGGL((decode_kernel<KB, KQ, VB, true>), dim3((unsigned)grid), dim3(256), 0, st, p); \
+        else                                                                                         \
+            hipLaunchKernelGGL((decode_kernel<KB, KQ, VB, false>), dim3((unsigned)grid), dim3(256), 0, st, p); \
+    } while (0)
     const int key = (k->bits * 10 + v->bits) * 2 + (k->qjl ? 1 : 0);
     switch (key) {
         case 44: TQ_DEC(2, false, 2); break;
