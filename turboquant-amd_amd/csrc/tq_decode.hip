@@ -6,15 +6,23 @@
 // replicated 32x across LDS banks so lanes 0-31 never conflict.
 //
 // Per tile (all MFMA accumulation in fp32):
-//   S^T[token][head]  = K_dq[16 x 128] . Q^T[128 x 16]      4 x mfma_f32_16x16x32_f16
-//   QJL^T[token][head]= (+-1)[16 x 128] . (-QP)^T            4 x mfma_f32_16x16x32_f16
+//   S^T[token][head]   = K_dq[16 x 128] . Q^T[128 x 16]       4 x mfma_f32_16x16x32_f16
+//   QJL^T[token][head] = (+-1)[16 x 128] . (-QP)^T             4 x mfma_f32_16x16x32_f16
 //   score = norm * S + corr_scale * rnorm * QJL   (log2 domain: Q pre-scaled by sm_scale*log2 e)
 //   online softmax per head; Sparse-V mask from a ballot over the GQA group
 //   acc^T[dim][head] += V_dq^T[128 x 16] . (p * vnorm)[16 x 16]  8 x mfma_f32_16x16x16f16
 // MFMA output layout (16x16): lane l holds rows 4*(l/16)+r, column l%16, so after the QK
 // product lane (head n = l%16, g = l/16) owns tokens 4g..4g+3 of head n, which is exactly the
 // B-operand layout of the PV product: no data movement between the two products.
-// Each unit writes (m, l, acc[128]) per head; tq_decode_reduce combines chunks:
+//
+// Memory: every per-token stream is read with buffer loads whose base (the tile's address,
+// computed once per tile in scalar registers) is uniform and whose per-lane offsets are loop
+// invariant; the next tile is loaded while the current one is computed (two register sets,
+// loop unrolled by two).  In a paged cache all rows of a block are allocated, so tiles are read
+// whole and rows past the sequence end are masked in the softmax; in a contiguous layout rows
+// past the end get an out-of-range offset and read as zero.
+//
+// Each unit writes (m, l, acc[128]) per head; decode_reduce_kernel combines chunks:
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:121-140)
 #include "tq_common.h"
 
@@ -22,11 +30,9 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
+constexpr uint32_t kOOB = 0x80000000u;  // >= num_records: buffer loads return zero
 
-struct Region {
-    const uint8_t* ptr;
-    int64_t stride_block, stride_head, stride_seq, stride_row;
-};
+enum { R_KIDX = 0, R_KSIG, R_KNORM, R_KRNORM, R_VIDX, R_VNORM, R_COUNT };
 
 struct DecodeParams {
     const void* q;
@@ -34,13 +40,17 @@ struct DecodeParams {
     const void* qp;
     int64_t qp_ss, qp_sh;
     int q_dtype;
+    int q_vec;          // q and qp rows 16-byte aligned: vector loads
     int num_seqs, hq, hkv, group;
-    Region k_idx, k_sig, k_norm, k_rnorm;
-    Region v_idx, v_norm;
+    const uint8_t* rptr[R_COUNT];
+    int64_t rhead[R_COUNT];
+    int64_t rseq[R_COUNT];
+    int32_t rrow[R_COUNT];
+    int64_t sb_k, sb_v;  // block strides shared by the K regions and by the V regions (paged)
     const float* k_cent;
     const float* v_cent;
-    float k_cscale, v_cscale;  // tables hold fp16(c * cscale) ...
-    float k_cinv, v_cinv;      // ... and norms carry 1 / cscale
+    float k_cscale, v_cscale;  // tables hold fp16(c * cscale); the scale is divided back out
+    float v_cinv;
     int k_perm;
     int block_size;
     int64_t num_blocks;
@@ -48,7 +58,8 @@ struct DecodeParams {
     int64_t bt_stride;
     int max_blocks;
     const int32_t* seq_lens;
-    float q_scale;     // sm_scale * log2(e)
+    float q_scale;     // sm_scale * log2(e) / k_cscale  (MSE operand)
+    float qp_scale;    // sm_scale * log2(e)             (QJL operand)
     float corr_scale;
     float thresh;      // > 0: Sparse-V on
     int chunk;
@@ -58,10 +69,6 @@ struct DecodeParams {
     float* ws_l;
     unsigned long long* skip_stats;
 };
-
-// Buffer resource over [base, base + 2 GiB): loads at offsets >= kOOB return zero, which is how
-// rows past the end of a sequence are masked without branches.
-constexpr uint32_t kOOB = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint8_t* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, 0x7fffffff, 0x00020000);
@@ -75,33 +82,33 @@ __device__ __forceinline__ uint32_t pick_halves(uint32_t hi_src, uint32_t lo_src
 __device__ __forceinline__ float f16lo(uint32_t w) { return tq_f16_to_f32(w & 0xffffu); }
 __device__ __forceinline__ float f16hi(uint32_t w) { return tq_f16_to_f32(w >> 16); }
 
-// Raw per-lane data of one 16-token tile (see the load plan in decode_kernel).
+// Raw per-lane data of one 16-token tile.
 template <int KB, bool KQJL, int VB>
 struct TileRaw {
-    uint32_t kw[KB];                      // 32 dims of token n: 32*KB bits
-    uint32_t ks;                          // 32 sign bits of token n
+    uint32_t kw[KB];                      // dims 32g..32g+31 of token n: 32*KB bits
+    uint32_t ks;                          // sign bits of the same dims
     uint32_t kn[2], krn[2], vn[2];        // fp16 norms of tokens 4g..4g+3
     uint32_t vw[4][VB == 3 ? 2 : 1];      // dims 8n..8n+7 of tokens 4g..4g+3
 };
 
-struct LaneOffsets {
-    uint32_t kidx, ksig;
-    uint32_t kn[4], krn[4], vn[4];        // per token 4g+r (u16 loads)
-    uint32_t kn8, krn8, vn8;              // 4 consecutive fp16 (b64 load) when rows are 2 bytes apart
+struct LaneOff {
+    uint32_t kidx, ksig, kn, krn, vn;     // kn/krn/vn: token 4g (next tokens at +row stride)
     uint32_t vidx[4];
-    int vshift;                           // VB == 3: bit offset of the 24-bit field in the 8-byte window
+    int vshift;                           // VB == 3: bit offset of the 24-bit field in its 8-byte window
 };
 
-struct TileBases {
-    const uint8_t *kidx, *ksig, *kn, *krn, *vidx, *vn;
+struct Tile {
+    const uint8_t* base[R_COUNT];
+    int nvalid;                           // rows of this tile inside the sequence (0: unreadable)
 };
 
-template <int KB, bool KQJL, int VB>
-__device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const TileBases& b, const LaneOffsets& o,
-                                          int nvalid, int n, int g, bool norm_vec) {
-    const bool krow = n < nvalid;
+// MASKED: rows >= nvalid may lie outside the allocation (contiguous layout, last tile).
+template <int KB, bool KQJL, int VB, bool MASKED>
+__device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const Tile& tl, const LaneOff& o,
+                                          const int32_t* rrow, int n, int g, bool norm_vec) {
+    const bool krow = !MASKED || n < tl.nvalid;
     {
-        auto r = make_rsrc(b.kidx);
+        auto r = make_rsrc(tl.base[R_KIDX]);
         const uint32_t off = krow ? o.kidx : kOOB;
         if (KB == 2) {
             tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
@@ -115,34 +122,37 @@ __device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const TileBa
             t.kw[0] = v[0]; t.kw[1 % KB] = v[1]; t.kw[2 % KB] = v[2]; t.kw[3 % KB] = v[3];
         }
     }
-    if (KQJL) t.ks = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(b.ksig), krow ? o.ksig : kOOB, 0, 0);
-    const bool all4 = 4 * g + 3 < nvalid;
-    if (norm_vec && all4) {
-        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(b.kn), o.kn8, 0, 0);
+    if (KQJL) t.ks = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(tl.base[R_KSIG]), krow ? o.ksig : kOOB, 0, 0);
+    if (!MASKED && norm_vec) {
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_KNORM]), o.kn, 0, 0);
         t.kn[0] = a[0]; t.kn[1] = a[1];
-        tq_u32x2 c = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(b.vn), o.vn8, 0, 0);
+        tq_u32x2 c = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_VNORM]), o.vn, 0, 0);
         t.vn[0] = c[0]; t.vn[1] = c[1];
         if (KQJL) {
-            tq_u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(b.krn), o.krn8, 0, 0);
+            tq_u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_KRNORM]), o.krn, 0, 0);
             t.krn[0] = d[0]; t.krn[1] = d[1];
         }
     } else {
         uint32_t kv[4], vv[4], rv[4];
+        auto rk = make_rsrc(tl.base[R_KNORM]);
+        auto rvn = make_rsrc(tl.base[R_VNORM]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const bool ok = 4 * g + r < nvalid;
-            kv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(b.kn), ok ? o.kn[r] : kOOB, 0, 0);
-            vv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(b.vn), ok ? o.vn[r] : kOOB, 0, 0);
-            if (KQJL) rv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(b.krn), ok ? o.krn[r] : kOOB, 0, 0);
+            const bool ok = !MASKED || 4 * g + r < tl.nvalid;
+            kv[r] = __builtin_amdgcn_raw_buffer_load_b16(rk, ok ? o.kn + r * rrow[R_KNORM] : kOOB, 0, 0);
+            vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rvn, ok ? o.vn + r * rrow[R_VNORM] : kOOB, 0, 0);
+            if (KQJL)
+                rv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(tl.base[R_KRNORM]),
+                                                             ok ? o.krn + r * rrow[R_KRNORM] : kOOB, 0, 0);
         }
         t.kn[0] = kv[0] | (kv[1] << 16); t.kn[1] = kv[2] | (kv[3] << 16);
         t.vn[0] = vv[0] | (vv[1] << 16); t.vn[1] = vv[2] | (vv[3] << 16);
         if (KQJL) { t.krn[0] = rv[0] | (rv[1] << 16); t.krn[1] = rv[2] | (rv[3] << 16); }
     }
-    auto rv = make_rsrc(b.vidx);
+    auto rv = make_rsrc(tl.base[R_VIDX]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const uint32_t off = (4 * g + r < nvalid) ? o.vidx[r] : kOOB;
+        const uint32_t off = (!MASKED || 4 * g + r < tl.nvalid) ? o.vidx[r] : kOOB;
         if (VB == 3) {
             tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
             t.vw[r][0] = w[0]; t.vw[r][VB == 3 ? 1 : 0] = w[1];
@@ -154,10 +164,160 @@ __device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const TileBa
     }
 }
 
+// Online-softmax state of one wave.
+struct SoftmaxState {
+    float m, lsum;
+    tq_floatx4 acc[8];
+    unsigned long long n_skip, n_tot;
+};
+
+template <int KB, bool KQJL, int VB, bool QCOLS>
+__device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB>& cur, int nvalid, SoftmaxState& st,
+                                             const tq_half8 (&qop)[4], const tq_half8 (&qlo)[QCOLS ? 1 : 4],
+                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], const uint32_t* s_ktab,
+                                             const uint32_t* s_vtab, uint32_t bank, const LaneOff& o, int n, int g,
+                                             bool hvalid, const DecodeParams& p, bool sparse, bool count) {
+    constexpr int VENT = 1 << (2 * VB);
+    // ---------------- QK products ----------------
+    tq_floatx4 s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        tq_u32x4 a;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = tq_field(cur.kw, 2 * KB * (4 * cc + j), 2 * KB);
+            a[j] = s_ktab[(e << 5) | bank];
+        }
+        const tq_half8 ah = __builtin_bit_cast(tq_half8, a);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qop[cc], s1, 0, 0, 0);
+        if (!QCOLS) s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[cc % (QCOLS ? 1 : 4)], s1, 0, 0, 0);
+    }
+    tq_floatx4 s2 = {0.f, 0.f, 0.f, 0.f};
+    if (KQJL) {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            tq_u32x4 a;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pp = 4 * cc + j;
+                a[j] = ((cur.ks << (15 - pp)) & 0x80008000u) | 0x3C003C00u;
+            }
+            s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), qpop[cc % (KQJL ? 4 : 1)], s2,
+                                                        0, 0, 0);
+        }
+    }
+    // Scalar copies on purpose: shuffling elements of an ext_vector in place miscompiles (the
+    // backend reuses one shuffle result for the other elements).
+    float s1v[4], s2v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        s1v[r] = s1[r];
+        s2v[r] = s2[r];
+    }
+    if (QCOLS) {
+        // column n (hi part of q) + column n ^ 8 (lo part): swizzle xor 8 inside each 16-lane row
+        int sw[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sw[r] = __builtin_amdgcn_ds_swizzle(__float_as_int(s1v[r]), 0x201f);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s1v[r] += __int_as_float(sw[r]);
+    }
+
+    // ---------------- online softmax ----------------
+    const float kn[4] = {f16lo(cur.kn[0]), f16hi(cur.kn[0]), f16lo(cur.kn[1]), f16hi(cur.kn[1])};
+    const float vn[4] = {f16lo(cur.vn[0]), f16hi(cur.vn[0]), f16lo(cur.vn[1]), f16hi(cur.vn[1])};
+    float sc[4];
+    bool tv[4];
+    float mt = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        tv[r] = 4 * g + r < nvalid;
+        float v = kn[r] * s1v[r];
+        if (KQJL) {
+            const float rn = (r & 1) ? f16hi(cur.krn[r >> 1]) : f16lo(cur.krn[r >> 1]);
+            v = __builtin_fmaf(rn * p.corr_scale, s2v[r], v);
+        }
+        sc[r] = tv[r] ? v : kNegInf;
+        mt = fmaxf(mt, sc[r]);
+    }
+    mt = fmaxf(mt, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(mt), 0x401f)));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float m_new = fmaxf(st.m, mt);
+    const float mref = m_new == kNegInf ? 0.f : m_new;
+    float pr[4];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        pr[r] = __builtin_amdgcn_exp2f(sc[r] - mref);
+        psum += pr[r];
+    }
+    // Rescale only when some head's running max moved (alpha == 1 otherwise).
+    if (__ballot(hvalid && m_new > st.m) != 0) {
+        const float alpha = __builtin_amdgcn_exp2f(st.m - mref);
+        st.lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+    }
+    st.lsum += psum;
+    st.m = m_new;
+
+    // Sparse-V: token significant when some head of the group has p > thresh.
+    bool sig[4] = {true, true, true, true};
+    bool any = true;
+    if (sparse) {
+        uint64_t orall = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint64_t bal = __ballot(hvalid && pr[r] > p.thresh);
+            orall |= bal;
+            sig[r] = ((bal >> (16 * g)) & 0xffffull) != 0;
+        }
+        any = orall != 0;
+        if (count && n == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                st.n_tot += tv[r] ? 1 : 0;
+                st.n_skip += (tv[r] && !sig[r]) ? 1 : 0;
+            }
+        }
+    }
+    if (!any) return;
+
+    // ---------------- PV product ----------------
+    float pv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pv[r] = (tv[r] && sig[r]) ? pr[r] * vn[r] : 0.f;
+    tq_u32x2 bw = {tq_pack_half2(pv[0], pv[1]), tq_pack_half2(pv[2], pv[3])};
+    const tq_half4 bop = __builtin_bit_cast(tq_half4, bw);
+    uint32_t w[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        if (VB == 3) {
+            const uint32_t hi = cur.vw[r][VB == 3 ? 1 : 0], lo = cur.vw[r][0];
+            w[r] = o.vshift >= 32 ? (hi >> (o.vshift - 32)) : __builtin_amdgcn_alignbit(hi, lo, o.vshift);
+        } else {
+            w[r] = cur.vw[r][0];
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // dims 8n+2q, 8n+2q+1 of tokens 4g..4g+3
+        uint32_t vp[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vp[r] = s_vtab[(((w[r] >> (2 * VB * q)) & (VENT - 1)) << 5) | bank];
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+            tq_u32x2 aw = {pick_halves(vp[1], vp[0], hs), pick_halves(vp[3], vp[2], hs)};
+            st.acc[2 * q + hs] =
+                __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(tq_half4, aw), bop, st.acc[2 * q + hs], 0, 0, 0);
+        }
+    }
+}
+
 // QCOLS: the GQA group fits in 8 heads, so the 16 columns of the QK product carry q (hi part,
 // columns 0..7) and q - hi (lo part, columns 8..15); a lane swizzle merges them.
 template <int KB, bool KQJL, int VB, bool QCOLS>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_kernel(DecodeParams p) {
     constexpr int KENT = 1 << (2 * KB);
     constexpr int VENT = 1 << (2 * VB);
     __shared__ uint32_t s_ktab[KENT * 32];
@@ -177,9 +337,12 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;   // lane group: dims 32g.. (K), tokens 4g..4g+3 (scores, V)
     const int n = lane & 15;   // head column (Q/P/out), token row (K loads), dim row (V)
-    const uint32_t bank4 = (uint32_t)(lane & 31) << 2;
+    const uint32_t bank = (uint32_t)(lane & 31);
 
-    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    // The wave index is uniform across the wave; saying so keeps every per-unit value in SGPRs
+    // (otherwise buffer descriptors built from it are treated as divergent).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
     const int c = (int)(unit % p.n_chunks);
     const int64_t sk = unit / p.n_chunks;
     const int kh = (int)(sk % p.hkv);
@@ -203,15 +366,35 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
     tq_half8 qlo[QCOLS ? 1 : 4];
     tq_half8 qpop[KQJL ? 4 : 1];
     {
-        const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh;
+        float qv[32], qpv[32];
+        const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
         const int64_t qpoff = s * p.qp_ss + (int64_t)head * p.qp_sh;
+        if (qload && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tq_load8(p.q, qoff + 8 * i, p.q_dtype, &qv[8 * i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) qv[i] = qload ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
+        }
+        if (KQJL) {
+            if (hvalid && p.q_vec && !p.k_perm) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) tq_load8(p.qp, qpoff + 32 * g + 8 * i, p.q_dtype, &qpv[8 * i]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 32; ++k) {
+                    const int dim = p.k_perm ? 4 * k + g : 32 * g + k;
+                    qpv[k] = hvalid ? tq_load1(p.qp, qpoff + dim, p.q_dtype) : 0.f;
+                }
+            }
+        }
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float qv = qload ? tq_load1(p.q, qoff + 32 * g + 8 * cc + j, p.q_dtype) * p.q_scale : 0.f;
-                const _Float16 qh = (_Float16)qv;
-                const _Float16 ql = (_Float16)(qv - (float)qh);
+                const float x = qv[8 * cc + j] * p.q_scale;
+                const _Float16 qh = (_Float16)x;
+                const _Float16 ql = (_Float16)(x - (float)qh);
                 if (QCOLS) {
                     qop[cc][j] = n < 8 ? qh : ql;
                 } else {
@@ -219,257 +402,127 @@ __global__ __launch_bounds__(256) void decode_kernel(DecodeParams p) {
                     qlo[cc % (QCOLS ? 1 : 4)][j] = ql;
                 }
                 if (KQJL) {
+                    // sign operand slot j of MFMA cc holds bit 4cc + j/2 + 16(j&1) of the lane's 32
                     const int bit = 4 * cc + (j >> 1) + 16 * (j & 1);
-                    const int dim = p.k_perm ? 4 * bit + g : 32 * g + bit;
-                    const float qpv = hvalid ? -tq_load1(p.qp, qpoff + dim, p.q_dtype) * p.q_scale : 0.f;
-                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)qpv;
+                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)(-qpv[bit] * p.qp_scale);
                 }
             }
         }
     }
 
     // ---- loop-invariant per-lane byte offsets inside a tile ----
-    LaneOffsets o;
-    o.kidx = (uint32_t)(n * p.k_idx.stride_row + 4 * KB * g);
-    o.ksig = KQJL ? (uint32_t)(n * p.k_sig.stride_row + 4 * g) : 0u;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int tok = 4 * g + r;
-        o.kn[r] = (uint32_t)(tok * p.k_norm.stride_row);
-        o.vn[r] = (uint32_t)(tok * p.v_norm.stride_row);
-        o.krn[r] = KQJL ? (uint32_t)(tok * p.k_rnorm.stride_row) : 0u;
+    LaneOff o;
+    o.kidx = (uint32_t)(n * p.rrow[R_KIDX] + 4 * KB * g);
+    o.ksig = (uint32_t)(n * p.rrow[R_KSIG] + 4 * g);
+    o.kn = (uint32_t)(4 * g * p.rrow[R_KNORM]);
+    o.krn = (uint32_t)(4 * g * p.rrow[R_KRNORM]);
+    o.vn = (uint32_t)(4 * g * p.rrow[R_VNORM]);
+    {
+        int start = VB * n;
+        o.vshift = 0;
         if (VB == 3) {
             const int byte0 = 3 * n;
-            int start = (byte0 >> 2) << 2;
-            start = start < 40 ? start : 40;      // 8-byte window kept inside the 48-byte row
-            o.vidx[r] = (uint32_t)(tok * p.v_idx.stride_row + start);
+            start = (byte0 >> 2) << 2;
+            start = start < 40 ? start : 40;  // 8-byte window kept inside the 48-byte row
             o.vshift = 8 * (byte0 - start);
-        } else {
-            o.vidx[r] = (uint32_t)(tok * p.v_idx.stride_row + VB * n);
-            o.vshift = 0;
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o.vidx[r] = (uint32_t)((4 * g + r) * p.rrow[R_VIDX] + start);
     }
-    o.kn8 = o.kn[0];
-    o.vn8 = o.vn[0];
-    o.krn8 = o.krn[0];
-    // Norm rows 2 bytes apart inside allocated blocks: one 8-byte load per region.
-    const bool norm_vec = paged && p.k_norm.stride_row == 2 && p.v_norm.stride_row == 2 &&
-                          (!KQJL || p.k_rnorm.stride_row == 2);
+    // Norm rows 2 bytes apart: one 8-byte load per region.
+    const bool norm_vec = p.rrow[R_KNORM] == 2 && p.rrow[R_VNORM] == 2 && (!KQJL || p.rrow[R_KRNORM] == 2);
 
-    // Per-unit parts of the tile bases (uniform).
-    const int64_t seq_off_k = paged ? 0 : s * p.k_idx.stride_seq;
-    auto bases_for = [&](int64_t blk, int st) {
-        TileBases b;
-        const int64_t so = paged ? 0 : s;
-        b.kidx = p.k_idx.ptr + blk * p.k_idx.stride_block + kh * p.k_idx.stride_head + so * p.k_idx.stride_seq + st * p.k_idx.stride_row;
-        b.kn = p.k_norm.ptr + blk * p.k_norm.stride_block + kh * p.k_norm.stride_head + so * p.k_norm.stride_seq + st * p.k_norm.stride_row;
-        b.vidx = p.v_idx.ptr + blk * p.v_idx.stride_block + kh * p.v_idx.stride_head + so * p.v_idx.stride_seq + st * p.v_idx.stride_row;
-        b.vn = p.v_norm.ptr + blk * p.v_norm.stride_block + kh * p.v_norm.stride_head + so * p.v_norm.stride_seq + st * p.v_norm.stride_row;
-        if (KQJL) {
-            b.ksig = p.k_sig.ptr + blk * p.k_sig.stride_block + kh * p.k_sig.stride_head + so * p.k_sig.stride_seq + st * p.k_sig.stride_row;
-            b.krn = p.k_rnorm.ptr + blk * p.k_rnorm.stride_block + kh * p.k_rnorm.stride_head + so * p.k_rnorm.stride_seq + st * p.k_rnorm.stride_row;
-        } else {
-            b.ksig = b.kidx;
-            b.krn = b.kn;
-        }
-        return b;
-    };
-    (void)seq_off_k;
-    // Tile t0 -> (bases, rows valid); a block-table entry outside [0, num_blocks) reads nothing.
-    auto locate = [&](int t0, TileBases& b, int& nvalid) {
+    // Per-unit part of every region's address.
+    const uint8_t* ub[R_COUNT];
+#pragma unroll
+    for (int r = 0; r < R_COUNT; ++r) ub[r] = p.rptr[r] + kh * p.rhead[r] + (paged ? 0 : s * p.rseq[r]);
+
+    // Block table window: lane i holds entry lb0 + i (refilled every 64 blocks).
+    const int nblk_seq = (L + p.block_size - 1) / p.block_size;
+    int bt_lb0 = -64;
+    int bt_vec = 0;
+    auto locate = [&](int t0, Tile& tl) {
         const int lb = t0 / p.block_size;
         const int st = t0 - lb * p.block_size;
-        int64_t blk = lb;
-        nvalid = (t_end - t0 < 16) ? t_end - t0 : 16;
+        tl.nvalid = (t_end - t0 < 16) ? t_end - t0 : 16;
+        int64_t offk = 0, offv = 0;
         if (paged) {
-            blk = p.bt[s * p.bt_stride + lb];
+            if (lb - bt_lb0 >= 64) {
+                bt_lb0 = lb;
+                const int e = lb + lane;
+                bt_vec = e < nblk_seq ? p.bt[s * p.bt_stride + e] : 0;
+            }
+            int64_t blk = __builtin_amdgcn_readlane(bt_vec, lb - bt_lb0);
             if (blk < 0 || blk >= p.num_blocks) {
                 blk = 0;
-                nvalid = 0;
+                tl.nvalid = 0;
             }
+            offk = blk * p.sb_k;
+            offv = blk * p.sb_v;
         }
-        b = bases_for(blk, st);
+        const int rowbase = paged ? st : t0;
+#pragma unroll
+        for (int r = 0; r < R_COUNT; ++r)
+            tl.base[r] = ub[r] + (r >= R_VIDX ? offv : offk) + (int64_t)rowbase * p.rrow[r];
     };
 
-    float m = kNegInf;
-    float lsum = 0.f;
-    tq_floatx4 acc[8];
+    SoftmaxState sm;
+    sm.m = kNegInf;
+    sm.lsum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
-    unsigned long long n_skip = 0, n_tot = 0;
+    for (int i = 0; i < 8; ++i) sm.acc[i] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+    sm.n_skip = 0;
+    sm.n_tot = 0;
     const bool sparse = p.thresh > 0.f;
+    const bool count = sparse && p.skip_stats != nullptr;
 
-    TileRaw<KB, KQJL, VB> cur = {}, nxt = {};
-    int cur_valid, nxt_valid = 0;
-    {
-        TileBases b;
-        locate(t_begin, b, cur_valid);
-        load_tile<KB, KQJL, VB>(cur, b, o, cur_valid, n, g, norm_vec);
+    // Loads of the tile at t0: whole tiles in a paged cache (rows allocated), masked rows past the
+    // end in a contiguous layout; a tile with an unreadable block entry loads nothing.
+    auto fetch = [&](int t0, TileRaw<KB, KQJL, VB>& raw, int& nvalid) {
+        Tile tl;
+        locate(t0, tl);
+        nvalid = tl.nvalid;
+        if (tl.nvalid == 0) return;
+        if (paged || tl.nvalid == 16)
+            load_tile<KB, KQJL, VB, false>(raw, tl, o, p.rrow, n, g, norm_vec);
+        else
+            load_tile<KB, KQJL, VB, true>(raw, tl, o, p.rrow, n, g, norm_vec);
+    };
+
+    TileRaw<KB, KQJL, VB> ra = {}, rb = {};
+    int va = 0, vb = 0;
+    fetch(t_begin, ra, va);
+    for (int t0 = t_begin; t0 < t_end; t0 += 32) {
+        if (t0 + 16 < t_end) fetch(t0 + 16, rb, vb);
+        compute_tile<KB, KQJL, VB, QCOLS>(ra, va, sm, qop, qlo, qpop, s_ktab, s_vtab, bank, o, n, g, hvalid, p, sparse,
+                                          count);
+        if (t0 + 16 >= t_end) break;
+        if (t0 + 32 < t_end) fetch(t0 + 32, ra, va);
+        compute_tile<KB, KQJL, VB, QCOLS>(rb, vb, sm, qop, qlo, qpop, s_ktab, s_vtab, bank, o, n, g, hvalid, p, sparse,
+                                          count);
     }
 
-    for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-        const bool more = t0 + 16 < t_end;
-        if (more) {  // prefetch the next tile while this one is computed
-            TileBases b;
-            locate(t0 + 16, b, nxt_valid);
-            load_tile<KB, KQJL, VB>(nxt, b, o, nxt_valid, n, g, norm_vec);
-        }
-
-        // ---------------- QK products ----------------
-        tq_floatx4 s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            tq_u32x4 a;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t e = tq_field(cur.kw, 2 * KB * (4 * cc + j), 2 * KB);
-                a[j] = s_ktab[(e << 5) | (bank4 >> 2)];
-            }
-            const tq_half8 ah = __builtin_bit_cast(tq_half8, a);
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qop[cc], s1, 0, 0, 0);
-            if (!QCOLS) s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[cc % (QCOLS ? 1 : 4)], s1, 0, 0, 0);
-        }
-        tq_floatx4 s2 = {0.f, 0.f, 0.f, 0.f};
-        if (KQJL) {
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                tq_u32x4 a;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int pp = 4 * cc + j;
-                    a[j] = ((cur.ks << (15 - pp)) & 0x80008000u) | 0x3C003C00u;
-                }
-                s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), qpop[cc % (KQJL ? 4 : 1)], s2, 0, 0, 0);
-            }
-        }
-        float s1v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s1v[r] = s1[r];
-        if (QCOLS) {
-            // column n (hi part) + column n ^ 8 (lo part): swizzle xor 8 inside each 16-lane row.
-            // Scalar copies on purpose: shuffling elements of an ext_vector in place miscompiles
-            // (the backend reuses one shuffle result for the other elements).
-            int sw[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sw[r] = __builtin_amdgcn_ds_swizzle(__float_as_int(s1v[r]), 0x201f);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) s1v[r] += __int_as_float(sw[r]);
-        }
-
-        // ---------------- online softmax ----------------
-        float sc[4], kn[4], vn[4];
-        kn[0] = f16lo(cur.kn[0]); kn[1] = f16hi(cur.kn[0]); kn[2] = f16lo(cur.kn[1]); kn[3] = f16hi(cur.kn[1]);
-        vn[0] = f16lo(cur.vn[0]); vn[1] = f16hi(cur.vn[0]); vn[2] = f16lo(cur.vn[1]); vn[3] = f16hi(cur.vn[1]);
-        float mt = kNegInf;
-        bool tv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            tv[r] = 4 * g + r < cur_valid;
-            float v = kn[r] * p.k_cinv * s1v[r];
-            if (KQJL) {
-                const float rn = (r & 1) ? f16hi(cur.krn[r >> 1]) : f16lo(cur.krn[r >> 1]);
-                v = __builtin_fmaf(rn * p.corr_scale, s2[r], v);
-            }
-            sc[r] = tv[r] ? v : kNegInf;
-            mt = fmaxf(mt, sc[r]);
-        }
-        mt = fmaxf(mt, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, mt), 0x401f)));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float m_new = fmaxf(m, mt);
-        const float mref = m_new == kNegInf ? 0.f : m_new;
-        float pr[4];
-        float psum = 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            pr[r] = __builtin_amdgcn_exp2f(sc[r] - mref);
-            psum += pr[r];
-        }
-        // Rescale only when some head's running max moved (alpha == 1 otherwise).
-        if (__ballot(hvalid && m_new > m) != 0) {
-            const float alpha = __builtin_amdgcn_exp2f(m - mref);
-            lsum *= alpha;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-        }
-        lsum += psum;
-        m = m_new;
-
-        // Sparse-V: token significant when some head of the group has p > thresh.
-        bool sig[4] = {true, true, true, true};
-        bool any = true;
-        if (sparse) {
-            uint64_t orall = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint64_t bal = __ballot(hvalid && pr[r] > p.thresh);
-                orall |= bal;
-                sig[r] = ((bal >> (16 * g)) & 0xffffull) != 0;
-            }
-            any = orall != 0;
-            if (p.skip_stats && n == 0) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    n_tot += tv[r] ? 1 : 0;
-                    n_skip += (tv[r] && !sig[r]) ? 1 : 0;
-                }
-            }
-        }
-
-        if (any) {
-            float pv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pv[r] = (tv[r] && sig[r]) ? pr[r] * (vn[r] * p.v_cinv) : 0.f;
-            tq_u32x2 bw = {tq_pack_half2(pv[0], pv[1]), tq_pack_half2(pv[2], pv[3])};
-            const tq_half4 bop = __builtin_bit_cast(tq_half4, bw);
-            // V dequant: vp[r][q] = half2(dims 8n+2q, 8n+2q+1) of token 4g+r.
-            uint32_t vp[4][4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint32_t w;
-                if (VB == 3) {
-                    const uint32_t hi = cur.vw[r][VB == 3 ? 1 : 0], lo = cur.vw[r][0];
-                    w = o.vshift >= 32 ? (hi >> (o.vshift - 32)) : __builtin_amdgcn_alignbit(hi, lo, o.vshift);
-                } else {
-                    w = cur.vw[r][0];
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t e = (w >> (2 * VB * q)) & (VENT - 1);
-                    vp[r][q] = s_vtab[(e << 5) | (bank4 >> 2)];
-                }
-            }
-#pragma unroll
-            for (int nn = 0; nn < 8; ++nn) {
-                const int q = nn >> 1, hs = nn & 1;
-                tq_u32x2 aw = {pick_halves(vp[1][q], vp[0][q], hs), pick_halves(vp[3][q], vp[2][q], hs)};
-                acc[nn] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(tq_half4, aw), bop, acc[nn], 0, 0, 0);
-            }
-        }
-        if (more) {
-            cur = nxt;
-            cur_valid = nxt_valid;
-        }
-    }
-
-    lsum += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, lsum), 0x401f));
+    float lsum = sm.lsum;
+    lsum += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(lsum), 0x401f));
     lsum += __shfl_xor(lsum, 32);
 
     if (hvalid) {
         const int64_t slot = ((s * p.hq + head) * (int64_t)p.n_chunks + c);
         if (g == 0) {
-            p.ws_m[slot] = m;
+            p.ws_m[slot] = sm.m;
             p.ws_l[slot] = lsum;
         }
-        // acc[nn][r] is dim 8*(4g+r)+nn = 32g + 8r + nn.
+        // acc[nn][r] is dim 8*(4g+r)+nn = 32g + 8r + nn; v_cinv undoes the V table scale.
+        const float vs = p.v_cinv;
         float4* dst = reinterpret_cast<float4*>(p.ws_acc + slot * TQ_HEAD_DIM + 32 * g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            dst[2 * r] = make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
-            dst[2 * r + 1] = make_float4(acc[4][r], acc[5][r], acc[6][r], acc[7][r]);
+            dst[2 * r] = make_float4(sm.acc[0][r] * vs, sm.acc[1][r] * vs, sm.acc[2][r] * vs, sm.acc[3][r] * vs);
+            dst[2 * r + 1] = make_float4(sm.acc[4][r] * vs, sm.acc[5][r] * vs, sm.acc[6][r] * vs, sm.acc[7][r] * vs);
         }
     }
-    if (sparse && p.skip_stats) {
-        unsigned long long a = n_skip, b = n_tot;
+    if (count) {
+        unsigned long long a = sm.n_skip, b = sm.n_tot;
         a += __shfl_xor(a, 16);
         a += __shfl_xor(a, 32);
         b += __shfl_xor(b, 16);
@@ -521,6 +574,7 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     tq_store1(p.out, o + 1, p.out_dtype, a1 * inv);
 }
 
+
 bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 
 int check_region(const tq_region& r, int align) {
@@ -528,22 +582,18 @@ int check_region(const tq_region& r, int align) {
     if (!aligned(r.ptr, align) || r.stride_block % align || r.stride_head % align || r.stride_seq % align ||
         r.stride_row % align)
         return TQ_ERR_ALIGNMENT;
+    if (r.stride_row <= 0 || r.stride_row > (1 << 20)) return TQ_ERR_INVALID_ARGUMENT;
     return TQ_OK;
-}
-
-Region to_region(const tq_region& r) {
-    Region o;
-    o.ptr = static_cast<const uint8_t*>(r.ptr);
-    o.stride_block = r.stride_block;
-    o.stride_head = r.stride_head;
-    o.stride_seq = r.stride_seq;
-    o.stride_row = r.stride_row;
-    return o;
 }
 
 int n_chunks_for(int max_seq_len, int chunk) { return max_seq_len <= 0 ? 1 : (max_seq_len + chunk - 1) / chunk; }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
+    const int64_t es = dtype == TQ_F32 ? 4 : 2;
+    return aligned(q, 16) && (ss * es) % 16 == 0 && (sh * es) % 16 == 0;
+}
 
 }  // namespace
 
@@ -591,6 +641,22 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         if ((rc = check_region(k->signs, 4))) return rc;
         if ((rc = check_region(k->rnorm, 2))) return rc;
     }
+    const tq_region* regs[R_COUNT] = {&k->idx, k->qjl ? &k->signs : &k->idx, &k->norm,
+                                      k->qjl ? &k->rnorm : &k->norm, &v->idx, &v->norm};
+    int64_t max_row = 0;
+    for (int r = 0; r < R_COUNT; ++r) max_row = regs[r]->stride_row > max_row ? regs[r]->stride_row : max_row;
+    if (block_tables) {
+        // paged: the K regions share one block stride, the V regions another
+        for (int r = 1; r < R_VIDX; ++r)
+            if (regs[r]->stride_block != regs[R_KIDX]->stride_block) return TQ_ERR_INVALID_ARGUMENT;
+        if (regs[R_VNORM]->stride_block != regs[R_VIDX]->stride_block) return TQ_ERR_INVALID_ARGUMENT;
+        if ((int64_t)block_size * max_row >= (1ll << 30)) return TQ_ERR_INVALID_ARGUMENT;
+    } else {
+        // contiguous: token rows follow each other across blocks
+        for (int r = 0; r < R_COUNT; ++r)
+            if (regs[r]->stride_block != 16 * regs[r]->stride_row) return TQ_ERR_INVALID_ARGUMENT;
+        if ((int64_t)(max_blocks_per_seq + 1) * block_size * max_row >= (1ll << 30)) return TQ_ERR_INVALID_ARGUMENT;
+    }
     const int n_chunks = n_chunks_for(max_seq_len, tokens_per_chunk);
     const size_t need = tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return TQ_ERR_WORKSPACE;
@@ -609,23 +675,23 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     p.qp_ss = q_proj ? qp_stride_seq : q_stride_seq;
     p.qp_sh = q_proj ? qp_stride_head : q_stride_head;
     p.q_dtype = q_dtype;
+    p.q_vec = q_vector_ok(p.q, q_dtype, p.q_ss, p.q_sh) && q_vector_ok(p.qp, q_dtype, p.qp_ss, p.qp_sh);
     p.num_seqs = num_seqs;
     p.hq = num_q_heads;
     p.hkv = num_kv_heads;
     p.group = group;
-    p.k_idx = to_region(k->idx);
-    p.k_norm = to_region(k->norm);
-    if (k->qjl) {
-        p.k_sig = to_region(k->signs);
-        p.k_rnorm = to_region(k->rnorm);
+    for (int r = 0; r < R_COUNT; ++r) {
+        p.rptr[r] = static_cast<const uint8_t*>(regs[r]->ptr);
+        p.rhead[r] = regs[r]->stride_head;
+        p.rseq[r] = regs[r]->stride_seq;
+        p.rrow[r] = (int32_t)regs[r]->stride_row;
     }
-    p.v_idx = to_region(v->idx);
-    p.v_norm = to_region(v->norm);
+    p.sb_k = regs[R_KIDX]->stride_block;
+    p.sb_v = regs[R_VIDX]->stride_block;
     p.k_cent = k->centroids;
     p.v_cent = v->centroids;
     p.k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
     p.v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
-    p.k_cinv = 1.f / p.k_cscale;
     p.v_cinv = 1.f / p.v_cscale;
     p.k_perm = k->signs_permuted ? 1 : 0;
     p.block_size = block_size;
@@ -634,7 +700,8 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     p.bt_stride = block_table_stride;
     p.max_blocks = max_blocks_per_seq;
     p.seq_lens = seq_lens;
-    p.q_scale = sm_scale * kLog2e;
+    p.qp_scale = sm_scale * kLog2e;
+    p.q_scale = p.qp_scale / p.k_cscale;
     p.corr_scale = corr_scale;
     p.thresh = sparse_threshold > 0.f ? sparse_threshold : 0.f;
     p.chunk = tokens_per_chunk;
