@@ -30,7 +30,6 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_huge_valf();
-constexpr uint32_t kOOB = 0x80000000u;  // >= num_records: buffer loads return zero
 
 enum { R_KIDX = 0, R_KSIG, R_KNORM, R_KRNORM, R_VIDX, R_VNORM, R_COUNT };
 
@@ -51,6 +50,7 @@ struct DecodeParams {
     const float* v_cent;
     float k_cscale, v_cscale;  // tables hold fp16(c * cscale); the scale is divided back out
     float v_cinv;
+    int share_tab;      // K and V pair tables identical: one LDS table
     int k_perm;
     int block_size;
     int64_t num_blocks;
@@ -70,8 +70,33 @@ struct DecodeParams {
     unsigned long long* skip_stats;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint8_t* base) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+// nrec = 0 turns every load through the descriptor into a zero read (unreadable block).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint8_t* base, uint32_t nrec) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, nrec, 0x00020000);
+}
+
+// Scalar operands of buffer loads: a wave-uniform value the compiler may have placed in a
+// vector register would otherwise be served by a waterfall loop.
+__device__ __forceinline__ int sgpr(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+
+// Pair-table read.  Tables are placed at LDS addresses that are multiples of their size, so
+// (entry << 7) and (table address + 4 * bank) have disjoint bits and OR forms the address.
+__device__ __forceinline__ uint32_t lds_read(uint32_t addr) { return *(lds_u32*)(uintptr_t)addr; }
+
+// LDS address of the pair-table entry held in bits [pos, pos + W) of the word array w:
+// the field is moved to bit 7 (one shift or funnel shift) and merged with the lane's bank
+// address (one and-or).
+template <int W, int N>
+__device__ __forceinline__ uint32_t pair_addr(const uint32_t (&w)[N], int pos, uint32_t bank_addr) {
+    const int wi = pos >> 5, sh = pos & 31;
+    uint32_t f;
+    if (sh + W <= 32 || wi + 1 >= N)
+        f = sh >= 7 ? (w[wi] >> (sh - 7)) : (w[wi] << (7 - sh));
+    else
+        f = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - 7);
+    return (f & (((1u << W) - 1u) << 7)) | bank_addr;
 }
 
 // Half2 dword from two fp16 lanes of two dwords: selects the low (s=0) or high (s=1) halves.
@@ -83,83 +108,103 @@ __device__ __forceinline__ float f16lo(uint32_t w) { return tq_f16_to_f32(w & 0x
 __device__ __forceinline__ float f16hi(uint32_t w) { return tq_f16_to_f32(w >> 16); }
 
 // Raw per-lane data of one 16-token tile.
-template <int KB, bool KQJL, int VB>
+// NV: norm rows 2 bytes apart, the norms of tokens 4g..4g+3 arrive as two half2 words;
+// otherwise one 16-bit load (one word) per token.
+template <int KB, bool KQJL, int VB, bool NV>
 struct TileRaw {
     uint32_t kw[KB];                      // dims 32g..32g+31 of token n: 32*KB bits
     uint32_t ks;                          // sign bits of the same dims
-    uint32_t kn[2], krn[2], vn[2];        // fp16 norms of tokens 4g..4g+3
+    uint32_t kn[NV ? 2 : 4], krn[NV ? 2 : 4], vn[NV ? 2 : 4];  // fp16 norms of tokens 4g..4g+3
     uint32_t vw[4][VB == 3 ? 2 : 1];      // dims 8n..8n+7 of tokens 4g..4g+3
 };
 
+template <bool NV>
+__device__ __forceinline__ float norm_at(const uint32_t* w, int r) {
+    return tq_f16_to_f32(NV ? ((r & 1) ? (w[r >> 1] >> 16) : (w[r >> 1] & 0xffffu)) : (w[r] & 0xffffu));
+}
+
+// Loop-invariant per-lane byte offsets inside a tile (norm and V streams: row 4g).
 struct LaneOff {
-    uint32_t kidx, ksig, kn, krn, vn;     // kn/krn/vn: token 4g (next tokens at +row stride)
-    uint32_t vidx[4];
-    int vshift;                           // VB == 3: bit offset of the 24-bit field in its 8-byte window
+    uint32_t kidx, ksig, kn, krn, vn;     // kn/krn/vn: token 4g
+    uint32_t vidx;                        // token 4g
+    uint32_t vsel;                        // VB == 3: byte selector of the 3-byte field in its 8-byte window
 };
 
 struct Tile {
     const uint8_t* base[R_COUNT];
+    uint32_t nrec;                        // buffer record count: 0 for an unreadable block
     int nvalid;                           // rows of this tile inside the sequence (0: unreadable)
 };
 
-// MASKED: rows >= nvalid may lie outside the allocation (contiguous layout, last tile).
-template <int KB, bool KQJL, int VB, bool MASKED>
-__device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const Tile& tl, const LaneOff& o,
-                                          const int32_t* rrow, int n, int g, bool norm_vec) {
-    const bool krow = !MASKED || n < tl.nvalid;
+// Full tiles (MASKED = false): every row is readable; rows 4g+1..4g+3 of the norm and V streams
+// are addressed through the scalar offset.  MASKED (contiguous layout, last tile): rows >= nvalid
+// may lie outside the allocation, so each region's record count ends at row nvalid and those
+// rows read as zero; the row offsets then go into the vector offset, which the range check sees.
+template <int KB, bool KQJL, int VB, bool NV, bool MASKED>
+__device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB, NV>& t, const Tile& tl, const LaneOff& o,
+                                          const int32_t* rrow) {
+    auto nrec = [&](int r) -> uint32_t { return MASKED ? (uint32_t)(tl.nvalid * rrow[r]) : tl.nrec; };
     {
-        auto r = make_rsrc(tl.base[R_KIDX]);
-        const uint32_t off = krow ? o.kidx : kOOB;
+        auto r = make_rsrc(tl.base[R_KIDX], nrec(R_KIDX));
         if (KB == 2) {
-            tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+            tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, o.kidx, 0, 0);
             t.kw[0] = v[0]; t.kw[1 % KB] = v[1];
         } else if (KB == 3) {
             typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-            u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+            u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, o.kidx, 0, 0);
             t.kw[0] = v[0]; t.kw[1 % KB] = v[1]; t.kw[2 % KB] = v[2];
         } else {
-            tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+            tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, o.kidx, 0, 0);
             t.kw[0] = v[0]; t.kw[1 % KB] = v[1]; t.kw[2 % KB] = v[2]; t.kw[3 % KB] = v[3];
         }
     }
-    if (KQJL) t.ks = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(tl.base[R_KSIG]), krow ? o.ksig : kOOB, 0, 0);
-    if (!MASKED && norm_vec) {
-        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_KNORM]), o.kn, 0, 0);
+    if (KQJL) t.ks = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(tl.base[R_KSIG], nrec(R_KSIG)), o.ksig, 0, 0);
+    if (!MASKED && NV) {
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_KNORM], tl.nrec), o.kn, 0, 0);
         t.kn[0] = a[0]; t.kn[1] = a[1];
-        tq_u32x2 c = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_VNORM]), o.vn, 0, 0);
+        tq_u32x2 c = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_VNORM], tl.nrec), o.vn, 0, 0);
         t.vn[0] = c[0]; t.vn[1] = c[1];
         if (KQJL) {
-            tq_u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_KRNORM]), o.krn, 0, 0);
+            tq_u32x2 d = __builtin_amdgcn_raw_buffer_load_b64(make_rsrc(tl.base[R_KRNORM], tl.nrec), o.krn, 0, 0);
             t.krn[0] = d[0]; t.krn[1] = d[1];
         }
     } else {
         uint32_t kv[4], vv[4], rv[4];
-        auto rk = make_rsrc(tl.base[R_KNORM]);
-        auto rvn = make_rsrc(tl.base[R_VNORM]);
+        auto rk = make_rsrc(tl.base[R_KNORM], nrec(R_KNORM));
+        auto rvn = make_rsrc(tl.base[R_VNORM], nrec(R_VNORM));
+        auto rrn = make_rsrc(tl.base[R_KRNORM], nrec(R_KRNORM));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const bool ok = !MASKED || 4 * g + r < tl.nvalid;
-            kv[r] = __builtin_amdgcn_raw_buffer_load_b16(rk, ok ? o.kn + r * rrow[R_KNORM] : kOOB, 0, 0);
-            vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rvn, ok ? o.vn + r * rrow[R_VNORM] : kOOB, 0, 0);
-            if (KQJL)
-                rv[r] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(tl.base[R_KRNORM]),
-                                                             ok ? o.krn + r * rrow[R_KRNORM] : kOOB, 0, 0);
+            if (MASKED) {
+                kv[r] = __builtin_amdgcn_raw_buffer_load_b16(rk, o.kn + r * rrow[R_KNORM], 0, 0);
+                vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rvn, o.vn + r * rrow[R_VNORM], 0, 0);
+                if (KQJL) rv[r] = __builtin_amdgcn_raw_buffer_load_b16(rrn, o.krn + r * rrow[R_KRNORM], 0, 0);
+            } else {
+                kv[r] = __builtin_amdgcn_raw_buffer_load_b16(rk, o.kn, sgpr(r * rrow[R_KNORM]), 0);
+                vv[r] = __builtin_amdgcn_raw_buffer_load_b16(rvn, o.vn, sgpr(r * rrow[R_VNORM]), 0);
+                if (KQJL) rv[r] = __builtin_amdgcn_raw_buffer_load_b16(rrn, o.krn, sgpr(r * rrow[R_KRNORM]), 0);
+            }
         }
-        t.kn[0] = kv[0] | (kv[1] << 16); t.kn[1] = kv[2] | (kv[3] << 16);
-        t.vn[0] = vv[0] | (vv[1] << 16); t.vn[1] = vv[2] | (vv[3] << 16);
-        if (KQJL) { t.krn[0] = rv[0] | (rv[1] << 16); t.krn[1] = rv[2] | (rv[3] << 16); }
+        // Kept one word per token unless NV (then combined: only the masked path gets here).
+#pragma unroll
+        for (int r = 0; r < (NV ? 2 : 4); ++r) {
+            t.kn[r] = NV ? (kv[2 * r] | (kv[2 * r + 1] << 16)) : kv[r];
+            t.vn[r] = NV ? (vv[2 * r] | (vv[2 * r + 1] << 16)) : vv[r];
+            if (KQJL) t.krn[r] = NV ? (rv[2 * r] | (rv[2 * r + 1] << 16)) : rv[r];
+        }
     }
-    auto rv = make_rsrc(tl.base[R_VIDX]);
+    auto rv = make_rsrc(tl.base[R_VIDX], nrec(R_VIDX));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const uint32_t off = (!MASKED || 4 * g + r < tl.nvalid) ? o.vidx[r] : kOOB;
+        const uint32_t off = MASKED ? o.vidx + r * rrow[R_VIDX] : o.vidx;
+        const int soff = MASKED ? 0 : sgpr(r * rrow[R_VIDX]);
         if (VB == 3) {
-            tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, 0, 0);
+            tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, soff, 0);
             t.vw[r][0] = w[0]; t.vw[r][VB == 3 ? 1 : 0] = w[1];
         } else if (VB == 4) {
-            t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, 0, 0);
+            t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, soff, 0);
         } else {
-            t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, 0, 0);
+            t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, soff, 0);
         }
     }
 }
@@ -168,26 +213,38 @@ __device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB>& t, const Tile& 
 struct SoftmaxState {
     float m, lsum;
     tq_floatx4 acc[8];
-    unsigned long long n_skip, n_tot;
+    uint32_t n_skip, n_tot;  // wave-uniform (built from ballots)
 };
 
-template <int KB, bool KQJL, int VB, bool QCOLS>
-__device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB>& cur, int nvalid, SoftmaxState& st,
+// Max / sum of a value over the four lanes l, l^16, l^32, l^48 (VALU lane swaps, no LDS pipe).
+__device__ __forceinline__ float max_over_groups(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// FULL: all 16 rows valid (no masking).  kbank/vbank: LDS byte address of the lane's bank
+// replica in the K / V pair table; one = 0x3C003C00 (half2 of 1.0) held in a vector register.
+template <int KB, bool KQJL, int VB, bool NV, bool QCOLS, bool FULL>
+__device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cur, int nvalid, SoftmaxState& st,
                                              const tq_half8 (&qop)[4], const tq_half8 (&qlo)[QCOLS ? 1 : 4],
-                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], const uint32_t* s_ktab,
-                                             const uint32_t* s_vtab, uint32_t bank, const LaneOff& o, int n, int g,
-                                             bool hvalid, const DecodeParams& p, bool sparse, bool count) {
-    constexpr int VENT = 1 << (2 * VB);
+                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], uint32_t kbank, uint32_t vbank,
+                                             uint32_t one, const LaneOff& o, int g, uint64_t hmask,
+                                             uint64_t gmask, const DecodeParams& p, bool sparse, bool count) {
     // ---------------- QK products ----------------
     tq_floatx4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
         tq_u32x4 a;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t e = tq_field(cur.kw, 2 * KB * (4 * cc + j), 2 * KB);
-            a[j] = s_ktab[(e << 5) | bank];
-        }
+        for (int j = 0; j < 4; ++j) a[j] = lds_read(pair_addr<2 * KB>(cur.kw, 2 * KB * (4 * cc + j), kbank));
         const tq_half8 ah = __builtin_bit_cast(tq_half8, a);
         s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qop[cc], s1, 0, 0, 0);
         if (!QCOLS) s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, qlo[cc % (QCOLS ? 1 : 4)], s1, 0, 0, 0);
@@ -199,8 +256,9 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB>& cur, i
             tq_u32x4 a;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                // fp16 sign bits: bit pp of the lane's signs (low half), bit pp + 16 (high half)
                 const int pp = 4 * cc + j;
-                a[j] = ((cur.ks << (15 - pp)) & 0x80008000u) | 0x3C003C00u;
+                a[j] = ((cur.ks << (15 - pp)) & 0x80008000u) | one;
             }
             s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), qpop[cc % (KQJL ? 4 : 1)], s2,
                                                         0, 0, 0);
@@ -215,44 +273,35 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB>& cur, i
         s2v[r] = s2[r];
     }
     if (QCOLS) {
-        // column n (hi part of q) + column n ^ 8 (lo part): swizzle xor 8 inside each 16-lane row
-        int sw[4];
+        // column n (hi part of q) + column n ^ 8 (lo part): rotate each 16-lane row by 8 (DPP)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sw[r] = __builtin_amdgcn_ds_swizzle(__float_as_int(s1v[r]), 0x201f);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s1v[r] += __int_as_float(sw[r]);
+        for (int r = 0; r < 4; ++r)
+            s1v[r] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s1v[r]), 0x128, 0xf, 0xf, true));
     }
 
     // ---------------- online softmax ----------------
-    const float kn[4] = {f16lo(cur.kn[0]), f16hi(cur.kn[0]), f16lo(cur.kn[1]), f16hi(cur.kn[1])};
-    const float vn[4] = {f16lo(cur.vn[0]), f16hi(cur.vn[0]), f16lo(cur.vn[1]), f16hi(cur.vn[1])};
+    // score = norm * S (+ rnorm * QJL; corr_scale is folded into the QJL operand)
     float sc[4];
-    bool tv[4];
     float mt = kNegInf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        tv[r] = 4 * g + r < nvalid;
-        float v = kn[r] * s1v[r];
-        if (KQJL) {
-            const float rn = (r & 1) ? f16hi(cur.krn[r >> 1]) : f16lo(cur.krn[r >> 1]);
-            v = __builtin_fmaf(rn * p.corr_scale, s2v[r], v);
-        }
-        sc[r] = tv[r] ? v : kNegInf;
+        float v = norm_at<NV>(cur.kn, r) * s1v[r];
+        if (KQJL) v = __builtin_fmaf(norm_at<NV>(cur.krn, r), s2v[r], v);
+        sc[r] = (FULL || 4 * g + r < nvalid) ? v : kNegInf;
         mt = fmaxf(mt, sc[r]);
     }
-    mt = fmaxf(mt, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(mt), 0x401f)));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = max_over_groups(mt);
     const float m_new = fmaxf(st.m, mt);
     const float mref = m_new == kNegInf ? 0.f : m_new;
     float pr[4];
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        pr[r] = __builtin_amdgcn_exp2f(sc[r] - mref);
+        pr[r] = __builtin_amdgcn_exp2f(sc[r] - mref);  // 0 for rows past the end
         psum += pr[r];
     }
     // Rescale only when some head's running max moved (alpha == 1 otherwise).
-    if (__ballot(hvalid && m_new > st.m) != 0) {
+    if (__builtin_amdgcn_ballot_w64(m_new > st.m) & hmask) {
         const float alpha = __builtin_amdgcn_exp2f(st.m - mref);
         st.lsum *= alpha;
 #pragma unroll
@@ -261,50 +310,47 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB>& cur, i
     st.lsum += psum;
     st.m = m_new;
 
-    // Sparse-V: token significant when some head of the group has p > thresh.
-    bool sig[4] = {true, true, true, true};
-    bool any = true;
-    if (sparse) {
-        uint64_t orall = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint64_t bal = __ballot(hvalid && pr[r] > p.thresh);
-            orall |= bal;
-            sig[r] = ((bal >> (16 * g)) & 0xffffull) != 0;
-        }
-        any = orall != 0;
-        if (count && n == 0) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                st.n_tot += tv[r] ? 1 : 0;
-                st.n_skip += (tv[r] && !sig[r]) ? 1 : 0;
-            }
-        }
-    }
-    if (!any) return;
-
-    // ---------------- PV product ----------------
+    // P * vnorm; rows past the end may hold any bits in a paged block, so they are zeroed.
     float pv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pv[r] = (tv[r] && sig[r]) ? pr[r] * vn[r] : 0.f;
+    for (int r = 0; r < 4; ++r) {
+        pv[r] = norm_at<NV>(cur.vn, r) * pr[r];
+        if (!FULL) pv[r] = 4 * g + r < nvalid ? pv[r] : 0.f;
+    }
+    // Sparse-V: token 4g + r is kept when some head of the group has p > thresh, i.e. when
+    // lane group g of the ballot is non-zero (gmask: the 16 lanes of this lane's group).
+    if (sparse) {
+        uint64_t orall = 0;
+        uint32_t nsig = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(pr[r] > p.thresh) & hmask;
+            orall |= bal;
+            const bool keep = (bal & gmask) != 0;
+            pv[r] = keep ? pv[r] : 0.f;
+            if (count) nsig += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(keep) & 0x0001000100010001ull);
+        }
+        if (count) {
+            const uint32_t nv = FULL ? 16u : (uint32_t)nvalid;
+            st.n_tot += nv;
+            st.n_skip += nv - nsig;
+        }
+        if (orall == 0) return;
+    }
+
+    // ---------------- PV product ----------------
     tq_u32x2 bw = {tq_pack_half2(pv[0], pv[1]), tq_pack_half2(pv[2], pv[3])};
     const tq_half4 bop = __builtin_bit_cast(tq_half4, bw);
-    uint32_t w[4];
+    uint32_t w[4][1];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        if (VB == 3) {
-            const uint32_t hi = cur.vw[r][VB == 3 ? 1 : 0], lo = cur.vw[r][0];
-            w[r] = o.vshift >= 32 ? (hi >> (o.vshift - 32)) : __builtin_amdgcn_alignbit(hi, lo, o.vshift);
-        } else {
-            w[r] = cur.vw[r][0];
-        }
-    }
+    for (int r = 0; r < 4; ++r)
+        w[r][0] = VB == 3 ? __builtin_amdgcn_perm(cur.vw[r][VB == 3 ? 1 : 0], cur.vw[r][0], o.vsel) : cur.vw[r][0];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         // dims 8n+2q, 8n+2q+1 of tokens 4g..4g+3
         uint32_t vp[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vp[r] = s_vtab[(((w[r] >> (2 * VB * q)) & (VENT - 1)) << 5) | bank];
+        for (int r = 0; r < 4; ++r) vp[r] = lds_read(pair_addr<2 * VB>(w[r], 2 * VB * q, vbank));
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) {
             tq_u32x2 aw = {pick_halves(vp[1], vp[0], hs), pick_halves(vp[3], vp[2], hs)};
@@ -316,28 +362,54 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB>& cur, i
 
 // QCOLS: the GQA group fits in 8 heads, so the 16 columns of the QK product carry q (hi part,
 // columns 0..7) and q - hi (lo part, columns 8..15); a lane swizzle merges them.
+#ifndef TQ_DECODE_DEPTH
+#define TQ_DECODE_DEPTH 2
+#endif
+#ifndef TQ_DECODE_WAVES
+#define TQ_DECODE_WAVES 3
+#endif
+// Tiles in flight per wave (register ring) and waves per SIMD.
+constexpr int kDepth = TQ_DECODE_DEPTH;
+
 template <int KB, bool KQJL, int VB, bool QCOLS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_kernel(DecodeParams p) {
+constexpr int decode_waves() {
+    return (TQ_DECODE_WAVES == 3 && !QCOLS && KQJL && VB == 3 && KB >= 3) ? 2 : TQ_DECODE_WAVES;
+}
+
+template <int KB, bool KQJL, int VB, bool QCOLS, bool NV>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decode_waves<KB, KQJL, VB, QCOLS>(),
+                                                                     decode_waves<KB, KQJL, VB, QCOLS>())))
+void decode_kernel(DecodeParams p) {
     constexpr int KENT = 1 << (2 * KB);
     constexpr int VENT = 1 << (2 * VB);
-    __shared__ uint32_t s_ktab[KENT * 32];
-    __shared__ uint32_t s_vtab[VENT * 32];
+    // Dynamic LDS only (no static LDS in this kernel): s_lds sits at LDS address 0.  The larger
+    // table goes first, so each table's address is a multiple of its size (see pair_addr).
+    // K and V share one table when they use the same codebook (p.share_tab).
+    extern __shared__ uint32_t s_lds[];
+    uint32_t* s_ktab = (KENT >= VENT || p.share_tab) ? s_lds : s_lds + VENT * 32;
+    uint32_t* s_vtab = p.share_tab ? s_lds : (KENT >= VENT ? s_lds + KENT * 32 : s_lds);
 
     // Pair tables: entry e -> half2(c[e & (2^b - 1)], c[e >> b]) * cscale, 32 bank replicas.
     for (int i = threadIdx.x; i < KENT * 32; i += 256) {
         int e = i >> 5;
         s_ktab[i] = tq_pack_half2(p.k_cent[e & ((1 << KB) - 1)] * p.k_cscale, p.k_cent[e >> KB] * p.k_cscale);
     }
-    for (int i = threadIdx.x; i < VENT * 32; i += 256) {
-        int e = i >> 5;
-        s_vtab[i] = tq_pack_half2(p.v_cent[e & ((1 << VB) - 1)] * p.v_cscale, p.v_cent[e >> VB] * p.v_cscale);
+    if (!p.share_tab) {
+        for (int i = threadIdx.x; i < VENT * 32; i += 256) {
+            int e = i >> 5;
+            s_vtab[i] = tq_pack_half2(p.v_cent[e & ((1 << VB) - 1)] * p.v_cscale, p.v_cent[e >> VB] * p.v_cscale);
+        }
     }
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4;   // lane group: dims 32g.. (K), tokens 4g..4g+3 (scores, V)
     const int n = lane & 15;   // head column (Q/P/out), token row (K loads), dim row (V)
-    const uint32_t bank = (uint32_t)(lane & 31);
+    const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
+    const uint32_t kbank = (uint32_t)(uintptr_t)(lds_u32*)s_ktab + bank4;
+    const uint32_t vbank = (uint32_t)(uintptr_t)(lds_u32*)s_vtab + bank4;
+    uint32_t one;  // half2(1, 1) in a vector register: lets the sign operand build use one and-or
+    asm("v_mov_b32 %0, 0x3c003c00" : "=v"(one));
 
     // The wave index is uniform across the wave; saying so keeps every per-unit value in SGPRs
     // (otherwise buffer descriptors built from it are treated as divergent).
@@ -404,7 +476,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                 if (KQJL) {
                     // sign operand slot j of MFMA cc holds bit 4cc + j/2 + 16(j&1) of the lane's 32
                     const int bit = 4 * cc + (j >> 1) + 16 * (j & 1);
-                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)(-qpv[bit] * p.qp_scale);
+                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)(-qpv[bit] * p.qp_scale * p.corr_scale);
                 }
             }
         }
@@ -419,48 +491,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     o.vn = (uint32_t)(4 * g * p.rrow[R_VNORM]);
     {
         int start = VB * n;
-        o.vshift = 0;
+        o.vsel = 0;
         if (VB == 3) {
+            // 8-byte window at a 4-byte boundary, kept inside the 48-byte row; the field starts
+            // at byte b (0..5) of it and v_perm picks bytes b..b+2 (selector 0x0c: zero byte)
             const int byte0 = 3 * n;
             start = (byte0 >> 2) << 2;
-            start = start < 40 ? start : 40;  // 8-byte window kept inside the 48-byte row
-            o.vshift = 8 * (byte0 - start);
+            start = start < 40 ? start : 40;
+            const uint32_t b = (uint32_t)(byte0 - start);
+            o.vsel = b | ((b + 1) << 8) | ((b + 2) << 16) | 0x0c000000u;
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o.vidx[r] = (uint32_t)((4 * g + r) * p.rrow[R_VIDX] + start);
+        o.vidx = (uint32_t)(4 * g * p.rrow[R_VIDX] + start);
     }
-    // Norm rows 2 bytes apart: one 8-byte load per region.
-    const bool norm_vec = p.rrow[R_KNORM] == 2 && p.rrow[R_VNORM] == 2 && (!KQJL || p.rrow[R_KRNORM] == 2);
-
     // Per-unit part of every region's address.
     const uint8_t* ub[R_COUNT];
 #pragma unroll
     for (int r = 0; r < R_COUNT; ++r) ub[r] = p.rptr[r] + kh * p.rhead[r] + (paged ? 0 : s * p.rseq[r]);
 
-    // Block table window: lane i holds entry lb0 + i (refilled every 64 blocks).
-    const int nblk_seq = (L + p.block_size - 1) / p.block_size;
-    int bt_lb0 = -64;
-    int bt_vec = 0;
-    auto locate = [&](int t0, Tile& tl) {
-        const int lb = t0 / p.block_size;
-        const int st = t0 - lb * p.block_size;
-        tl.nvalid = (t_end - t0 < 16) ? t_end - t0 : 16;
+    // Tile at t0: region bases and record count.  live = false (a tile past the end) and an
+    // unreadable block entry give nrec = 0, so the loads return zeros: every fetch issues the
+    // same loads, which keeps the compiler's outstanding-load counts exact and lets the
+    // prefetched tiles stay in flight.  Block-table entries are wave-uniform scalar loads.
+    const int nblk_seq = (L + p.block_size - 1) / p.block_size;  // >= 1
+    const int32_t* bt_row = paged ? p.bt + s * p.bt_stride : nullptr;
+    auto locate = [&](int t0, bool live, Tile& tl) {
+        tl.nvalid = live ? ((t_end - t0 < 16) ? t_end - t0 : 16) : 0;
+        tl.nrec = live ? 0x7fffffffu : 0u;
         int64_t offk = 0, offv = 0;
+        int rowbase = t0;
         if (paged) {
-            if (lb - bt_lb0 >= 64) {
-                bt_lb0 = lb;
-                const int e = lb + lane;
-                bt_vec = e < nblk_seq ? p.bt[s * p.bt_stride + e] : 0;
-            }
-            int64_t blk = __builtin_amdgcn_readlane(bt_vec, lb - bt_lb0);
+            int lb = t0 / p.block_size;
+            lb = lb < nblk_seq ? lb : nblk_seq - 1;
+            rowbase = t0 - lb * p.block_size;
+            int64_t blk = bt_row[lb];
             if (blk < 0 || blk >= p.num_blocks) {
                 blk = 0;
                 tl.nvalid = 0;
+                tl.nrec = 0;
             }
             offk = blk * p.sb_k;
             offv = blk * p.sb_v;
         }
-        const int rowbase = paged ? st : t0;
 #pragma unroll
         for (int r = 0; r < R_COUNT; ++r)
             tl.base[r] = ub[r] + (r >= R_VIDX ? offv : offk) + (int64_t)rowbase * p.rrow[r];
@@ -475,36 +546,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     sm.n_tot = 0;
     const bool sparse = p.thresh > 0.f;
     const bool count = sparse && p.skip_stats != nullptr;
+    const uint64_t hmask = __builtin_amdgcn_ballot_w64(hvalid);  // lanes of real heads
+    const uint64_t gmask = 0xffffull << (16 * g);                  // this lane's 16-lane group
 
-    // Loads of the tile at t0: whole tiles in a paged cache (rows allocated), masked rows past the
-    // end in a contiguous layout; a tile with an unreadable block entry loads nothing.
-    auto fetch = [&](int t0, TileRaw<KB, KQJL, VB>& raw, int& nvalid) {
+    auto fetch = [&](int t0, bool live, TileRaw<KB, KQJL, VB, NV>& raw, int& nvalid) {
         Tile tl;
-        locate(t0, tl);
+        locate(t0, live, tl);
         nvalid = tl.nvalid;
-        if (tl.nvalid == 0) return;
-        if (paged || tl.nvalid == 16)
-            load_tile<KB, KQJL, VB, false>(raw, tl, o, p.rrow, n, g, norm_vec);
-        else
-            load_tile<KB, KQJL, VB, true>(raw, tl, o, p.rrow, n, g, norm_vec);
+        load_tile<KB, KQJL, VB, NV, false>(raw, tl, o, p.rrow);
     };
 
-    TileRaw<KB, KQJL, VB> ra = {}, rb = {};
-    int va = 0, vb = 0;
-    fetch(t_begin, ra, va);
-    for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-        if (t0 + 16 < t_end) fetch(t0 + 16, rb, vb);
-        compute_tile<KB, KQJL, VB, QCOLS>(ra, va, sm, qop, qlo, qpop, s_ktab, s_vtab, bank, o, n, g, hvalid, p, sparse,
-                                          count);
-        if (t0 + 16 >= t_end) break;
-        if (t0 + 32 < t_end) fetch(t0 + 32, ra, va);
-        compute_tile<KB, KQJL, VB, QCOLS>(rb, vb, sm, qop, qlo, qpop, s_ktab, s_vtab, bank, o, n, g, hvalid, p, sparse,
-                                          count);
+    // Tiles 0..nfull-1 are complete.  A paged cache allocates whole blocks, so its partial last
+    // tile is loaded whole (and prefetched like the others); in a contiguous layout it is loaded
+    // with masking after the loop.  The partial tile is computed with row masking.
+    // Loads run kDepth - 1 tiles ahead of the compute through a ring of kDepth register tiles;
+    // tile T lives in slot T % kDepth.
+    constexpr int D = kDepth;
+    const int ntiles = (t_end - t_begin + 15) >> 4;
+    const int nfull = (t_end - t_begin) >> 4;
+    const int nload = paged ? ntiles : nfull;
+    TileRaw<KB, KQJL, VB, NV> ring[D];
+    int nv[D];
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k) fetch(t_begin + 16 * k, k < nload, ring[k], nv[k]);
+    for (int i = 0; i < nfull; i += D) {
+        bool done = false;
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int t = i + k;
+            if (t >= nfull) {
+                done = true;
+                break;
+            }
+            const int ahead = t + D - 1;
+            fetch(t_begin + 16 * ahead, ahead < nload, ring[(k + D - 1) % D], nv[(k + D - 1) % D]);
+            if (nv[k])
+                compute_tile<KB, KQJL, VB, NV, QCOLS, true>(ring[k], nv[k], sm, qop, qlo, qpop, kbank, vbank, one, o,
+                                                            g, hmask, gmask, p, sparse, count);
+        }
+        if (done) break;
+    }
+    if (nfull < ntiles) {
+        TileRaw<KB, KQJL, VB, NV> tr;
+        int tv;
+        if (paged) {
+            const int slot = nfull % D;
+            tr = ring[0];
+            tv = nv[0];
+#pragma unroll
+            for (int k = 1; k < D; ++k)
+                if (slot == k) {
+                    tr = ring[k];
+                    tv = nv[k];
+                }
+        } else {
+            Tile tl;
+            locate(t_begin + 16 * nfull, true, tl);
+            tv = tl.nvalid;
+            load_tile<KB, KQJL, VB, NV, true>(tr, tl, o, p.rrow);
+        }
+        if (tv)
+            compute_tile<KB, KQJL, VB, NV, QCOLS, false>(tr, tv, sm, qop, qlo, qpop, kbank, vbank, one, o, g, hmask,
+                                                         gmask, p, sparse, count);
     }
 
-    float lsum = sm.lsum;
-    lsum += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(lsum), 0x401f));
-    lsum += __shfl_xor(lsum, 32);
+    const float lsum = sum_over_groups(sm.lsum);
 
     if (hvalid) {
         const int64_t slot = ((s * p.hq + head) * (int64_t)p.n_chunks + c);
@@ -521,16 +627,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             dst[2 * r + 1] = make_float4(sm.acc[4][r] * vs, sm.acc[5][r] * vs, sm.acc[6][r] * vs, sm.acc[7][r] * vs);
         }
     }
-    if (count) {
-        unsigned long long a = sm.n_skip, b = sm.n_tot;
-        a += __shfl_xor(a, 16);
-        a += __shfl_xor(a, 32);
-        b += __shfl_xor(b, 16);
-        b += __shfl_xor(b, 32);
-        if (lane == 0) {
-            atomicAdd(p.skip_stats, a);
-            atomicAdd(p.skip_stats + 1, b);
-        }
+    if (count && lane == 0) {
+        atomicAdd(p.skip_stats, (unsigned long long)sm.n_skip);
+        atomicAdd(p.skip_stats + 1, (unsigned long long)sm.n_tot);
     }
 }
 
@@ -589,6 +688,10 @@ int check_region(const tq_region& r, int align) {
 int n_chunks_for(int max_seq_len, int chunk) { return max_seq_len <= 0 ? 1 : (max_seq_len + chunk - 1) / chunk; }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+size_t lds_bytes(int kb, int vb, int share) {
+    return ((size_t)1 << (2 * kb)) * 32 * 4 + (share ? 0 : ((size_t)1 << (2 * vb)) * 32 * 4);
+}
 
 bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
     const int64_t es = dtype == TQ_F32 ? 4 : 2;
@@ -693,6 +796,7 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     p.k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
     p.v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
     p.v_cinv = 1.f / p.v_cscale;
+    p.share_tab = (k->centroids == v->centroids && k->bits == v->bits && p.k_cscale == p.v_cscale) ? 1 : 0;
     p.k_perm = k->signs_permuted ? 1 : 0;
     p.block_size = block_size;
     p.num_blocks = block_tables ? num_blocks : (int64_t)1 << 62;
@@ -715,12 +819,20 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     const int64_t grid = (units + 3) / 4;
     if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
     hipStream_t st = (hipStream_t)stream;
-#define TQ_DEC(KB, KQ, VB)                                                                           \
-    do {                                                                                             \
-        if (group <= 8)                                                                              \
-            hipLaunchKernelGGL((decode_kernel<KB, KQ, VB, true>), dim3((unsigned)grid), dim3(256), 0, st, p); \
-        else                                                                                         \
-            hipLaunchKernelGGL((decode_kernel<KB, KQ, VB, false>), dim3((unsigned)grid), dim3(256), 0, st, p); \
+    // Norm rows 2 bytes apart: one 8-byte load per norm stream per tile.
+    const bool nv = p.rrow[R_KNORM] == 2 && p.rrow[R_VNORM] == 2 && (!k->qjl || p.rrow[R_KRNORM] == 2);
+    const size_t lds = lds_bytes(k->bits, v->bits, p.share_tab);
+#define TQ_DEC_QN(KB, KQ, VB, QC, NV) \
+    hipLaunchKernelGGL((decode_kernel<KB, KQ, VB, QC, NV>), dim3((unsigned)grid), dim3(256), lds, st, p)
+#define TQ_DEC(KB, KQ, VB)                              \
+    do {                                                \
+        if (group <= 8) {                               \
+            if (nv) TQ_DEC_QN(KB, KQ, VB, true, true);  \
+            else TQ_DEC_QN(KB, KQ, VB, true, false);    \
+        } else {                                        \
+            if (nv) TQ_DEC_QN(KB, KQ, VB, false, true); \
+            else TQ_DEC_QN(KB, KQ, VB, false, false);   \
+        }                                               \
     } while (0)
     const int key = (k->bits * 10 + v->bits) * 2 + (k->qjl ? 1 : 0);
     switch (key) {
@@ -745,6 +857,7 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         default: return TQ_ERR_BITS;
     }
 #undef TQ_DEC
+#undef TQ_DEC_QN
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
 
