@@ -90,7 +90,7 @@ def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_len
 def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, steps, warmup, extra_compress=None):
     import torch
     from turboquant.core import make_codebook
-    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, choose_tokens_per_chunk, decode_paged
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged, plan_tokens_per_chunk
 
     gen = torch.Generator(device=dev).manual_seed(seed)
     kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
@@ -107,14 +107,15 @@ def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, 
     bt = bt.to(dev)
     lens = torch.tensor(lens_host, dtype=torch.int32, device=dev)
     kc, kbnd = make_codebook(D, kb, device=dev)
-    vc, vbnd = make_codebook(D, vb, device=dev)
+    # one codebook tensor per bit width, shared by K and V as a serving stack holds it
+    vc, vbnd = (kc, kbnd) if vb == kb else make_codebook(D, vb, device=dev)
     k_cache = allocate_cache(nb, Hkv, kf, device=dev)
     v_cache = allocate_cache(nb, Hkv, vf, device=dev)
     fill_paged((k_cache, v_cache), (kf, vf), (kc, vc), (kbnd, vbnd), bt, lens_host, Hkv, gen, dev)
     q = torch.randn((B, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
     out = torch.empty_like(q)
     msl = max(lens_host)
-    chunk = choose_tokens_per_chunk(B, Hkv, msl)
+    chunk = plan_tokens_per_chunk(dev, B, Hq, Hkv, msl, kf, vf, kc is vc, lens_host)
     from turboquant import _lib
     ws = torch.empty(_lib.lib().tq_decode_workspace_bytes(B, Hq, msl, chunk), dtype=torch.uint8, device=dev)
     stats = torch.zeros(2, dtype=torch.int64, device=dev)
@@ -274,11 +275,15 @@ def main():
     dev = torch.device("cuda:0")
     steps, warmup = args.steps, args.warmup
     if args.copy_calibration:
+        # Two kernels of known traffic: the runtime's device copy and an elementwise multiply,
+        # each reading 256 MiB and writing 256 MiB.
         src = torch.ones(1 << 26, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         dst.copy_(src)
+        torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
-        print("# copy calibration: 268435456 bytes read, 268435456 bytes written", file=sys.stderr, flush=True)
+        print("# copy calibration: copyBuffer and mul kernels, 268435456 bytes read and 268435456 bytes "
+              "written each", file=sys.stderr, flush=True)
         del src, dst
     extra = {}
     import random

@@ -174,6 +174,16 @@ int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride
 
 size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk);
 
+/* Work units (one per sequence, KV head and chunk of tokens_per_chunk tokens) that tq_decode
+ * can run at once on the current device for this configuration: resident waves per compute
+ * unit of the kernel variant tq_decode would pick, times the compute units.  Callers size
+ * tokens_per_chunk from it so that the grid fills whole rounds.  No counterpart in the
+ * reference (its Triton launcher sizes the split from a fixed program target,
+ * kernels/attention.py:202-211).
+ * norm_row_bytes: row stride of the K / V norm streams (2 for the paged tile layout). */
+int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int num_q_heads, int num_kv_heads,
+                               int norm_row_bytes, int share_codebook, int* units);
+
 /* ---- packing helpers ----------------------------------------------------------- */
 
 /* Reorder sign rows [n_rows, 16] natural -> stride-4 permuted (out bit 32c+k = in bit 4k+c).

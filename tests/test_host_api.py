@@ -124,8 +124,27 @@ def test_paged_format_geometry():
     assert PagedKVFormat(bits=2, qjl=True).token_bytes + PagedKVFormat(bits=2).token_bytes == 86
     with pytest.raises(ValueError):
         PagedKVFormat(block_size=24)
-    ch = choose_tokens_per_chunk(64, 8, 32768)
-    assert ch % 16 == 0 and 64 <= ch <= 4096
+
+
+def test_chunk_choice_fills_whole_rounds():
+    # Uniform lengths: brute force over every chunk length (multiple of 16) of the cost
+    # rounds * (tiles per chunk + overhead) must not beat the choice.
+    from turboquant.kernels.paged import choose_tokens_per_chunk
+    for S, H, L, slots in [(64, 8, 32768, 3072), (64, 8, 32768, 2048), (32, 8, 8192, 3072), (3, 2, 300, 3072),
+                           (256, 8, 4096, 3072), (1, 1, 100000, 3072)]:
+        ch = choose_tokens_per_chunk(S, H, L, slots, unit_overhead_tiles=2.0)
+        assert ch % 16 == 0 and ch >= 64
+
+        def cost(c):
+            nch = math.ceil(L / c)
+            return math.ceil(S * H * nch / slots) * (math.ceil(L / 16 / nch) + 2.0)
+        best = min(cost(c) for c in range(64, 65537, 16))
+        assert cost(ch) <= best + 0.01 * math.ceil(L / ch) + 1e-9, (S, H, L, slots, ch)
+    # config4's shape: 64 x 8 x 6 chunks = 3072 units, one full round
+    assert math.ceil(32768 / choose_tokens_per_chunk(64, 8, 32768, 3072)) == 6
+    # variable lengths on the host shrink chunks towards the balanced load
+    lens = [2048] * 63 + [131072]
+    assert choose_tokens_per_chunk(64, 8, 131072, 3072, lens) < choose_tokens_per_chunk(64, 8, 131072, 3072)
 
 
 # ---------------------------------------------------------------- C ABI

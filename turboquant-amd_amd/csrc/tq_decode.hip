@@ -414,11 +414,13 @@ void decode_kernel(DecodeParams p) {
     // The wave index is uniform across the wave; saying so keeps every per-unit value in SGPRs
     // (otherwise buffer descriptors built from it are treated as divergent).
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Units in (sequence, chunk, KV head) order: the four waves of a workgroup (which holds its
+    // CU slot until all four finish) get the same chunk of one sequence, so equal work.
     const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
-    const int c = (int)(unit % p.n_chunks);
-    const int64_t sk = unit / p.n_chunks;
-    const int kh = (int)(sk % p.hkv);
-    const int64_t s = sk / p.hkv;
+    const int kh = (int)(unit % p.hkv);
+    const int64_t sc = unit / p.hkv;
+    const int c = (int)(sc % p.n_chunks);
+    const int64_t s = sc / p.n_chunks;
     if (s >= p.num_seqs) return;
 
     int L = p.seq_lens[s];
@@ -693,6 +695,21 @@ size_t lds_bytes(int kb, int vb, int share) {
     return ((size_t)1 << (2 * kb)) * 32 * 4 + (share ? 0 : ((size_t)1 << (2 * vb)) * 32 * 4);
 }
 
+// The decode_kernel instance for a configuration (nullptr: unsupported bit widths).
+const void* decode_kernel_ptr(int kb, bool kq, int vb, bool qcols, bool nv) {
+#define TQ_KP(KB, KQ, VB)                                                                          \
+    if (kb == KB && kq == KQ && vb == VB)                                                          \
+        return qcols ? (nv ? (const void*)decode_kernel<KB, KQ, VB, true, true>                    \
+                           : (const void*)decode_kernel<KB, KQ, VB, true, false>)                  \
+                     : (nv ? (const void*)decode_kernel<KB, KQ, VB, false, true>                   \
+                           : (const void*)decode_kernel<KB, KQ, VB, false, false>);
+#define TQ_KP_V(KB, KQ) TQ_KP(KB, KQ, 2) TQ_KP(KB, KQ, 3) TQ_KP(KB, KQ, 4)
+    TQ_KP_V(2, false) TQ_KP_V(2, true) TQ_KP_V(3, false) TQ_KP_V(3, true) TQ_KP_V(4, false) TQ_KP_V(4, true)
+#undef TQ_KP_V
+#undef TQ_KP
+    return nullptr;
+}
+
 bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
     const int64_t es = dtype == TQ_F32 ? 4 : 2;
     return aligned(q, 16) && (ss * es) % 16 == 0 && (sh * es) % 16 == 0;
@@ -704,6 +721,25 @@ extern "C" size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int m
     if (num_seqs <= 0 || num_q_heads <= 0 || tokens_per_chunk <= 0) return 0;
     const size_t slots = (size_t)num_seqs * num_q_heads * n_chunks_for(max_seq_len, tokens_per_chunk);
     return align_up(slots * TQ_HEAD_DIM * sizeof(float), 256) + 2 * align_up(slots * sizeof(float), 256);
+}
+
+extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int num_q_heads, int num_kv_heads,
+                                          int norm_row_bytes, int share_codebook, int* units) {
+    if (!units) return TQ_ERR_INVALID_ARGUMENT;
+    if (k_bits < 2 || k_bits > 4 || v_bits < 2 || v_bits > 4) return TQ_ERR_BITS;
+    if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return TQ_ERR_GQA;
+    const int group = num_q_heads / num_kv_heads;
+    if (group > 16) return TQ_ERR_GQA;
+    const void* kern = decode_kernel_ptr(k_bits, k_qjl != 0, v_bits, group <= 8, norm_row_bytes == 2);
+    if (!kern) return TQ_ERR_BITS;
+    const int share = (share_codebook && k_bits == v_bits) ? 1 : 0;
+    int blocks = 0, dev = 0, cus = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds_bytes(k_bits, v_bits, share));
+    if (e == hipSuccess) e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return (int)e;
+    *units = blocks * 4 * cus;  // 4 units (waves) per 256-thread workgroup
+    return TQ_OK;
 }
 
 extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
@@ -821,43 +857,12 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     hipStream_t st = (hipStream_t)stream;
     // Norm rows 2 bytes apart: one 8-byte load per norm stream per tile.
     const bool nv = p.rrow[R_KNORM] == 2 && p.rrow[R_VNORM] == 2 && (!k->qjl || p.rrow[R_KRNORM] == 2);
-    const size_t lds = lds_bytes(k->bits, v->bits, p.share_tab);
-#define TQ_DEC_QN(KB, KQ, VB, QC, NV) \
-    hipLaunchKernelGGL((decode_kernel<KB, KQ, VB, QC, NV>), dim3((unsigned)grid), dim3(256), lds, st, p)
-#define TQ_DEC(KB, KQ, VB)                              \
-    do {                                                \
-        if (group <= 8) {                               \
-            if (nv) TQ_DEC_QN(KB, KQ, VB, true, true);  \
-            else TQ_DEC_QN(KB, KQ, VB, true, false);    \
-        } else {                                        \
-            if (nv) TQ_DEC_QN(KB, KQ, VB, false, true); \
-            else TQ_DEC_QN(KB, KQ, VB, false, false);   \
-        }                                               \
-    } while (0)
-    const int key = (k->bits * 10 + v->bits) * 2 + (k->qjl ? 1 : 0);
-    switch (key) {
-        case 44: TQ_DEC(2, false, 2); break;
-        case 45: TQ_DEC(2, true, 2); break;
-        case 46: TQ_DEC(2, false, 3); break;
-        case 47: TQ_DEC(2, true, 3); break;
-        case 48: TQ_DEC(2, false, 4); break;
-        case 49: TQ_DEC(2, true, 4); break;
-        case 64: TQ_DEC(3, false, 2); break;
-        case 65: TQ_DEC(3, true, 2); break;
-        case 66: TQ_DEC(3, false, 3); break;
-        case 67: TQ_DEC(3, true, 3); break;
-        case 68: TQ_DEC(3, false, 4); break;
-        case 69: TQ_DEC(3, true, 4); break;
-        case 84: TQ_DEC(4, false, 2); break;
-        case 85: TQ_DEC(4, true, 2); break;
-        case 86: TQ_DEC(4, false, 3); break;
-        case 87: TQ_DEC(4, true, 3); break;
-        case 88: TQ_DEC(4, false, 4); break;
-        case 89: TQ_DEC(4, true, 4); break;
-        default: return TQ_ERR_BITS;
-    }
-#undef TQ_DEC
-#undef TQ_DEC_QN
+    const void* kern = decode_kernel_ptr(k->bits, k->qjl != 0, v->bits, group <= 8, nv);
+    if (!kern) return TQ_ERR_BITS;
+    void* args[] = {&p};
+    hipError_t le = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(256), args,
+                                    lds_bytes(k->bits, v->bits, p.share_tab), st);
+    if (le != hipSuccess) return (int)le;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
 

@@ -20,6 +20,7 @@ Slot addressing follows vLLM: token t goes to slot_mapping[t] = block * block_si
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -136,13 +137,80 @@ def compress_paged(
 
 
 def choose_tokens_per_chunk(num_seqs: int, num_kv_heads: int, max_seq_len: int,
-                            waves_per_cu: int = 16, min_chunk: int = 64, max_chunk: int = 4096) -> int:
-    """Split-K chunk length (multiple of 16) aiming at ~waves_per_cu work units per CU."""
-    units = max(1, num_seqs * num_kv_heads)
-    target = MI355X_CUS * waves_per_cu
-    per = math.ceil(max(1, max_seq_len) * units / target)
-    chunk = max(min_chunk, min(max_chunk, per))
-    return int(math.ceil(chunk / 16) * 16)
+                            concurrent_units: int = MI355X_CUS * 4 * 3, seq_lens_host=None,
+                            unit_overhead_tiles: float = 2.0, max_chunk: int = 65536) -> int:
+    """Split-K chunk length (multiple of 16) for tq_decode.
+
+    The grid has one work unit per (sequence, KV head, chunk of the sequence); concurrent_units
+    of them run at once (tq_decode_concurrent_units).  With every sequence max_seq_len long the
+    kernel takes ceil(units / concurrent_units) rounds of (chunk tiles + a fixed per-unit
+    cost), and the chunk count per sequence minimising that is chosen (chunks balanced: the last
+    is at most one tile shorter).  With the sequence lengths known on the host (seq_lens_host),
+    the estimate is the balanced load (all work / concurrent_units) plus half a unit of tail,
+    and never less than the longest unit.
+    """
+    slots = max(1, concurrent_units)
+    ovh = unit_overhead_tiles
+    tiles_max = max(1, -(-max(1, max_seq_len) // 16))
+    lens = None
+    if seq_lens_host is not None:
+        lens = [max(0, -(-min(int(x), max(1, max_seq_len)) // 16)) for x in seq_lens_host]
+        if not any(lens) or len(set(lens)) == 1:
+            tiles_max = max(lens) if any(lens) else tiles_max
+            lens = None  # uniform: the round model is exact
+    base = max(1, num_seqs * num_kv_heads)
+    max_nch = max(1, -(-tiles_max // 4))  # chunks of at least 4 tiles (64 tokens)
+    best = None
+    for nch in range(1, max_nch + 1):
+        ct = -(-tiles_max // nch)
+        if ct * 16 > max_chunk:
+            continue
+        if lens is None:
+            cost = -(-(base * nch) // slots) * (ct + ovh)
+        else:
+            units = num_kv_heads * sum(-(-t // ct) for t in lens)
+            work = num_kv_heads * sum(lens) + ovh * units
+            cost = max(work / slots + (0.5 * (ct + ovh) if units > slots else 0.0), ct + ovh)
+        cost += 0.01 * nch  # partial results to merge
+        if best is None or cost < best[0]:
+            best = (cost, ct)
+    if best is None:
+        return max_chunk // 16 * 16
+    return best[1] * 16
+
+
+@functools.lru_cache(maxsize=256)
+def _concurrent_units(device: int, k_bits: int, k_qjl: bool, v_bits: int, hq: int, hkv: int, norm_row: int,
+                      share: bool) -> int:
+    out = ctypes.c_int(0)
+    with torch.cuda.device(device):
+        _lib.check(_lib.lib().tq_decode_concurrent_units(k_bits, int(k_qjl), v_bits, hq, hkv, norm_row, int(share),
+                                                         ctypes.byref(out)), "tq_decode_concurrent_units")
+    return int(out.value)
+
+
+def plan_tokens_per_chunk(device: torch.device, num_seqs: int, num_q_heads: int, num_kv_heads: int,
+                          max_seq_len: int, k_fmt: "PagedKVFormat", v_fmt: "PagedKVFormat",
+                          share_codebook: bool = False, seq_lens_host=None, norm_row_bytes: int = 2) -> int:
+    """tokens_per_chunk for tq_decode on this device and configuration.
+
+    Per-unit cost beyond its tiles: about two tiles of set-up, plus writing and re-reading its
+    partial results (group heads x 128 fp32, twice) expressed in tiles of K+V data.
+    """
+    group = num_q_heads // max(1, num_kv_heads)
+    tile_bytes = 16 * (k_fmt.token_bytes + v_fmt.token_bytes)
+    overhead = 2.0 + group * 1024.0 / tile_bytes
+    units = concurrent_units(device, k_fmt.bits, k_fmt.qjl, v_fmt.bits, num_q_heads, num_kv_heads,
+                             norm_row_bytes, share_codebook)
+    return choose_tokens_per_chunk(num_seqs, num_kv_heads, max_seq_len, units, seq_lens_host, overhead)
+
+
+def concurrent_units(device: torch.device, k_bits: int, k_qjl: bool, v_bits: int, num_q_heads: int,
+                     num_kv_heads: int, norm_row_bytes: int = 2, share_codebook: bool = False) -> int:
+    """Decode work units resident at once on `device` for this configuration (occupancy query)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _concurrent_units(idx, k_bits, bool(k_qjl), v_bits, num_q_heads, num_kv_heads, norm_row_bytes,
+                             bool(share_codebook))
 
 
 def _region(ptr: int, stride_block: int, stride_head: int, stride_row: int, stride_seq: int = 0) -> _lib.TQRegion:
@@ -239,6 +307,7 @@ def decode_paged(
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
     skip_stats: Optional[torch.Tensor] = None,
+    seq_lens_host=None,
 ) -> torch.Tensor:
     """Decode attention of q [S, Hq, 128] (rotated space) over paged packed K/V caches.
 
@@ -247,7 +316,9 @@ def decode_paged(
     corr_scale defaults to sqrt(pi/2)/128 (reference/pytorch_reference.py:153-154).
     block_tables: int32 [S, max_blocks]; seq_lens: int32 [S]; max_seq_len: host-side upper
     bound of seq_lens (default: max_blocks * block_size).  sparse_threshold > 0 enables
-    Sparse-V.  Output dtype = out.dtype or q.dtype.
+    Sparse-V.  Output dtype = out.dtype or q.dtype.  seq_lens_host: the same lengths as a host
+    sequence, if the caller has them; they only size the split-K chunks.  Passing one tensor as
+    k_centroids and v_centroids (same codebook) lets the kernel keep one LDS table.
     """
     dev = _lib.require_gpu("decode_paged", q, k_cache, v_cache, block_tables, seq_lens, k_centroids, v_centroids)
     if q.dim() != 3 or q.shape[2] != 128:
@@ -280,13 +351,15 @@ def decode_paged(
     max_blocks = block_tables.shape[1]
     cap = max_blocks * k_fmt.block_size
     msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
-    chunk = tokens_per_chunk or choose_tokens_per_chunk(S, Hkv, msl)
     if out is None:
         out = torch.empty_like(q)
     kc = k_centroids.to(device=dev, dtype=torch.float32).contiguous()
     vc = v_centroids.to(device=dev, dtype=torch.float32).contiguous()
     if kc.numel() != 2 ** k_fmt.bits or vc.numel() != 2 ** v_fmt.bits:
         raise ValueError("centroid counts must match the formats' bit widths")
+    # One tensor for both codebooks lets the kernel keep a single LDS pair table.
+    share = kc.data_ptr() == vc.data_ptr()
+    chunk = tokens_per_chunk or plan_tokens_per_chunk(dev, S, Hq, Hkv, msl, k_fmt, v_fmt, share, seq_lens_host)
     kv = paged_view(k_cache, k_fmt, kc)
     vv = paged_view(v_cache, v_fmt, vc)
     return run_decode(

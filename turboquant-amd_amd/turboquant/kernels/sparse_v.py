@@ -18,7 +18,7 @@ from __future__ import annotations
 import torch
 
 from turboquant import _lib
-from turboquant.kernels.paged import choose_tokens_per_chunk, run_decode
+from turboquant.kernels.paged import choose_tokens_per_chunk, concurrent_units, run_decode
 
 D = 128
 DQ3 = D * 3 // 8  # 48 index bytes per slot
@@ -63,7 +63,8 @@ def tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, sc
     max_blocks = block_tables.shape[1]
     cap = max_blocks * bs
     msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
-    chunk = tokens_per_chunk or choose_tokens_per_chunk(S, hkv, msl)
+    chunk = tokens_per_chunk or choose_tokens_per_chunk(
+        S, hkv, msl, concurrent_units(dev, 3, False, 3, Hq, hkv, tq_cache.stride(2), True))
     kv = _aos_view(tq_cache, 0, cb)
     vv = _aos_view(tq_cache, 1, cb)
     target = out if out.stride(2) == 1 else torch.empty_like(out)
