@@ -153,7 +153,9 @@ typedef struct tq_kv_view {
  * out: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
  * block_tables: int32 [num_seqs, block_table_stride]; entries outside [0, num_blocks) are skipped.
  * max_seq_len: an upper bound of seq_lens (sizes the grid); longer sequences are truncated.
- * workspace: >= tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk).
+ * workspace: >= tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk),
+ *   256-byte aligned (split-K partial results; no initial contents needed).  Calls that overlap
+ *   in time must not share a workspace.
  * skip_stats: NULL or device uint64[2], incremented by (skipped, total) (token, KV head) pairs.
  * Replaces packed_attention (kernels/packed_attention.py:290-344) and the paged
  * _tq_v12_sparse_v_kernel / _tq_v11_single_kernel (kernels/sparse_v.py:25-261).

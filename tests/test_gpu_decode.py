@@ -163,6 +163,32 @@ def test_decode_sparse_v_matches_chunked_oracle(dev):
     np.testing.assert_allclose(dense, want_dense, rtol=RTOL, atol=ATOL)
 
 
+def test_decode_workspace_reuse(dev):
+    """One workspace across repeated and differently shaped calls (split into several chunks,
+    one chunk, and empty sequences) keeps matching the oracle."""
+    from turboquant import _lib
+    from turboquant.kernels.paged import PagedKVFormat, decode_paged
+
+    ws = torch.full((1 << 22,), 0x7f, dtype=torch.uint8, device=dev)  # stale contents do not matter
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    for rep, (lens, chunk) in enumerate([([300, 17, 64], 32), ([300, 17, 64], 32), ([1000, 0, 5, 77], 48)]):
+        S, Hq, Hkv = len(lens), 8, 2
+        case = build_case(40 + rep, S, Hq, Hkv, lens, 3, True, 3, 16)
+        kf, vf = PagedKVFormat(bits=3, qjl=True), PagedKVFormat(bits=3)
+        cb = _cb(3).to(dev)
+        q = torch.from_numpy(case["q"]).to(torch.bfloat16).to(dev)
+        msl = max(lens)
+        out = decode_paged(q, torch.from_numpy(case["k_cache"]).to(dev), kf, cb,
+                           torch.from_numpy(case["v_cache"]).to(dev), vf, cb,
+                           torch.from_numpy(case["bt"]).to(dev), torch.from_numpy(case["seq_lens"]).to(dev),
+                           sm_scale=sm, corr_scale=cs, max_seq_len=msl, tokens_per_chunk=chunk, workspace=ws)
+        torch.cuda.synchronize()
+        qr = q.float().cpu().numpy().astype(np.float64)
+        want, _, _ = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, q_round=qr)
+        np.testing.assert_allclose(out.float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+        assert _lib.lib().tq_decode_workspace_bytes(S, Hq, msl, chunk) <= ws.numel()
+
+
 def test_decode_bad_block_entries_are_skipped(dev):
     """Block-table entries outside [0, num_blocks) are ignored instead of read."""
     lens = [40]

@@ -22,7 +22,8 @@
 // whole and rows past the sequence end are masked in the softmax; in a contiguous layout rows
 // past the end get an out-of-range offset and read as zero.
 //
-// Each unit writes (m, l, acc[128]) per head; decode_reduce_kernel combines chunks:
+// A sequence of one chunk is normalised and written directly.  Otherwise each unit writes
+// (m, l, acc[128]) per head to the workspace and decode_reduce_kernel combines the chunks:
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:121-140)
 #include "tq_common.h"
 
@@ -68,6 +69,9 @@ struct DecodeParams {
     float* ws_m;       // [num_seqs][hq][n_chunks]  (log2 domain)
     float* ws_l;
     unsigned long long* skip_stats;
+    void* out;
+    int out_dtype;
+    int64_t out_ss, out_sh;
 };
 
 // nrec = 0 turns every load through the descriptor into a zero read (unreadable block).
@@ -613,25 +617,40 @@ void decode_kernel(DecodeParams p) {
     }
 
     const float lsum = sum_over_groups(sm.lsum);
+    if (count && lane == 0) {
+        atomicAdd(p.skip_stats, (unsigned long long)sm.n_skip);
+        atomicAdd(p.skip_stats + 1, (unsigned long long)sm.n_tot);
+    }
+    // acc[nn][r] is dim 8*(4g+r)+nn = 32g + 8r + nn; v_cinv undoes the V table scale.
+    const float vs = p.v_cinv;
+    int nch = (L + p.chunk - 1) / p.chunk;
+    nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len are not processed
 
+    if (nch == 1) {  // the only chunk: normalise and write the output directly
+        if (hvalid) {
+            const float inv = lsum > 0.f ? vs / lsum : 0.f;
+            const int64_t ob = s * p.out_ss + (int64_t)head * p.out_sh + 32 * g;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int nn = 0; nn < 8; ++nn) tq_store1(p.out, ob + 8 * r + nn, p.out_dtype, sm.acc[nn][r] * inv);
+        }
+        return;
+    }
+
+    // Partial results of this chunk: (m, l, acc) per head.
     if (hvalid) {
         const int64_t slot = ((s * p.hq + head) * (int64_t)p.n_chunks + c);
         if (g == 0) {
             p.ws_m[slot] = sm.m;
             p.ws_l[slot] = lsum;
         }
-        // acc[nn][r] is dim 8*(4g+r)+nn = 32g + 8r + nn; v_cinv undoes the V table scale.
-        const float vs = p.v_cinv;
         float4* dst = reinterpret_cast<float4*>(p.ws_acc + slot * TQ_HEAD_DIM + 32 * g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             dst[2 * r] = make_float4(sm.acc[0][r] * vs, sm.acc[1][r] * vs, sm.acc[2][r] * vs, sm.acc[3][r] * vs);
             dst[2 * r + 1] = make_float4(sm.acc[4][r] * vs, sm.acc[5][r] * vs, sm.acc[6][r] * vs, sm.acc[7][r] * vs);
         }
-    }
-    if (count && lane == 0) {
-        atomicAdd(p.skip_stats, (unsigned long long)sm.n_skip);
-        atomicAdd(p.skip_stats + 1, (unsigned long long)sm.n_tot);
     }
 }
 
@@ -646,7 +665,9 @@ struct ReduceParams {
     int64_t out_ss, out_sh;
 };
 
-// One wave per (sequence, query head); lane d covers dims 2d, 2d+1.
+// Split-K merge, one wave per (sequence, query head); lane d covers dims 2d, 2d+1:
+//   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:128-140)
+// Sequences of one chunk were written by decode_kernel; empty ones are written as zero here.
 __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     const int64_t sh = blockIdx.x;
     const int64_t s = sh / p.hq;
@@ -656,6 +677,7 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     L = L < p.cap ? L : p.cap;
     int nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
     nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
+    if (nch == 1) return;
     const int64_t base = sh * p.n_chunks;
     float M = kNegInf;
     for (int c = 0; c < nch; ++c) M = fmaxf(M, p.ws_m[base + c]);
@@ -674,7 +696,6 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     tq_store1(p.out, o, p.out_dtype, a0 * inv);
     tq_store1(p.out, o + 1, p.out_dtype, a1 * inv);
 }
-
 
 bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 
@@ -720,6 +741,7 @@ bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
 extern "C" size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk) {
     if (num_seqs <= 0 || num_q_heads <= 0 || tokens_per_chunk <= 0) return 0;
     const size_t slots = (size_t)num_seqs * num_q_heads * n_chunks_for(max_seq_len, tokens_per_chunk);
+    // acc, m, l per (sequence, query head, chunk)
     return align_up(slots * TQ_HEAD_DIM * sizeof(float), 256) + 2 * align_up(slots * sizeof(float), 256);
 }
 
@@ -850,6 +872,10 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     p.ws_m = ws_m;
     p.ws_l = ws_l;
     p.skip_stats = skip_stats;
+    p.out = out;
+    p.out_dtype = out_dtype;
+    p.out_ss = out_stride_seq;
+    p.out_sh = out_stride_head;
 
     const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
     const int64_t grid = (units + 3) / 4;

@@ -136,6 +136,24 @@ def compress_paged(
     return cache
 
 
+_WORKSPACES: dict = {}
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """tq_decode workspace of at least nbytes for `device` and its current stream.
+
+    One buffer per stream is reused (calls on one stream are ordered; calls that overlap in
+    time must not share a workspace).
+    """
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, _lib.stream_handle(device))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def choose_tokens_per_chunk(num_seqs: int, num_kv_heads: int, max_seq_len: int,
                             concurrent_units: int = MI355X_CUS * 4 * 3, seq_lens_host=None,
                             unit_overhead_tiles: float = 2.0, max_chunk: int = 65536) -> int:
@@ -263,7 +281,7 @@ def run_decode(
     L = _lib.lib()
     need = L.tq_decode_workspace_bytes(S, Hq, max_seq_len, tokens_per_chunk)
     if workspace is None or workspace.numel() < need or workspace.data_ptr() % 256:
-        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        workspace = decode_workspace(dev, need)
     if skip_stats is not None and (skip_stats.dtype != torch.int64 or skip_stats.numel() < 2 or not skip_stats.is_cuda):
         raise ValueError("skip_stats must be a device int64 tensor with 2 elements")
     bt_ptr = block_tables.data_ptr() if block_tables is not None else None
