@@ -40,6 +40,23 @@ def outlier_kv(T, H, gen, device, dtype):
     return (torch.randn(T, H, D, generator=gen, device=device) * scale).to(dtype)
 
 
+def profiled_traffic(head):
+    """HBM bytes per launch of the headline decode kernel from the committed rocprof summary.
+
+    profiles/decode_kernel_config4_pmc.md holds FETCH_SIZE and WRITE_SIZE of the kernel (two
+    rocprofv3 --pmc runs of this script with --copy-calibration), scaled by what the same
+    counters read for two kernels of known traffic.  Returned only for the config 4 headline.
+    """
+    import re
+    path = ROOT / "profiles" / "decode_kernel_config4_pmc.md"
+    if not head.get("workload", "").startswith("config4") or not path.exists():
+        return None, None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", path.read_text(), re.M)
+    if not m:
+        return None, None
+    return int(m.group(1)), "profiles/decode_kernel_config4_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)"
+
+
 def timed(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -321,6 +338,7 @@ def main():
     if state4 is not None and not args.no_cpu_baseline:
         cpu = cpu_baseline_decode(state4)
     us = head["us_per_layer"]
+    traffic, traffic_src = profiled_traffic(head)
     line = {
         "metric": METRIC,
         "value": round(us, 3),
@@ -341,7 +359,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(head.get("frac_of_8tbs", 0.0), 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
         },
         "cpu_baseline": cpu,
         "details": {"headline": head, **extra,
