@@ -81,6 +81,37 @@ int tq_polarquant_compress(const void* x, int x_dtype, int64_t x_row_stride, int
                            tq_stream_t stream);
 
 /*
+ * polarquant_compress with a general rotation matrix (core/quantizer.py:111-183,
+ * rotation_matrix not the Walsh-Hadamard matrix): x_rot = x @ rotation, then the same math and
+ * outputs as tq_polarquant_compress.  rotation: f32 [128][128] row-major (contiguous).  The
+ * product is fp32 (FMA over d ascending).
+ */
+int tq_polarquant_compress_matrix(const void* x, int x_dtype, int64_t x_row_stride, int64_t n_rows,
+                                  int head_dim, const float* rotation,
+                                  const float* centroids, const float* boundaries, int bits, int use_qjl,
+                                  int64_t* indices, float* norms, float* k_mse, float* signs, float* rnorm,
+                                  tq_stream_t stream);
+
+/*
+ * Packed K / V compression with explicit rotation matrices.  Replaces compress_k / compress_v
+ * and the _fully_packed_k / _fully_packed_v kernels (kernels/packed_compress.py:44-142,157-177,
+ * 226-240):
+ *   norm = |x|; x_n = x * (1 / (norm + 1e-8)); rot = x_n @ pit; idx = #{boundaries <= rot};
+ *   K (pist != NULL): resid = (rot - centroids[idx]) * norm; rnorm = |resid|;
+ *                     proj = resid @ pist; sign bit = proj >= 0.
+ * pit, pist: f32 [128][128] row-major.  Products in fp32 (the reference's fp16 dot products
+ * are not reproduced).  Outputs (contiguous rows): idx_out u8 [n_rows][16*bits] little-endian
+ * bit stream (2 bits: byte j = sum_c idx[4j+c] << 2c), signs_out u8 [n_rows][16] (bit b of byte
+ * j = dim 8j+b), rnorm_out / norm_out fp16 [n_rows] (uint16 storage).  signs_out and rnorm_out
+ * are read only with pist.  bits: 1..4 (the reference: 2).  Needs 140 KB (K) / 76 KB (V) of LDS
+ * per workgroup; TQ_ERR_WORKSPACE if the device has less.
+ */
+int tq_compress_packed(const void* x, int x_dtype, int64_t x_row_stride, int64_t n_rows, int head_dim,
+                       const float* pit, const float* pist, const float* centroids, const float* boundaries,
+                       int bits, uint8_t* idx_out, uint8_t* signs_out, uint16_t* rnorm_out, uint16_t* norm_out,
+                       tq_stream_t stream);
+
+/*
  * Fused paged compression: x [num_tokens, num_heads, 128] -> packed rows written into the
  * paged cache at slot_mapping[t] (block = slot / block_size, row = slot % block_size).
  * Negative slots are skipped (the reference clamps them to 0, integration/vllm_backend.py:223-230).

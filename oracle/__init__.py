@@ -14,6 +14,9 @@ Modules and what pins each function (beyond restating the reference's formula):
   compress  polarquant_compress (core/quantizer.py:111-183) pinned by an fp64 shadow
             computation (indices equal except within a rounding band of a boundary), basis
             and zero vectors with known answers, and the reference tests' invariants.
+            compress_packed (kernels/packed_compress.py:64-142) pinned by agreement with the
+            polarquant shadow for PiT = WHT, PiST = I (the two orders of operations differ only
+            inside the band), and by basis vectors with PiT = I that pin the >= tie rule.
   packing   bit formats (Appendix-A rules: packed_compress.py:79-106,145-154,180-216;
             sparse_v.py:57-98; AITER_TURBO4_DESIGN.md:57-76) pinned by brute force over every
             field value / bit position and pack-unpack round trips.

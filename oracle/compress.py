@@ -119,3 +119,30 @@ def classify_index_mismatch(idx_test: torch.Tensor, idx_ref: torch.Tensor, xn_re
     adjacent = (t[mism] - r[mism]).abs() == 1
     ok = (band <= band_ulps) & adjacent
     return n, int(ok.sum()), int((~ok).sum()), float(band.max())
+
+
+def compress_packed(x: np.ndarray, pit: np.ndarray, pist: np.ndarray | None, centroids: np.ndarray,
+                    boundaries: np.ndarray):
+    """Restates _fully_packed_k / _fully_packed_v (kernels/packed_compress.py:64-106,118-142) in
+    float64 with exact products (the reference's fp16 tl.dot rounding is not a target):
+        norm = |x|; x_n = x * (1 / (norm + 1e-8)); rot = x_n @ PiT; idx = #{b <= rot}  (>= rule)
+        resid = (rot - c[idx]) * norm; rnorm = |resid|; proj = resid @ PiST; sign = proj >= 0.
+    Returns a dict of float64 / int arrays with the decision margins the tests classify by:
+    rot_margin = |rot - nearest boundary|, proj_scale = sum_d |resid_d * PiST_dj| (the size of
+    the terms summed into proj_j)."""
+    x = np.asarray(x, dtype=np.float64).reshape(-1, x.shape[-1])
+    c = np.asarray(centroids, dtype=np.float64)
+    b = np.asarray(boundaries, dtype=np.float64)
+    norm = np.sqrt((x * x).sum(axis=1))
+    xn = x * (1.0 / (norm + 1e-8))[:, None]
+    rot = xn @ np.asarray(pit, dtype=np.float64)
+    idx = (rot[..., None] >= b).sum(axis=-1)
+    out = {"norm": norm, "rot": rot, "idx": idx,
+           "rot_margin": np.abs(rot[..., None] - b).min(axis=-1) if b.size else np.full(rot.shape, np.inf)}
+    if pist is not None:
+        P = np.asarray(pist, dtype=np.float64)
+        resid = (rot - c[idx]) * norm[:, None]
+        proj = resid @ P
+        out.update(resid=resid, rnorm=np.sqrt((resid * resid).sum(axis=1)), proj=proj,
+                   sign=(proj >= 0).astype(np.uint8), proj_scale=np.abs(resid) @ np.abs(P))
+    return out

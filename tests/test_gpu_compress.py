@@ -33,11 +33,11 @@ def _report(name, stats):
     print(f"[{name}] index mismatches {n} (in band {ok}, out of band {bad}, max band {band:.2f} ulp)")
 
 
-def check_against_oracle(res, ref, cent, bnd, bits, use_qjl, name):
+def check_against_oracle(res, ref, cent, bnd, bits, use_qjl, name, band_ulps=BAND_ULPS):
     xn = ref["x_normalized"].reshape(-1, 128)
     idx_gpu = res["indices"].cpu().reshape(-1, 128)
     idx_ref = ref["indices"].reshape(-1, 128)
-    stats = ocomp.classify_index_mismatch(idx_gpu, idx_ref, xn, bnd, BAND_ULPS)
+    stats = ocomp.classify_index_mismatch(idx_gpu, idx_ref, xn, bnd, band_ulps)
     _report(name, stats)
     assert stats[2] == 0, f"{name}: {stats[2]} index mismatches outside the boundary band"
     assert stats[0] <= max(4, idx_ref.numel() // 20000), f"{name}: too many boundary mismatches {stats[0]}"
@@ -53,7 +53,7 @@ def check_against_oracle(res, ref, cent, bnd, bits, use_qjl, name):
         sr = ref["signs"].reshape(-1, 128)
         diff = sg != sr
         cb = ocomp.centroid_band(xn, cent, idx_ref.reshape(-1, 128))
-        explained = (~same) | (cb <= BAND_ULPS)
+        explained = (~same) | (cb <= band_ulps)
         assert not (diff & ~explained).any(), f"{name}: sign flips away from centroids/boundaries"
         rows_clean = same.all(dim=1)
         torch.testing.assert_close(res["rot_residual_norm"].cpu()[rows_clean], ref["rot_residual_norm"][rows_clean],
@@ -93,6 +93,117 @@ def test_polarquant_variants(dev, bits, use_qjl, dtype, rotate):
     res = polarquant_compress(x.to(dev), cent.to(dev), bnd.to(dev), cfg, None if H is None else H.to(dev))
     ref = ocomp.polarquant_compress(x.float(), cent, bnd, 2 ** bits, use_qjl, H)
     check_against_oracle(res, ref, cent, bnd, bits, use_qjl, f"b{bits} q{int(use_qjl)} {dtype} rot{int(rotate)}")
+
+
+def _random_rotation(seed):
+    """Pi (orthogonal, from QR with the sign fix) and S (Gaussian) as the reference builds them
+    (kernels/packed_compress.py:265-273): PiT = Pi^T, PiST = Pi S^T."""
+    g = torch.Generator().manual_seed(seed)
+    G = torch.randn(128, 128, generator=g, dtype=torch.float64)
+    Q, R = torch.linalg.qr(G)
+    ds = torch.sign(torch.diag(R))
+    ds[ds == 0] = 1.0
+    Pi = Q * ds.unsqueeze(0)
+    S = torch.randn(128, 128, generator=torch.Generator().manual_seed(seed + 10000), dtype=torch.float64)
+    return Pi.T.contiguous().float(), (Pi @ S.T).contiguous().float()
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_polarquant_general_rotation(dev, bits, dtype):
+    """rotation_matrix that is not a WHT: fp32 product kernel vs the oracle's torch op sequence.
+    The two sum x_d R_dj in different orders; the band allows 64 ulps at the coordinate scale."""
+    from turboquant.core import PolarQuantConfig, polarquant_compress
+    g = torch.Generator().manual_seed(2000 + bits)
+    x = (torch.randn(515, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 0.5)).to(dtype)
+    R, _ = _random_rotation(40 + bits)
+    cent, bnd = _codebook(bits)
+    for use_qjl in (False, True):
+        cfg = PolarQuantConfig(head_dim=128, bits=bits, use_qjl=use_qjl)
+        res = polarquant_compress(x.to(dev), cent.to(dev), bnd.to(dev), cfg, R.to(dev))
+        ref = ocomp.polarquant_compress(x.float(), cent, bnd, 2 ** bits, use_qjl, R)
+        check_against_oracle(res, ref, cent, bnd, bits, use_qjl, f"general b{bits} q{int(use_qjl)} {dtype}",
+                             band_ulps=64.0)
+
+
+# compress_k / compress_v: decisions compared with the float64 restatement.  A GPU decision may
+# differ only where the oracle's margin is within fp32 rounding: |rot - boundary| <= ROT_BAND, or
+# |proj| <= PROJ_REL * sum_d |resid_d PiST_dj|; rows with an index difference are exempt from the
+# sign comparison (their residual differs).
+ROT_BAND = 1e-6
+PROJ_REL = 1e-5
+
+
+def _kernel_codebook(bits):
+    from oracle import codebook as ocb
+    c = np.array(ocb.kernel_codebook(128, bits), dtype=np.float32)
+    b = ((c[:-1] + c[1:]) / 2.0).astype(np.float32)
+    return torch.from_numpy(c), torch.from_numpy(b)
+
+
+@pytest.mark.parametrize("bits", [2, 1, 3, 4])
+@pytest.mark.parametrize("n", [1, 1023, 4096])
+def test_compress_k_v_against_oracle(dev, bits, n):
+    from turboquant.kernels.packed_compress import compress_k, compress_k_permuted, compress_v
+    g = torch.Generator().manual_seed(3000 + bits * 7 + n)
+    K = torch.randn(n, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 0.5)
+    PiT, PiST = _random_rotation(11 + bits)
+    cent, bnd = _kernel_codebook(bits)
+    t = lambda a: a.to(dev)  # noqa: E731
+    k_idx, k_signs, k_rnorm, k_norm = compress_k(t(K), t(PiT), t(PiST), t(cent), t(bnd))
+    torch.cuda.synchronize()
+    assert k_idx.dtype == torch.uint8 and k_idx.shape == (n, 16 * bits)
+    assert k_signs.shape == (n, 16) and k_rnorm.dtype == torch.float16 and k_norm.dtype == torch.float16
+    ref = ocomp.compress_packed(K.double().numpy(), PiT.double().numpy(), PiST.double().numpy(),
+                                cent.double().numpy(), bnd.double().numpy())
+    idx_gpu = opack.unpack_indices(k_idx.cpu().numpy(), bits)
+    diff = idx_gpu != ref["idx"]
+    assert not (diff & (ref["rot_margin"] > ROT_BAND)).any(), "index differences outside the band"
+    assert (np.abs(idx_gpu[diff].astype(int) - ref["idx"][diff]) == 1).all()
+    print(f"[compress_k b{bits} n{n}] index differences in band: {int(diff.sum())}")
+    # the kernel's bytes are exactly the oracle's packing of the oracle's decisions, where the
+    # band-exempt elements take the GPU's value
+    merged = np.where(diff, idx_gpu, ref["idx"])
+    np.testing.assert_array_equal(k_idx.cpu().numpy(), opack.pack_indices(merged, bits))
+    rows_ok = ~diff.any(axis=1)
+    sg = opack.unpack_signs(k_signs.cpu().numpy())
+    sdiff = (sg != ref["sign"]) & rows_ok[:, None]
+    assert not (sdiff & (np.abs(ref["proj"]) > PROJ_REL * ref["proj_scale"])).any(), "sign flips outside the band"
+    print(f"[compress_k b{bits} n{n}] sign differences in band: {int(sdiff.sum())}, rows exempt: {int((~rows_ok).sum())}")
+    merged_s = np.where(sdiff | ~rows_ok[:, None], sg, ref["sign"])
+    np.testing.assert_array_equal(k_signs.cpu().numpy(), opack.pack_signs(merged_s))
+    np.testing.assert_allclose(k_norm.float().cpu().numpy(), ref["norm"], rtol=1e-3)
+    np.testing.assert_allclose(k_rnorm.float().cpu().numpy()[rows_ok], ref["rnorm"][rows_ok], rtol=1e-3, atol=1e-6)
+    # permuted variant = permutation of the natural signs
+    _, k_sp, _, _ = compress_k_permuted(t(K), t(PiT), t(PiST), t(cent), t(bnd))
+    np.testing.assert_array_equal(k_sp.cpu().numpy(), opack.permute_signs(k_signs.cpu().numpy()))
+    # V: same rotation and quantizer, no residual
+    v_idx, v_norm = compress_v(t(K), t(PiT), t(cent), t(bnd))
+    np.testing.assert_array_equal(v_idx.cpu().numpy(), k_idx.cpu().numpy())
+    np.testing.assert_array_equal(v_norm.cpu().numpy(), k_norm.cpu().numpy())
+
+
+def test_compress_k_v_input_dtypes_and_rejections(dev):
+    from turboquant.kernels.packed_compress import compress_k, compress_v
+    PiT, PiST = _random_rotation(5)
+    cent, bnd = _kernel_codebook(2)
+    K = torch.randn(64, 128, generator=torch.Generator().manual_seed(9))
+    t = lambda a: a.to(dev)  # noqa: E731
+    base = compress_k(t(K), t(PiT), t(PiST), t(cent), t(bnd))
+    for dt in (torch.bfloat16, torch.float16):
+        Kd = K.to(dt)
+        got = compress_k(t(Kd), t(PiT), t(PiST), t(cent), t(bnd))
+        ref = ocomp.compress_packed(Kd.double().numpy(), PiT.double().numpy(), PiST.double().numpy(),
+                                    cent.double().numpy(), bnd.double().numpy())
+        idx = opack.unpack_indices(got[0].cpu().numpy(), 2)
+        assert not ((idx != ref["idx"]) & (ref["rot_margin"] > ROT_BAND)).any()
+    with pytest.raises(ValueError):
+        compress_k(t(K[:, :64]), t(PiT), t(PiST), t(cent), t(bnd))
+    with pytest.raises(ValueError):
+        compress_v(t(K), t(PiT), t(cent[:3]), t(bnd))
+    with pytest.raises(ValueError):
+        compress_k(K, PiT, PiST, cent, bnd)  # CPU tensors: no CPU fallback
+    assert base[0].shape == (64, 32)
 
 
 def test_polarquant_3d_and_edge_rows(dev):

@@ -115,6 +115,51 @@ def test_compress_oracle_vs_fp64_shadow(bits, use_qjl):
         np.testing.assert_allclose(ref["rot_residual_norm"].numpy(), sh["rot_residual_norm"].numpy(), rtol=1e-4)
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_compress_packed_agrees_with_polarquant_shadow_for_wht(bits):
+    """compress_packed (norm first, multiply by the reciprocal, >= rule, residual through PiST)
+    and the polarquant fp64 shadow (rotate first, divide, > rule, residual signs) describe the
+    same quantizer when PiT is the WHT and PiST = I: indices, signs and norms must agree except
+    at exact ties.  A slip in either restatement (order, the 1e-8, the residual scaling, the
+    sign convention) breaks this."""
+    torch.manual_seed(7)
+    x = torch.randn(400, 128) * torch.exp(torch.randn(128) * 0.5)
+    c, b = ocb.solve_codebook_quad(128, bits)
+    c, b = torch.tensor(c), torch.tensor(b)
+    h = float(ocomp.wht_matrix(128)[0, 0])
+    H = ocomp.wht_closed_form(128, h)
+    pk = ocomp.compress_packed(x.double().numpy(), H, np.eye(128), c.numpy(), b.numpy())
+    sh = ocomp.polarquant_compress_fp64(x, c, b, use_qjl=True, rotate=True)
+    np.testing.assert_array_equal(pk["idx"], sh["indices"].numpy())
+    # |x| vs |x H|: H's entries are the fp32-rounded h, so H is orthogonal to ~2e-8 only
+    np.testing.assert_allclose(pk["norm"], sh["norms"].numpy(), rtol=5e-8)
+    np.testing.assert_allclose(pk["rnorm"], sh["rot_residual_norm"].numpy(), rtol=5e-7)
+    sign_sh = (sh["signs"].numpy() > 0).astype(np.uint8)
+    np.testing.assert_array_equal(pk["sign"], sign_sh)
+
+
+def test_compress_packed_tie_rule_on_basis_vectors():
+    """Known answers with PiT = PiST = I: rows 3 e_d against c = (-1.5, -0.5, 0.5, 1.5)/s,
+    b = (-1, 0, 1)/s.  Zero coordinates sit exactly on the middle boundary: the >= rule gives
+    index 2 (searchsorted-left would give 1), residual (0 - c2) * 3 < 0 -> sign bit 0; the unit
+    coordinate gives index 3, residual (1 - c3) * 3 > 0 -> sign bit 1."""
+    s = math.sqrt(128)
+    c = np.array([-1.5, -0.5, 0.5, 1.5]) / s
+    b = np.array([-1.0, 0.0, 1.0]) / s
+    x = 3.0 * np.eye(128)
+    pk = ocomp.compress_packed(x, np.eye(128), np.eye(128), c, b)
+    want_idx = np.full((128, 128), 2)
+    np.fill_diagonal(want_idx, 3)
+    np.testing.assert_array_equal(pk["idx"], want_idx)
+    np.testing.assert_allclose(pk["norm"], 3.0)
+    want_sign = np.eye(128, dtype=np.uint8)
+    np.testing.assert_array_equal(pk["sign"], want_sign)
+    # the unit coordinate is u = 3 * (1 / (3 + 1e-8)); rnorm^2 = 127 * (0.5/s * 3)^2 + ((u - 1.5/s) * 3)^2
+    u = 3.0 * (1.0 / (3.0 + 1e-8))
+    want_rn = math.sqrt(127 * (1.5 / s) ** 2 + (3 * (u - 1.5 / s)) ** 2)
+    np.testing.assert_allclose(pk["rnorm"], want_rn, rtol=1e-12)
+
+
 def test_compress_oracle_known_answers():
     c, b = ocb.solve_codebook_quad(128, 3)
     cent, bnd = torch.tensor(c), torch.tensor(b)

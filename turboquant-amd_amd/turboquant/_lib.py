@@ -91,6 +91,10 @@ SIGNATURES = {
     ),
     "tq_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "tq_decode_concurrent_units": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
+    "tq_polarquant_compress_matrix": (
+        _i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tq_compress_packed": (
+        _i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp]),
     "tq_permute_signs": (_i32, [_vp, _vp, _i64, _i32, _vp]),
     "tq_unpack_bits": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp]),
 }

@@ -87,16 +87,15 @@ class PolarQuantConfig:
 
 
 def _rotation_mode(rotation_matrix: Optional[torch.Tensor], d: int) -> tuple[int, float]:
+    """(1, h) for a Walsh-Hadamard matrix with entries +-h (rotated in registers), (0, 1) for
+    None, (-1, 0) for any other [d, d] matrix (fp32 product kernel)."""
     if rotation_matrix is None:
         return 0, 1.0
     if tuple(rotation_matrix.shape) != (d, d):
         raise ValueError(f"rotation_matrix must be [{d}, {d}], got {tuple(rotation_matrix.shape)}")
     h = wht_magnitude(rotation_matrix)
     if h is None:
-        raise NotImplementedError(
-            "polarquant_compress on the GPU supports rotation_matrix=None or a Walsh-Hadamard matrix "
-            "(make_wht_matrix); use turboquant.kernels.packed_compress.compress_k for a general rotation"
-        )
+        return -1, 0.0
     return 1, h
 
 
@@ -109,8 +108,9 @@ def polarquant_compress(
 ) -> dict:
     """Compress vectors with PolarQuant on the GPU (core/quantizer.py:111-183).
 
-    x: [N, D] or [B, H, D] (f32/f16/bf16, D = 128) on a GPU. rotation_matrix: the WHT matrix,
-    or None for pre-rotated input.  Returns the reference's dictionary:
+    x: [N, D] or [B, H, D] (f32/f16/bf16, D = 128) on a GPU. rotation_matrix: None for
+    pre-rotated input, the WHT matrix (rotated in registers) or any [D, D] matrix (fp32 product,
+    x_rot = x @ rotation_matrix).  Returns the reference's dictionary:
       indices [*, D] int64, norms [N] f32 (flat also for 3-D input), k_mse_rot [*, D] f32 and,
       with config.use_qjl, signs [*, D] f32 (+-1) and rot_residual_norm [N] f32.
     """
@@ -142,13 +142,23 @@ def polarquant_compress(
     rnorm = torch.empty((n,), dtype=torch.float32, device=dev) if use_qjl else None
 
     L = _lib.lib()
-    rc = L.tq_polarquant_compress(
-        x.data_ptr(), _lib.dtype_code(x), x.stride(0), n, d, rotate, scale,
-        cent.data_ptr(), bnd.data_ptr(), bits, int(use_qjl),
-        indices.data_ptr(), norms.data_ptr(), k_mse.data_ptr(), _lib.ptr(signs), _lib.ptr(rnorm),
-        _lib.stream_handle(dev),
-    )
-    _lib.check(rc, "tq_polarquant_compress")
+    if rotate < 0:
+        rot = rotation_matrix.to(device=dev, dtype=torch.float32).contiguous()
+        rc = L.tq_polarquant_compress_matrix(
+            x.data_ptr(), _lib.dtype_code(x), x.stride(0), n, d, rot.data_ptr(),
+            cent.data_ptr(), bnd.data_ptr(), bits, int(use_qjl),
+            indices.data_ptr(), norms.data_ptr(), k_mse.data_ptr(), _lib.ptr(signs), _lib.ptr(rnorm),
+            _lib.stream_handle(dev),
+        )
+        _lib.check(rc, "tq_polarquant_compress_matrix")
+    else:
+        rc = L.tq_polarquant_compress(
+            x.data_ptr(), _lib.dtype_code(x), x.stride(0), n, d, rotate, scale,
+            cent.data_ptr(), bnd.data_ptr(), bits, int(use_qjl),
+            indices.data_ptr(), norms.data_ptr(), k_mse.data_ptr(), _lib.ptr(signs), _lib.ptr(rnorm),
+            _lib.stream_handle(dev),
+        )
+        _lib.check(rc, "tq_polarquant_compress")
 
     result = {"indices": indices, "norms": norms, "k_mse_rot": k_mse}
     if use_qjl:

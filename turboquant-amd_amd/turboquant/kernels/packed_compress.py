@@ -91,3 +91,63 @@ def permute_signs_for_chunked(signs_packed: torch.Tensor, D: int = 128) -> torch
     rc = _lib.lib().tq_permute_signs(rows.data_ptr(), out.data_ptr(), n, D, _lib.stream_handle(rows.device))
     _lib.check(rc, "tq_permute_signs")
     return out.reshape(shape)
+
+
+def _packed_compress(x: torch.Tensor, pit: torch.Tensor, pist, centroids: torch.Tensor,
+                     boundaries: torch.Tensor, what: str):
+    dev = _lib.require_gpu(what, x, pit, *( [pist] if pist is not None else []))
+    if x.dim() != 2 or x.shape[1] != _lib.HEAD_DIM:
+        raise ValueError(f"{what}: input must be [N, {_lib.HEAD_DIM}], got {tuple(x.shape)}")
+    n, d = x.shape
+    nc = centroids.numel()
+    bits = nc.bit_length() - 1
+    if nc != 2 ** bits or not 1 <= bits <= 4 or boundaries.numel() != nc - 1:
+        raise ValueError(f"{what}: need 2^b centroids and 2^b - 1 boundaries (b = 1..4)")
+    for name, m in (("PiT", pit), ("PiST", pist)):
+        if m is not None and tuple(m.shape) != (d, d):
+            raise ValueError(f"{what}: {name} must be [{d}, {d}]")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        x = x.float()
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    f32 = lambda t: t.to(device=dev, dtype=torch.float32).contiguous()  # noqa: E731
+    pit_f, cent, bnd = f32(pit), f32(centroids), f32(boundaries)
+    pist_f = f32(pist) if pist is not None else None
+    idx = torch.empty((n, d * bits // 8), dtype=torch.uint8, device=dev)
+    norm = torch.empty((n,), dtype=torch.float16, device=dev)
+    signs = torch.empty((n, d // 8), dtype=torch.uint8, device=dev) if pist is not None else None
+    rnorm = torch.empty((n,), dtype=torch.float16, device=dev) if pist is not None else None
+    rc = _lib.lib().tq_compress_packed(
+        x.data_ptr(), _lib.dtype_code(x), x.stride(0), n, d, pit_f.data_ptr(), _lib.ptr(pist_f),
+        cent.data_ptr(), bnd.data_ptr(), bits, idx.data_ptr(), _lib.ptr(signs), _lib.ptr(rnorm),
+        norm.data_ptr(), _lib.stream_handle(dev))
+    _lib.check(rc, "tq_compress_packed")
+    return idx, signs, rnorm, norm
+
+
+def compress_k(K: torch.Tensor, PiT: torch.Tensor, PiST: torch.Tensor, centroids: torch.Tensor,
+               boundaries: torch.Tensor):
+    """Packed K compression with explicit rotations (kernels/packed_compress.py:44-106,157-177).
+
+    norm = |k|; k_n = k * (1 / (norm + 1e-8)); rot = k_n @ PiT; idx = #{boundaries <= rot};
+    resid = (rot - centroids[idx]) * norm; rnorm = |resid|; sign bit = (resid @ PiST >= 0).
+    Returns (k_idx uint8 [N, D*b/8], k_signs uint8 [N, D/8], k_rnorm fp16 [N], k_norm fp16 [N]);
+    b = log2(#centroids) (the reference: 2, i.e. 4 indices per byte).  The products are fp32
+    (the reference uses fp16 dot products, whose rounding is not reproduced)."""
+    idx, signs, rnorm, norm = _packed_compress(K, PiT, PiST, centroids, boundaries, "compress_k")
+    return idx, signs, rnorm, norm
+
+
+def compress_k_permuted(K: torch.Tensor, PiT: torch.Tensor, PiST: torch.Tensor, centroids: torch.Tensor,
+                        boundaries: torch.Tensor):
+    """compress_k with the signs in the stride-4 order of permute_signs_for_chunked
+    (kernels/packed_compress.py:219-223)."""
+    idx, signs, rnorm, norm = compress_k(K, PiT, PiST, centroids, boundaries)
+    return idx, permute_signs_for_chunked(signs), rnorm, norm
+
+
+def compress_v(V: torch.Tensor, PiT: torch.Tensor, centroids: torch.Tensor, boundaries: torch.Tensor):
+    """Packed V compression (kernels/packed_compress.py:109-142,226-240): as compress_k without
+    the residual.  Returns (v_idx uint8 [N, D*b/8], v_norm fp16 [N])."""
+    idx, _, _, norm = _packed_compress(V, PiT, None, centroids, boundaries, "compress_v")
+    return idx, norm
