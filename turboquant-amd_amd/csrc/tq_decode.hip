@@ -26,6 +26,10 @@
 // (m, l, acc[128]) per head to the workspace and decode_reduce_kernel combines the chunks:
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:121-140)
 #include "tq_common.h"
+#include "tq_decode_internal.h"
+
+#include <cmath>
+#include <cstdlib>
 
 namespace {
 
@@ -736,6 +740,68 @@ bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
     return aligned(q, 16) && (ss * es) % 16 == 0 && (sh * es) % 16 == 0;
 }
 
+int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num_q_heads, int n_chunks, int chunk,
+                  int cap, const int32_t* seq_lens, void* out, int out_dtype, int64_t out_ss, int64_t out_sh,
+                  hipStream_t st) {
+    ReduceParams rp;
+    rp.ws_acc = ws_acc;
+    rp.ws_m = ws_m;
+    rp.ws_l = ws_l;
+    rp.num_seqs = num_seqs;
+    rp.hq = num_q_heads;
+    rp.n_chunks = n_chunks;
+    rp.chunk = chunk;
+    rp.cap = cap;
+    rp.seq_lens = seq_lens;
+    rp.out = out;
+    rp.out_dtype = out_dtype;
+    rp.out_ss = out_ss;
+    rp.out_sh = out_sh;
+    hipLaunchKernelGGL(decode_reduce_kernel, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(64), 0, st, rp);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TQ_OK : (int)e;
+}
+
+bool fast_path_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("TQ_DECODE_FAST");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// The fast kernel reads this library's tile layout: per cache one block stride and one head
+// stride for all regions, rows of 16*bits index bytes, 16 sign bytes and 2-byte norms, the
+// other regions after the index region of the same tile, and every tile reachable with 31-bit
+// offsets from the head's base.
+bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block_size, int64_t num_blocks,
+                  const int32_t* block_tables) {
+    // num_blocks >= 1: unreadable table entries are redirected to block 0 and masked
+    if (!fast_path_enabled() || !block_tables || num_blocks < 1 || group > 8 || k->signs_permuted) return false;
+    if (block_size & (block_size - 1)) return false;  // 16 << tile_shift
+    auto same = [](const tq_region& a, const tq_region& b) {
+        return a.stride_block == b.stride_block && a.stride_head == b.stride_head;
+    };
+    auto delta_ok = [](const tq_region& base, const tq_region& r, int64_t rows_bytes) {
+        const int64_t d = static_cast<const uint8_t*>(r.ptr) - static_cast<const uint8_t*>(base.ptr);
+        return d >= 0 && d + rows_bytes < (1ll << 30);
+    };
+    const int64_t bs = block_size;
+    if (k->idx.stride_row != 16 * k->bits || k->norm.stride_row != 2 || !same(k->idx, k->norm)) return false;
+    if (!delta_ok(k->idx, k->norm, 2 * bs)) return false;
+    if (k->qjl) {
+        if (k->signs.stride_row != 16 || k->rnorm.stride_row != 2 || !same(k->idx, k->signs) || !same(k->idx, k->rnorm))
+            return false;
+        if (!delta_ok(k->idx, k->signs, 16 * bs) || !delta_ok(k->idx, k->rnorm, 2 * bs)) return false;
+    }
+    if (v->idx.stride_row != 16 * v->bits || v->norm.stride_row != 2 || !same(v->idx, v->norm)) return false;
+    if (!delta_ok(v->idx, v->norm, 2 * bs)) return false;
+    auto span_ok = [&](const tq_region& r) {
+        return r.stride_block > 0 && r.stride_block < (1ll << 30) && num_blocks * r.stride_block < (1ll << 31) - (1ll << 16);
+    };
+    return span_ok(k->idx) && span_ok(v->idx);
+}
+
 }  // namespace
 
 extern "C" size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk) {
@@ -755,8 +821,15 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     const void* kern = decode_kernel_ptr(k_bits, k_qjl != 0, v_bits, group <= 8, norm_row_bytes == 2);
     if (!kern) return TQ_ERR_BITS;
     const int share = (share_codebook && k_bits == v_bits) ? 1 : 0;
+    size_t lds = lds_bytes(k_bits, v_bits, share);
+    if (norm_row_bytes == 2 && group <= 8 && fast_path_enabled()) {
+        // the paged fast path (library tile layout)
+        kern = tq_decode_fast_kernel_ptr(k_bits, k_qjl != 0, v_bits);
+        uint32_t a, b, c;
+        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &a, &b, &c, &lds);
+    }
     int blocks = 0, dev = 0, cus = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds_bytes(k_bits, v_bits, share));
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds);
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return (int)e;
@@ -824,6 +897,76 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
 
     const size_t slots = (size_t)num_seqs * num_q_heads * n_chunks;
     uint8_t* ws = static_cast<uint8_t*>(workspace);
+    const float k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
+    const float v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
+    const bool share = k->centroids == v->centroids && k->bits == v->bits && k_cscale == v_cscale;
+    if (fast_path_ok(k, v, group, block_size, num_blocks, block_tables)) {
+        FastDecodeParams f = {};
+        f.q = q;
+        f.q_ss = q_stride_seq;
+        f.q_sh = q_stride_head;
+        f.qp = q_proj ? q_proj : q;
+        f.qp_ss = q_proj ? qp_stride_seq : q_stride_seq;
+        f.qp_sh = q_proj ? qp_stride_head : q_stride_head;
+        f.q_dtype = q_dtype;
+        f.q_vec = q_vector_ok(f.q, q_dtype, f.q_ss, f.q_sh) && q_vector_ok(f.qp, q_dtype, f.qp_ss, f.qp_sh);
+        f.num_seqs = num_seqs;
+        f.hq = num_q_heads;
+        f.hkv = num_kv_heads;
+        f.group = group;
+        const uint8_t* kb = static_cast<const uint8_t*>(k->idx.ptr);
+        f.kbase = kb;
+        f.k_sh = k->idx.stride_head;
+        f.k_sb = (uint32_t)k->idx.stride_block;
+        f.d_kn = (uint32_t)(static_cast<const uint8_t*>(k->norm.ptr) - kb);
+        if (k->qjl) {
+            f.d_ksig = (uint32_t)(static_cast<const uint8_t*>(k->signs.ptr) - kb);
+            f.d_krn = (uint32_t)(static_cast<const uint8_t*>(k->rnorm.ptr) - kb);
+        }
+        const uint8_t* vb = static_cast<const uint8_t*>(v->idx.ptr);
+        f.vbase = vb;
+        f.v_sh = v->idx.stride_head;
+        f.v_sb = (uint32_t)v->idx.stride_block;
+        f.d_vn = (uint32_t)(static_cast<const uint8_t*>(v->norm.ptr) - vb);
+        f.k_cent = k->centroids;
+        f.v_cent = v->centroids;
+        f.k_cscale = k_cscale;
+        f.v_cscale = v_cscale;
+        f.v_cinv = 1.f / v_cscale;
+        size_t lds_total = 0;
+        tq_decode_fast_lds_layout(k->bits, k->qjl != 0, v->bits, share, &f.lds_sign, &f.lds_k, &f.lds_v, &lds_total);
+        f.block_size = block_size;
+        int tsh = 0;
+        while ((16 << tsh) < block_size) ++tsh;
+        f.tile_shift = tsh;
+        f.num_blocks = num_blocks;
+        f.bt = block_tables;
+        f.bt_stride = block_table_stride;
+        f.max_blocks = max_blocks_per_seq;
+        f.seq_lens = seq_lens;
+        f.c_exp = sm_scale * kLog2e / k_cscale;
+        f.sparse = sparse_threshold > 0.f ? 1 : 0;
+        f.thr_log = f.sparse ? std::log2(sparse_threshold) / f.c_exp : 0.f;
+        f.qp_mul = corr_scale * k_cscale;
+        f.chunk = tokens_per_chunk;
+        f.n_chunks = n_chunks;
+        f.ws_acc = reinterpret_cast<float*>(ws);
+        f.ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));
+        f.ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(f.ws_m) + align_up(slots * sizeof(float), 256));
+        f.skip_stats = skip_stats;
+        f.out = out;
+        f.out_dtype = out_dtype;
+        f.out_ss = out_stride_seq;
+        f.out_sh = out_stride_head;
+        const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
+        const int64_t grid = (units + 3) / 4;
+        if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
+        int frc = tq_decode_fast_launch(f, k->bits, k->qjl != 0, v->bits, grid, lds_total, (hipStream_t)stream);
+        if (frc) return frc;
+        return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
+                             max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq,
+                             out_stride_head, (hipStream_t)stream);
+    }
     float* ws_acc = reinterpret_cast<float*>(ws);
     float* ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));
     float* ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws_m) + align_up(slots * sizeof(float), 256));
@@ -892,21 +1035,7 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
 
-    ReduceParams rp;
-    rp.ws_acc = ws_acc;
-    rp.ws_m = ws_m;
-    rp.ws_l = ws_l;
-    rp.num_seqs = num_seqs;
-    rp.hq = num_q_heads;
-    rp.n_chunks = n_chunks;
-    rp.chunk = tokens_per_chunk;
-    rp.cap = max_blocks_per_seq * block_size;
-    rp.seq_lens = seq_lens;
-    rp.out = out;
-    rp.out_dtype = out_dtype;
-    rp.out_ss = out_stride_seq;
-    rp.out_sh = out_stride_head;
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(64), 0, st, rp);
-    e = hipGetLastError();
-    return e == hipSuccess ? TQ_OK : (int)e;
+    return launch_reduce(ws_acc, ws_m, ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
+                         max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq, out_stride_head,
+                         st);
 }

@@ -1,0 +1,660 @@
+// Packed asymmetric split-K decode attention for gfx950: the paged fast path.
+//
+// Used by tq_decode when the caches are in this library's tile layout (one tile of 16-token
+// rows per (physical block, KV head), see tq_compress_paged) and the GQA group has at most 8
+// query heads.  Other layouts go through decode_kernel (tq_decode.hip).
+//
+// Work unit = one wave64 = (sequence, KV head, chunk of tokens_per_chunk tokens), walked in
+// pairs of 16-token tiles (A, B).  Per pair (fp32 accumulation throughout):
+//   S_X^T[token][col] = K_X[16 x 128] . Q^T[128 x 16]         4 x mfma_f32_16x16x32_f16 per tile
+//       K_X: a pair of packed indices -> half2 of centroids through an LDS table;
+//       column col of Q holds query head col & 7, so both halves of the output hold all heads.
+//   QJL_X^T = (+-1)[16 x 128] . QP^T                           2 x mfma_scale_f32_16x16x128_f8f6f4
+//       sign bits -> fp4 +-1 through a byte-indexed LDS table (one dword per 8 signs); q_proj
+//       in fp8 as hi + lo parts with E8M0 block scales (relative error <= 2^-8 on a term that
+//       is a small correction of the score).
+//   Lanes with col < 8 keep tile A's scores and lanes with col >= 8 tile B's, so after the
+//   merge one wave holds 32 tokens x 8 heads of scores (4 per lane): the online softmax, the
+//   Sparse-V test and the conversions run once per pair.
+//   acc^T[dim][col] += V^T[128 x 32] . P^T[32 x 16]           8 x mfma_f32_16x16x32_f16 per pair
+//       k-slots 0-3 of lane group g are tile A's tokens 4g..4g+3, slots 4-7 tile B's; column
+//       col < 8 takes tile A's p from its own lane and tile B's from lane col + 8 (DPP row
+//       rotate), so columns 0-7 accumulate both tiles and columns 8-15 are ignored.
+// MFMA output layout (16x16): lane l holds rows 4(l/16)+r, column l%16 - after the QK product
+// lane (col, g) owns tokens 4g..4g+3, the B-operand layout of the PV product.
+//
+// Scores stay in "raw" units (q . k * centroid_scale, no softmax scale): q enters the MFMA as
+// fp16 without scaling (exact for bf16/fp16 queries) and the softmax scale is applied in the
+// exponent: p = exp2(c * (s - m)), c = sm_scale * log2(e) / centroid_scale.
+//
+// Memory: the K and V buffer descriptors are loop invariant (base = cache + head offset); a
+// tile is addressed by scalar offsets (block * block_stride + region offset), which needs the
+// cache to span less than 2 GiB (checked on the host; larger caches use decode_kernel).  The
+// norm streams are read once per pair: lanes of tile A and tile B differ in their vector offset.
+// Block-table entries of the next pair are fetched with one vector load per pair and read with
+// readlane, so the tile walk never waits on a scalar load.  Loads run one pair ahead.
+//
+// Sparse-V (kernels/sparse_v.py:108-149): for tile X, m_X = running max through tile X; token t
+// is dropped from PV when no head of the group has exp2(c (s - m_X)) > threshold, tested as
+// s > m_X + log2(threshold)/c with a ballot; dropped tokens stay in the denominator.
+#include "tq_common.h"
+#include "tq_decode_internal.h"
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+#ifndef TQ_FAST_WAVES
+#define TQ_FAST_WAVES 0
+#endif
+
+typedef int tq_i32x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint8_t* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+__device__ __forceinline__ uint32_t lds_read(uint32_t addr) { return *(lds_u32*)(uintptr_t)addr; }
+
+// LDS address of the table entry held in bits [pos, pos + W) of the word array w: the field is
+// moved to bit 7 (one shift or funnel shift) and merged with the lane's replica address (one
+// and-or).  Tables sit at LDS offsets that are multiples of their size.
+template <int W, int N>
+__device__ __forceinline__ uint32_t entry_addr(const uint32_t (&w)[N], int pos, uint32_t bank_addr) {
+    const int wi = pos >> 5, sh = pos & 31;
+    uint32_t f;
+    if (sh + W <= 32 || wi + 1 >= N)
+        f = sh >= 7 ? (w[wi] >> (sh - 7)) : (w[wi] << (7 - sh));
+    else
+        f = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - 7);
+    return (f & (((1u << W) - 1u) << 7)) | bank_addr;
+}
+
+__device__ __forceinline__ uint32_t pick_halves(uint32_t hi_src, uint32_t lo_src, int s) {
+    return __builtin_amdgcn_perm(hi_src, lo_src, s ? 0x07060302u : 0x05040100u);
+}
+
+__device__ __forceinline__ float half_at(const uint32_t (&w)[2], int r) {
+    const uint32_t b = (r & 1) ? (w[r >> 1] >> 16) : (w[r >> 1] & 0xffffu);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+// Value of lane l ^ 8 within its row of 16 lanes (DPP row_ror:8).
+__device__ __forceinline__ uint32_t row_swap8(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float row_swap8f(float x) { return __uint_as_float(row_swap8(__float_as_uint(x))); }
+
+__device__ __forceinline__ float max_over_groups(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// fp16 of vn * p, rounded to nearest (v_fma_mix*_f16).
+__device__ __forceinline__ _Float16 scale_to_half(float vn, float pr) { return (_Float16)__builtin_fmaf(vn, pr, 0.0f); }
+
+// Raw data of one pair of tiles.  K part: loaded one pair ahead; V part: loaded at the start
+// of its own pair (it is first needed after the QK products and the softmax).
+template <int KB, bool KQJL>
+struct KRaw {
+    uint32_t kwA[KB], kwB[KB];  // dims 32g..32g+31 of token n, tiles A and B
+    uint32_t ksA, ksB;          // sign bits of the same dims
+    uint32_t kn[2], krn[2];     // fp16 norms of tokens 4g..4g+3 of the lane's tile
+};
+struct VRaw {
+    uint32_t vwA[4], vwB[4];    // index bits of dims 8n..8n+7 of tokens 4g..4g+3 (bits 0 .. 8*VB-1)
+    uint32_t vn[2];             // fp16 norms of tokens 4g..4g+3 of the lane's tile
+};
+// Wave-uniform description of a pair.
+struct PairInfo {
+    uint32_t vbA, vbB;          // scalar byte offsets of the tiles' blocks in the V cache
+    uint32_t r0A, r0B;          // first row of each tile inside its block
+    int nvA, nvB;               // valid rows (0: past the end or unreadable block)
+};
+
+struct Softmax {
+    float m;        // running max per head (raw score units), equal in lanes col and col ^ 8
+    float lsum;     // this lane's tokens, relative to m
+    tq_floatx4 acc[8];
+    uint32_t n_tot, n_kept;  // wave-uniform
+};
+
+// Per-lane constants of the compute step.
+struct LaneCtx {
+    tq_half8 qop[4];            // q (fp16), MFMA chunk cc: dims 32g + 8cc + j
+    tq_i32x8 qph, qpl;          // q_proj * corr * cscale * 2^b in fp8: hi, (x - hi) * 16
+    int sc_hi, sc_lo;           // E8M0 scales undoing 2^b and 2^(b+4)
+    uint32_t kbank, vbank, sbank;
+    uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
+    uint64_t hmask;             // lanes of real heads
+    bool lo8;                   // column < 8: tile A
+};
+
+template <int KB>
+__device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const LaneCtx& c) {
+    tq_floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        tq_u32x4 a;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = lds_read(entry_addr<2 * KB>(kw, 2 * KB * (4 * cc + j), c.kbank));
+        s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), c.qop[cc], s, 0, 0, 0);
+    }
+    return s;
+}
+
+__device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, const LaneCtx& c) {
+    const uint32_t w[1] = {ks};
+    tq_i32x8 a;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) a[b] = (int)lds_read(entry_addr<8>(w, 8 * b, c.sbank));
+#pragma unroll
+    for (int b = 4; b < 8; ++b) a[b] = 0;  // fp4 operand: only the first four dwords are read
+    tq_floatx4 t = {0.f, 0.f, 0.f, 0.f};
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qph, t, 4, 0, 0, 127, 0, c.sc_hi);
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qpl, t, 4, 0, 0, 127, 0, c.sc_lo);
+    return t;
+}
+
+// Lanes (col, g) whose tile row 4g + r is valid: tile A in columns 0-7, tile B in 8-15.
+__device__ __forceinline__ uint64_t row_mask(int nvA, int nvB, int r) {
+    auto groups = [](int nv, int r) -> uint64_t {
+        int ng = (nv - r + 3) >> 2;  // lane groups g with 4g + r < nv
+        ng = ng < 0 ? 0 : ng;
+        return ng >= 4 ? ~0ull : ((1ull << (16 * ng)) - 1ull);
+    };
+    return (groups(nvA, r) & 0x00ff00ff00ff00ffull) | (groups(nvB, r) & 0xff00ff00ff00ff00ull);
+}
+
+// One pair of tiles.
+template <int KB, bool KQJL, int VB>
+__device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRaw& vr, const PairInfo& pi,
+                                             Softmax& st, const LaneCtx& c, const FastDecodeParams& p, bool sparse) {
+    // ---------------- scores ----------------
+    const tq_floatx4 sA = qk_tile<KB>(kr.kwA, c);
+    const tq_floatx4 sB = qk_tile<KB>(kr.kwB, c);
+    tq_floatx4 tA = {0.f, 0.f, 0.f, 0.f}, tB = {0.f, 0.f, 0.f, 0.f};
+    if (KQJL) {
+        tA = qjl_tile(kr.ksA, c);
+        tB = qjl_tile(kr.ksB, c);
+    }
+    uint64_t rm[4];
+    if (pi.nvA == 16 && pi.nvB == 16) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rm[r] = ~0ull;
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rm[r] = row_mask(pi.nvA, pi.nvB, r);
+    }
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        // Scalar copies: shuffling ext_vector elements in place has miscompiled before.
+        const float s1 = c.lo8 ? sA[r] : sB[r];
+        float v;
+        if (KQJL) {
+            const float s2 = c.lo8 ? tA[r] : tB[r];
+            v = __builtin_fmaf(half_at(kr.kn, r), s1, __builtin_fmaf(half_at(kr.krn, r), s2, 0.0f));
+        } else {
+            v = half_at(kr.kn, r) * s1;
+        }
+        sc[r] = __builtin_amdgcn_inverse_ballot_w64(rm[r]) ? v : kNegInf;
+    }
+
+    // ---------------- online softmax ----------------
+    float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mt = max_over_groups(mt);                 // this tile's max for the lane's head
+    const float other = row_swap8f(mt);       // the other tile's max for the same head
+    const float m_old = st.m;
+    const float m_new = fmaxf(fmaxf(m_old, mt), other);
+    const float cexp = p.c_exp;
+    if (__builtin_amdgcn_ballot_w64(m_new > m_old) & c.hmask) {
+        const float alpha = __builtin_amdgcn_exp2f(cexp * (m_old - m_new));  // 0 while m_old = -inf
+        st.lsum *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+    }
+    st.m = m_new;
+    const float nb = m_new == kNegInf ? 0.f : -cexp * m_new;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], cexp, nb));  // 0 for masked rows
+    st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+
+    // ---------------- Sparse-V ----------------
+    if (sparse) {
+        const float m_skip = c.lo8 ? fmaxf(m_old, mt) : m_new;
+        const float thr = m_skip + p.thr_log;
+        uint32_t kept = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(sc[r] > thr) & c.hmask;
+            // some head of this lane's 8-lane group (its tile's token 4g + r) passes
+            const bool keep = (uint32_t)((bal << c.shl8) >> 32) >= (1u << 24);
+            pr[r] = keep ? pr[r] : 0.f;
+            kept += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(keep) & 0x0101010101010101ull);
+        }
+        st.n_tot += (uint32_t)(pi.nvA + pi.nvB);
+        st.n_kept += kept;
+    }
+
+    // ---------------- PV ----------------
+    // Rows past the end may hold any bits in a paged block: their norms are replaced by 0.
+    union {
+        _Float16 h[2];
+        uint32_t u;
+    } p01, p23;
+    float vnr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vnr[r] = __builtin_amdgcn_inverse_ballot_w64(rm[r]) ? half_at(vr.vn, r) : 0.f;
+    p01.h[0] = scale_to_half(vnr[0], pr[0]);
+    p01.h[1] = scale_to_half(vnr[1], pr[1]);
+    p23.h[0] = scale_to_half(vnr[2], pr[2]);
+    p23.h[1] = scale_to_half(vnr[3], pr[3]);
+    const tq_u32x4 bw = {p01.u, p23.u, row_swap8(p01.u), row_swap8(p23.u)};
+    const tq_half8 bop = __builtin_bit_cast(tq_half8, bw);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t la[4], lb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
+            la[r] = lds_read(entry_addr<2 * VB>(wa, 2 * VB * q, c.vbank));
+            lb[r] = lds_read(entry_addr<2 * VB>(wb, 2 * VB * q, c.vbank));
+        }
+#pragma unroll
+        for (int hs = 0; hs < 2; ++hs) {
+            const tq_u32x4 aw = {pick_halves(la[1], la[0], hs), pick_halves(la[3], la[2], hs),
+                                 pick_halves(lb[1], lb[0], hs), pick_halves(lb[3], lb[2], hs)};
+            st.acc[2 * q + hs] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, aw), bop, st.acc[2 * q + hs], 0, 0, 0);
+        }
+    }
+}
+
+// Waves per SIMD (register budget 512 / waves): QJL keys need the fp8 q_proj operands.
+template <int KB, bool KQJL, int VB>
+constexpr int fast_waves() {
+    return TQ_FAST_WAVES > 0 ? TQ_FAST_WAVES : (KQJL ? 3 : 4);
+}
+
+template <int KB, bool KQJL, int VB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
+                                                                     fast_waves<KB, KQJL, VB>())))
+void decode_fast_kernel(FastDecodeParams p) {
+    constexpr int KENT = 1 << (2 * KB);
+    constexpr int VENT = 1 << (2 * VB);
+    extern __shared__ uint32_t s_lds[];
+    // Tables (32 bank replicas each): fp4 sign table (QJL), K pair table, V pair table, at the
+    // byte offsets chosen by the host (multiples of each table's size).
+    if (KQJL) {
+        uint32_t* t = s_lds + p.lds_sign / 4;
+        for (int i = threadIdx.x; i < 256 * 32; i += 256) {
+            const uint32_t e = (uint32_t)i >> 5;
+            uint32_t w = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) w |= (((e >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);  // fp4 +1 / -1
+            t[i] = w;
+        }
+    }
+    {
+        uint32_t* t = s_lds + p.lds_k / 4;
+        for (int i = threadIdx.x; i < KENT * 32; i += 256) {
+            const int e = i >> 5;
+            t[i] = tq_pack_half2(p.k_cent[e & ((1 << KB) - 1)] * p.k_cscale, p.k_cent[e >> KB] * p.k_cscale);
+        }
+    }
+    if (p.lds_v != p.lds_k) {
+        uint32_t* t = s_lds + p.lds_v / 4;
+        for (int i = threadIdx.x; i < VENT * 32; i += 256) {
+            const int e = i >> 5;
+            t[i] = tq_pack_half2(p.v_cent[e & ((1 << VB) - 1)] * p.v_cscale, p.v_cent[e >> VB] * p.v_cscale);
+        }
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    const int n = lane & 15;
+    const int hcol = n & 7;
+    LaneCtx c;
+    c.lo8 = n < 8;
+    const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
+    c.kbank = lds0 + p.lds_k + bank4;
+    c.vbank = lds0 + p.lds_v + bank4;
+    c.sbank = lds0 + p.lds_sign + bank4;
+    c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // Units in (sequence, chunk, KV head) order: the four waves of a workgroup get the same
+    // chunk of one sequence (equal work).
+    const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
+    const int kh = (int)(unit % p.hkv);
+    const int64_t sc_ = unit / p.hkv;
+    const int ci = (int)(sc_ % p.n_chunks);
+    const int64_t s = sc_ / p.n_chunks;
+    if (s >= p.num_seqs) return;
+    int L = p.seq_lens[s];
+    const int cap = p.max_blocks * p.block_size;
+    L = L < cap ? L : cap;
+    const int t_begin = ci * p.chunk;
+    if (t_begin >= L) return;
+    const int t_end = (t_begin + p.chunk < L) ? t_begin + p.chunk : L;
+
+    // ---- query operands ----
+    const int head = kh * p.group + hcol;
+    const bool hvalid = hcol < p.group;
+    c.hmask = __builtin_amdgcn_ballot_w64(hvalid);
+    {
+        float qv[32];
+        const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
+        if (hvalid && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tq_load8(p.q, qoff + 8 * i, p.q_dtype, &qv[8 * i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) qv[i] = hvalid ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) c.qop[cc][j] = (_Float16)qv[8 * cc + j];
+    }
+    if (KQJL) {
+        // fp8 operand element m (byte m of 32) of lane group g is dim (m < 16 ? 0 : 64) + 16 g + (m & 15)
+        // (the pairing of an fp4 A operand with an fp8 B operand in the 16x16x128 MFMA).
+        float x[32];
+        const int64_t off = s * p.qp_ss + (int64_t)head * p.qp_sh + 16 * g;
+        if (hvalid && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                tq_load8(p.qp, off + 8 * i, p.q_dtype, &x[8 * i]);
+                tq_load8(p.qp, off + 64 + 8 * i, p.q_dtype, &x[16 + 8 * i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                x[i] = hvalid ? tq_load1(p.qp, off + i, p.q_dtype) : 0.f;
+                x[16 + i] = hvalid ? tq_load1(p.qp, off + 64 + i, p.q_dtype) : 0.f;
+            }
+        }
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            x[i] *= p.qp_mul;
+            amax = fmaxf(amax, fabsf(x[i]));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+        // 2^b brings the largest magnitude into [128, 256): inside the fp8 e4m3 normal range
+        int b = 0;
+        if (amax > 0.f && amax < __builtin_huge_valf()) b = 7 - ilogbf(amax);
+        b = b < -100 ? -100 : (b > 100 ? 100 : b);
+        c.sc_hi = 127 - b;
+        c.sc_lo = 127 - b - 4;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            float xs[4], rs[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xs[k] = ldexpf(x[4 * d + k], b);
+            int wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[0], xs[1], 0, false);
+            wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[2], xs[3], wh, true);
+            rs[0] = (xs[0] - __builtin_amdgcn_cvt_f32_fp8(wh, 0)) * 16.f;
+            rs[1] = (xs[1] - __builtin_amdgcn_cvt_f32_fp8(wh, 1)) * 16.f;
+            rs[2] = (xs[2] - __builtin_amdgcn_cvt_f32_fp8(wh, 2)) * 16.f;
+            rs[3] = (xs[3] - __builtin_amdgcn_cvt_f32_fp8(wh, 3)) * 16.f;
+            int wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[0], rs[1], 0, false);
+            wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[2], rs[3], wl, true);
+            c.qph[d] = wh;
+            c.qpl[d] = wl;
+        }
+    } else {
+        c.sc_hi = c.sc_lo = 127;
+    }
+
+    // ---- loop-invariant lane offsets inside a tile ----
+    const uint32_t o_kidx = (uint32_t)(n * 16 * KB + 4 * KB * g);
+    const uint32_t o_ksig = (uint32_t)(16 * n + 4 * g);
+    const uint32_t o_norm = (uint32_t)(8 * g);  // tokens 4g..4g+3, 2 bytes each
+    // V: dims 8n..8n+7 of token 4g+r start at byte VB*n of its row; one dword per token, read at
+    // that (for VB = 3 unaligned) byte offset, holds them in bits 0 .. 8*VB-1
+    const uint32_t o_vidx = (uint32_t)(4 * g * 16 * VB + VB * n);
+    const auto rk = rsrc(p.kbase + (int64_t)kh * p.k_sh);
+    const auto rv = rsrc(p.vbase + (int64_t)kh * p.v_sh);
+    const uint64_t hi8 = 0xff00ff00ff00ff00ull;
+
+    // ---- tile walk ----
+    const int nblk_seq = (L + p.block_size - 1) / p.block_size;  // >= 1
+    const int32_t* bt_row = p.bt + s * p.bt_stride;
+    const int tile0 = t_begin >> 4;                               // absolute tile index of the chunk start
+    const int tmask = (1 << p.tile_shift) - 1;
+    // block number of tile (2 * pi + (lane & 1)) of the chunk; clamped into the sequence's blocks
+    auto bt_load = [&](int pi) -> int {
+        int lb = (tile0 + 2 * pi + (lane & 1)) >> p.tile_shift;
+        lb = lb < nblk_seq ? lb : nblk_seq - 1;
+        return bt_row[lb];
+    };
+    int btn = bt_load(0);
+
+    // Norm rows of tiles A (lanes col < 8) and B (col >= 8) in one load: the scalar offset
+    // addresses the nearer tile, lanes of the farther one add the distance.
+    struct NormAddr {
+        uint32_t vo, so;
+    };
+    auto norm_addr = [&](uint32_t oA, uint32_t oB) -> NormAddr {
+        const uint32_t lo = oA < oB ? oA : oB;
+        const uint32_t d = (oA < oB ? oB : oA) - lo;
+        const uint64_t up = oB > oA ? hi8 : ~hi8;
+        return NormAddr{o_norm + (((up >> lane) & 1) ? d : 0u), lo};
+    };
+
+    // K part of pair pi (and the block numbers of pair pi + 1); fills the V offsets of pi.
+    auto fetch_k = [&](int pi, KRaw<KB, KQJL>& kr, PairInfo& info) {
+        int blk[2] = {__builtin_amdgcn_readlane(btn, 0), __builtin_amdgcn_readlane(btn, 1)};
+        btn = bt_load(pi + 1);
+        uint32_t kb[2], r0[2];
+        int nv[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int i = 2 * pi + x;
+            const int t0 = t_begin + 16 * i;
+            int nvr = t_end - t0;
+            nvr = nvr < 0 ? 0 : (nvr > 16 ? 16 : nvr);
+            int bk = blk[x];
+            if (bk < 0 || (int64_t)bk >= p.num_blocks) {  // unreadable entry: read block 0, mask it
+                bk = 0;
+                nvr = 0;
+            }
+            blk[x] = bk;
+            nv[x] = nvr;
+            r0[x] = (uint32_t)(((tile0 + i) & tmask) << 4);
+            kb[x] = (uint32_t)bk * p.k_sb;
+        }
+        info.nvA = nv[0];
+        info.nvB = nv[1];
+        info.vbA = (uint32_t)blk[0] * p.v_sb;
+        info.vbB = (uint32_t)blk[1] * p.v_sb;
+        info.r0A = r0[0];
+        info.r0B = r0[1];
+        auto load_kw = [&](uint32_t (&kw)[KB], uint32_t soff) {
+            if (KB == 2) {
+                tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, o_kidx, soff, 0);
+                kw[0] = v[0];
+                kw[1 % KB] = v[1];
+            } else if (KB == 3) {
+                typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+                u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rk, o_kidx, soff, 0);
+                kw[0] = v[0];
+                kw[1 % KB] = v[1];
+                kw[2 % KB] = v[2];
+            } else {
+                tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, o_kidx, soff, 0);
+                kw[0] = v[0];
+                kw[1 % KB] = v[1];
+                kw[2 % KB] = v[2];
+                kw[3 % KB] = v[3];
+            }
+        };
+        load_kw(kr.kwA, kb[0] + r0[0] * (uint32_t)(16 * KB));
+        load_kw(kr.kwB, kb[1] + r0[1] * (uint32_t)(16 * KB));
+        if (KQJL) {
+            kr.ksA = __builtin_amdgcn_raw_buffer_load_b32(rk, o_ksig, kb[0] + p.d_ksig + r0[0] * 16u, 0);
+            kr.ksB = __builtin_amdgcn_raw_buffer_load_b32(rk, o_ksig, kb[1] + p.d_ksig + r0[1] * 16u, 0);
+        }
+        const NormAddr na = norm_addr(kb[0] + 2u * r0[0], kb[1] + 2u * r0[1]);
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_kn, 0);
+        kr.kn[0] = a[0];
+        kr.kn[1] = a[1];
+        if (KQJL) {
+            tq_u32x2 bb = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_krn, 0);
+            kr.krn[0] = bb[0];
+            kr.krn[1] = bb[1];
+        }
+    };
+    auto load_v = [&](const PairInfo& info, VRaw& vr) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t off = o_vidx + (uint32_t)(r * 16 * VB);
+            const uint32_t sA = info.vbA + info.r0A * (uint32_t)(16 * VB);
+            const uint32_t sB = info.vbB + info.r0B * (uint32_t)(16 * VB);
+            if (VB == 2) {
+                vr.vwA[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, sA, 0);
+                vr.vwB[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, sB, 0);
+            } else {
+                vr.vwA[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, sA, 0);
+                vr.vwB[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, sB, 0);
+            }
+        }
+        // norm of row j of a tile at row0 of its block: d_vn + 2 (row0 + j)
+        const NormAddr na = norm_addr(info.vbA + 2u * info.r0A, info.vbB + 2u * info.r0B);
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, na.vo, na.so + p.d_vn, 0);
+        vr.vn[0] = a[0];
+        vr.vn[1] = a[1];
+    };
+
+    Softmax st;
+    st.m = kNegInf;
+    st.lsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+    st.n_tot = 0;
+    st.n_kept = 0;
+    const bool sparse = p.sparse != 0;
+
+    const int ntiles = (t_end - t_begin + 15) >> 4;
+    const int npairs = (ntiles + 1) >> 1;
+    KRaw<KB, KQJL> kr[2];
+    PairInfo info[2];
+    VRaw vr;
+    // Pairs past the end read block data that is never used (every fetch issues the same
+    // loads, which keeps the compiler's outstanding-load counts exact).
+    fetch_k(0, kr[0], info[0]);
+    for (int i = 0; i < npairs; i += 2) {
+        load_v(info[0], vr);
+        fetch_k(i + 1, kr[1], info[1]);
+        compute_pair<KB, KQJL, VB>(kr[0], vr, info[0], st, c, p, sparse);
+        if (i + 1 >= npairs) break;
+        load_v(info[1], vr);
+        fetch_k(i + 2, kr[0], info[0]);
+        compute_pair<KB, KQJL, VB>(kr[1], vr, info[1], st, c, p, sparse);
+    }
+
+    // ---- combine the lane groups and the two tile halves ----
+    float lsum = sum_over_groups(st.lsum);
+    lsum += row_swap8f(lsum);
+    if (sparse && p.skip_stats != nullptr && lane == 0) {
+        atomicAdd(p.skip_stats, (unsigned long long)(st.n_tot - st.n_kept));
+        atomicAdd(p.skip_stats + 1, (unsigned long long)st.n_tot);
+    }
+    const bool writer = c.lo8 && hvalid;
+    // acc[nn][r] is dim 8 * (4g + r) + nn of head col; v_cinv undoes the V table scale.
+    const float vs = p.v_cinv;
+    int nch = (L + p.chunk - 1) / p.chunk;
+    nch = nch < p.n_chunks ? nch : p.n_chunks;
+    if (nch == 1) {
+        if (writer) {
+            const float inv = lsum > 0.f ? vs / lsum : 0.f;
+            const int64_t ob = s * p.out_ss + (int64_t)head * p.out_sh + 32 * g;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int nn = 0; nn < 8; ++nn) tq_store1(p.out, ob + 8 * r + nn, p.out_dtype, st.acc[nn][r] * inv);
+        }
+        return;
+    }
+    if (writer) {
+        const int64_t slot = ((s * p.hq + head) * (int64_t)p.n_chunks + ci);
+        if (g == 0) {
+            p.ws_m[slot] = st.m == kNegInf ? kNegInf : st.m * p.c_exp;  // log2 units for the merge
+            p.ws_l[slot] = lsum;
+        }
+        float4* dst = reinterpret_cast<float4*>(p.ws_acc + slot * TQ_HEAD_DIM + 32 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            dst[2 * r] = make_float4(st.acc[0][r] * vs, st.acc[1][r] * vs, st.acc[2][r] * vs, st.acc[3][r] * vs);
+            dst[2 * r + 1] = make_float4(st.acc[4][r] * vs, st.acc[5][r] * vs, st.acc[6][r] * vs, st.acc[7][r] * vs);
+        }
+    }
+}
+
+}  // namespace
+
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb) {
+#define TQ_FP(KB, KQ, VB) \
+    if (kb == KB && kq == KQ && vb == VB) return (const void*)decode_fast_kernel<KB, KQ, VB>;
+#define TQ_FP_V(KB, KQ) TQ_FP(KB, KQ, 2) TQ_FP(KB, KQ, 3) TQ_FP(KB, KQ, 4)
+    TQ_FP_V(2, false) TQ_FP_V(2, true) TQ_FP_V(3, false) TQ_FP_V(3, true) TQ_FP_V(4, false) TQ_FP_V(4, true)
+#undef TQ_FP_V
+#undef TQ_FP
+    return nullptr;
+}
+
+void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
+                               uint32_t* lds_v, size_t* total) {
+    // Tables at offsets that are multiples of their sizes: largest first.
+    struct T {
+        size_t size;
+        uint32_t* off;
+    } t[3];
+    int n = 0;
+    uint32_t dummy = 0;
+    t[n++] = {kq ? (size_t)256 * 128 : 0, lds_sign};
+    t[n++] = {((size_t)1 << (2 * kb)) * 128, lds_k};
+    t[n++] = {share ? 0 : ((size_t)1 << (2 * vb)) * 128, share ? &dummy : lds_v};
+    for (int i = 0; i < n; ++i)
+        for (int j = i + 1; j < n; ++j)
+            if (t[j].size > t[i].size) {
+                T x = t[i];
+                t[i] = t[j];
+                t[j] = x;
+            }
+    size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+        *t[i].off = (uint32_t)off;
+        off += t[i].size;
+    }
+    if (share) *lds_v = *lds_k;
+    *total = off;
+}
+
+int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
+                          hipStream_t stream) {
+    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb);
+    if (!kern) return TQ_ERR_BITS;
+    FastDecodeParams p = prm;
+    void* args[] = {&p};
+    hipError_t le = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(256), args, lds_bytes, stream);
+    if (le != hipSuccess) return (int)le;
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TQ_OK : (int)e;
+}

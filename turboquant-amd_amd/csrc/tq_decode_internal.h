@@ -1,0 +1,60 @@
+// Internal interface between tq_decode (tq_decode.hip) and the paged fast-path decode kernel
+// (tq_decode_fast.hip).  Not part of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+struct FastDecodeParams {
+    const void* q;
+    int64_t q_ss, q_sh;
+    const void* qp;
+    int64_t qp_ss, qp_sh;
+    int q_dtype;
+    int q_vec;             // q and qp rows 16-byte aligned: vector loads
+    int num_seqs, hq, hkv, group;
+    // K cache: index region base, head stride, block stride; other regions as byte offsets
+    // from the index region of the same tile (rows: idx 16*bits, signs 16, norms 2 bytes)
+    const uint8_t* kbase;
+    int64_t k_sh;
+    uint32_t k_sb;
+    uint32_t d_ksig, d_kn, d_krn;
+    const uint8_t* vbase;
+    int64_t v_sh;
+    uint32_t v_sb;
+    uint32_t d_vn;
+    const float* k_cent;
+    const float* v_cent;
+    float k_cscale, v_cscale, v_cinv;
+    uint32_t lds_sign, lds_k, lds_v;  // byte offsets of the LDS tables
+    int block_size, tile_shift;       // block_size = 16 << tile_shift
+    int64_t num_blocks;
+    const int32_t* bt;
+    int64_t bt_stride;
+    int max_blocks;
+    const int32_t* seq_lens;
+    float c_exp;     // sm_scale * log2(e) / k_cscale: raw score units -> log2 units
+    float thr_log;   // log2(threshold) / c_exp
+    int sparse;
+    float qp_mul;    // corr_scale * k_cscale
+    int chunk, n_chunks;
+    float* ws_acc;   // [num_seqs][hq][n_chunks][128]
+    float* ws_m;     // [num_seqs][hq][n_chunks], log2 units
+    float* ws_l;
+    unsigned long long* skip_stats;
+    void* out;
+    int out_dtype;
+    int64_t out_ss, out_sh;
+};
+
+// decode_fast_kernel<kb, kq, vb> (nullptr: unsupported bit widths).
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb);
+
+// LDS byte offsets of the fp4 sign table, the K and the V pair tables, and the total.
+void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
+                               uint32_t* lds_v, size_t* total);
+
+// Launch decode_fast_kernel (grid of 256-thread workgroups, 4 work units each).
+int tq_decode_fast_launch(const FastDecodeParams& p, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
+                          hipStream_t stream);
