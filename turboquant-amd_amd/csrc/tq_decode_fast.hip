@@ -60,15 +60,35 @@ __device__ __forceinline__ uint32_t lds_read(uint32_t addr) { return *(lds_u32*)
 // LDS address of the table entry held in bits [pos, pos + W) of the word array w: the field is
 // moved to bit 7 (one shift or funnel shift) and merged with the lane's replica address (one
 // and-or).  Tables sit at LDS offsets that are multiples of their size.
-template <int W, int N>
+template <int W, int N, int P = 7>
 __device__ __forceinline__ uint32_t entry_addr(const uint32_t (&w)[N], int pos, uint32_t bank_addr) {
     const int wi = pos >> 5, sh = pos & 31;
     uint32_t f;
     if (sh + W <= 32 || wi + 1 >= N)
-        f = sh >= 7 ? (w[wi] >> (sh - 7)) : (w[wi] << (7 - sh));
+        f = sh >= P ? (w[wi] >> (sh - P)) : (w[wi] << (P - sh));
     else
-        f = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - 7);
-    return (f & (((1u << W) - 1u) << 7)) | bank_addr;
+        f = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - P);
+    return (f & (((1u << W) - 1u) << P)) | bank_addr;
+}
+
+__device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
+    typedef __attribute__((address_space(3))) const tq_u32x2 lds_u32x2;
+    return *(lds_u32x2*)(uintptr_t)addr;
+}
+
+#ifndef TQ_FAST_QUAD
+#define TQ_FAST_QUAD 1
+#endif
+// 3-bit indices are looked up four at a time (a 12-bit field -> 4 fp16 centroids, one 8-byte
+// entry of a 4096-entry table, not replicated) instead of in pairs.
+template <int B>
+constexpr bool quad_table() {
+    return TQ_FAST_QUAD && B == 3;
+}
+// Replicas of the fp4 sign table (fewer when a quad table takes the LDS).
+template <int KB, int VB>
+constexpr int sign_replicas() {
+    return (quad_table<KB>() || quad_table<VB>()) ? 16 : 32;
 }
 
 __device__ __forceinline__ uint32_t pick_halves(uint32_t hi_src, uint32_t lo_src, int s) {
@@ -133,7 +153,8 @@ struct LaneCtx {
     tq_half8 qop[4];            // q (fp16), MFMA chunk cc: dims 32g + 8cc + j
     tq_i32x8 qph, qpl;          // q_proj * corr * cscale * 2^b in fp8: hi, (x - hi) * 16
     int sc_hi, sc_lo;           // E8M0 scales undoing 2^b and 2^(b+4)
-    uint32_t kbank, vbank, sbank;
+    uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
+    uint32_t kquad, vquad;         // quad tables: table base only
     uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
     uint64_t hmask;             // lanes of real heads
     bool lo8;                   // column < 8: tile A
@@ -145,18 +166,30 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
         tq_u32x4 a;
+        if (quad_table<KB>()) {
+            // dims 8cc..8cc+7 of the lane's 32: two 12-bit quads
+            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc), c.kquad));
+            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc + 1), c.kquad));
+            a[0] = lo[0];
+            a[1] = lo[1];
+            a[2] = hi[0];
+            a[3] = hi[1];
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = lds_read(entry_addr<2 * KB>(kw, 2 * KB * (4 * cc + j), c.kbank));
+            for (int j = 0; j < 4; ++j) a[j] = lds_read(entry_addr<2 * KB>(kw, 2 * KB * (4 * cc + j), c.kbank));
+        }
         s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), c.qop[cc], s, 0, 0, 0);
     }
     return s;
 }
 
+template <int SREP>
 __device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, const LaneCtx& c) {
+    constexpr int P = SREP == 32 ? 7 : 6;  // entry stride: SREP replicas x 4 bytes
     const uint32_t w[1] = {ks};
     tq_i32x8 a;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) a[b] = (int)lds_read(entry_addr<8>(w, 8 * b, c.sbank));
+    for (int b = 0; b < 4; ++b) a[b] = (int)lds_read(entry_addr<8, 1, P>(w, 8 * b, c.sbank));
 #pragma unroll
     for (int b = 4; b < 8; ++b) a[b] = 0;  // fp4 operand: only the first four dwords are read
     tq_floatx4 t = {0.f, 0.f, 0.f, 0.f};
@@ -184,8 +217,8 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     const tq_floatx4 sB = qk_tile<KB>(kr.kwB, c);
     tq_floatx4 tA = {0.f, 0.f, 0.f, 0.f}, tB = {0.f, 0.f, 0.f, 0.f};
     if (KQJL) {
-        tA = qjl_tile(kr.ksA, c);
-        tB = qjl_tile(kr.ksB, c);
+        tA = qjl_tile<sign_replicas<KB, VB>()>(kr.ksA, c);
+        tB = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, c);
     }
     uint64_t rm[4];
     if (pi.nvA == 16 && pi.nvB == 16) {
@@ -262,21 +295,44 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     p23.h[1] = scale_to_half(vnr[3], pr[3]);
     const tq_u32x4 bw = {p01.u, p23.u, row_swap8(p01.u), row_swap8(p23.u)};
     const tq_half8 bop = __builtin_bit_cast(tq_half8, bw);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        uint32_t la[4], lb[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
-            la[r] = lds_read(entry_addr<2 * VB>(wa, 2 * VB * q, c.vbank));
-            lb[r] = lds_read(entry_addr<2 * VB>(wb, 2 * VB * q, c.vbank));
-        }
+    auto pv_mfma = [&](const uint32_t (&la)[4], const uint32_t (&lb)[4], int q) {
 #pragma unroll
         for (int hs = 0; hs < 2; ++hs) {
             const tq_u32x4 aw = {pick_halves(la[1], la[0], hs), pick_halves(la[3], la[2], hs),
                                  pick_halves(lb[1], lb[0], hs), pick_halves(lb[3], lb[2], hs)};
             st.acc[2 * q + hs] =
                 __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, aw), bop, st.acc[2 * q + hs], 0, 0, 0);
+        }
+    };
+    if (quad_table<VB>()) {
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+            // dims 8n + 4qh .. 8n + 4qh + 3 of each token: one quad -> pairs q = 2qh, 2qh + 1
+            uint32_t la[2][4], lb[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
+                const tq_u32x2 xa = lds_read2(entry_addr<4 * VB, 1, 3>(wa, 4 * VB * qh, c.vquad));
+                const tq_u32x2 xb = lds_read2(entry_addr<4 * VB, 1, 3>(wb, 4 * VB * qh, c.vquad));
+                la[0][r] = xa[0];
+                la[1][r] = xa[1];
+                lb[0][r] = xb[0];
+                lb[1][r] = xb[1];
+            }
+            pv_mfma(la[0], lb[0], 2 * qh);
+            pv_mfma(la[1], lb[1], 2 * qh + 1);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t la[4], lb[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
+                la[r] = lds_read(entry_addr<2 * VB>(wa, 2 * VB * q, c.vbank));
+                lb[r] = lds_read(entry_addr<2 * VB>(wb, 2 * VB * q, c.vbank));
+            }
+            pv_mfma(la, lb, q);
         }
     }
 }
@@ -291,35 +347,40 @@ template <int KB, bool KQJL, int VB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
                                                                      fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
-    constexpr int KENT = 1 << (2 * KB);
-    constexpr int VENT = 1 << (2 * VB);
     extern __shared__ uint32_t s_lds[];
     // Tables (32 bank replicas each): fp4 sign table (QJL), K pair table, V pair table, at the
     // byte offsets chosen by the host (multiples of each table's size).
+    constexpr int SREP = sign_replicas<KB, VB>();
     if (KQJL) {
         uint32_t* t = s_lds + p.lds_sign / 4;
-        for (int i = threadIdx.x; i < 256 * 32; i += 256) {
-            const uint32_t e = (uint32_t)i >> 5;
+        for (int i = threadIdx.x; i < 256 * SREP; i += 256) {
+            const uint32_t e = (uint32_t)i / SREP;
             uint32_t w = 0;
 #pragma unroll
             for (int j = 0; j < 8; ++j) w |= (((e >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);  // fp4 +1 / -1
             t[i] = w;
         }
     }
-    {
-        uint32_t* t = s_lds + p.lds_k / 4;
-        for (int i = threadIdx.x; i < KENT * 32; i += 256) {
-            const int e = i >> 5;
-            t[i] = tq_pack_half2(p.k_cent[e & ((1 << KB) - 1)] * p.k_cscale, p.k_cent[e >> KB] * p.k_cscale);
+    // pair table: entry e -> half2(c[e & (2^b - 1)], c[e >> b]), 32 replicas;
+    // quad table: entry e -> 4 x fp16 c[(e >> 3j) & 7], j = 0..3
+    auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad) {
+        uint32_t* t = s_lds + off / 4;
+        const int mask = (1 << bits) - 1;
+        if (quad) {
+            for (int i = threadIdx.x; i < 4096 * 2; i += 256) {
+                const int e = i >> 1, j0 = 2 * (i & 1);
+                t[i] = tq_pack_half2(cent[(e >> (3 * j0)) & 7] * cs, cent[(e >> (3 * j0 + 3)) & 7] * cs);
+            }
+        } else {
+            const int ent = 1 << (2 * bits);
+            for (int i = threadIdx.x; i < ent * 32; i += 256) {
+                const int e = i >> 5;
+                t[i] = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
+            }
         }
-    }
-    if (p.lds_v != p.lds_k) {
-        uint32_t* t = s_lds + p.lds_v / 4;
-        for (int i = threadIdx.x; i < VENT * 32; i += 256) {
-            const int e = i >> 5;
-            t[i] = tq_pack_half2(p.v_cent[e & ((1 << VB) - 1)] * p.v_cscale, p.v_cent[e >> VB] * p.v_cscale);
-        }
-    }
+    };
+    fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>());
+    if (p.lds_v != p.lds_k) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>());
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
@@ -332,7 +393,9 @@ void decode_fast_kernel(FastDecodeParams p) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
     c.kbank = lds0 + p.lds_k + bank4;
     c.vbank = lds0 + p.lds_v + bank4;
-    c.sbank = lds0 + p.lds_sign + bank4;
+    c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
+    c.kquad = lds0 + p.lds_k;
+    c.vquad = lds0 + p.lds_v;
     c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -628,9 +691,10 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
     } t[3];
     int n = 0;
     uint32_t dummy = 0;
-    t[n++] = {kq ? (size_t)256 * 128 : 0, lds_sign};
-    t[n++] = {((size_t)1 << (2 * kb)) * 128, lds_k};
-    t[n++] = {share ? 0 : ((size_t)1 << (2 * vb)) * 128, share ? &dummy : lds_v};
+    const bool kquad = TQ_FAST_QUAD && kb == 3, vquad = TQ_FAST_QUAD && vb == 3;
+    t[n++] = {kq ? (size_t)256 * 4 * ((kquad || vquad) ? 16 : 32) : 0, lds_sign};
+    t[n++] = {kquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * kb)) * 128, lds_k};
+    t[n++] = {share ? 0 : (vquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * vb)) * 128), share ? &dummy : lds_v};
     for (int i = 0; i < n; ++i)
         for (int j = i + 1; j < n; ++j)
             if (t[j].size > t[i].size) {
