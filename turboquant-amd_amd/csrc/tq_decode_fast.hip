@@ -154,7 +154,7 @@ struct LaneCtx {
     tq_i32x8 qph, qpl;          // q_proj * corr * cscale * 2^b in fp8: hi, (x - hi) * 16
     int sc_hi, sc_lo;           // E8M0 scales undoing 2^b and 2^(b+4)
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
-    uint32_t kquad, vquad;         // quad tables: table base only
+    uint32_t vquad;                // V quad table base (the K quad table is at address 0)
     uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
     uint64_t hmask;             // lanes of real heads
     bool lo8;                   // column < 8: tile A
@@ -168,8 +168,9 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
         tq_u32x4 a;
         if (quad_table<KB>()) {
             // dims 8cc..8cc+7 of the lane's 32: two 12-bit quads
-            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc), c.kquad));
-            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc + 1), c.kquad));
+            // the K quad table sits at LDS address 0: the address is the field times 8
+            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc), 0u));
+            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc + 1), 0u));
             a[0] = lo[0];
             a[1] = lo[1];
             a[2] = hi[0];
@@ -394,8 +395,10 @@ void decode_fast_kernel(FastDecodeParams p) {
     c.kbank = lds0 + p.lds_k + bank4;
     c.vbank = lds0 + p.lds_v + bank4;
     c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
-    c.kquad = lds0 + p.lds_k;
+    // V quad table: address 0 when it is the K quad table, else its base from a VGPR (a VALU
+    // op takes one scalar operand, and the field mask is one)
     c.vquad = lds0 + p.lds_v;
+    if (!(quad_table<KB>() && p.lds_v == 0)) asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
     c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -518,7 +521,7 @@ void decode_fast_kernel(FastDecodeParams p) {
         const uint32_t lo = oA < oB ? oA : oB;
         const uint32_t d = (oA < oB ? oB : oA) - lo;
         const uint64_t up = oB > oA ? hi8 : ~hi8;
-        return NormAddr{o_norm + (((up >> lane) & 1) ? d : 0u), lo};
+        return NormAddr{o_norm + (__builtin_amdgcn_inverse_ballot_w64(up) ? d : 0u), lo};
     };
 
     // K part of pair pi (and the block numbers of pair pi + 1); fills the V offsets of pi.
@@ -616,20 +619,22 @@ void decode_fast_kernel(FastDecodeParams p) {
 
     const int ntiles = (t_end - t_begin + 15) >> 4;
     const int npairs = (ntiles + 1) >> 1;
+    // All data of a pair is loaded one pair ahead (two register sets).  Pairs past the end read
+    // block data that is never used (every fetch issues the same loads, which keeps the
+    // compiler's outstanding-load counts exact).
     KRaw<KB, KQJL> kr[2];
     PairInfo info[2];
-    VRaw vr;
-    // Pairs past the end read block data that is never used (every fetch issues the same
-    // loads, which keeps the compiler's outstanding-load counts exact).
+    VRaw vr[2];
     fetch_k(0, kr[0], info[0]);
+    load_v(info[0], vr[0]);
     for (int i = 0; i < npairs; i += 2) {
-        load_v(info[0], vr);
         fetch_k(i + 1, kr[1], info[1]);
-        compute_pair<KB, KQJL, VB>(kr[0], vr, info[0], st, c, p, sparse);
+        load_v(info[1], vr[1]);
+        compute_pair<KB, KQJL, VB>(kr[0], vr[0], info[0], st, c, p, sparse);
         if (i + 1 >= npairs) break;
-        load_v(info[1], vr);
         fetch_k(i + 2, kr[0], info[0]);
-        compute_pair<KB, KQJL, VB>(kr[1], vr, info[1], st, c, p, sparse);
+        load_v(info[0], vr[0]);
+        compute_pair<KB, KQJL, VB>(kr[1], vr[1], info[1], st, c, p, sparse);
     }
 
     // ---- combine the lane groups and the two tile halves ----
@@ -702,8 +707,18 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
                 t[i] = t[j];
                 t[j] = x;
             }
+    // A K quad table goes first: the kernel addresses it from LDS address 0.
+    if (kquad)
+        for (int i = 1; i < n; ++i)
+            if (t[i].off == lds_k) {
+                T x = t[0];
+                t[0] = t[i];
+                t[i] = x;
+            }
     size_t off = 0;
     for (int i = 0; i < n; ++i) {
+        // each table at a multiple of its size (pair tables are addressed by OR)
+        if (t[i].size) off = (off + t[i].size - 1) / t[i].size * t[i].size;
         *t[i].off = (uint32_t)off;
         off += t[i].size;
     }
