@@ -210,9 +210,9 @@ __device__ __forceinline__ uint64_t row_mask(int nvA, int nvB, int r) {
 }
 
 // One pair of tiles.
-template <int KB, bool KQJL, int VB>
+template <int KB, bool KQJL, int VB, bool COUNT>
 __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRaw& vr, const PairInfo& pi,
-                                             Softmax& st, const LaneCtx& c, const FastDecodeParams& p, bool sparse) {
+                                             Softmax& st, const LaneCtx& c, const FastDecodeParams& p) {
     // ---------------- scores ----------------
     const tq_floatx4 sA = qk_tile<KB>(kr.kwA, c);
     const tq_floatx4 sB = qk_tile<KB>(kr.kwB, c);
@@ -222,12 +222,21 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
         tB = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, c);
     }
     uint64_t rm[4];
+    // Rows past the end may hold any bits in a paged block: masked out of the scores, and their
+    // value norms zeroed (bit-wise, before any arithmetic).
+    uint32_t vn[2] = {vr.vn[0], vr.vn[1]};
     if (pi.nvA == 16 && pi.nvB == 16) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) rm[r] = ~0ull;
     } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) rm[r] = row_mask(pi.nvA, pi.nvB, r);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t lo = __builtin_amdgcn_inverse_ballot_w64(rm[2 * k]) ? 0x0000ffffu : 0u;
+            const uint32_t hi = __builtin_amdgcn_inverse_ballot_w64(rm[2 * k + 1]) ? 0xffff0000u : 0u;
+            vn[k] &= lo | hi;
+        }
     }
     float sc[4];
 #pragma unroll
@@ -265,7 +274,7 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
     // ---------------- Sparse-V ----------------
-    if (sparse) {
+    if (p.sparse) {
         const float m_skip = c.lo8 ? fmaxf(m_old, mt) : m_new;
         const float thr = m_skip + p.thr_log;
         uint32_t kept = 0;
@@ -275,25 +284,23 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
             // some head of this lane's 8-lane group (its tile's token 4g + r) passes
             const bool keep = (uint32_t)((bal << c.shl8) >> 32) >= (1u << 24);
             pr[r] = keep ? pr[r] : 0.f;
-            kept += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(keep) & 0x0101010101010101ull);
+            if (COUNT) kept += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(keep) & 0x0101010101010101ull);
         }
-        st.n_tot += (uint32_t)(pi.nvA + pi.nvB);
-        st.n_kept += kept;
+        if (COUNT) {
+            st.n_tot += (uint32_t)(pi.nvA + pi.nvB);
+            st.n_kept += kept;
+        }
     }
 
     // ---------------- PV ----------------
-    // Rows past the end may hold any bits in a paged block: their norms are replaced by 0.
     union {
         _Float16 h[2];
         uint32_t u;
     } p01, p23;
-    float vnr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) vnr[r] = __builtin_amdgcn_inverse_ballot_w64(rm[r]) ? half_at(vr.vn, r) : 0.f;
-    p01.h[0] = scale_to_half(vnr[0], pr[0]);
-    p01.h[1] = scale_to_half(vnr[1], pr[1]);
-    p23.h[0] = scale_to_half(vnr[2], pr[2]);
-    p23.h[1] = scale_to_half(vnr[3], pr[3]);
+    p01.h[0] = scale_to_half(half_at(vn, 0), pr[0]);
+    p01.h[1] = scale_to_half(half_at(vn, 1), pr[1]);
+    p23.h[0] = scale_to_half(half_at(vn, 2), pr[2]);
+    p23.h[1] = scale_to_half(half_at(vn, 3), pr[3]);
     const tq_u32x4 bw = {p01.u, p23.u, row_swap8(p01.u), row_swap8(p23.u)};
     const tq_half8 bop = __builtin_bit_cast(tq_half8, bw);
     auto pv_mfma = [&](const uint32_t (&la)[4], const uint32_t (&lb)[4], int q) {
@@ -344,7 +351,9 @@ constexpr int fast_waves() {
     return TQ_FAST_WAVES > 0 ? TQ_FAST_WAVES : (KQJL ? 3 : 4);
 }
 
-template <int KB, bool KQJL, int VB>
+// COUNT: Sparse-V skip statistics requested (a separate instance keeps the counting off the
+// common path).
+template <int KB, bool KQJL, int VB, bool COUNT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
                                                                      fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
@@ -615,7 +624,6 @@ void decode_fast_kernel(FastDecodeParams p) {
     for (int i = 0; i < 8; ++i) st.acc[i] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
     st.n_tot = 0;
     st.n_kept = 0;
-    const bool sparse = p.sparse != 0;
 
     const int ntiles = (t_end - t_begin + 15) >> 4;
     const int npairs = (ntiles + 1) >> 1;
@@ -630,17 +638,17 @@ void decode_fast_kernel(FastDecodeParams p) {
     for (int i = 0; i < npairs; i += 2) {
         fetch_k(i + 1, kr[1], info[1]);
         load_v(info[1], vr[1]);
-        compute_pair<KB, KQJL, VB>(kr[0], vr[0], info[0], st, c, p, sparse);
+        compute_pair<KB, KQJL, VB, COUNT>(kr[0], vr[0], info[0], st, c, p);
         if (i + 1 >= npairs) break;
         fetch_k(i + 2, kr[0], info[0]);
         load_v(info[0], vr[0]);
-        compute_pair<KB, KQJL, VB>(kr[1], vr[1], info[1], st, c, p, sparse);
+        compute_pair<KB, KQJL, VB, COUNT>(kr[1], vr[1], info[1], st, c, p);
     }
 
     // ---- combine the lane groups and the two tile halves ----
     float lsum = sum_over_groups(st.lsum);
     lsum += row_swap8f(lsum);
-    if (sparse && p.skip_stats != nullptr && lane == 0) {
+    if (COUNT && lane == 0) {
         atomicAdd(p.skip_stats, (unsigned long long)(st.n_tot - st.n_kept));
         atomicAdd(p.skip_stats + 1, (unsigned long long)st.n_tot);
     }
@@ -677,9 +685,10 @@ void decode_fast_kernel(FastDecodeParams p) {
 
 }  // namespace
 
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb) {
-#define TQ_FP(KB, KQ, VB) \
-    if (kb == KB && kq == KQ && vb == VB) return (const void*)decode_fast_kernel<KB, KQ, VB>;
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count) {
+#define TQ_FP(KB, KQ, VB)                                                                              \
+    if (kb == KB && kq == KQ && vb == VB)                                                              \
+        return count ? (const void*)decode_fast_kernel<KB, KQ, VB, true> : (const void*)decode_fast_kernel<KB, KQ, VB, false>;
 #define TQ_FP_V(KB, KQ) TQ_FP(KB, KQ, 2) TQ_FP(KB, KQ, 3) TQ_FP(KB, KQ, 4)
     TQ_FP_V(2, false) TQ_FP_V(2, true) TQ_FP_V(3, false) TQ_FP_V(3, true) TQ_FP_V(4, false) TQ_FP_V(4, true)
 #undef TQ_FP_V
@@ -728,7 +737,7 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream) {
-    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb);
+    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats);
     if (!kern) return TQ_ERR_BITS;
     FastDecodeParams p = prm;
     void* args[] = {&p};

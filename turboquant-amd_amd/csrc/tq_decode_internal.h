@@ -48,8 +48,8 @@ struct FastDecodeParams {
     int64_t out_ss, out_sh;
 };
 
-// decode_fast_kernel<kb, kq, vb> (nullptr: unsupported bit widths).
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb);
+// decode_fast_kernel<kb, kq, vb, count> (nullptr: unsupported bit widths).
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false);
 
 // LDS byte offsets of the fp4 sign table, the K and the V pair tables, and the total.
 void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
