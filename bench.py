@@ -304,7 +304,6 @@ def main():
         del src, dst
     extra = {}
     import random
-    rng = random.Random(3)
 
     head = None
     state4 = None
@@ -314,12 +313,14 @@ def main():
             64, 48, 8, [32768] * 64, 3, True, 3, 1e-4, 16, 4, dev, steps, warmup)
         print(f"# config4 {head['us_per_layer']:.1f} us/layer, {head['hbm_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     if args.only in (None, "config3"):
+        rng = random.Random(3)  # one generator per workload: --only gives the same lengths
         lens3 = [rng.randint(1024, 8192) for _ in range(32)]
         r3, _ = decode_case("config3: turbo4 decode, B=32, Hq 32 / Hkv 8, ctx U[1K,8K], bs 16",
                             32, 32, 8, lens3, 4, False, 4, 0.0, 16, 3, dev, steps, warmup)
         extra["config3"] = r3
         print(f"# config3 {r3['us_per_layer']:.1f} us/layer", file=sys.stderr, flush=True)
     if args.only in (None, "config5"):
+        rng = random.Random(5)
         lens5 = [int(round(math.exp(rng.uniform(math.log(2048), math.log(131072))))) for _ in range(64)]
         r5, _ = decode_case("config5: turbo2+QJL compress 64 new tokens + decode, B=64, Hq 64 / Hkv 8, "
                             "ctx log-U[2K,128K], bs 16", 64, 64, 8, lens5, 2, True, 2, 0.0, 16, 5, dev, steps, warmup,

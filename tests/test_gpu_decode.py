@@ -104,7 +104,8 @@ def run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, dtype=torch.bfloat16, ch
 
 
 @pytest.mark.parametrize("kb,kq,vb", [(4, False, 4), (3, True, 3), (2, True, 2), (3, False, 3),
-                                      (4, True, 2), (2, False, 4), (3, True, 4), (4, False, 3)])
+                                      (4, True, 2), (2, False, 4), (3, True, 4), (4, False, 3),
+                                      (2, True, 3), (3, False, 2), (2, False, 2)])
 def test_decode_bit_widths(dev, kb, kq, vb):
     S, Hq, Hkv, bs = 3, 8, 2, 16
     lens = [37, 1, 300]

@@ -79,11 +79,17 @@ __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
 #ifndef TQ_FAST_QUAD
 #define TQ_FAST_QUAD 1
 #endif
-// 3-bit indices are looked up four at a time (a 12-bit field -> 4 fp16 centroids, one 8-byte
-// entry of a 4096-entry table, not replicated) instead of in pairs.
+// 2- and 3-bit indices are looked up four at a time (a 4B-bit field -> 4 fp16 centroids, one
+// 8-byte entry) instead of in pairs.  3 bits: 4096 entries, not replicated (32 KB); 2 bits: 256
+// entries x 16 bank replicas, entry stride 128 bytes (32 KB).
 template <int B>
 constexpr bool quad_table() {
-    return TQ_FAST_QUAD && B == 3;
+    return TQ_FAST_QUAD && (B == 3 || B == 2);
+}
+// Bit position of the field in a quad table address (log2 of the entry stride).
+template <int B>
+constexpr int quad_shift() {
+    return B == 2 ? 7 : 3;
 }
 // Replicas of the fp4 sign table (fewer when a quad table takes the LDS).
 template <int KB, int VB>
@@ -154,7 +160,7 @@ struct LaneCtx {
     tq_i32x8 qph, qpl;          // q_proj * corr * cscale * 2^b in fp8: hi, (x - hi) * 16
     int sc_hi, sc_lo;           // E8M0 scales undoing 2^b and 2^(b+4)
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
-    uint32_t vquad;                // V quad table base (the K quad table is at address 0)
+    uint32_t vquad;                // V quad table base (+ replica offset; a 3-bit K quad table is at address 0)
     uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
     uint64_t hmask;             // lanes of real heads
     bool lo8;                   // column < 8: tile A
@@ -167,10 +173,11 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
     for (int cc = 0; cc < 4; ++cc) {
         tq_u32x4 a;
         if (quad_table<KB>()) {
-            // dims 8cc..8cc+7 of the lane's 32: two 12-bit quads
-            // the K quad table sits at LDS address 0: the address is the field times 8
-            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc), 0u));
-            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, 3>(kw, 4 * KB * (2 * cc + 1), 0u));
+            // dims 8cc..8cc+7 of the lane's 32: two quads
+            // a 3-bit K quad table sits at LDS address 0: the address is the field times 8
+            const uint32_t base = KB == 3 ? 0u : c.kbank;
+            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc), base));
+            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc + 1), base));
             a[0] = lo[0];
             a[1] = lo[1];
             a[2] = hi[0];
@@ -320,8 +327,8 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
-                const tq_u32x2 xa = lds_read2(entry_addr<4 * VB, 1, 3>(wa, 4 * VB * qh, c.vquad));
-                const tq_u32x2 xb = lds_read2(entry_addr<4 * VB, 1, 3>(wb, 4 * VB * qh, c.vquad));
+                const tq_u32x2 xa = lds_read2(entry_addr<4 * VB, 1, quad_shift<VB>()>(wa, 4 * VB * qh, c.vquad));
+                const tq_u32x2 xb = lds_read2(entry_addr<4 * VB, 1, quad_shift<VB>()>(wb, 4 * VB * qh, c.vquad));
                 la[0][r] = xa[0];
                 la[1][r] = xa[1];
                 lb[0][r] = xb[0];
@@ -372,14 +379,19 @@ void decode_fast_kernel(FastDecodeParams p) {
         }
     }
     // pair table: entry e -> half2(c[e & (2^b - 1)], c[e >> b]), 32 replicas;
-    // quad table: entry e -> 4 x fp16 c[(e >> 3j) & 7], j = 0..3
+    // quad table: entry e -> 4 x fp16 c[(e >> bj) & (2^b - 1)], j = 0..3
     auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad) {
         uint32_t* t = s_lds + off / 4;
         const int mask = (1 << bits) - 1;
-        if (quad) {
+        if (quad && bits == 3) {
             for (int i = threadIdx.x; i < 4096 * 2; i += 256) {
                 const int e = i >> 1, j0 = 2 * (i & 1);
                 t[i] = tq_pack_half2(cent[(e >> (3 * j0)) & 7] * cs, cent[(e >> (3 * j0 + 3)) & 7] * cs);
+            }
+        } else if (quad) {
+            for (int i = threadIdx.x; i < 256 * 16 * 2; i += 256) {
+                const int e = i >> 5, j0 = 2 * (i & 1);
+                t[i] = tq_pack_half2(cent[(e >> (2 * j0)) & 3] * cs, cent[(e >> (2 * j0 + 2)) & 3] * cs);
             }
         } else {
             const int ent = 1 << (2 * bits);
@@ -401,13 +413,15 @@ void decode_fast_kernel(FastDecodeParams p) {
     c.lo8 = n < 8;
     const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
-    c.kbank = lds0 + p.lds_k + bank4;
+    const uint32_t bank8 = 8u * (uint32_t)(lane & 15);  // 2-bit quad tables: 16 replicas of 8 bytes
+    c.kbank = lds0 + p.lds_k + (KB == 2 && quad_table<KB>() ? bank8 : bank4);
     c.vbank = lds0 + p.lds_v + bank4;
     c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
     // V quad table: address 0 when it is the K quad table, else its base from a VGPR (a VALU
     // op takes one scalar operand, and the field mask is one)
     c.vquad = lds0 + p.lds_v;
-    if (!(quad_table<KB>() && p.lds_v == 0)) asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
+    if (VB == 2) c.vquad += bank8;
+    else if (!(quad_table<KB>() && KB == 3 && p.lds_v == 0)) asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
     c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -705,7 +719,7 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
     } t[3];
     int n = 0;
     uint32_t dummy = 0;
-    const bool kquad = TQ_FAST_QUAD && kb == 3, vquad = TQ_FAST_QUAD && vb == 3;
+    const bool kquad = TQ_FAST_QUAD && (kb == 3 || kb == 2), vquad = TQ_FAST_QUAD && (vb == 3 || vb == 2);
     t[n++] = {kq ? (size_t)256 * 4 * ((kquad || vquad) ? 16 : 32) : 0, lds_sign};
     t[n++] = {kquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * kb)) * 128, lds_k};
     t[n++] = {share ? 0 : (vquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * vb)) * 128), share ? &dummy : lds_v};
@@ -716,8 +730,8 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
                 t[i] = t[j];
                 t[j] = x;
             }
-    // A K quad table goes first: the kernel addresses it from LDS address 0.
-    if (kquad)
+    // A 3-bit K quad table goes first: the kernel addresses it from LDS address 0.
+    if (kquad && kb == 3)
         for (int i = 1; i < n; ++i)
             if (t[i].off == lds_k) {
                 T x = t[0];
