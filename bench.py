@@ -43,18 +43,18 @@ def outlier_kv(T, H, gen, device, dtype):
 def profiled_traffic(head):
     """HBM bytes per launch of the headline decode kernel from the committed rocprof summary.
 
-    profiles/decode_kernel_config4_pmc.md holds FETCH_SIZE and WRITE_SIZE of the kernel (two
+    profiles/decode_fast_kernel_config4_pmc.md holds FETCH_SIZE and WRITE_SIZE of the kernel (two
     rocprofv3 --pmc runs of this script with --copy-calibration), scaled by what the same
     counters read for two kernels of known traffic.  Returned only for the config 4 headline.
     """
     import re
-    path = ROOT / "profiles" / "decode_kernel_config4_pmc.md"
+    path = ROOT / "profiles" / "decode_fast_kernel_config4_pmc.md"
     if not head.get("workload", "").startswith("config4") or not path.exists():
         return None, None
     m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", path.read_text(), re.M)
     if not m:
         return None, None
-    return int(m.group(1)), "profiles/decode_kernel_config4_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)"
+    return int(m.group(1)), "profiles/decode_fast_kernel_config4_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)"
 
 
 def timed(fn, steps, warmup):
