@@ -1,8 +1,9 @@
 // PolarQuant compression kernels for gfx950.
 //
-// One 128-dim row per 16 lanes: lane c holds dims 8c..8c+7, so a wave64 works on 4 rows
-// and a 256-thread workgroup on 16 rows.  The Walsh-Hadamard rotation is 3 in-register
-// butterfly stages (dim bits 0-2) plus 4 cross-lane stages (dim bits 3-6 = lane bits 0-3).
+// One 128-dim row per 16 lanes (8 dims each), so a wave64 works on 4 rows and a 256-thread
+// workgroup on 16 rows.  The Walsh-Hadamard rotation is 3 in-register butterfly stages (dim
+// bits 0-2) plus 4 cross-lane stages (DPP / permlane16_swap, no LDS); indices come from a
+// 256-cell LDS table of the boundaries (one compare per value).
 // Row math follows turboquant/core/quantizer.py:141-174:
 //   x_rot = x @ H; norm = |x_rot|; x_n = x_rot / (norm + 1e-8); idx = #{b < x_n};
 //   r = (x_n - c[idx]) * norm; rnorm = |r|; sign = r >= 0.
@@ -30,6 +31,7 @@ struct CompressParams {
     uint8_t* cache;
     int64_t stride_block, stride_head, num_blocks;
     int block_size;
+    int idx32;  // rows and slots below 2^31: 32-bit index arithmetic
     int64_t off_signs, off_norm, off_rnorm;
     // unpacked output
     int64_t* indices;
@@ -39,12 +41,130 @@ struct CompressParams {
     float* rnorm;
 };
 
-__device__ __forceinline__ float xor_sum16(float v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
-    return v;
+// Lane layout: lane L of a wave holds dims 8c..8c+7 of row rho of the wave's 4 rows, with
+//   c = L bits {0, 1, 3, 4},  rho = L bits {2, 5}.
+// The 16 lanes of a row then differ in lane bits 0, 1, 3, 4, and every exchange inside a row is
+// a DPP quad_perm (bits 0, 1), a DPP row_ror:8 (bit 3) or a permlane16_swap (bit 4): no LDS.
+__device__ __forceinline__ int lane_dims(int L) { return (L & 3) | ((L >> 1) & 12); }
+__device__ __forceinline__ int lane_row(int L) { return ((L >> 2) & 1) | ((L >> 4) & 2); }
+
+constexpr int kDppXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
+constexpr int kDppXor8 = 0x128;  // row_ror:8 (lane l <- l ^ 8 inside a row of 16)
+template <int CTRL>
+__device__ __forceinline__ float dppf(float x) {
+    // bound_ctrl with a zero old value: lets the compiler fold the move into the consuming add
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppu(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xf, 0xf, false);
+}
+// Values of lanes L & ~16 and L | 16.
+__device__ __forceinline__ void rows16(float x, float& even, float& odd) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    even = __uint_as_float(r[0]);
+    odd = __uint_as_float(r[1]);
+}
+
+// Sum over the 16 lanes of a row, in the order of an xor butterfly over dims bits 3, 4, 5, 6:
+// every lane of the row gets the same bits.
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dppf<kDppXor1>(v);
+    v += dppf<kDppXor2>(v);
+    v += dppf<kDppXor8>(v);
+    float e, o;
+    rows16(v, e, o);
+    return e + o;
+}
+
+// Normalised Hadamard transform of a row in the lane layout above (dims 8c + k in v[k]):
+// butterflies (u, w) -> (u + w, u - w) over dims bits 0..6, then the scale h.  A cross-lane
+// stage computes partner + s * own with s = -1 in the upper lane (u - w there, exactly), the
+// partner read through DPP or permlane16_swap.
+__device__ __forceinline__ void wht_row(float (&v)[8], int L, float h) {
+#pragma unroll
+    for (int b = 1; b < 8; b <<= 1) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (!(k & b)) {
+                const float u = v[k], w = v[k | b];
+                v[k] = u + w;
+                v[k | b] = u - w;
+            }
+        }
+    }
+    auto stage = [&](auto dpp, float s) {
+        float t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = v[k] * s;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = dpp(v[k]) + t[k];
+    };
+    stage([](float x) { return dppf<kDppXor1>(x); }, (L & 1) ? -1.f : 1.f);
+    stage([](float x) { return dppf<kDppXor2>(x); }, (L & 2) ? -1.f : 1.f);
+    stage([](float x) { return dppf<kDppXor8>(x); }, (L & 8) ? -1.f : 1.f);
+    const float s4 = (L & 16) ? -1.f : 1.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        float e, o;
+        rows16(v[k], e, o);
+        v[k] = __builtin_fmaf(o, s4, e);  // lower lane: e + o, upper lane: e - o
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] *= h;
+}
+
+// Left searchsorted over NB sorted boundaries (count of boundaries < x; NaN -> NB) through a
+// table of 256 equal cells over [lo, hi] (one cell of margin past the outer boundaries): cell k
+// holds c0 = #{b < edge_k - eps} and the one boundary inside [edge_k - eps, edge_k+1 + eps] (or
+// +inf), so idx = c0 + (b < x) for any x whose computed cell is within eps of its true cell
+// (|x| <= 1 here, the cell arithmetic errs by < 1e-6 * (hi - lo) = eps / 10).  A codebook with two
+// boundaries in one such cell sets `bad` and the kernel counts linearly instead.
+constexpr int kCells = 256;
+struct CellQuant {
+    float inv_w, c;  // cell = trunc(x * inv_w + c)
+};
+template <int NB>
+__device__ __forceinline__ CellQuant build_cells(const float (&bd)[NB], const float* boundaries, uint2* tab,
+                                                 int* bad) {
+    float span = bd[NB - 1] - bd[0];
+    span = span > 0.f ? span : 1.f;
+    const float lo = bd[0] - span * (1.f / 64.f);
+    const float hi = bd[NB - 1] + span * (1.f / 64.f);
+    const float w = (hi - lo) * (1.f / kCells);
+    const float eps = (hi - lo) * 1e-5f;
+    for (int k = threadIdx.x; k < kCells; k += blockDim.x) {
+        const float e0 = lo + (float)k * w - eps, e1 = lo + (float)(k + 1) * w + eps;
+        int c0 = 0, c1 = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            c0 += bd[i] < e0 ? 1 : 0;
+            c1 += bd[i] <= e1 ? 1 : 0;
+        }
+        if (c1 - c0 > 1 || !(w > 0.f)) atomicOr(bad, 1);
+        const float b = c1 > c0 ? boundaries[c0] : __builtin_huge_valf();
+        tab[k] = make_uint2(__float_as_uint(b), (uint32_t)c0);
+    }
+    CellQuant q;
+    q.inv_w = (float)kCells / (hi - lo);
+    q.c = -lo * q.inv_w;
+    return q;
+}
+template <int NB>
+__device__ __forceinline__ int quant_cell(float x, const CellQuant& q, const uint2* tab) {
+    int cell = (int)__builtin_fmaf(x, q.inv_w, q.c);
+    cell = cell < 0 ? 0 : (cell > kCells - 1 ? kCells - 1 : cell);
+    const uint2 e = tab[cell];
+    const int idx = (int)e.y + (__uint_as_float(e.x) < x ? 1 : 0);
+    return x != x ? NB : idx;  // searchsorted puts NaN last
+}
+template <int NB>
+__device__ __forceinline__ int quant_linear(float x, const float (&bd)[NB]) {
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) cnt += (bd[i] < x) ? 1 : 0;
+    return x != x ? NB : cnt;
 }
 
 template <int BITS, bool QJL, int MODE>
@@ -52,17 +172,22 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
     constexpr int NC = 1 << BITS;
     constexpr int NB = NC - 1;
     __shared__ float s_cent[NC];
+    __shared__ uint2 s_cells[kCells];
+    __shared__ int s_bad;
     if (threadIdx.x < NC) s_cent[threadIdx.x] = p.centroids[threadIdx.x];
-    __syncthreads();
-
+    if (threadIdx.x == 0) s_bad = 0;
     // Boundaries are uniform: the loads below become scalar loads kept in SGPRs.
     float bd[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) bd[i] = p.boundaries[i];
+    __syncthreads();
+    const CellQuant cq = build_cells<NB>(bd, p.boundaries, s_cells, &s_bad);
+    __syncthreads();
+    const bool cells = s_bad == 0;
 
-    const int lane = threadIdx.x & 63;
-    const int c = lane & 15;                       // dims 8c..8c+7
-    const int row_in_wg = (threadIdx.x >> 4);      // 0..15
+    const int L = threadIdx.x & 63;
+    const int c = lane_dims(L);                                      // dims 8c..8c+7
+    const int row_in_wg = 4 * (int)(threadIdx.x >> 6) + lane_row(L);  // 0..15
 
     for (int64_t row0 = (int64_t)blockIdx.x * 16; row0 < p.n_rows; row0 += (int64_t)gridDim.x * 16) {
         const int64_t row = row0 + row_in_wg;
@@ -70,8 +195,15 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
         // Paged rows are head-major so that a workgroup's 16 rows are 16 consecutive tokens.
         int64_t tok, head;
         if (MODE == MODE_PAGED) {
-            head = row_ok ? row / p.num_tokens : 0;
-            tok = row_ok ? row - head * p.num_tokens : 0;
+            if (p.idx32) {
+                const uint32_t r = row_ok ? (uint32_t)row : 0u, nt = (uint32_t)p.num_tokens;
+                const uint32_t h = r / nt;
+                head = h;
+                tok = r - h * nt;
+            } else {
+                head = row_ok ? row / p.num_tokens : 0;
+                tok = row_ok ? row - head * p.num_tokens : 0;
+            }
         } else {
             head = 0;
             tok = row_ok ? row : 0;
@@ -84,37 +216,12 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) v[k] = 0.f;
         }
-
-        if (p.rotate) {
-            // Natural-order Hadamard: stage for index bit b maps (u, v) -> (u + v, u - v).
-#pragma unroll
-            for (int b = 1; b < 8; b <<= 1) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    if (!(k & b)) {
-                        float u = v[k], w = v[k | b];
-                        v[k] = u + w;
-                        v[k | b] = u - w;
-                    }
-                }
-            }
-#pragma unroll
-            for (int m = 1; m < 16; m <<= 1) {
-                const bool upper = (c & m) != 0;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    float o = __shfl_xor(v[k], m);
-                    v[k] = upper ? (o - v[k]) : (v[k] + o);
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] *= p.wht_scale;
-        }
+        if (p.rotate) wht_row(v, L, p.wht_scale);
 
         float ss = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(v[k], v[k], ss);
-        ss = xor_sum16(ss);
+        ss = row_sum16(ss);
         const float norm = __builtin_sqrtf(ss);
         const float den = norm + 1e-8f;
         const float rcp = 1.0f / den;
@@ -122,12 +229,13 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
         int idx[8];
         float xn[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            xn[k] = tq_div_rn(v[k], den, rcp);
-            int cnt = 0;
+        for (int k = 0; k < 8; ++k) xn[k] = tq_div_rn(v[k], den, rcp);
+        if (cells) {
 #pragma unroll
-            for (int i = 0; i < NB; ++i) cnt += (bd[i] < xn[k]) ? 1 : 0;
-            idx[k] = (xn[k] != xn[k]) ? NB : cnt;  // searchsorted puts NaN last
+            for (int k = 0; k < 8; ++k) idx[k] = quant_cell<NB>(xn[k], cq, s_cells);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) idx[k] = quant_linear<NB>(xn[k], bd);
         }
 
         float rn = 0.f;
@@ -145,7 +253,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
                 rs = __builtin_fmaf(r, r, rs);
                 sbits |= (r >= 0.f ? 1u : 0u) << k;
             }
-            rn = __builtin_sqrtf(xor_sum16(rs));
+            rn = __builtin_sqrtf(row_sum16(rs));
         }
 
         if (MODE == MODE_UNPACKED) {
@@ -174,18 +282,28 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
                                   : (int64_t) static_cast<const int32_t*>(p.slot_mapping)[tok];
             }
             const bool write = row_ok && slot >= 0 && slot < p.num_blocks * p.block_size;
-            const int64_t blk = write ? slot / p.block_size : 0;
-            const int64_t r_in_blk = write ? slot - blk * p.block_size : 0;
+            int64_t blk, r_in_blk;
+            if (p.idx32) {
+                const uint32_t sl = write ? (uint32_t)slot : 0u, bs = (uint32_t)p.block_size;
+                const uint32_t b = sl / bs;
+                blk = b;
+                r_in_blk = sl - b * bs;
+            } else {
+                blk = write ? slot / p.block_size : 0;
+                r_in_blk = write ? slot - blk * p.block_size : 0;
+            }
             uint8_t* tile = p.cache + blk * p.stride_block + head * p.stride_head;
 
             uint32_t w = 0;
 #pragma unroll
             for (int k = 0; k < 8; ++k) w |= (uint32_t)idx[k] << (BITS * k);
             uint8_t* irow = tile + r_in_blk * (16 * BITS);
+            // lanes c..c+3 of a row (c % 4 == 0) are one quad: the first lane gathers the others
+            const bool quad0 = (L & 3) == 0;
             if (BITS == 3) {
-                // 24 bits per lane: lanes 4j..4j+3 assemble 12 aligned bytes.
-                uint32_t w1 = __shfl_down(w, 1), w2 = __shfl_down(w, 2), w3 = __shfl_down(w, 3);
-                if (write && (c & 3) == 0) {
+                // 24 bits per lane: the quad's four lanes make 12 aligned bytes.
+                const uint32_t w1 = dppu<0x55>(w), w2 = dppu<0xAA>(w), w3 = dppu<0xFF>(w);
+                if (write && quad0) {
                     uint32_t* dst = reinterpret_cast<uint32_t*>(irow + 12 * (c >> 2));
                     dst[0] = w | (w1 << 24);
                     dst[1] = (w1 >> 8) | (w2 << 16);
@@ -199,8 +317,8 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
                 if (write) irow[c] = (uint8_t)w;
             }
             if (QJL) {
-                uint32_t s1 = __shfl_down(sbits, 1), s2 = __shfl_down(sbits, 2), s3 = __shfl_down(sbits, 3);
-                if (write && (c & 3) == 0) {
+                const uint32_t s1 = dppu<0x55>(sbits), s2 = dppu<0xAA>(sbits), s3 = dppu<0xFF>(sbits);
+                if (write && quad0) {
                     uint32_t* dst = reinterpret_cast<uint32_t*>(tile + p.off_signs + r_in_blk * 16 + 4 * (c >> 2));
                     *dst = sbits | (s1 << 8) | (s2 << 16) | (s3 << 24);
                 }
@@ -217,8 +335,9 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
 template <int MODE>
 int launch_compress(const CompressParams& p, int bits, int qjl, hipStream_t stream) {
     if (p.n_rows <= 0) return TQ_OK;
+    // Workgroups loop over 16-row groups; 2048 of them (8 per CU) amortise the LDS set-up.
     int64_t groups = (p.n_rows + 15) / 16;
-    int grid = (int)(groups < 65536 ? groups : 65536);
+    int grid = (int)(groups < 2048 ? groups : 2048);
 #define TQ_LAUNCH(B, Q)                                                                     \
     hipLaunchKernelGGL((compress_kernel<B, Q, MODE>), dim3(grid), dim3(256), 0, stream, p)
     switch (bits * 2 + (qjl ? 1 : 0)) {
@@ -341,5 +460,6 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
     p.off_signs = g.off_signs;
     p.off_norm = g.off_norm;
     p.off_rnorm = g.off_rnorm;
+    p.idx32 = (p.n_rows < (1ll << 31) && num_blocks * (int64_t)block_size < (1ll << 31)) ? 1 : 0;
     return launch_compress<MODE_PAGED>(p, bits, use_qjl, (hipStream_t)stream);
 }

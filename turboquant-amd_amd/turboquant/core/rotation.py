@@ -11,6 +11,7 @@ those successive divisions (h == float32(1/sqrt(d)) for d = 128), H symmetric an
 
 from __future__ import annotations
 
+import functools
 import math
 
 import torch
@@ -26,8 +27,11 @@ def make_wht_matrix(d: int, device: torch.device = None) -> torch.Tensor:
     return H[:d, :d]
 
 
+@functools.lru_cache(maxsize=None)
 def wht_scale(d: int = 128) -> float:
-    """The magnitude h shared by all entries of make_wht_matrix(d), as the kernels use it."""
+    """The magnitude h shared by all entries of make_wht_matrix(d), as the kernels use it.
+
+    Computed once per d (building the matrix costs ~60 us of host time per call)."""
     return float(make_wht_matrix(d)[0, 0].item())
 
 
