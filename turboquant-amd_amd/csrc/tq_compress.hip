@@ -1,9 +1,9 @@
 // PolarQuant compression kernels for gfx950.
 //
-// One 128-dim row per 16 lanes (8 dims each), so a wave64 works on 4 rows and a 256-thread
-// workgroup on 16 rows.  The Walsh-Hadamard rotation is 3 in-register butterfly stages (dim
-// bits 0-2) plus 4 cross-lane stages (DPP / permlane16_swap, no LDS); indices come from a
-// 256-cell LDS table of the boundaries (one compare per value).
+// One 128-dim row per 4 lanes (32 dims each), so a wave64 works on 16 rows and a 256-thread
+// workgroup on 64 rows.  The Walsh-Hadamard rotation is 5 in-register butterfly stages (dim
+// bits 0-4) plus 2 cross-lane stages (DPP, no LDS); indices come from a 257-cell LDS table of
+// the boundaries (one compare per value); each lane stores its 4 * bits packed bytes at once.
 // Row math follows turboquant/core/quantizer.py:141-174:
 //   x_rot = x @ H; norm = |x_rot|; x_n = x_rot / (norm + 1e-8); idx = #{b < x_n};
 //   r = (x_n - c[idx]) * norm; rnorm = |r|; sign = r >= 0.
@@ -41,52 +41,43 @@ struct CompressParams {
     float* rnorm;
 };
 
-// Lane layout: lane L of a wave holds dims 8c..8c+7 of row rho of the wave's 4 rows, with
-//   c = L bits {0, 1, 3, 4},  rho = L bits {2, 5}.
-// The 16 lanes of a row then differ in lane bits 0, 1, 3, 4, and every exchange inside a row is
-// a DPP quad_perm (bits 0, 1), a DPP row_ror:8 (bit 3) or a permlane16_swap (bit 4): no LDS.
-__device__ __forceinline__ int lane_dims(int L) { return (L & 3) | ((L >> 1) & 12); }
-__device__ __forceinline__ int lane_row(int L) { return ((L >> 2) & 1) | ((L >> 4) & 2); }
-
-constexpr int kDppXor1 = 0xB1;   // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;   // quad_perm [2, 3, 0, 1]
-constexpr int kDppXor8 = 0x128;  // row_ror:8 (lane l <- l ^ 8 inside a row of 16)
+// Lane layout: 4 lanes per 128-dim row, lane q = L & 3 of the row holding dims 32q..32q+31;
+// a wave works on 16 rows and a 256-thread workgroup on 64.  Five Hadamard stages (dims bits
+// 0-4) run in registers, two (dims bits 5, 6 = lane bits 0, 1) through DPP quad_perm.
+constexpr int kRowsPerWG = 64;
+constexpr int kDppXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
 template <int CTRL>
 __device__ __forceinline__ float dppf(float x) {
-    // bound_ctrl with a zero old value: lets the compiler fold the move into the consuming add
+    // bound_ctrl with a zero old value: lets the compiler fold the move into a consuming add
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
 }
-template <int CTRL>
-__device__ __forceinline__ uint32_t dppu(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xf, 0xf, false);
-}
-// Values of lanes L & ~16 and L | 16.
-__device__ __forceinline__ void rows16(float x, float& even, float& odd) {
-    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    even = __uint_as_float(r[0]);
-    odd = __uint_as_float(r[1]);
+
+// Sum of x[k]^2 over the row, associated as an 8-term fma chain per 8 dims followed by an xor
+// butterfly over dims bits 3, 4, 5, 6 (the order is part of the result: every lane of the row
+// gets the same bits, and the same bits as a 16-lanes-per-row butterfly would).
+__device__ __forceinline__ float row_sumsq(const float (&x)[32]) {
+    float s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        s[j] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s[j] = __builtin_fmaf(x[8 * j + k], x[8 * j + k], s[j]);
+    }
+    float t = (s[0] + s[1]) + (s[2] + s[3]);
+    t += dppf<kDppXor1>(t);
+    t += dppf<kDppXor2>(t);
+    return t;
 }
 
-// Sum over the 16 lanes of a row, in the order of an xor butterfly over dims bits 3, 4, 5, 6:
-// every lane of the row gets the same bits.
-__device__ __forceinline__ float row_sum16(float v) {
-    v += dppf<kDppXor1>(v);
-    v += dppf<kDppXor2>(v);
-    v += dppf<kDppXor8>(v);
-    float e, o;
-    rows16(v, e, o);
-    return e + o;
-}
-
-// Normalised Hadamard transform of a row in the lane layout above (dims 8c + k in v[k]):
-// butterflies (u, w) -> (u + w, u - w) over dims bits 0..6, then the scale h.  A cross-lane
-// stage computes partner + s * own with s = -1 in the upper lane (u - w there, exactly), the
-// partner read through DPP or permlane16_swap.
-__device__ __forceinline__ void wht_row(float (&v)[8], int L, float h) {
+// Normalised Hadamard transform of the row (dims 32q + k in v[k]): butterflies
+// (u, w) -> (u + w, u - w) over dims bits 0..6, then the scale h.  A cross-lane stage computes
+// partner + s * own with s = -1 in the upper lane (exactly u - w there).
+__device__ __forceinline__ void wht_row(float (&v)[32], int q, float h) {
 #pragma unroll
-    for (int b = 1; b < 8; b <<= 1) {
+    for (int b = 1; b < 32; b <<= 1) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < 32; ++k) {
             if (!(k & b)) {
                 const float u = v[k], w = v[k | b];
                 v[k] = u + w;
@@ -94,70 +85,41 @@ __device__ __forceinline__ void wht_row(float (&v)[8], int L, float h) {
             }
         }
     }
-    auto stage = [&](auto dpp, float s) {
-        float t[8];
+    const float s0 = (q & 1) ? -1.f : 1.f, s1 = (q & 2) ? -1.f : 1.f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) t[k] = v[k] * s;
+    for (int k = 0; k < 32; ++k) v[k] = dppf<kDppXor1>(v[k]) + v[k] * s0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = dpp(v[k]) + t[k];
-    };
-    stage([](float x) { return dppf<kDppXor1>(x); }, (L & 1) ? -1.f : 1.f);
-    stage([](float x) { return dppf<kDppXor2>(x); }, (L & 2) ? -1.f : 1.f);
-    stage([](float x) { return dppf<kDppXor8>(x); }, (L & 8) ? -1.f : 1.f);
-    const float s4 = (L & 16) ? -1.f : 1.f;
+    for (int k = 0; k < 32; ++k) v[k] = dppf<kDppXor2>(v[k]) + v[k] * s1;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        float e, o;
-        rows16(v[k], e, o);
-        v[k] = __builtin_fmaf(o, s4, e);  // lower lane: e + o, upper lane: e - o
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] *= h;
+    for (int k = 0; k < 32; ++k) v[k] *= h;
 }
 
-// Left searchsorted over NB sorted boundaries (count of boundaries < x; NaN -> NB) through a
-// table of 256 equal cells over [lo, hi] (one cell of margin past the outer boundaries): cell k
-// holds c0 = #{b < edge_k - eps} and the one boundary inside [edge_k - eps, edge_k+1 + eps] (or
-// +inf), so idx = c0 + (b < x) for any x whose computed cell is within eps of its true cell
-// (|x| <= 1 here, the cell arithmetic errs by < 1e-6 * (hi - lo) = eps / 10).  A codebook with two
-// boundaries in one such cell sets `bad` and the kernel counts linearly instead.
-constexpr int kCells = 256;
-struct CellQuant {
-    float inv_w, c;  // cell = trunc(x * inv_w + c)
-};
+// Left searchsorted over NB sorted boundaries (count of boundaries < x) for |x| <= 1 through a
+// table of 256 cells of width 1/128 over [-1, 1] (plus one cell for x = 1): cell k holds
+// c0 = #{b < edge_k - eps} and the one boundary inside [edge_k - eps, edge_k+1 + eps] (or +inf),
+// so idx = c0 + (b < x).  The cell is trunc(128 x + 128), exact to 2^-16 in cell units (eps =
+// 1e-5 is 160 times that).  A codebook with two boundaries in one such cell sets `bad`, and the
+// kernel then counts linearly.  NaN is handled by the caller.
+constexpr int kCells = 257;
 template <int NB>
-__device__ __forceinline__ CellQuant build_cells(const float (&bd)[NB], const float* boundaries, uint2* tab,
-                                                 int* bad) {
-    float span = bd[NB - 1] - bd[0];
-    span = span > 0.f ? span : 1.f;
-    const float lo = bd[0] - span * (1.f / 64.f);
-    const float hi = bd[NB - 1] + span * (1.f / 64.f);
-    const float w = (hi - lo) * (1.f / kCells);
-    const float eps = (hi - lo) * 1e-5f;
+__device__ __forceinline__ void build_cells(const float (&bd)[NB], const float* boundaries, uint2* tab, int* bad) {
+    constexpr float eps = 1e-5f;
     for (int k = threadIdx.x; k < kCells; k += blockDim.x) {
-        const float e0 = lo + (float)k * w - eps, e1 = lo + (float)(k + 1) * w + eps;
+        const float e0 = -1.f + (float)k * (1.f / 128.f) - eps, e1 = -1.f + (float)(k + 1) * (1.f / 128.f) + eps;
         int c0 = 0, c1 = 0;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             c0 += bd[i] < e0 ? 1 : 0;
             c1 += bd[i] <= e1 ? 1 : 0;
         }
-        if (c1 - c0 > 1 || !(w > 0.f)) atomicOr(bad, 1);
+        if (c1 - c0 > 1) atomicOr(bad, 1);
         const float b = c1 > c0 ? boundaries[c0] : __builtin_huge_valf();
         tab[k] = make_uint2(__float_as_uint(b), (uint32_t)c0);
     }
-    CellQuant q;
-    q.inv_w = (float)kCells / (hi - lo);
-    q.c = -lo * q.inv_w;
-    return q;
 }
-template <int NB>
-__device__ __forceinline__ int quant_cell(float x, const CellQuant& q, const uint2* tab) {
-    int cell = (int)__builtin_fmaf(x, q.inv_w, q.c);
-    cell = cell < 0 ? 0 : (cell > kCells - 1 ? kCells - 1 : cell);
-    const uint2 e = tab[cell];
-    const int idx = (int)e.y + (__uint_as_float(e.x) < x ? 1 : 0);
-    return x != x ? NB : idx;  // searchsorted puts NaN last
+__device__ __forceinline__ int quant_cell(float x, const uint2* tab) {
+    const uint2 e = tab[(int)__builtin_fmaf(x, 128.f, 128.f)];
+    return (int)e.y + (__uint_as_float(e.x) < x ? 1 : 0);
 }
 template <int NB>
 __device__ __forceinline__ int quant_linear(float x, const float (&bd)[NB]) {
@@ -167,7 +129,7 @@ __device__ __forceinline__ int quant_linear(float x, const float (&bd)[NB]) {
     return x != x ? NB : cnt;
 }
 
-template <int BITS, bool QJL, int MODE>
+template <int BITS, bool QJL, int MODE, int DT>
 __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
     constexpr int NC = 1 << BITS;
     constexpr int NB = NC - 1;
@@ -181,18 +143,17 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) bd[i] = p.boundaries[i];
     __syncthreads();
-    const CellQuant cq = build_cells<NB>(bd, p.boundaries, s_cells, &s_bad);
+    build_cells<NB>(bd, p.boundaries, s_cells, &s_bad);
     __syncthreads();
     const bool cells = s_bad == 0;
 
-    const int L = threadIdx.x & 63;
-    const int c = lane_dims(L);                                      // dims 8c..8c+7
-    const int row_in_wg = 4 * (int)(threadIdx.x >> 6) + lane_row(L);  // 0..15
+    const int q = threadIdx.x & 3;              // dims 32q..32q+31
+    const int row_in_wg = threadIdx.x >> 2;     // 0..63
 
-    for (int64_t row0 = (int64_t)blockIdx.x * 16; row0 < p.n_rows; row0 += (int64_t)gridDim.x * 16) {
+    for (int64_t row0 = (int64_t)blockIdx.x * kRowsPerWG; row0 < p.n_rows; row0 += (int64_t)gridDim.x * kRowsPerWG) {
         const int64_t row = row0 + row_in_wg;
         const bool row_ok = row < p.n_rows;
-        // Paged rows are head-major so that a workgroup's 16 rows are 16 consecutive tokens.
+        // Paged rows are head-major so that a workgroup's rows are consecutive tokens.
         int64_t tok, head;
         if (MODE == MODE_PAGED) {
             if (p.idx32) {
@@ -209,68 +170,62 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
             tok = row_ok ? row : 0;
         }
 
-        float v[8];
+        float v[32];
         if (row_ok) {
-            tq_load8(p.x, tok * p.x_stride_token + head * p.x_stride_head + 8 * c, p.x_dtype, v);
+            int64_t off;
+            if (p.idx32) off = (uint32_t)tok * (uint32_t)p.x_stride_token + (uint32_t)head * (uint32_t)p.x_stride_head + 32u * q;
+            else off = tok * p.x_stride_token + head * p.x_stride_head + 32 * q;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tq_load8(p.x, off + 8 * i, DT, &v[8 * i]);
         } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = 0.f;
+            for (int k = 0; k < 32; ++k) v[k] = 0.f;
         }
-        if (p.rotate) wht_row(v, L, p.wht_scale);
+        if (p.rotate) wht_row(v, q, p.wht_scale);
 
-        float ss = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ss = __builtin_fmaf(v[k], v[k], ss);
-        ss = row_sum16(ss);
-        const float norm = __builtin_sqrtf(ss);
+        const float norm = __builtin_sqrtf(row_sumsq(v));
         const float den = norm + 1e-8f;
         const float rcp = 1.0f / den;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) v[k] = tq_div_rn(v[k], den, rcp);  // x / (norm + 1e-8)
 
-        int idx[8];
-        float xn[8];
+        int idx[32];
+        // |x| <= 1 unless the norm is not finite (then x may be NaN: searchsorted puts it last)
+        if (cells && !__builtin_amdgcn_ballot_w64(!(norm < __builtin_huge_valf()))) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) xn[k] = tq_div_rn(v[k], den, rcp);
-        if (cells) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) idx[k] = quant_cell<NB>(xn[k], cq, s_cells);
+            for (int k = 0; k < 32; ++k) idx[k] = quant_cell(v[k], s_cells);
         } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) idx[k] = quant_linear<NB>(xn[k], bd);
+            for (int k = 0; k < 32; ++k) idx[k] = quant_linear<NB>(v[k], bd);
         }
 
         float rn = 0.f;
         uint32_t sbits = 0;
-        float cv[8];
-        if (QJL || MODE == MODE_UNPACKED) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) cv[k] = s_cent[idx[k]];
-        }
         if (QJL) {
-            float rs = 0.f;
+            float r[32];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                float r = (xn[k] - cv[k]) * norm;
-                rs = __builtin_fmaf(r, r, rs);
-                sbits |= (r >= 0.f ? 1u : 0u) << k;
+            for (int k = 0; k < 32; ++k) {
+                r[k] = (v[k] - s_cent[idx[k]]) * norm;
+                sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
             }
-            rn = __builtin_sqrtf(row_sum16(rs));
+            rn = __builtin_sqrtf(row_sumsq(r));
         }
 
         if (MODE == MODE_UNPACKED) {
             if (row_ok) {
-                int64_t* ip = p.indices + row * TQ_HEAD_DIM + 8 * c;
-                float* kp = p.k_mse + row * TQ_HEAD_DIM + 8 * c;
+                int64_t* ip = p.indices + row * TQ_HEAD_DIM + 32 * q;
+                float* kp = p.k_mse + row * TQ_HEAD_DIM + 32 * q;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
+                for (int k = 0; k < 32; ++k) {
                     ip[k] = idx[k];
-                    kp[k] = cv[k] * norm;
+                    kp[k] = s_cent[idx[k]] * norm;
                 }
                 if (QJL) {
-                    float* sp = p.signs + row * TQ_HEAD_DIM + 8 * c;
+                    float* sp = p.signs + row * TQ_HEAD_DIM + 32 * q;
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) sp[k] = ((sbits >> k) & 1u) ? 1.f : -1.f;
+                    for (int k = 0; k < 32; ++k) sp[k] = ((sbits >> k) & 1u) ? 1.f : -1.f;
                 }
-                if (c == 0) {
+                if (q == 0) {
                     p.norms[row] = norm;
                     if (QJL) p.rnorm[row] = rn;
                 }
@@ -293,40 +248,26 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
                 r_in_blk = write ? slot - blk * p.block_size : 0;
             }
             uint8_t* tile = p.cache + blk * p.stride_block + head * p.stride_head;
-
-            uint32_t w = 0;
+            // this lane's 32 indices: 4 * BITS bytes of the row's little-endian bit stream
+            uint32_t w[BITS];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) w |= (uint32_t)idx[k] << (BITS * k);
-            uint8_t* irow = tile + r_in_blk * (16 * BITS);
-            // lanes c..c+3 of a row (c % 4 == 0) are one quad: the first lane gathers the others
-            const bool quad0 = (L & 3) == 0;
-            if (BITS == 3) {
-                // 24 bits per lane: the quad's four lanes make 12 aligned bytes.
-                const uint32_t w1 = dppu<0x55>(w), w2 = dppu<0xAA>(w), w3 = dppu<0xFF>(w);
-                if (write && quad0) {
-                    uint32_t* dst = reinterpret_cast<uint32_t*>(irow + 12 * (c >> 2));
-                    dst[0] = w | (w1 << 24);
-                    dst[1] = (w1 >> 8) | (w2 << 16);
-                    dst[2] = (w2 >> 16) | (w3 << 8);
-                }
-            } else if (BITS == 4) {
-                if (write) reinterpret_cast<uint32_t*>(irow)[c] = w;
-            } else if (BITS == 2) {
-                if (write) reinterpret_cast<uint16_t*>(irow)[c] = (uint16_t)w;
-            } else {
-                if (write) irow[c] = (uint8_t)w;
+            for (int j = 0; j < BITS; ++j) w[j] = 0;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) {
+                const int pos = BITS * k, wi = pos >> 5, sh = pos & 31;
+                w[wi] |= (uint32_t)idx[k] << sh;
+                if (sh + BITS > 32) w[wi + 1] |= (uint32_t)idx[k] >> (32 - sh);
             }
-            if (QJL) {
-                const uint32_t s1 = dppu<0x55>(sbits), s2 = dppu<0xAA>(sbits), s3 = dppu<0xFF>(sbits);
-                if (write && quad0) {
-                    uint32_t* dst = reinterpret_cast<uint32_t*>(tile + p.off_signs + r_in_blk * 16 + 4 * (c >> 2));
-                    *dst = sbits | (s1 << 8) | (s2 << 16) | (s3 << 24);
+            uint32_t* irow = reinterpret_cast<uint32_t*>(tile + r_in_blk * (16 * BITS) + 4 * BITS * q);
+            if (write) {
+#pragma unroll
+                for (int j = 0; j < BITS; ++j) irow[j] = w[j];
+                if (QJL) *reinterpret_cast<uint32_t*>(tile + p.off_signs + r_in_blk * 16 + 4 * q) = sbits;
+                if (q == 0) {
+                    reinterpret_cast<uint16_t*>(tile + p.off_norm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(norm);
+                    if (QJL)
+                        reinterpret_cast<uint16_t*>(tile + p.off_rnorm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(rn);
                 }
-            }
-            if (write && c == 0) {
-                reinterpret_cast<uint16_t*>(tile + p.off_norm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(norm);
-                if (QJL)
-                    reinterpret_cast<uint16_t*>(tile + p.off_rnorm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(rn);
             }
         }
     }
@@ -335,11 +276,16 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
 template <int MODE>
 int launch_compress(const CompressParams& p, int bits, int qjl, hipStream_t stream) {
     if (p.n_rows <= 0) return TQ_OK;
-    // Workgroups loop over 16-row groups; 2048 of them (8 per CU) amortise the LDS set-up.
-    int64_t groups = (p.n_rows + 15) / 16;
+    // Workgroups loop over 64-row groups; 2048 of them (8 per CU) amortise the LDS set-up.
+    int64_t groups = (p.n_rows + kRowsPerWG - 1) / kRowsPerWG;
     int grid = (int)(groups < 2048 ? groups : 2048);
-#define TQ_LAUNCH(B, Q)                                                                     \
-    hipLaunchKernelGGL((compress_kernel<B, Q, MODE>), dim3(grid), dim3(256), 0, stream, p)
+#define TQ_LAUNCH_DT(B, Q, DT) hipLaunchKernelGGL((compress_kernel<B, Q, MODE, DT>), dim3(grid), dim3(256), 0, stream, p)
+#define TQ_LAUNCH(B, Q)                                   \
+    do {                                                  \
+        if (p.x_dtype == TQ_BF16) TQ_LAUNCH_DT(B, Q, TQ_BF16); \
+        else if (p.x_dtype == TQ_F16) TQ_LAUNCH_DT(B, Q, TQ_F16); \
+        else TQ_LAUNCH_DT(B, Q, TQ_F32);                  \
+    } while (0)
     switch (bits * 2 + (qjl ? 1 : 0)) {
         case 2: TQ_LAUNCH(1, false); break;
         case 3: TQ_LAUNCH(1, true); break;
@@ -352,6 +298,7 @@ int launch_compress(const CompressParams& p, int bits, int qjl, hipStream_t stre
         default: return TQ_ERR_BITS;
     }
 #undef TQ_LAUNCH
+#undef TQ_LAUNCH_DT
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TQ_OK : (int)e;
 }
@@ -397,6 +344,7 @@ extern "C" int tq_polarquant_compress(const void* x, int x_dtype, int64_t x_row_
     p.k_mse = k_mse;
     p.signs = signs;
     p.rnorm = rnorm;
+    p.idx32 = (n_rows * x_row_stride < (1ll << 31)) ? 1 : 0;
     return launch_compress<MODE_UNPACKED>(p, bits, use_qjl, (hipStream_t)stream);
 }
 
@@ -460,6 +408,10 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
     p.off_signs = g.off_signs;
     p.off_norm = g.off_norm;
     p.off_rnorm = g.off_rnorm;
-    p.idx32 = (p.n_rows < (1ll << 31) && num_blocks * (int64_t)block_size < (1ll << 31)) ? 1 : 0;
+    // rows, slots and x element offsets all below 2^31
+    p.idx32 = (p.n_rows < (1ll << 31) && num_blocks * (int64_t)block_size < (1ll << 31) &&
+               num_tokens * x_stride_token + (int64_t)num_heads * x_stride_head < (1ll << 31))
+                  ? 1
+                  : 0;
     return launch_compress<MODE_PAGED>(p, bits, use_qjl, (hipStream_t)stream);
 }
