@@ -313,3 +313,59 @@ def test_config2_full_size_roundtrip(dev):
     want_norm = ref["norms"].numpy().astype(np.float16).astype(np.float32)
     np.testing.assert_allclose(got_norm, want_norm, rtol=NORM_RTOL, atol=NORM_ATOL)
     assert np.mean(got_norm == want_norm) > 0.999
+
+
+def _quantizer_probe_rows(values):
+    """Rows [t, c, 0, ...] with c = sqrt(1 - t^2) in fp32: the row norm is 1 (or within an ulp),
+    so x / (norm + 1e-8) lands on t itself when the norm rounds to 1."""
+    t = np.asarray(values, dtype=np.float32)
+    c = np.sqrt(np.maximum(0.0, 1.0 - t.astype(np.float64) ** 2)).astype(np.float32)
+    x = np.zeros((t.size, 128), dtype=np.float32)
+    x[:, 0] = t
+    x[:, 1] = c
+    return x
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_searchsorted_at_boundaries_and_cell_edges(dev, bits):
+    """Index of values exactly on every boundary, one fp32 ulp either side of it, on the edges of
+    the kernel's 1/128-wide lookup cells and their neighbours, and at 0 and +-1, against
+    np.searchsorted (left) of the same fp32 quotient."""
+    from turboquant.core import PolarQuantConfig, polarquant_compress
+    cent, bnd = _codebook(bits)
+    b = bnd.numpy().astype(np.float32)
+    edges = (-1.0 + np.arange(257, dtype=np.float64) / 128.0).astype(np.float32)
+    vals = []
+    for v in np.concatenate([b, edges, np.float32([0.0, 0.5, -0.5])]):
+        vals += [v, np.nextafter(v, np.float32(np.inf)), np.nextafter(v, np.float32(-np.inf))]
+    vals = np.asarray([v for v in vals if abs(v) <= 1.0], dtype=np.float32)
+    x = torch.from_numpy(_quantizer_probe_rows(vals))
+    cfg = PolarQuantConfig(head_dim=128, bits=bits, use_qjl=False)
+    res = polarquant_compress(x.to(dev), cent.to(dev), bnd.to(dev), cfg, None)
+    norms = res["norms"].cpu().numpy().astype(np.float32)
+    assert (norms == np.float32(1.0)).mean() > 0.5, "probe rows should mostly have norm exactly 1"
+    xn = vals / (norms + np.float32(1e-8))                     # fp32, correctly rounded
+    want = np.searchsorted(b, xn, side="left")
+    got = res["indices"].cpu().numpy()[:, 0]
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"bits {bits}: x={xn[bad[:5]]} got {got[bad[:5]]} want {want[bad[:5]]}"
+
+
+def test_searchsorted_close_boundaries_fallback(dev):
+    """A codebook with two boundaries 1e-4 apart (inside one lookup cell) still quantizes exactly
+    (the kernel counts linearly for such codebooks)."""
+    from turboquant.core import PolarQuantConfig, polarquant_compress
+    bnd = torch.tensor([-0.3, -0.05, 0.0, 1e-4, 0.02, 0.1, 0.4], dtype=torch.float32)
+    cent = torch.tensor([-0.5, -0.2, -0.02, 5e-5, 0.01, 0.05, 0.2, 0.6], dtype=torch.float32)
+    vals = []
+    for v in np.concatenate([bnd.numpy(), np.float32([0.0, 5e-5, -1.0, 1.0, 0.99])]):
+        vals += [v, np.nextafter(v, np.float32(np.inf)), np.nextafter(v, np.float32(-np.inf))]
+    vals = np.asarray([v for v in vals if abs(v) <= 1.0], dtype=np.float32)
+    x = torch.from_numpy(_quantizer_probe_rows(vals))
+    cfg = PolarQuantConfig(head_dim=128, bits=3, use_qjl=False)
+    res = polarquant_compress(x.to(dev), cent.to(dev), bnd.to(dev), cfg, None)
+    norms = res["norms"].cpu().numpy().astype(np.float32)
+    xn = vals / (norms + np.float32(1e-8))
+    want = np.searchsorted(bnd.numpy(), xn, side="left")
+    got = res["indices"].cpu().numpy()[:, 0]
+    np.testing.assert_array_equal(got, want)
