@@ -799,12 +799,6 @@ bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block
     auto span_ok = [&](const tq_region& r) {
         return r.stride_block > 0 && r.stride_block < (1ll << 30) && num_blocks * r.stride_block < (1ll << 31) - (1ll << 16);
     };
-    // 16-byte aligned regions and strides: a tile is fetched in 16-byte chunks
-    auto al16 = [](const tq_region& r) {
-        return (reinterpret_cast<uintptr_t>(r.ptr) & 15) == 0 && (r.stride_block & 15) == 0 && (r.stride_head & 15) == 0;
-    };
-    if (!al16(k->idx) || !al16(k->norm) || !al16(v->idx) || !al16(v->norm)) return false;
-    if (k->qjl && (!al16(k->signs) || !al16(k->rnorm))) return false;
     return span_ok(k->idx) && span_ok(v->idx);
 }
 
@@ -828,22 +822,18 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     if (!kern) return TQ_ERR_BITS;
     const int share = (share_codebook && k_bits == v_bits) ? 1 : 0;
     size_t lds = lds_bytes(k_bits, v_bits, share);
-    int nw = 4;  // units (waves) per workgroup
     if (norm_row_bytes == 2 && group <= 8 && fast_path_enabled()) {
         // the paged fast path (library tile layout)
-        FastPlan pl;
-        const int rc = tq_decode_fast_plan(k_bits, k_qjl != 0, v_bits, share != 0, false, &pl);
-        if (rc) return rc;
-        kern = pl.kern;
-        lds = pl.lds;
-        nw = pl.nw;
+        kern = tq_decode_fast_kernel_ptr(k_bits, k_qjl != 0, v_bits);
+        uint32_t a, b, c;
+        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &a, &b, &c, &lds);
     }
     int blocks = 0, dev = 0, cus = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * nw, lds);
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds);
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return (int)e;
-    *units = blocks * nw * cus;
+    *units = blocks * 4 * cus;  // 4 units (waves) per 256-thread workgroup
     return TQ_OK;
 }
 
@@ -943,14 +933,8 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         f.k_cscale = k_cscale;
         f.v_cscale = v_cscale;
         f.v_cinv = 1.f / v_cscale;
-        FastPlan pl;
-        const bool want_stats = sparse_threshold > 0.f && skip_stats != nullptr;
-        const int prc = tq_decode_fast_plan(k->bits, k->qjl != 0, v->bits, share, want_stats, &pl);
-        if (prc) return prc;
-        f.lds_sign = pl.lds_sign;
-        f.lds_k = pl.lds_k;
-        f.lds_v = pl.lds_v;
-        f.lds_stage = pl.lds_stage;
+        size_t lds_total = 0;
+        tq_decode_fast_lds_layout(k->bits, k->qjl != 0, v->bits, share, &f.lds_sign, &f.lds_k, &f.lds_v, &lds_total);
         f.block_size = block_size;
         int tsh = 0;
         while ((16 << tsh) < block_size) ++tsh;
@@ -975,9 +959,9 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         f.out_ss = out_stride_seq;
         f.out_sh = out_stride_head;
         const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
-        const int64_t grid = (units + pl.nw - 1) / pl.nw;
+        const int64_t grid = (units + 3) / 4;
         if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
-        int frc = tq_decode_fast_launch(f, pl, grid, (hipStream_t)stream);
+        int frc = tq_decode_fast_launch(f, k->bits, k->qjl != 0, v->bits, grid, lds_total, (hipStream_t)stream);
         if (frc) return frc;
         return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
                              max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq,

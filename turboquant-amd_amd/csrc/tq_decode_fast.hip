@@ -37,8 +37,6 @@
 // Sparse-V (kernels/sparse_v.py:108-149): for tile X, m_X = running max through tile X; token t
 // is dropped from PV when no head of the group has exp2(c (s - m_X)) > threshold, tested as
 // s > m_X + log2(threshold)/c with a ballot; dropped tokens stay in the denominator.
-#include <cstdlib>
-
 #include "tq_common.h"
 #include "tq_decode_internal.h"
 
@@ -84,29 +82,20 @@ __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
 // 2- and 3-bit indices are looked up four at a time (a 4B-bit field -> 4 fp16 centroids, one
 // 8-byte entry) instead of in pairs.  3 bits: 4096 entries, not replicated (32 KB); 2 bits: 256
 // entries x 16 bank replicas, entry stride 128 bytes (32 KB).
-#ifndef TQ_FAST_VQUAD
-#define TQ_FAST_VQUAD 1
-#endif
 template <int B>
 constexpr bool quad_table() {
     return TQ_FAST_QUAD && (B == 3 || B == 2);
-}
-// V lookups use a quad table too (else pair tables, conflict-free but twice the lookups).
-template <int B>
-constexpr bool vquad_table() {
-    return quad_table<B>() && TQ_FAST_VQUAD;
 }
 // Bit position of the field in a quad table address (log2 of the entry stride).
 template <int B>
 constexpr int quad_shift() {
     return B == 2 ? 7 : 3;
 }
-// Replicas of the fp4 sign table (fewer when a quad table or the staging ring takes the LDS).
-template <int KB, int VB, int NW>
+// Replicas of the fp4 sign table (fewer when a quad table takes the LDS).
+template <int KB, int VB>
 constexpr int sign_replicas() {
-    return NW > 4 ? 4 : ((quad_table<KB>() || vquad_table<VB>()) ? 16 : 32);
+    return (quad_table<KB>() || quad_table<VB>()) ? 16 : 32;
 }
-constexpr int ilog2c(int x) { return x <= 1 ? 0 : 1 + ilog2c(x >> 1); }
 
 __device__ __forceinline__ uint32_t pick_halves(uint32_t hi_src, uint32_t lo_src, int s) {
     return __builtin_amdgcn_perm(hi_src, lo_src, s ? 0x07060302u : 0x05040100u);
@@ -204,7 +193,7 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
 
 template <int SREP>
 __device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, const LaneCtx& c) {
-    constexpr int P = 2 + ilog2c(SREP);  // entry stride: SREP replicas x 4 bytes
+    constexpr int P = SREP == 32 ? 7 : 6;  // entry stride: SREP replicas x 4 bytes
     const uint32_t w[1] = {ks};
     tq_i32x8 a;
 #pragma unroll
@@ -228,7 +217,7 @@ __device__ __forceinline__ uint64_t row_mask(int nvA, int nvB, int r) {
 }
 
 // One pair of tiles.
-template <int KB, bool KQJL, int VB, bool COUNT, int NW>
+template <int KB, bool KQJL, int VB, bool COUNT>
 __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRaw& vr, const PairInfo& pi,
                                              Softmax& st, const LaneCtx& c, const FastDecodeParams& p) {
     // ---------------- scores ----------------
@@ -236,8 +225,8 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     const tq_floatx4 sB = qk_tile<KB>(kr.kwB, c);
     tq_floatx4 tA = {0.f, 0.f, 0.f, 0.f}, tB = {0.f, 0.f, 0.f, 0.f};
     if (KQJL) {
-        tA = qjl_tile<sign_replicas<KB, VB, NW>()>(kr.ksA, c);
-        tB = qjl_tile<sign_replicas<KB, VB, NW>()>(kr.ksB, c);
+        tA = qjl_tile<sign_replicas<KB, VB>()>(kr.ksA, c);
+        tB = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, c);
     }
     uint64_t rm[4];
     // Rows past the end may hold any bits in a paged block: masked out of the scores, and their
@@ -330,7 +319,7 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
                 __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, aw), bop, st.acc[2 * q + hs], 0, 0, 0);
         }
     };
-    if (vquad_table<VB>()) {
+    if (quad_table<VB>()) {
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
             // dims 8n + 4qh .. 8n + 4qh + 3 of each token: one quad -> pairs q = 2qh, 2qh + 1
@@ -363,74 +352,25 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     }
 }
 
-// Waves per SIMD (register budget 512 / waves): QJL keys need the fp8 q_proj operands.  A
-// staged workgroup (NW > 4 waves, one per CU) runs NW / 4 waves per SIMD.
-template <int KB, bool KQJL, int VB, int NW>
-constexpr int fast_waves() {
-    return NW > 4 ? NW / 4 : (TQ_FAST_WAVES > 0 ? TQ_FAST_WAVES : (KQJL ? 3 : 4));
-}
-
-// ---- LDS staging (NW > 4) ----
-// A staged workgroup fills one LDS copy of the tables for all its NW waves, and each wave owns a
-// ring of two pair slots that direct-to-LDS buffer loads fill one pair ahead: 16 bytes per lane
-// per instruction (buffer_load_dwordx4 ... lds writes lane l's 16 bytes at M0 + 16 l), so a
-// 16-token tile arrives in one or two instructions and no VGPRs hold data in flight.  Slot:
-// [K tile A][K tile B][V tile A][V tile B]; a K tile is [idx 256 KB][signs 256 (QJL)]
-// [norms 32][residual norms 32 (QJL)], a V tile [idx 256 VB][norms 32].
+// Waves per SIMD (register budget 512 / waves): QJL keys need the fp8 q_proj operands.
 template <int KB, bool KQJL, int VB>
-struct Stage {
-    static constexpr uint32_t KT = 256u * KB + (KQJL ? 320u : 32u);
-    static constexpr uint32_t VT = 256u * VB + 32u;
-    static constexpr uint32_t PAIR = 2 * KT + 2 * VT;
-    static constexpr int KCH = (int)(KT / 16), VCH = (int)(VT / 16);  // 16-byte chunks
-    static constexpr int KI = (KCH + 63) / 64, VI = (VCH + 63) / 64;  // instructions per tile
-    static constexpr int NDMA = 2 * (KI + VI);                         // instructions per pair
-    static_assert(KI <= 2 && VI <= 2, "a tile is at most 128 chunks");
-    static constexpr uint64_t mask(int chunks, int j) {
-        return chunks - 64 * j >= 64 ? ~0ull : ((1ull << (chunks - 64 * j)) - 1ull);
-    }
-};
-
-// One direct-to-LDS load of 16 bytes per active lane.  M0 is written right before the load
-// (one wait state between them); lanes outside `mask` are switched off for this instruction
-// only.  Counted by vmcnt like any vector load, and waited for explicitly (wait_vm).
-template <uint64_t MASK>
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff, uint32_t m0) {
-    if constexpr (MASK == ~0ull) {
-        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                     :
-                     : "s"(m0), "v"(voff), "s"(rs), "s"(soff)
-                     : "memory", "m0");
-    } else {
-        uint64_t saved;
-        asm volatile(
-            "s_mov_b64 %0, exec\n\ts_mov_b64 exec, %5\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
-            "buffer_load_dwordx4 %2, %3, %4 offen lds\n\ts_mov_b64 exec, %0"
-            : "=&s"(saved)
-            : "s"(m0), "v"(voff), "s"(rs), "s"(soff), "s"(MASK)
-            : "memory", "m0");
-    }
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+constexpr int fast_waves() {
+    return TQ_FAST_WAVES > 0 ? TQ_FAST_WAVES : (KQJL ? 3 : 4);
 }
 
 // COUNT: Sparse-V skip statistics requested (a separate instance keeps the counting off the
-// common path).  NW: waves per workgroup (4: loads into registers, 12 or 16: LDS staging).
-template <int KB, bool KQJL, int VB, bool COUNT, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB, NW>(),
-                                                                         fast_waves<KB, KQJL, VB, NW>())))
+// common path).
+template <int KB, bool KQJL, int VB, bool COUNT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
+                                                                     fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
     extern __shared__ uint32_t s_lds[];
-    constexpr int NT = 64 * NW;
-    constexpr bool STAGED = NW > 4;
-    // Tables: fp4 sign table (QJL), K table, V table, at the byte offsets chosen by the host
-    // (multiples of each table's size).
-    constexpr int SREP = sign_replicas<KB, VB, NW>();
+    // Tables (32 bank replicas each): fp4 sign table (QJL), K pair table, V pair table, at the
+    // byte offsets chosen by the host (multiples of each table's size).
+    constexpr int SREP = sign_replicas<KB, VB>();
     if (KQJL) {
         uint32_t* t = s_lds + p.lds_sign / 4;
-        for (int i = threadIdx.x; i < 256 * SREP; i += NT) {
+        for (int i = threadIdx.x; i < 256 * SREP; i += 256) {
             const uint32_t e = (uint32_t)i / SREP;
             uint32_t w = 0;
 #pragma unroll
@@ -444,25 +384,25 @@ void decode_fast_kernel(FastDecodeParams p) {
         uint32_t* t = s_lds + off / 4;
         const int mask = (1 << bits) - 1;
         if (quad && bits == 3) {
-            for (int i = threadIdx.x; i < 4096 * 2; i += NT) {
+            for (int i = threadIdx.x; i < 4096 * 2; i += 256) {
                 const int e = i >> 1, j0 = 2 * (i & 1);
                 t[i] = tq_pack_half2(cent[(e >> (3 * j0)) & 7] * cs, cent[(e >> (3 * j0 + 3)) & 7] * cs);
             }
         } else if (quad) {
-            for (int i = threadIdx.x; i < 256 * 16 * 2; i += NT) {
+            for (int i = threadIdx.x; i < 256 * 16 * 2; i += 256) {
                 const int e = i >> 5, j0 = 2 * (i & 1);
                 t[i] = tq_pack_half2(cent[(e >> (2 * j0)) & 3] * cs, cent[(e >> (2 * j0 + 2)) & 3] * cs);
             }
         } else {
             const int ent = 1 << (2 * bits);
-            for (int i = threadIdx.x; i < ent * 32; i += NT) {
+            for (int i = threadIdx.x; i < ent * 32; i += 256) {
                 const int e = i >> 5;
                 t[i] = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
             }
         }
     };
     fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>());
-    if (p.lds_v != p.lds_k) fill(p.lds_v, p.v_cent, p.v_cscale, VB, vquad_table<VB>());
+    if (p.lds_v != p.lds_k) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>());
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
@@ -476,19 +416,18 @@ void decode_fast_kernel(FastDecodeParams p) {
     const uint32_t bank8 = 8u * (uint32_t)(lane & 15);  // 2-bit quad tables: 16 replicas of 8 bytes
     c.kbank = lds0 + p.lds_k + (KB == 2 && quad_table<KB>() ? bank8 : bank4);
     c.vbank = lds0 + p.lds_v + bank4;
-    c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (SREP - 1));
+    c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
     // V quad table: address 0 when it is the K quad table, else its base from a VGPR (a VALU
     // op takes one scalar operand, and the field mask is one)
     c.vquad = lds0 + p.lds_v;
     if (VB == 2) c.vquad += bank8;
-    else if (vquad_table<VB>() && !(quad_table<KB>() && KB == 3 && p.lds_v == 0))
-        asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
+    else if (!(quad_table<KB>() && KB == 3 && p.lds_v == 0)) asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
     c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // Units in (sequence, chunk, KV head) order: the four waves of a workgroup get the same
     // chunk of one sequence (equal work).
-    const int64_t unit = (int64_t)blockIdx.x * NW + wave;
+    const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
     const int kh = (int)(unit % p.hkv);
     const int64_t sc_ = unit / p.hkv;
     const int ci = (int)(sc_ % p.n_chunks);
@@ -702,179 +641,22 @@ void decode_fast_kernel(FastDecodeParams p) {
 
     const int ntiles = (t_end - t_begin + 15) >> 4;
     const int npairs = (ntiles + 1) >> 1;
-    if constexpr (STAGED) {
-        using S = Stage<KB, KQJL, VB>;
-        // Per-lane source offset of chunk (64 j + lane) of a tile whose first row is r0 of its
-        // block: base + r0 * mult, relative to the block's index region.
-        uint32_t kbo[S::KI], kmu[S::KI], vbo[S::VI], vmu[S::VI];
-#pragma unroll
-        for (int j = 0; j < S::KI; ++j) {
-            int ch = 64 * j + lane;
-            uint32_t b = 0, m = 0;
-            if (ch < 16 * KB) {
-                b = 16u * ch, m = 16u * KB;
-            } else {
-                ch -= 16 * KB;
-                if (KQJL && ch < 16) {
-                    b = p.d_ksig + 16u * ch, m = 16u;
-                } else {
-                    ch -= KQJL ? 16 : 0;
-                    if (ch < 2) b = p.d_kn + 16u * ch, m = 2u;
-                    else if (KQJL && ch < 4) b = p.d_krn + 16u * (ch - 2), m = 2u;
-                }
-            }
-            kbo[j] = b;
-            kmu[j] = m;
-        }
-#pragma unroll
-        for (int j = 0; j < S::VI; ++j) {
-            const int ch = 64 * j + lane;
-            uint32_t b = 0, m = 0;
-            if (ch < 16 * VB) b = 16u * ch, m = 16u * VB;
-            else if (ch < 16 * VB + 2) b = p.d_vn + 16u * (ch - 16 * VB), m = 2u;
-            vbo[j] = b;
-            vmu[j] = m;
-        }
-        const uint32_t stage = lds0 + p.lds_stage + (uint32_t)wave * 2u * S::PAIR;
-        // block numbers through the scalar cache: no compiler-issued vector load may sit between
-        // the staged loads and their waits
-        typedef __attribute__((address_space(4))) const int32_t bt_s;
-        const bt_s* bts = (const bt_s*)(uintptr_t)bt_row;
-        auto blocks_of = [&](int pi, int (&blk)[2]) {
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-                int lb = (tile0 + 2 * pi + x) >> p.tile_shift;
-                lb = lb < nblk_seq ? lb : nblk_seq - 1;
-                blk[x] = bts[lb];
-            }
-        };
-        // Stage pair pi into slot k (its blocks in blk); fills info.
-        auto issue = [&](int pi, const uint32_t k, PairInfo& info, const int (&blk)[2]) {
-            int nv[2];
-            uint32_t r0[2], kso[2], vso[2];
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-                const int t0 = t_begin + 16 * (2 * pi + x);
-                int nvr = t_end - t0;
-                nvr = nvr < 0 ? 0 : (nvr > 16 ? 16 : nvr);
-                int bk = blk[x];
-                if (bk < 0 || (int64_t)bk >= p.num_blocks) {  // unreadable entry: read block 0, mask it
-                    bk = 0;
-                    nvr = 0;
-                }
-                nv[x] = nvr;
-                r0[x] = (uint32_t)(((tile0 + 2 * pi + x) & tmask) << 4);
-                kso[x] = (uint32_t)bk * p.k_sb;
-                vso[x] = (uint32_t)bk * p.v_sb;
-            }
-            info.nvA = nv[0];
-            info.nvB = nv[1];
-            // the slot's previous pair has been read (its LDS reads are complete)
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            const uint32_t sb = stage + k * S::PAIR;
-            // (at most two instructions per tile: 16-byte chunks <= 128)
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-                dma16<S::mask(S::KCH, 0)>(rk, kbo[0] + r0[x] * kmu[0], kso[x], sb + x * S::KT);
-                if constexpr (S::KI > 1)
-                    dma16<S::mask(S::KCH, 1)>(rk, kbo[S::KI - 1] + r0[x] * kmu[S::KI - 1], kso[x], sb + x * S::KT + 1024u);
-            }
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-                dma16<S::mask(S::VCH, 0)>(rv, vbo[0] + r0[x] * vmu[0], vso[x], sb + 2 * S::KT + x * S::VT);
-                if constexpr (S::VI > 1)
-                    dma16<S::mask(S::VCH, 1)>(rv, vbo[S::VI - 1] + r0[x] * vmu[S::VI - 1], vso[x],
-                                              sb + 2 * S::KT + x * S::VT + 1024u);
-            }
-        };
-        // LDS addresses of this lane's operands in slot 0 (slot 1: + PAIR)
-        const uint32_t a_kidx = stage + o_kidx;
-        const uint32_t a_ksig = stage + 256u * KB + o_ksig;
-        const uint32_t a_kn = stage + (c.lo8 ? 0u : S::KT) + 256u * KB + (KQJL ? 256u : 0u) + 8u * (uint32_t)g;
-        const uint32_t vsh = 8u * (((uint32_t)VB * (uint32_t)n) & 3u);  // bit offset of the lane's fields
-        const uint32_t a_vidx = stage + 2 * S::KT + (uint32_t)(64 * g * VB) + 4u * (((uint32_t)VB * (uint32_t)n) >> 2);
-        const uint32_t a_vn = stage + 2 * S::KT + (c.lo8 ? 0u : S::VT) + 256u * VB + 8u * (uint32_t)g;
-        auto read_pair = [&](const uint32_t k, KRaw<KB, KQJL>& kr, VRaw& vr) {
-            const uint32_t o = k * S::PAIR;
-#pragma unroll
-            for (int w = 0; w < KB; ++w) {
-                kr.kwA[w] = lds_read(a_kidx + o + 4u * w);
-                kr.kwB[w] = lds_read(a_kidx + o + S::KT + 4u * w);
-            }
-            if (KQJL) {
-                kr.ksA = lds_read(a_ksig + o);
-                kr.ksB = lds_read(a_ksig + o + S::KT);
-            }
-            const tq_u32x2 kn = lds_read2(a_kn + o);
-            kr.kn[0] = kn[0];
-            kr.kn[1] = kn[1];
-            if (KQJL) {
-                const tq_u32x2 krn = lds_read2(a_kn + o + 32u);
-                kr.krn[0] = krn[0];
-                kr.krn[1] = krn[1];
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t ra = a_vidx + o + (uint32_t)(r * 16 * VB);
-                if (VB == 3) {
-                    vr.vwA[r] = __builtin_amdgcn_alignbit(lds_read(ra + 4u), lds_read(ra), vsh);
-                    vr.vwB[r] = __builtin_amdgcn_alignbit(lds_read(ra + S::VT + 4u), lds_read(ra + S::VT), vsh);
-                } else {
-                    vr.vwA[r] = lds_read(ra) >> vsh;
-                    vr.vwB[r] = lds_read(ra + S::VT) >> vsh;
-                }
-            }
-            const tq_u32x2 vn = lds_read2(a_vn + o);
-            vr.vn[0] = vn[0];
-            vr.vn[1] = vn[1];
-        };
-
-        // Pairs past the end (the last odd one) are staged from readable blocks and masked.
-        PairInfo info[2];
-        int blk[2];
-        blocks_of(0, blk);
-        issue(0, 0u, info[0], blk);
-        blocks_of(1, blk);
-        for (int i = 0; i < npairs; i += 2) {
-            issue(i + 1, 1u, info[1], blk);
-            blocks_of(i + 2, blk);
-            wait_vm<S::NDMA>();  // pair i has landed
-            {
-                KRaw<KB, KQJL> kr;
-                VRaw vr;
-                read_pair(0u, kr, vr);
-                compute_pair<KB, KQJL, VB, COUNT, NW>(kr, vr, info[0], st, c, p);
-            }
-            if (i + 1 >= npairs) break;
-            issue(i + 2, 0u, info[0], blk);
-            blocks_of(i + 3, blk);
-            wait_vm<S::NDMA>();
-            {
-                KRaw<KB, KQJL> kr;
-                VRaw vr;
-                read_pair(1u, kr, vr);
-                compute_pair<KB, KQJL, VB, COUNT, NW>(kr, vr, info[1], st, c, p);
-            }
-        }
-        wait_vm<0>();
-    } else {
-        // All data of a pair is loaded one pair ahead (two register sets).  Pairs past the end
-        // read block data that is never used (every fetch issues the same loads, which keeps the
-        // compiler's outstanding-load counts exact).
-        KRaw<KB, KQJL> kr[2];
-        PairInfo info[2];
-        VRaw vr[2];
-        fetch_k(0, kr[0], info[0]);
+    // All data of a pair is loaded one pair ahead (two register sets).  Pairs past the end read
+    // block data that is never used (every fetch issues the same loads, which keeps the
+    // compiler's outstanding-load counts exact).
+    KRaw<KB, KQJL> kr[2];
+    PairInfo info[2];
+    VRaw vr[2];
+    fetch_k(0, kr[0], info[0]);
+    load_v(info[0], vr[0]);
+    for (int i = 0; i < npairs; i += 2) {
+        fetch_k(i + 1, kr[1], info[1]);
+        load_v(info[1], vr[1]);
+        compute_pair<KB, KQJL, VB, COUNT>(kr[0], vr[0], info[0], st, c, p);
+        if (i + 1 >= npairs) break;
+        fetch_k(i + 2, kr[0], info[0]);
         load_v(info[0], vr[0]);
-        for (int i = 0; i < npairs; i += 2) {
-            fetch_k(i + 1, kr[1], info[1]);
-            load_v(info[1], vr[1]);
-            compute_pair<KB, KQJL, VB, COUNT, NW>(kr[0], vr[0], info[0], st, c, p);
-            if (i + 1 >= npairs) break;
-            fetch_k(i + 2, kr[0], info[0]);
-            load_v(info[0], vr[0]);
-            compute_pair<KB, KQJL, VB, COUNT, NW>(kr[1], vr[1], info[1], st, c, p);
-        }
+        compute_pair<KB, KQJL, VB, COUNT>(kr[1], vr[1], info[1], st, c, p);
     }
 
     // ---- combine the lane groups and the two tile halves ----
@@ -917,38 +699,30 @@ void decode_fast_kernel(FastDecodeParams p) {
 
 }  // namespace
 
-namespace {
-
-const void* kernel_ptr(int kb, bool kq, int vb, bool count, int nw) {
-#define TQ_FP_N(KB, KQ, VB, NW) \
-    if (nw == NW) return count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, NW> : (const void*)decode_fast_kernel<KB, KQ, VB, false, NW>;
-#define TQ_FP(KB, KQ, VB)                                      \
-    if (kb == KB && kq == KQ && vb == VB) {                    \
-        TQ_FP_N(KB, KQ, VB, 4) TQ_FP_N(KB, KQ, VB, 12) TQ_FP_N(KB, KQ, VB, 16) return nullptr; \
-    }
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count) {
+#define TQ_FP(KB, KQ, VB)                                                                              \
+    if (kb == KB && kq == KQ && vb == VB)                                                              \
+        return count ? (const void*)decode_fast_kernel<KB, KQ, VB, true> : (const void*)decode_fast_kernel<KB, KQ, VB, false>;
 #define TQ_FP_V(KB, KQ) TQ_FP(KB, KQ, 2) TQ_FP(KB, KQ, 3) TQ_FP(KB, KQ, 4)
     TQ_FP_V(2, false) TQ_FP_V(2, true) TQ_FP_V(3, false) TQ_FP_V(3, true) TQ_FP_V(4, false) TQ_FP_V(4, true)
 #undef TQ_FP_V
 #undef TQ_FP
-#undef TQ_FP_N
     return nullptr;
 }
 
-// Table offsets (largest first, each at a multiple of its size; a 3-bit K quad table at 0),
-// then the staging ring (NW > 4: NW waves x 2 pair slots).
-void lds_layout(int kb, bool kq, int vb, bool share, int nw, FastPlan* pl) {
+void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
+                               uint32_t* lds_v, size_t* total) {
+    // Tables at offsets that are multiples of their sizes: largest first.
     struct T {
         size_t size;
         uint32_t* off;
     } t[3];
     int n = 0;
     uint32_t dummy = 0;
-    const bool kquad = TQ_FAST_QUAD && (kb == 3 || kb == 2), vquad = TQ_FAST_QUAD && TQ_FAST_VQUAD && (vb == 3 || vb == 2);
-    share = share && kquad == vquad;  // one table serves both only when it has one form
-    const int srep = nw > 4 ? 4 : ((kquad || vquad) ? 16 : 32);
-    t[n++] = {kq ? (size_t)256 * 4 * srep : 0, &pl->lds_sign};
-    t[n++] = {kquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * kb)) * 128, &pl->lds_k};
-    t[n++] = {share ? 0 : (vquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * vb)) * 128), share ? &dummy : &pl->lds_v};
+    const bool kquad = TQ_FAST_QUAD && (kb == 3 || kb == 2), vquad = TQ_FAST_QUAD && (vb == 3 || vb == 2);
+    t[n++] = {kq ? (size_t)256 * 4 * ((kquad || vquad) ? 16 : 32) : 0, lds_sign};
+    t[n++] = {kquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * kb)) * 128, lds_k};
+    t[n++] = {share ? 0 : (vquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * vb)) * 128), share ? &dummy : lds_v};
     for (int i = 0; i < n; ++i)
         for (int j = i + 1; j < n; ++j)
             if (t[j].size > t[i].size) {
@@ -956,65 +730,32 @@ void lds_layout(int kb, bool kq, int vb, bool share, int nw, FastPlan* pl) {
                 t[i] = t[j];
                 t[j] = x;
             }
+    // A 3-bit K quad table goes first: the kernel addresses it from LDS address 0.
     if (kquad && kb == 3)
         for (int i = 1; i < n; ++i)
-            if (t[i].off == &pl->lds_k) {
+            if (t[i].off == lds_k) {
                 T x = t[0];
                 t[0] = t[i];
                 t[i] = x;
             }
     size_t off = 0;
     for (int i = 0; i < n; ++i) {
+        // each table at a multiple of its size (pair tables are addressed by OR)
         if (t[i].size) off = (off + t[i].size - 1) / t[i].size * t[i].size;
         *t[i].off = (uint32_t)off;
         off += t[i].size;
     }
-    if (share) pl->lds_v = pl->lds_k;
-    off = (off + 15) & ~(size_t)15;
-    pl->lds_stage = (uint32_t)off;
-    if (nw > 4) {
-        const size_t kt = 256u * kb + (kq ? 320u : 32u), vt = 256u * vb + 32u;
-        off += (size_t)nw * 2 * (2 * kt + 2 * vt);
-    }
-    pl->lds = off;
+    if (share) *lds_v = *lds_k;
+    *total = off;
 }
 
-// Waves per workgroup: TQ_DECODE_STAGE (0: registers, 12, 16) or the default, reduced while the
-// LDS does not hold the tables and the staging ring.
-int choose_nw(int kb, bool kq, int vb, bool share) {
-    int want = 4;
-    if (const char* e = std::getenv("TQ_DECODE_STAGE")) {
-        const int v = std::atoi(e);
-        want = v >= 16 ? 16 : (v >= 12 ? 12 : 4);
-    }
-    for (int nw : {16, 12}) {
-        if (nw > want) continue;
-        FastPlan pl;
-        lds_layout(kb, kq, vb, share, nw, &pl);
-        if (pl.lds <= kMaxLds) return nw;
-    }
-    return 4;
-}
-
-}  // namespace
-
-int tq_decode_fast_plan(int kb, bool kq, int vb, bool share, bool count, FastPlan* pl) {
-    const int nw = choose_nw(kb, kq, vb, share);
-    pl->nw = nw;
-    pl->kern = kernel_ptr(kb, kq, vb, count, nw);
-    if (!pl->kern) return TQ_ERR_BITS;
-    lds_layout(kb, kq, vb, share, nw, pl);
-    if (pl->lds > 65536) {
-        hipError_t e = hipFuncSetAttribute(pl->kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl->lds);
-        if (e != hipSuccess) return (int)e;
-    }
-    return TQ_OK;
-}
-
-int tq_decode_fast_launch(const FastDecodeParams& prm, const FastPlan& pl, int64_t grid, hipStream_t stream) {
+int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
+                          hipStream_t stream) {
+    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats);
+    if (!kern) return TQ_ERR_BITS;
     FastDecodeParams p = prm;
     void* args[] = {&p};
-    hipError_t le = hipLaunchKernel(pl.kern, dim3((unsigned)grid), dim3(64 * pl.nw), args, pl.lds, stream);
+    hipError_t le = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(256), args, lds_bytes, stream);
     if (le != hipSuccess) return (int)le;
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TQ_OK : (int)e;

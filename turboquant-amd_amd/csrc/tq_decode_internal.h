@@ -28,7 +28,6 @@ struct FastDecodeParams {
     const float* v_cent;
     float k_cscale, v_cscale, v_cinv;
     uint32_t lds_sign, lds_k, lds_v;  // byte offsets of the LDS tables
-    uint32_t lds_stage;               // byte offset of the staging ring (staged kernels)
     int block_size, tile_shift;       // block_size = 16 << tile_shift
     int64_t num_blocks;
     const int32_t* bt;
@@ -49,21 +48,13 @@ struct FastDecodeParams {
     int64_t out_ss, out_sh;
 };
 
-// LDS of one workgroup on gfx950.
-constexpr size_t kMaxLds = 160 * 1024;
+// decode_fast_kernel<kb, kq, vb, count> (nullptr: unsupported bit widths).
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false);
 
-// A launch configuration of decode_fast_kernel: the instance, waves per workgroup (4: loads
-// into registers; 12 or 16: one workgroup per CU, LDS staging), LDS byte offsets and total.
-struct FastPlan {
-    const void* kern;
-    int nw;
-    uint32_t lds_sign, lds_k, lds_v, lds_stage;
-    size_t lds;
-};
+// LDS byte offsets of the fp4 sign table, the K and the V pair tables, and the total.
+void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
+                               uint32_t* lds_v, size_t* total);
 
-// Choose the instance for these bit widths (TQ_DECODE_STAGE overrides the waves per
-// workgroup) and lay out its LDS.  count: Sparse-V skip statistics wanted.
-int tq_decode_fast_plan(int kb, bool kq, int vb, bool share, bool count, FastPlan* plan);
-
-// Launch a planned decode_fast_kernel on `grid` workgroups (plan.nw work units each).
-int tq_decode_fast_launch(const FastDecodeParams& p, const FastPlan& plan, int64_t grid, hipStream_t stream);
+// Launch decode_fast_kernel (grid of 256-thread workgroups, 4 work units each).
+int tq_decode_fast_launch(const FastDecodeParams& p, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
+                          hipStream_t stream);
