@@ -164,8 +164,11 @@ def choose_tokens_per_chunk(num_seqs: int, num_kv_heads: int, max_seq_len: int,
     kernel takes ceil(units / concurrent_units) rounds of (chunk tiles + a fixed per-unit
     cost), and the chunk count per sequence minimising that is chosen (chunks balanced: the last
     is at most one tile shorter).  With the sequence lengths known on the host (seq_lens_host),
-    the estimate is the balanced load (all work / concurrent_units) plus half a unit of tail,
-    and never less than the longest unit.
+    the estimate is the balanced load (all work / concurrent_units) plus a quarter unit of tail
+    (slots freed by short units are refilled, and waves left alone on a SIMD run faster), and
+    never less than the longest unit.  Measured on MI355X with config-5-like lengths
+    (log-uniform 2K..128K): chunks of ~170-260 tiles beat a single round of ~420-tile chunks by
+    about 8 %.
     """
     slots = max(1, concurrent_units)
     ovh = unit_overhead_tiles
@@ -188,7 +191,7 @@ def choose_tokens_per_chunk(num_seqs: int, num_kv_heads: int, max_seq_len: int,
         else:
             units = num_kv_heads * sum(-(-t // ct) for t in lens)
             work = num_kv_heads * sum(lens) + ovh * units
-            cost = max(work / slots + (0.5 * (ct + ovh) if units > slots else 0.0), ct + ovh)
+            cost = max(work / slots + 0.25 * (ct + ovh), ct + ovh)
         cost += 0.01 * nch  # partial results to merge
         if best is None or cost < best[0]:
             best = (cost, ct)
@@ -212,12 +215,14 @@ def plan_tokens_per_chunk(device: torch.device, num_seqs: int, num_q_heads: int,
                           share_codebook: bool = False, seq_lens_host=None, norm_row_bytes: int = 2) -> int:
     """tokens_per_chunk for tq_decode on this device and configuration.
 
-    Per-unit cost beyond its tiles: about two tiles of set-up, plus writing and re-reading its
-    partial results (group heads x 128 fp32, twice) expressed in tiles of K+V data.
+    Per-unit cost beyond its tiles: about fourteen tiles of set-up (the workgroup's LDS tables,
+    the query operands, the first loads; calibrated on MI355X with configs 3-5), plus writing
+    and re-reading its partial results (group heads x 128 fp32, twice) expressed in tiles of
+    K+V data.
     """
     group = num_q_heads // max(1, num_kv_heads)
     tile_bytes = 16 * (k_fmt.token_bytes + v_fmt.token_bytes)
-    overhead = 2.0 + group * 1024.0 / tile_bytes
+    overhead = 14.0 + group * 1024.0 / tile_bytes
     units = concurrent_units(device, k_fmt.bits, k_fmt.qjl, v_fmt.bits, num_q_heads, num_kv_heads,
                              norm_row_bytes, share_codebook)
     return choose_tokens_per_chunk(num_seqs, num_kv_heads, max_seq_len, units, seq_lens_host, overhead)
