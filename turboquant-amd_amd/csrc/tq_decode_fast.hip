@@ -31,8 +31,8 @@
 // tile is addressed by scalar offsets (block * block_stride + region offset), which needs the
 // cache to span less than 2 GiB (checked on the host; larger caches use decode_kernel).  The
 // norm streams are read once per pair: lanes of tile A and tile B differ in their vector offset.
-// Block-table entries of the next pair are fetched with one vector load per pair and read with
-// readlane, so the tile walk never waits on a scalar load.  Loads run one pair ahead.
+// Block-table entries of the next pair come through the scalar cache (a vector load would cost
+// the texture data path a whole wave of lanes for 8 bytes).  Loads run one pair ahead.
 //
 // Sparse-V (kernels/sparse_v.py:108-149): for tile X, m_X = running max through tile X; token t
 // is dropped from PV when no head of the group has exp2(c (s - m_X)) > threshold, tested as
@@ -527,13 +527,21 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int32_t* bt_row = p.bt + s * p.bt_stride;
     const int tile0 = t_begin >> 4;                               // absolute tile index of the chunk start
     const int tmask = (1 << p.tile_shift) - 1;
-    // block number of tile (2 * pi + (lane & 1)) of the chunk; clamped into the sequence's blocks
-    auto bt_load = [&](int pi) -> int {
-        int lb = (tile0 + 2 * pi + (lane & 1)) >> p.tile_shift;
-        lb = lb < nblk_seq ? lb : nblk_seq - 1;
-        return bt_row[lb];
+    // Block numbers of the two tiles of a pair (clamped into the sequence's blocks) through the
+    // scalar cache, one pair ahead: each vector load costs the texture data path a full wave of
+    // lanes, so the eight bytes are not fetched by 64 lanes.
+    typedef __attribute__((address_space(4))) const int32_t bt_s;
+    const bt_s* bts = (const bt_s*)(uintptr_t)bt_row;
+    auto bt_pair = [&](int pi, int (&b)[2]) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            int lb = (tile0 + 2 * pi + x) >> p.tile_shift;
+            lb = lb < nblk_seq ? lb : nblk_seq - 1;
+            b[x] = bts[lb];
+        }
     };
-    int btn = bt_load(0);
+    int bt_next[2];
+    bt_pair(0, bt_next);
 
     // Norm rows of tiles A (lanes col < 8) and B (col >= 8) in one load: the scalar offset
     // addresses the nearer tile, lanes of the farther one add the distance.
@@ -549,8 +557,8 @@ void decode_fast_kernel(FastDecodeParams p) {
 
     // K part of pair pi (and the block numbers of pair pi + 1); fills the V offsets of pi.
     auto fetch_k = [&](int pi, KRaw<KB, KQJL>& kr, PairInfo& info) {
-        int blk[2] = {__builtin_amdgcn_readlane(btn, 0), __builtin_amdgcn_readlane(btn, 1)};
-        btn = bt_load(pi + 1);
+        int blk[2] = {bt_next[0], bt_next[1]};
+        bt_pair(pi + 1, bt_next);
         uint32_t kb[2], r0[2];
         int nv[2];
 #pragma unroll
