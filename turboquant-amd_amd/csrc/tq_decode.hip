@@ -669,9 +669,23 @@ struct ReduceParams {
     int64_t out_ss, out_sh;
 };
 
-// Split-K merge, one wave per (sequence, query head); lane d covers dims 2d, 2d+1:
+// Split-K merge, one wave per (sequence, query head):
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:128-140)
-// Sequences of one chunk were written by decode_kernel; empty ones are written as zero here.
+// The chunk maxima and denominators are read one lane per chunk and reduced across the wave;
+// the rows acc_c are summed in chunk order with lane d covering dims 2d, 2d+1, eight rows in
+// flight at a time.  Sequences of one chunk were written by the decode kernel; empty ones are
+// written as zero here.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
+    return x;
+}
+
 __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     const int64_t sh = blockIdx.x;
     const int64_t s = sh / p.hq;
@@ -684,16 +698,39 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     if (nch == 1) return;
     const int64_t base = sh * p.n_chunks;
     float M = kNegInf;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, p.ws_m[base + c]);
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int c = c0 + lane;
+        M = fmaxf(M, c < nch ? p.ws_m[base + c] : kNegInf);
+    }
+    M = wave_max(M);
     float den = 0.f, a0 = 0.f, a1 = 0.f;
     if (M != kNegInf) {
-        for (int c = 0; c < nch; ++c) {
-            const float w = __builtin_amdgcn_exp2f(p.ws_m[base + c] - M);
-            den = __builtin_fmaf(w, p.ws_l[base + c], den);
-            const float2 v = reinterpret_cast<const float2*>(p.ws_acc + (base + c) * TQ_HEAD_DIM)[lane];
-            a0 = __builtin_fmaf(w, v.x, a0);
-            a1 = __builtin_fmaf(w, v.y, a1);
+        for (int c0 = 0; c0 < nch; c0 += 64) {
+            const int c = c0 + lane;
+            const float w = c < nch ? __builtin_amdgcn_exp2f(p.ws_m[base + c] - M) : 0.f;
+            if (c < nch) den = __builtin_fmaf(w, p.ws_l[base + c], den);
+            const int nb = nch - c0 < 64 ? nch - c0 : 64;
+            const float2* rows = reinterpret_cast<const float2*>(p.ws_acc + (base + c0) * TQ_HEAD_DIM) + lane;
+            int k = 0;
+            for (; k + 8 <= nb; k += 8) {
+                float2 v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = rows[(int64_t)(k + j) * (TQ_HEAD_DIM / 2)];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k + j));
+                    a0 = __builtin_fmaf(wj, v[j].x, a0);
+                    a1 = __builtin_fmaf(wj, v[j].y, a1);
+                }
+            }
+            for (; k < nb; ++k) {
+                const float2 v = rows[(int64_t)k * (TQ_HEAD_DIM / 2)];
+                const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k));
+                a0 = __builtin_fmaf(wk, v.x, a0);
+                a1 = __builtin_fmaf(wk, v.y, a1);
+            }
         }
+        den = wave_sum(den);
     }
     const float inv = den > 0.f ? 1.0f / den : 0.f;
     const int64_t o = s * p.out_ss + (int64_t)h * p.out_sh + 2 * lane;
