@@ -862,8 +862,8 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     if (norm_row_bytes == 2 && group <= 8 && fast_path_enabled()) {
         // the paged fast path (library tile layout)
         kern = tq_decode_fast_kernel_ptr(k_bits, k_qjl != 0, v_bits);
-        uint32_t a, b, c;
-        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &a, &b, &c, &lds);
+        uint32_t a, b, c, d;
+        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &a, &b, &c, &d, &lds);
     }
     int blocks = 0, dev = 0, cus = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds);
@@ -971,7 +971,8 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         f.v_cscale = v_cscale;
         f.v_cinv = 1.f / v_cscale;
         size_t lds_total = 0;
-        tq_decode_fast_lds_layout(k->bits, k->qjl != 0, v->bits, share, &f.lds_sign, &f.lds_k, &f.lds_v, &lds_total);
+        tq_decode_fast_lds_layout(k->bits, k->qjl != 0, v->bits, share, &f.lds_sign, &f.lds_k, &f.lds_v, &f.lds_scratch,
+                                  &lds_total);
         f.block_size = block_size;
         int tsh = 0;
         while ((16 << tsh) < block_size) ++tsh;

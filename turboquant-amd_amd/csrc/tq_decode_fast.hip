@@ -365,44 +365,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<
                                                                      fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
     extern __shared__ uint32_t s_lds[];
-    // Tables (32 bank replicas each): fp4 sign table (QJL), K pair table, V pair table, at the
-    // byte offsets chosen by the host (multiples of each table's size).
+    // Tables: fp4 sign table (QJL), K table, V table, at the byte offsets chosen by the host
+    // (multiples of each table's size).  A replicated table's entry is computed once and its
+    // replicas (consecutive) written with 16-byte stores: every workgroup builds its tables
+    // before reading a tile, so this is part of each unit's start-up.
     constexpr int SREP = sign_replicas<KB, VB>();
+    const int tid = threadIdx.x;
     if (KQJL) {
-        uint32_t* t = s_lds + p.lds_sign / 4;
-        for (int i = threadIdx.x; i < 256 * SREP; i += 256) {
-            const uint32_t e = (uint32_t)i / SREP;
-            uint32_t w = 0;
+        // entry e (one per thread): 8 sign bits -> 8 fp4 values +1 (0x2) / -1 (0xA)
+        uint32_t w = 0;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) w |= (((e >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);  // fp4 +1 / -1
-            t[i] = w;
-        }
+        for (int j = 0; j < 8; ++j) w |= ((((uint32_t)tid >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);
+        tq_u32x4* t = reinterpret_cast<tq_u32x4*>(s_lds + p.lds_sign / 4) + tid * (SREP / 4);
+#pragma unroll
+        for (int r = 0; r < SREP / 4; ++r) t[r] = tq_u32x4{w, w, w, w};
     }
     // pair table: entry e -> half2(c[e & (2^b - 1)], c[e >> b]), 32 replicas;
-    // quad table: entry e -> 4 x fp16 c[(e >> bj) & (2^b - 1)], j = 0..3
-    auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad) {
+    // quad table: entry e -> 4 x fp16 c[(e >> bj) & (2^b - 1)], j = 0..3 (2 bits: 16 replicas)
+    // 3-bit quads are assembled from the 64 pairs of 3-bit fields, staged in a 512-byte scratch
+    // area after the tables (a static __shared__ array would move the K quad table off address 0)
+    uint32_t* s_pair3 = s_lds + p.lds_scratch / 4;
+    auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad, int which) {
         uint32_t* t = s_lds + off / 4;
         const int mask = (1 << bits) - 1;
         if (quad && bits == 3) {
-            for (int i = threadIdx.x; i < 4096 * 2; i += 256) {
-                const int e = i >> 1, j0 = 2 * (i & 1);
-                t[i] = tq_pack_half2(cent[(e >> (3 * j0)) & 7] * cs, cent[(e >> (3 * j0 + 3)) & 7] * cs);
-            }
+            const uint32_t* pr = s_pair3 + 64 * which;
+            for (int e = tid; e < 4096; e += 256)
+                reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{pr[e & 63], pr[e >> 6]};
         } else if (quad) {
-            for (int i = threadIdx.x; i < 256 * 16 * 2; i += 256) {
-                const int e = i >> 5, j0 = 2 * (i & 1);
-                t[i] = tq_pack_half2(cent[(e >> (2 * j0)) & 3] * cs, cent[(e >> (2 * j0 + 2)) & 3] * cs);
-            }
+            // 256 entries, one per thread: 16 replicas x 8 bytes
+            const int e = tid;
+            const uint32_t lo = tq_pack_half2(cent[e & 3] * cs, cent[(e >> 2) & 3] * cs);
+            const uint32_t hi = tq_pack_half2(cent[(e >> 4) & 3] * cs, cent[(e >> 6) & 3] * cs);
+            tq_u32x4* d = reinterpret_cast<tq_u32x4*>(t) + e * 8;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) d[r] = tq_u32x4{lo, hi, lo, hi};
         } else {
+            // 2^(2 bits) entries (16, 64 or 256), 32 replicas x 4 bytes
             const int ent = 1 << (2 * bits);
-            for (int i = threadIdx.x; i < ent * 32; i += 256) {
-                const int e = i >> 5;
-                t[i] = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
+            for (int e = tid; e < ent; e += 256) {
+                const uint32_t w = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
+                tq_u32x4* d = reinterpret_cast<tq_u32x4*>(t) + e * 8;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) d[r] = tq_u32x4{w, w, w, w};
             }
         }
     };
-    fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>());
-    if (p.lds_v != p.lds_k) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>());
+    const bool vown = p.lds_v != p.lds_k;
+    if (quad_table<KB>() && KB == 3 && tid < 64)
+        s_pair3[tid] = tq_pack_half2(p.k_cent[tid & 7] * p.k_cscale, p.k_cent[tid >> 3] * p.k_cscale);
+    if (quad_table<VB>() && VB == 3 && vown && tid >= 64 && tid < 128)
+        s_pair3[tid] = tq_pack_half2(p.v_cent[tid & 7] * p.v_cscale, p.v_cent[(tid - 64) >> 3] * p.v_cscale);
+    if ((quad_table<KB>() && KB == 3) || (quad_table<VB>() && VB == 3)) __syncthreads();
+    fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>(), 0);
+    if (vown) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>(), 1);
     __syncthreads();
 
     const int lane = threadIdx.x & 63;
@@ -719,7 +735,7 @@ const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count) {
 }
 
 void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
-                               uint32_t* lds_v, size_t* total) {
+                               uint32_t* lds_v, uint32_t* lds_scratch, size_t* total) {
     // Tables at offsets that are multiples of their sizes: largest first.
     struct T {
         size_t size;
@@ -754,7 +770,8 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
         off += t[i].size;
     }
     if (share) *lds_v = *lds_k;
-    *total = off;
+    *lds_scratch = (uint32_t)off;  // 512 bytes: pairs of 3-bit fields while the quad tables are built
+    *total = off + 512;
 }
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,

@@ -28,6 +28,7 @@ struct FastDecodeParams {
     const float* v_cent;
     float k_cscale, v_cscale, v_cinv;
     uint32_t lds_sign, lds_k, lds_v;  // byte offsets of the LDS tables
+    uint32_t lds_scratch;             // 512-byte scratch after the tables
     int block_size, tile_shift;       // block_size = 16 << tile_shift
     int64_t num_blocks;
     const int32_t* bt;
@@ -51,9 +52,10 @@ struct FastDecodeParams {
 // decode_fast_kernel<kb, kq, vb, count> (nullptr: unsupported bit widths).
 const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false);
 
-// LDS byte offsets of the fp4 sign table, the K and the V pair tables, and the total.
+// LDS byte offsets of the fp4 sign table, the K and the V tables, a 512-byte scratch, and the
+// total.
 void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
-                               uint32_t* lds_v, size_t* total);
+                               uint32_t* lds_v, uint32_t* lds_scratch, size_t* total);
 
 // Launch decode_fast_kernel (grid of 256-thread workgroups, 4 work units each).
 int tq_decode_fast_launch(const FastDecodeParams& p, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
