@@ -205,6 +205,42 @@ int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride
               unsigned long long* skip_stats,
               tq_stream_t stream);
 
+/*
+ * tq_decode with the query and the output in the original (unrotated) basis: the kernels use
+ * q x H (and q_proj = q x H when q_proj == NULL; a given q_proj is used as it is) and write
+ * out x H, H = make_wht_matrix(128) (symmetric, H H = I).  Same arguments, workspace and
+ * results as tq_decode on pre-rotated queries followed by a rotation of the output.
+ * Replaces the rotate_query -> attention -> rotate_output sequence of the reference backend
+ * (integration/vllm_backend.py:158-177, TurboQuantFP8State.rotate_query / rotate_output) with
+ * the rotations fused into the decode prologue and the output write (the split-K merge when
+ * a sequence spans several chunks).
+ */
+int tq_decode_rotated(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+                      const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+                      int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                      const tq_kv_view* k, const tq_kv_view* v,
+                      int block_size, int64_t num_blocks,
+                      const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                      const int32_t* seq_lens, int max_seq_len,
+                      float sm_scale, float corr_scale, float sparse_threshold,
+                      int tokens_per_chunk,
+                      void* workspace, size_t workspace_bytes,
+                      void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+                      unsigned long long* skip_stats,
+                      tq_stream_t stream);
+
+/*
+ * y = x H for rows of 128 elements (H = make_wht_matrix(128)): x and y are
+ * [num_seqs, num_heads, 128] at the given element strides (f32/f16/bf16, fp32 arithmetic,
+ * one rounding on the store).  y may be x (in place).  Replaces
+ * TurboQuantFP8State.rotate_query / rotate_output (integration/vllm_backend.py:158-177) as
+ * stand-alone operations, for callers that rotate outside the decode call.
+ */
+int tq_wht_rows(const void* x, int x_dtype, int64_t x_stride_seq, int64_t x_stride_head,
+                int num_seqs, int num_heads, int head_dim,
+                void* y, int y_dtype, int64_t y_stride_seq, int64_t y_stride_head,
+                tq_stream_t stream);
+
 size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk);
 
 /* Work units (one per sequence, KV head and chunk of tokens_per_chunk tokens) that tq_decode

@@ -108,6 +108,38 @@ def test_polarquant_config_should_compress():
     assert PolarQuantConfig(protect_boundary_layers=False, num_layers=10).should_compress(0)
 
 
+def test_paged_backend_config_and_cache_geometry():
+    """Boundary-layer policy and combined-cache geometry of the paged backend (host logic)."""
+    from turboquant.integration import paged_backend as pb
+    c = pb.TurboQuantPagedConfig(num_layers=40, num_protected_layers=2, k_bits=3, k_qjl=True)
+    assert [c.should_compress(i) for i in (0, 1, 2, 37, 38, 39)] == [False, False, True, True, False, False]
+    assert c.get_state(0) is None and c.get_state(39) is None
+    st = c.get_state(5)
+    assert st is c.get_state(5) and (st.k_bits, st.v_bits, st.k_qjl) == (3, 3, True)
+    assert st.v_centroids is st.k_centroids  # one codebook tensor: one LDS table in decode
+    assert pb.TurboQuantPagedConfig(num_layers=0).should_compress(0)
+    assert pb.TurboQuantPagedConfig(protect_boundary_layers=False, num_layers=10).should_compress(0)
+    p = pb.TurboQuantPagedConfig(num_layers=8, k_bits=2, v_bits=2, k_qjl=True, protected_bits=4).get_state(7)
+    assert (p.k_bits, p.v_bits, p.k_qjl) == (4, 4, False)
+    a = pb.TurboQuantPagedState(k_bits=4, v_bits=2)
+    assert a.v_bits == 2 and a.v_centroids.numel() == 4 and a.k_centroids.numel() == 16
+    # K tile then V tile per (block, head): turbo3+QJL keys 1088 B + turbo3 values 800 B at block 16
+    assert pb.TurboQuantPagedImpl.get_kv_cache_shape(10, 16, 8, 128, k_bits=3, k_qjl=True) == (10, 8, 1888)
+    assert pb.TurboQuantPagedImpl.get_kv_cache_shape(10, 32, 8, 128, k_bits=4, v_bits=2) == (10, 8, 2112 + 1088)
+    with pytest.raises(ValueError):
+        pb.TurboQuantPagedImpl.get_kv_cache_shape(10, 24, 8, 128)
+    kv = st.allocate_kv_cache(6, 4)
+    k, v = st.split_kv_cache(kv)
+    assert k.shape == (6, 4, 1088) and v.shape == (6, 4, 800)
+    assert k.stride() == v.stride() == (4 * 1888, 1888, 1) and v.data_ptr() - kv.data_ptr() == 1088
+    with pytest.raises(ValueError):
+        st.split_kv_cache(torch.zeros(6, 4, 1000, dtype=torch.uint8))
+    pb.reset_tq_paged_config()
+    g = pb.get_tq_paged_config(num_layers=12, k_bits=2)
+    assert pb.get_tq_paged_config(k_bits=4) is g and g.k_bits == 2
+    pb.reset_tq_paged_config()
+
+
 def test_compute_entry_points_refuse_cpu_tensors():
     from turboquant.core import PolarQuantConfig, make_codebook, make_wht_matrix, polarquant_compress
     c, b = make_codebook(128, 3)
@@ -199,6 +231,12 @@ def test_host_side_argument_rejection():
                        fake, 1, 1, fake, 16, 0.1, 0.0, 0.0, 16, fake, 1 << 20, fake, 2, 128, 128, None, None) == -6
     assert L.tq_decode(fake, 2, 128, 128, None, 0, 0, 1, 8, 2, 128, ctypes.byref(kv), ctypes.byref(kv), 16, 10,
                        fake, 1, 1, fake, 16, 0.1, 0.0, 0.0, 24, fake, 1 << 20, fake, 2, 128, 128, None, None) == -9
+    assert L.tq_decode_rotated(fake, 2, 128, 128, None, 0, 0, 1, 8, 3, 128, ctypes.byref(kv), ctypes.byref(kv), 16,
+                               10, fake, 1, 1, fake, 16, 0.1, 0.0, 0.0, 16, fake, 1 << 20, fake, 2, 128, 128, None,
+                               None) == -6
+    assert L.tq_wht_rows(fake, 2, 128, 128, 4, 1, 64, fake, 2, 128, 128, None) == -2
+    assert L.tq_wht_rows(fake, 5, 128, 128, 4, 1, 128, fake, 2, 128, 128, None) == -7
+    assert L.tq_wht_rows(fake, 2, 128, 128, 0, 1, 128, fake, 2, 128, 128, None) == 0
     assert L.tq_permute_signs(fake, fake, 4, 64, None) == -2
     assert L.tq_unpack_bits(fake, fake, 4, 128, 0, None) == -3
 

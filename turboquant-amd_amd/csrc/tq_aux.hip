@@ -49,6 +49,43 @@ __global__ __launch_bounds__(256) void unpack_kernel(const uint8_t* in, int8_t* 
     }
 }
 
+// y = x H per 128-element row (H = make_wht_matrix(128)), 16 threads per row: thread t holds
+// elements 8t .. 8t+7 (butterflies over element bits 0-2 in registers, bits 3-6 across lanes
+// 1, 2, 4, 8 of the row).  Rows of a grid-stride step are block-uniform, so every lane takes
+// part in the exchanges; rows past the end carry zeros and store nothing.
+// Follows TurboQuantFP8State.rotate_query / rotate_output (integration/vllm_backend.py:158-177).
+__global__ __launch_bounds__(256) void wht_rows_kernel(const void* x, int x_dt, int64_t x_ss, int64_t x_sh, int hn,
+                                                       int64_t n_rows, int vec, void* y, int y_dt, int64_t y_ss,
+                                                       int64_t y_sh, float h) {
+    const int t = threadIdx.x & 15;
+    for (int64_t r0 = (int64_t)blockIdx.x * 16; r0 < n_rows; r0 += (int64_t)gridDim.x * 16) {
+        const int64_t row = r0 + (threadIdx.x >> 4);
+        const bool valid = row < n_rows;
+        const int64_t sq = valid ? row / hn : 0, hd = valid ? row - sq * hn : 0;
+        const int64_t xo = sq * x_ss + hd * x_sh + 8 * t;
+        float v[8];
+        if (valid && vec) {
+            tq_load8(x, xo, x_dt, v);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = valid ? tq_load1(x, xo + i, x_dt) : 0.f;
+        }
+        tq_wht_regs(v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float a = v[i];
+#pragma unroll
+            for (int m = 1; m < 16; m <<= 1) a = tq_wht_lane(a, m);
+            v[i] = a * h;
+        }
+        if (valid) {
+            const int64_t yo = sq * y_ss + hd * y_sh + 8 * t;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) tq_store1(y, yo + i, y_dt, v[i]);
+        }
+    }
+}
+
 int grid_for(int64_t items) {
     int64_t g = (items + 255) / 256;
     return (int)(g < 65536 ? (g > 0 ? g : 1) : 65536);
@@ -94,6 +131,29 @@ extern "C" int tq_unpack_bits(const uint8_t* in, int8_t* out, int64_t n_rows, in
     if (!in || !out) return TQ_ERR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(n_rows * TQ_HEAD_DIM)), dim3(256), 0, (hipStream_t)stream, in, out,
                        n_rows, bits);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TQ_OK : (int)e;
+}
+
+extern "C" int tq_wht_rows(const void* x, int x_dtype, int64_t x_stride_seq, int64_t x_stride_head,
+                           int num_seqs, int num_heads, int head_dim,
+                           void* y, int y_dtype, int64_t y_stride_seq, int64_t y_stride_head,
+                           tq_stream_t stream) {
+    if (head_dim != TQ_HEAD_DIM) return TQ_ERR_HEAD_DIM;
+    if (num_seqs < 0 || num_heads <= 0) return TQ_ERR_INVALID_ARGUMENT;
+    if (x_dtype != TQ_F32 && x_dtype != TQ_F16 && x_dtype != TQ_BF16) return TQ_ERR_DTYPE;
+    if (y_dtype != TQ_F32 && y_dtype != TQ_F16 && y_dtype != TQ_BF16) return TQ_ERR_DTYPE;
+    if (num_seqs == 0) return TQ_OK;
+    if (!x || !y) return TQ_ERR_INVALID_ARGUMENT;
+    const int64_t n_rows = (int64_t)num_seqs * num_heads;
+    // 8-element vector loads: 16-byte (f16/bf16) or 32-byte (f32) aligned rows
+    const uintptr_t al = x_dtype == TQ_F32 ? 32 : 16;
+    const int vec = ((uintptr_t)x % al == 0) && x_stride_seq % 8 == 0 && x_stride_head % 8 == 0;
+    const int64_t groups = (n_rows + 15) / 16;
+    const int grid = (int)(groups < 65536 ? groups : 65536);
+    hipLaunchKernelGGL(wht_rows_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, x, x_dtype, x_stride_seq,
+                       x_stride_head, num_heads, n_rows, vec, y, y_dtype, y_stride_seq, y_stride_head,
+                       0.08838834764831845f);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TQ_OK : (int)e;
 }

@@ -100,6 +100,39 @@ __device__ __forceinline__ float tq_div_rn(float x, float d, float rcp) {
     return __builtin_fmaf(e, rcp, q0);
 }
 
+// ---- Walsh-Hadamard butterflies: x -> x H for the Sylvester matrix H[i][j] = (-1)^popcount(i & j)
+// (unscaled; the caller multiplies by 1/sqrt(128)).  Each stage pairs the elements whose
+// index differs in one bit, so the stages may run in any order and over any mix of register
+// index bits and lane bits, as long as every index bit gets exactly one stage.
+template <int N>
+__device__ __forceinline__ void tq_wht_regs(float (&x)[N]) {
+    constexpr int kStages = N >= 32 ? 5 : N >= 16 ? 4 : N >= 8 ? 3 : N >= 4 ? 2 : 1;
+    static_assert(N == (1 << kStages), "N must be a power of two in 2..32");
+#pragma unroll
+    for (int st = 0; st < kStages; ++st)
+#pragma unroll
+        for (int j = 0; j < N / 2; ++j) {
+            // j-th pair of stage st: indices i (bit st clear) and i + 2^st
+            const int i = ((j >> st) << (st + 1)) | (j & ((1 << st) - 1));
+            const float a = x[i], b = x[i + (1 << st)];
+            x[i] = a + b;
+            x[i + (1 << st)] = a - b;
+        }
+}
+// The stage across lanes l and l ^ m (m a power of two below 64): the lower lane gets a + b, the
+// upper a - b, where a is the lower lane's value.  Every lane of the wave must take part.
+__device__ __forceinline__ float tq_wht_lane(float x, int m) {
+    const float y = __shfl_xor(x, m, 64);
+    return (__lane_id() & m) ? y - x : x + y;
+}
+// A 128-element row spread over lanes l, l^16, l^32, l^48, 32 elements each (lane group
+// g = l / 16 holds elements 32g + i in x[i], or any layout that maps the element bits 5-6 to
+// lane bits 4-5): x <- (x H) * h.
+__device__ __forceinline__ void tq_wht_row_g4(float (&x)[32], float h) {
+    tq_wht_regs(x);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] = tq_wht_lane(tq_wht_lane(x[i], 16), 32) * h;
+}
 // Paged tile geometry (must match tq_tile_bytes / tq_tile_offsets on the host).
 struct tq_tile_geom {
     int64_t off_signs, off_norm, off_rnorm, bytes;

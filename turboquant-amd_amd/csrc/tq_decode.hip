@@ -34,6 +34,7 @@
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kWhtH = 0.08838834764831845f;  // 1 / sqrt(128): the entries of the normalised H
 constexpr float kNegInf = -__builtin_huge_valf();
 
 enum { R_KIDX = 0, R_KSIG, R_KNORM, R_KRNORM, R_VIDX, R_VNORM, R_COUNT };
@@ -76,6 +77,8 @@ struct DecodeParams {
     void* out;
     int out_dtype;
     int64_t out_ss, out_sh;
+    int rot_q, rot_qp, rot_out;  // rotate q / q_proj by H on load, the output by H on the write
+    float wht_h;                 // 1 / sqrt(128)
 };
 
 // nrec = 0 turns every load through the descriptor into a zero read (unreadable block).
@@ -470,6 +473,9 @@ void decode_kernel(DecodeParams p) {
                 }
             }
         }
+        // q x H: elements 32g + i (or, for permuted signs, 4i + g) over lane groups g
+        if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);
+        if (KQJL && p.rot_qp) tq_wht_row_g4(qpv, p.wht_h);
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
 #pragma unroll
@@ -630,7 +636,9 @@ void decode_kernel(DecodeParams p) {
     int nch = (L + p.chunk - 1) / p.chunk;
     nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len are not processed
 
-    if (nch == 1) {  // the only chunk: normalise and write the output directly
+    // the only chunk: normalise and write the output directly (a rotated output is written by
+    // decode_reduce_kernel, which takes single chunks too)
+    if (nch == 1 && !p.rot_out) {
         if (hvalid) {
             const float inv = lsum > 0.f ? vs / lsum : 0.f;
             const int64_t ob = s * p.out_ss + (int64_t)head * p.out_sh + 32 * g;
@@ -667,14 +675,16 @@ struct ReduceParams {
     void* out;
     int out_dtype;
     int64_t out_ss, out_sh;
+    int rot_out;  // write out x H
+    float wht_h;
 };
 
 // Split-K merge, one wave per (sequence, query head):
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:128-140)
 // The chunk maxima and denominators are read one lane per chunk and reduced across the wave;
 // the rows acc_c are summed in chunk order with lane d covering dims 2d, 2d+1, eight rows in
-// flight at a time.  Sequences of one chunk were written by the decode kernel; empty ones are
-// written as zero here.
+// flight at a time.  Sequences of one chunk were written by the decode kernel (unless the output
+// is rotated: then every sequence is written here); empty ones are written as zero here.
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
@@ -695,7 +705,7 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     L = L < p.cap ? L : p.cap;
     int nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
     nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
-    if (nch == 1) return;
+    if (nch == 1 && !p.rot_out) return;
     const int64_t base = sh * p.n_chunks;
     float M = kNegInf;
     for (int c0 = 0; c0 < nch; c0 += 64) {
@@ -732,7 +742,19 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
         }
         den = wave_sum(den);
     }
-    const float inv = den > 0.f ? 1.0f / den : 0.f;
+    float inv = den > 0.f ? 1.0f / den : 0.f;
+    if (p.rot_out) {
+        // element 2 lane + e: bit 0 in registers, bits 1-6 over the lanes
+        const float b0 = a0 + a1, b1 = a0 - a1;
+        a0 = b0;
+        a1 = b1;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            a0 = tq_wht_lane(a0, m);
+            a1 = tq_wht_lane(a1, m);
+        }
+        inv *= p.wht_h;
+    }
     const int64_t o = s * p.out_ss + (int64_t)h * p.out_sh + 2 * lane;
     tq_store1(p.out, o, p.out_dtype, a0 * inv);
     tq_store1(p.out, o + 1, p.out_dtype, a1 * inv);
@@ -779,8 +801,10 @@ bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
 
 int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num_q_heads, int n_chunks, int chunk,
                   int cap, const int32_t* seq_lens, void* out, int out_dtype, int64_t out_ss, int64_t out_sh,
-                  hipStream_t st) {
+                  int rot_out, hipStream_t st) {
     ReduceParams rp;
+    rp.rot_out = rot_out;
+    rp.wht_h = kWhtH;
     rp.ws_acc = ws_acc;
     rp.ws_m = ws_m;
     rp.ws_l = ws_l;
@@ -874,19 +898,22 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     return TQ_OK;
 }
 
-extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
-                         const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
-                         int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
-                         const tq_kv_view* k, const tq_kv_view* v,
-                         int block_size, int64_t num_blocks,
-                         const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
-                         const int32_t* seq_lens, int max_seq_len,
-                         float sm_scale, float corr_scale, float sparse_threshold,
-                         int tokens_per_chunk,
-                         void* workspace, size_t workspace_bytes,
-                         void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
-                         unsigned long long* skip_stats,
-                         tq_stream_t stream) {
+namespace {
+
+// rotate: q (and q_proj when it is q) enter as q x H, the output leaves as out x H.
+int decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+                const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+                int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                const tq_kv_view* k, const tq_kv_view* v,
+                int block_size, int64_t num_blocks,
+                const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                const int32_t* seq_lens, int max_seq_len,
+                float sm_scale, float corr_scale, float sparse_threshold,
+                int tokens_per_chunk,
+                void* workspace, size_t workspace_bytes,
+                void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+                unsigned long long* skip_stats,
+                tq_stream_t stream) {
     if (head_dim != TQ_HEAD_DIM) return TQ_ERR_HEAD_DIM;
     if (!k || !v) return TQ_ERR_INVALID_ARGUMENT;
     if (num_seqs < 0 || num_q_heads <= 0 || num_kv_heads <= 0) return TQ_ERR_INVALID_ARGUMENT;
@@ -996,6 +1023,10 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         f.out_dtype = out_dtype;
         f.out_ss = out_stride_seq;
         f.out_sh = out_stride_head;
+        f.rot_q = rotate;
+        f.rot_qp = rotate && !q_proj;
+        f.rot_out = rotate;
+        f.wht_h = kWhtH;
         const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
         const int64_t grid = (units + 3) / 4;
         if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
@@ -1003,7 +1034,7 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
         if (frc) return frc;
         return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
                              max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq,
-                             out_stride_head, (hipStream_t)stream);
+                             out_stride_head, rotate, (hipStream_t)stream);
     }
     float* ws_acc = reinterpret_cast<float*>(ws);
     float* ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));
@@ -1057,6 +1088,10 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
     p.out_dtype = out_dtype;
     p.out_ss = out_stride_seq;
     p.out_sh = out_stride_head;
+    p.rot_q = rotate;
+    p.rot_qp = rotate && !q_proj;
+    p.rot_out = rotate;
+    p.wht_h = kWhtH;
 
     const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
     const int64_t grid = (units + 3) / 4;
@@ -1075,5 +1110,47 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
 
     return launch_reduce(ws_acc, ws_m, ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
                          max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq, out_stride_head,
-                         st);
+                         rotate, st);
+}
+
+}  // namespace
+
+extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+                         const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+                         int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                         const tq_kv_view* k, const tq_kv_view* v,
+                         int block_size, int64_t num_blocks,
+                         const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                         const int32_t* seq_lens, int max_seq_len,
+                         float sm_scale, float corr_scale, float sparse_threshold,
+                         int tokens_per_chunk,
+                         void* workspace, size_t workspace_bytes,
+                         void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+                         unsigned long long* skip_stats,
+                         tq_stream_t stream) {
+    return decode_impl(0, q, q_dtype, q_stride_seq, q_stride_head, q_proj, qp_stride_seq, qp_stride_head, num_seqs, num_q_heads,
+                       num_kv_heads, head_dim, k, v, block_size, num_blocks, block_tables, block_table_stride,
+                       max_blocks_per_seq, seq_lens, max_seq_len, sm_scale, corr_scale, sparse_threshold,
+                       tokens_per_chunk, workspace, workspace_bytes, out, out_dtype, out_stride_seq, out_stride_head,
+                       skip_stats, stream);
+}
+
+extern "C" int tq_decode_rotated(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+                                 const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+                                 int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                 const tq_kv_view* k, const tq_kv_view* v,
+                                 int block_size, int64_t num_blocks,
+                                 const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                                 const int32_t* seq_lens, int max_seq_len,
+                                 float sm_scale, float corr_scale, float sparse_threshold,
+                                 int tokens_per_chunk,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+                                 unsigned long long* skip_stats,
+                                 tq_stream_t stream) {
+    return decode_impl(1, q, q_dtype, q_stride_seq, q_stride_head, q_proj, qp_stride_seq, qp_stride_head, num_seqs, num_q_heads,
+                       num_kv_heads, head_dim, k, v, block_size, num_blocks, block_tables, block_table_stride,
+                       max_blocks_per_seq, seq_lens, max_seq_len, sm_scale, corr_scale, sparse_threshold,
+                       tokens_per_chunk, workspace, workspace_bytes, out, out_dtype, out_stride_seq, out_stride_head,
+                       skip_stats, stream);
 }

@@ -470,6 +470,7 @@ void decode_fast_kernel(FastDecodeParams p) {
 #pragma unroll
             for (int i = 0; i < 32; ++i) qv[i] = hvalid ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
         }
+        if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);  // q x H: elements 32g + i
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
@@ -493,6 +494,9 @@ void decode_fast_kernel(FastDecodeParams p) {
                 x[16 + i] = hvalid ? tq_load1(p.qp, off + 64 + i, p.q_dtype) : 0.f;
             }
         }
+        // q x H: x[i] is element 16g + (i & 15) + 64 (i >> 4), so register bits 0-3 and 4 are
+        // element bits 0-3 and 6, lane bits 4-5 element bits 4-5
+        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
@@ -695,7 +699,8 @@ void decode_fast_kernel(FastDecodeParams p) {
     const float vs = p.v_cinv;
     int nch = (L + p.chunk - 1) / p.chunk;
     nch = nch < p.n_chunks ? nch : p.n_chunks;
-    if (nch == 1) {
+    // (a rotated output is written by decode_reduce_kernel, which takes single chunks too)
+    if (nch == 1 && !p.rot_out) {
         if (writer) {
             const float inv = lsum > 0.f ? vs / lsum : 0.f;
             const int64_t ob = s * p.out_ss + (int64_t)head * p.out_sh + 32 * g;

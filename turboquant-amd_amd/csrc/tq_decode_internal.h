@@ -47,6 +47,8 @@ struct FastDecodeParams {
     void* out;
     int out_dtype;
     int64_t out_ss, out_sh;
+    int rot_q, rot_qp, rot_out;  // rotate q / q_proj by H on load, the output by H on the write
+    float wht_h;                 // 1 / sqrt(128)
 };
 
 // decode_fast_kernel<kb, kq, vb, count> (nullptr: unsupported bit widths).

@@ -279,8 +279,11 @@ def run_decode(
     workspace: Optional[torch.Tensor],
     skip_stats: Optional[torch.Tensor],
     keep_alive: tuple = (),
+    rotate: bool = False,
 ) -> torch.Tensor:
-    """Launch tq_decode for q [S, Hq, 128] given ready KV views (shared by all wrappers)."""
+    """Launch tq_decode for q [S, Hq, 128] given ready KV views (shared by all wrappers).
+
+    rotate=True launches tq_decode_rotated: q in the original basis, out returned in it."""
     dev = q.device
     S, Hq, D = q.shape
     L = _lib.lib()
@@ -291,7 +294,8 @@ def run_decode(
         raise ValueError("skip_stats must be a device int64 tensor with 2 elements")
     bt_ptr = block_tables.data_ptr() if block_tables is not None else None
     bt_stride = block_tables.stride(0) if block_tables is not None else 0
-    rc = L.tq_decode(
+    entry = L.tq_decode_rotated if rotate else L.tq_decode
+    rc = entry(
         q.data_ptr(), _lib.dtype_code(q), q.stride(0), q.stride(1),
         _lib.ptr(q_proj), q_proj.stride(0) if q_proj is not None else 0, q_proj.stride(1) if q_proj is not None else 0,
         S, Hq, num_kv_heads, D,
@@ -306,7 +310,7 @@ def run_decode(
         _lib.ptr(skip_stats),
         _lib.stream_handle(dev),
     )
-    _lib.check(rc, "tq_decode")
+    _lib.check(rc, "tq_decode_rotated" if rotate else "tq_decode")
     del keep_alive
     return out
 
@@ -331,8 +335,14 @@ def decode_paged(
     workspace: Optional[torch.Tensor] = None,
     skip_stats: Optional[torch.Tensor] = None,
     seq_lens_host=None,
+    rotate: bool = False,
 ) -> torch.Tensor:
     """Decode attention of q [S, Hq, 128] (rotated space) over paged packed K/V caches.
+
+    rotate=True: q is in the original basis and so is the result - the kernels apply
+    q @ make_wht_matrix(128) on load and rotate the output back on its write (the reference
+    backend's rotate_query / rotate_output, integration/vllm_backend.py:158-177, fused).  An
+    explicit q_proj is used as given; without one the QJL query is the rotated q.
 
     score = sm_scale * (q . k_mse + corr_scale * rnorm * (q_proj . signs)) with q_proj = q by
     default (QJL in the rotated basis, as polarquant_compress computes the signs);
@@ -391,7 +401,7 @@ def decode_paged(
         sm_scale=(1.0 / math.sqrt(128)) if sm_scale is None else sm_scale,
         corr_scale=(math.sqrt(math.pi / 2) / 128) if corr_scale is None else corr_scale,
         q_proj=q_proj, sparse_threshold=sparse_threshold, tokens_per_chunk=chunk, out=out,
-        workspace=workspace, skip_stats=skip_stats, keep_alive=(kc, vc),
+        workspace=workspace, skip_stats=skip_stats, keep_alive=(kc, vc), rotate=rotate,
     )
 
 
