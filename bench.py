@@ -104,7 +104,8 @@ def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_len
     flush()
 
 
-def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, steps, warmup, extra_compress=None):
+def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, steps, warmup, extra_compress=None,
+                time_rotated=False):
     import torch
     from turboquant.core import make_codebook
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged, plan_tokens_per_chunk
@@ -156,6 +157,13 @@ def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, 
             step_inner()
 
     ms = timed(step, steps, warmup)
+    ms_rot = None
+    if time_rotated:
+        # the same decode with q and the output in the model basis (rotations fused)
+        def step_rot():
+            decode_paged(q, k_cache, kf, kc, v_cache, vf, vc, bt, lens, sparse_threshold=thresh,
+                         max_seq_len=msl, tokens_per_chunk=chunk, out=out, workspace=ws, rotate=True)
+        ms_rot = timed(step_rot, steps, warmup)
     skip_frac = None
     if thresh > 0:
         decode_paged(q, k_cache, kf, kc, v_cache, vf, vc, bt, lens, sparse_threshold=thresh,
@@ -174,6 +182,8 @@ def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, 
     }
     if skip_frac is not None:
         res["sparse_v_skip_fraction"] = skip_frac
+    if ms_rot is not None:
+        res["rotated_us_per_layer"] = ms_rot * 1e3
     state = dict(q=q, k_cache=k_cache, v_cache=v_cache, kf=kf, vf=vf, kc=kc, vc=vc, bt=bt, lens=lens,
                  lens_host=lens_host, Hkv=Hkv, chunk=chunk)
     return res, state
@@ -313,7 +323,7 @@ def main():
     if args.only in (None, "config4"):
         head, state4 = decode_case(
             "config4: Sparse-V split-K decode, turbo3+QJL K / turbo3 V, B=64 x ctx 32768, Hq 48 / Hkv 8, bs 16, T=1e-4",
-            64, 48, 8, [32768] * 64, 3, True, 3, 1e-4, 16, 4, dev, steps, warmup)
+            64, 48, 8, [32768] * 64, 3, True, 3, 1e-4, 16, 4, dev, steps, warmup, time_rotated=True)
         print(f"# config4 {head['us_per_layer']:.1f} us/layer, {head['hbm_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     if args.only in (None, "config3"):
         rng = random.Random(3)  # one generator per workload: --only gives the same lengths
