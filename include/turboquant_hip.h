@@ -241,6 +241,35 @@ int tq_wht_rows(const void* x, int x_dtype, int64_t x_stride_seq, int64_t x_stri
                 void* y, int y_dtype, int64_t y_stride_seq, int64_t y_stride_head,
                 tq_stream_t stream);
 
+/*
+ * Prefill / extend attention over the packed paged cache: several query tokens per sequence.
+ * Sequence s has n_s = cu_seqlens_q[s+1] - cu_seqlens_q[s] query tokens, rows cu_seqlens_q[s] ..
+ * of q [T, num_q_heads, 128] (f32/f16/bf16 at the given element strides), and seq_lens[s] cache
+ * tokens in block_tables[s] (already holding the new tokens, written by tq_compress_paged).
+ * Query i of sequence s attends to cache tokens t with t <= seq_lens[s] - n_s + i when flags
+ * has TQ_PREFILL_CAUSAL (the new tokens are the last n_s of the sequence), to all of them
+ * otherwise.  Scores, QJL term and softmax as in tq_decode (no Sparse-V, no split-K); out
+ * [T, num_q_heads, 128].  TQ_PREFILL_ROTATE: q (and q_proj when NULL) and out in the original
+ * basis, as tq_decode_rotated.  Any GQA group; block-table entries outside [0, num_blocks) mask
+ * their tokens; num_blocks >= 1.  max_q_len >= every n_s (sizes the grid).
+ * Replaces the Sq > 1 tiled kernel _fused_general (kernels/attention.py:146-196, called from
+ * FusedAsymmetricAttention.forward, :248), reading the packed cache instead of dequantised
+ * K/V arrays, with the causal limit of an extend step (the reference FP4 backend's prefill
+ * fallback, integration/tq_fp4_backend.py:558-601).
+ */
+#define TQ_PREFILL_CAUSAL 1
+#define TQ_PREFILL_ROTATE 2
+int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+               const void* q_proj, int64_t qp_stride_token, int64_t qp_stride_head,
+               const int32_t* cu_seqlens_q, int num_seqs, int max_q_len,
+               int num_q_heads, int num_kv_heads, int head_dim,
+               const tq_kv_view* k, const tq_kv_view* v,
+               int block_size, int64_t num_blocks,
+               const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+               const int32_t* seq_lens, float sm_scale, float corr_scale, int flags,
+               void* out, int out_dtype, int64_t out_stride_token, int64_t out_stride_head,
+               tq_stream_t stream);
+
 size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk);
 
 /* Work units (one per sequence, KV head and chunk of tokens_per_chunk tokens) that tq_decode

@@ -97,3 +97,25 @@ def decode_chunked(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, chunk: i
     den = sum(np.exp(pm - M) * pl for pm, pl, _ in parts)
     num = sum(np.exp(pm - M)[:, None] * pa for pm, _, pa in parts)
     return num / den[:, None], skipped, L
+
+
+def prefill_dense(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, causal: bool = True):
+    """n query tokens [n, G, 128] (qp likewise, or None) over one KV head's L tokens, the new
+    tokens being the last n of them -> out [n, G, 128].
+
+    Query i sits at position L - n + i and, with causal, sees tokens 0 .. L - n + i (the limit
+    of a serving extend step); without, all L tokens (the Sq > 1 kernel of
+    kernels/attention.py:146-196 has no mask).  Each row is decode_dense over its visible tokens;
+    a row that sees none is zero.
+    """
+    n, L = q.shape[0], k_mse.shape[0]
+    out = np.zeros(q.shape)
+    for i in range(n):
+        lim = min(L, L - n + i + 1) if causal else L
+        if lim <= 0:
+            continue
+        sg = signs[:lim] if signs is not None else None
+        rn = rnorm[:lim] if rnorm is not None else None
+        out[i] = decode_dense(q[i], qp[i] if qp is not None else q[i], k_mse[:lim], sg, rn, v[:lim],
+                              sm_scale, corr_scale)
+    return out

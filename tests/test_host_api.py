@@ -235,6 +235,14 @@ def test_host_side_argument_rejection():
                                10, fake, 1, 1, fake, 16, 0.1, 0.0, 0.0, 16, fake, 1 << 20, fake, 2, 128, 128, None,
                                None) == -6
     assert L.tq_wht_rows(fake, 2, 128, 128, 4, 1, 64, fake, 2, 128, 128, None) == -2
+    pf = lambda hd, kv_, flags, nb: L.tq_prefill(  # noqa: E731
+        fake, 2, 1024, 128, None, 0, 0, fake, 1, 8, 8, 2, hd, ctypes.byref(kv_), ctypes.byref(kv_), 16, nb,
+        fake, 4, 4, fake, 0.1, 0.0, flags, fake, 2, 1024, 128, None)
+    assert pf(64, kv, 1, 10) == -2
+    kv.bits = 5
+    assert pf(128, kv, 1, 10) == -3
+    kv.bits = 3
+    assert pf(128, kv, 4, 10) == -1 and pf(128, kv, 1, 0) == -1
     assert L.tq_wht_rows(fake, 5, 128, 128, 4, 1, 128, fake, 2, 128, 128, None) == -7
     assert L.tq_wht_rows(fake, 2, 128, 128, 0, 1, 128, fake, 2, 128, 128, None) == 0
     assert L.tq_permute_signs(fake, fake, 4, 64, None) == -2

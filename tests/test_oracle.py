@@ -354,6 +354,38 @@ def test_decode_oracle_vs_python_loops():
             assert abs(out[h, d] - num / sum(w)) < 1e-12
 
 
+def test_prefill_oracle_vs_masked_score_matrix():
+    """prefill_dense (rows of decode_dense over a growing prefix) against one masked score
+    tensor [n, G, L] with the causal limit L - n + i written as a comparison of positions."""
+    rng = np.random.default_rng(12)
+    kc = np.array(ocb.solve_codebook_quad(128, 3)[0])
+    vc = np.array(ocb.solve_codebook_quad(128, 4)[0])
+    L, G, n = 23, 3, 7
+    kp, vp, _, _ = _tiny_case(rng, L, G, 3, True, 4)
+    k, sg, rn = odec.dequant_keys(kp, kc, 3, True)
+    v = odec.dequant_values(vp, vc, 4)
+    q = rng.standard_normal((n, G, 128))
+    qp = rng.standard_normal((n, G, 128))
+    sm, cs = 0.2, 0.03
+    s = sm * (np.einsum("igd,td->igt", q, k) + cs * np.einsum("igd,td->igt", qp, sg) * rn[None, None, :])
+    pos_q = (L - n + np.arange(n))[:, None, None]
+    s = np.where(np.arange(L)[None, None, :] <= pos_q, s, -np.inf)
+    w = np.exp(s - s.max(axis=2, keepdims=True))
+    want = np.einsum("igt,td->igd", w / w.sum(axis=2, keepdims=True), v)
+    got = odec.prefill_dense(q, qp, k, sg, rn, v, sm, cs, causal=True)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # the last new token sees the whole sequence: a decode step
+    np.testing.assert_allclose(got[-1], odec.decode_dense(q[-1], qp[-1], k, sg, rn, v, sm, cs), rtol=1e-12)
+    # without the mask every row is a full decode
+    nc = odec.prefill_dense(q, qp, k, sg, rn, v, sm, cs, causal=False)
+    for i in range(n):
+        np.testing.assert_allclose(nc[i], odec.decode_dense(q[i], qp[i], k, sg, rn, v, sm, cs), rtol=1e-12)
+    # more new tokens than cache tokens: the rows before the sequence start see nothing
+    few = odec.prefill_dense(q, qp, k[:4], sg[:4], rn[:4], v[:4], sm, cs)
+    assert np.all(few[:3] == 0.0) and np.all(np.isfinite(few))
+    np.testing.assert_allclose(few[3], odec.decode_dense(q[3], qp[3], k[:1], sg[:1], rn[:1], v[:1], sm, cs))
+
+
 def test_decode_chunked_equals_dense_without_threshold():
     rng = np.random.default_rng(3)
     kc = np.array(ocb.solve_codebook_quad(128, 4)[0])

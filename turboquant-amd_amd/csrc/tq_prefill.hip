@@ -1,0 +1,515 @@
+// Packed paged prefill / extend attention for gfx950: several query tokens per sequence over
+// the packed K/V cache.  The tiled Sq > 1 path of kernels/attention.py:146-196 (_fused_general:
+// one online softmax per query row over 16x128 key tiles, fp16 MFMA products with fp32
+// accumulation), reading the packed paged cache directly instead of dequantised arrays, with
+// the causal limit of a serving extend step (query i of a sequence of length L with n new
+// tokens sits at position L - n + i and sees keys 0 .. L - n + i).
+//
+// Workgroup (256 threads, 4 waves) = (sequence s, KV head kh, block of 64 rows); a row is one
+// (new token i, query head of the GQA group) pair, rows ordered token-major, so a workgroup
+// serves 64 / G tokens with all G heads of the group and each K/V tile is dequantised once for
+// all of them.  The cache is walked in 16-token tiles (a tile never spans two blocks).  Per
+// tile the 256 threads dequantise into one of two LDS buffers (thread t: token t / 16, dims
+// 8 (t % 16) .. + 7) while the waves compute on the other:
+//   Khat [16 tok][128] fp16 = c[idx] * cscale       row stride 272 B (16 B pad: no bank clash)
+//   Shat [16 tok][128] fp16 = +-1                    QJL keys only
+//   VhatT [128 dim][16 tok] fp16 = c[vidx] * cscale  transposed: the PV A operand
+//   kn1, kr2, vn [16] f32 = norm * c1, rnorm * c2, vnorm (c1, c2 below)
+// Each wave computes for its 16 rows (MFMA layout: lane l, n = l % 16, g = l / 16):
+//   S^T [16 tok x 16 rows] = Khat . Q^T     4 x mfma_f32_16x16x32_f16 (B: q row n in registers)
+//   T^T = Shat . QP^T                        4 x mfma_f32_16x16x32_f16 (QJL keys)
+//   lane (n, g) holds tokens 4g + r of row n: s = kn1 * S + kr2 * T (log2 units), masked;
+//   online softmax per row (column) with the maxima and sums reduced over the lane groups;
+//   fp16(p * vnorm) of tokens 4g..4g+3 is exactly the B operand of
+//   O^T [128 x 16 rows] += VhatT . P^T        8 x mfma_f32_16x16x16_f16
+// Output: lane (n, g) holds dims 16j + 4g + r of row n, divided by the row's denominator.
+#include "tq_common.h"
+
+#include <cmath>
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kWhtH = 0.08838834764831845f;  // 1 / sqrt(128)
+
+constexpr int kRowsPerWG = 64;
+constexpr int kKRow = 272;                       // bytes per token row of Khat / Shat
+constexpr int kOffS = 16 * kKRow;                // Shat
+constexpr int kOffV = 2 * 16 * kKRow;            // VhatT: 128 rows of 32 bytes
+constexpr int kOffN = kOffV + 128 * 32;          // kn1[16], kr2[16], vn[16]
+constexpr int kBuf = kOffN + 3 * 16 * 4;         // one tile buffer
+constexpr int kOffTab = 2 * kBuf;                // pair tables: K then V, 256 x 4 bytes each
+constexpr int kLdsBytes = kOffTab + 2 * 1024;
+
+struct PrefillParams {
+    const void* q;
+    int64_t q_st, q_sh;
+    const void* qp;
+    int64_t qp_st, qp_sh;
+    int q_dtype, q_vec;
+    const int32_t* cu_q;
+    int num_seqs, hq, hkv, group, n_rb;
+    tq_region kidx, ksig, knorm, krnorm, vidx, vnorm;
+    const float* k_cent;
+    const float* v_cent;
+    int k_perm;
+    float k_cs, v_cs, v_cinv;
+    int block_size;
+    int64_t num_blocks;
+    const int32_t* bt;
+    int64_t bt_stride;
+    int max_blocks;
+    const int32_t* seq_lens;
+    float c1;   // sm_scale * log2(e) / k_cs: MSE term in log2 units
+    float c2;   // sm_scale * log2(e) * corr_scale: QJL term in log2 units
+    int causal;
+    int rot_q, rot_qp, rot_out;
+    void* out;
+    int out_dtype;
+    int64_t out_st, out_sh;
+};
+
+typedef _Float16 tq_half4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float max_over_groups(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float sum_over_groups(float x) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Raw packed data one thread dequantises for a tile.
+struct Raw {
+    uint32_t kw[2], vw[2];   // dwords holding the 8 index fields (funnel-shifted by the byte offset)
+    uint32_t sg0, sg1, sg2, sg3;  // sign bits (QJL keys): sg0 = dword of byte pp, or the whole row if permuted
+    uint32_t nrm;            // fp16 norm bits (threads 0-47: K norm, K residual norm, V norm)
+};
+
+// The 8 index fields of dims 8pp..8pp+7: bytes bits*pp .. of the token's index row, read as
+// the two aligned dwords around them (the second one clamped to the row: a field that ends in
+// the row's last dword lies entirely in it).
+__device__ __forceinline__ void load_fields(const uint8_t* row, int bits, int pp, uint32_t (&w)[2]) {
+    const int o = bits * pp;
+    const int w0 = o >> 2;
+    const int w1 = (w0 + 1 < 4 * bits) ? w0 + 1 : w0;
+    const uint32_t* r32 = reinterpret_cast<const uint32_t*>(row);
+    w[0] = r32[w0];
+    w[1] = r32[w1];
+}
+__device__ __forceinline__ uint32_t fields(const uint32_t (&w)[2], int bits, int pp) {
+    return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)((bits * pp) & 3) * 8u);
+}
+
+template <int KB, bool KQJL, int VB>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t s_lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+
+    const int rb = (int)(blockIdx.x % (unsigned)p.n_rb);
+    const int skh = (int)(blockIdx.x / (unsigned)p.n_rb);
+    const int kh = skh % p.hkv;
+    const int s = skh / p.hkv;
+    const int q0 = p.cu_q[s];
+    const int nq = p.cu_q[s + 1] - q0;
+    const int G = p.group;
+    if (nq <= 0 || rb * kRowsPerWG >= nq * G) return;  // block-uniform
+    int L = p.seq_lens[s];
+    const int cap = p.max_blocks * p.block_size;
+    L = L < cap ? L : cap;
+    L = L > 0 ? L : 0;
+
+    // ---- pair tables: entry e -> half2(c[e & m], c[e >> b]) * cscale ----
+    {
+        uint32_t* tk = reinterpret_cast<uint32_t*>(s_lds + kOffTab);
+        uint32_t* tv = tk + 256;
+        if (tid < (1 << (2 * KB)))
+            tk[tid] = tq_pack_half2(p.k_cent[tid & ((1 << KB) - 1)] * p.k_cs, p.k_cent[tid >> KB] * p.k_cs);
+        if (tid < (1 << (2 * VB)))
+            tv[tid] = tq_pack_half2(p.v_cent[tid & ((1 << VB) - 1)] * p.v_cs, p.v_cent[tid >> VB] * p.v_cs);
+    }
+
+    // ---- this lane's row: (token i, head gh) ----
+    const int R = rb * kRowsPerWG + wave * 16 + n;
+    const int i = R / G;
+    const int gh = R - i * G;
+    const bool rvalid = i < nq;
+    const int head = kh * G + gh;
+    const int qpos = p.causal ? L - nq + i : L - 1;  // last key position the row sees
+    // last key position any row of the workgroup sees (rows are token-major)
+    int imax = (rb * kRowsPerWG + kRowsPerWG - 1) / G;
+    imax = imax < nq - 1 ? imax : nq - 1;
+    int t_end = p.causal ? L - nq + imax + 1 : L;
+    t_end = t_end < L ? t_end : L;
+    t_end = t_end > 0 ? t_end : 0;
+    const int ntiles = (t_end + 15) >> 4;
+
+    // ---- query operands (B of the score products): dims 32cc + 8g + j of row n ----
+    tq_half8 qop[4], qpop[4];
+    {
+        float x[32];
+        const int64_t off = (int64_t)(q0 + (rvalid ? i : 0)) * p.q_st + (int64_t)head * p.q_sh + 8 * g;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            if (rvalid && p.q_vec) {
+                tq_load8(p.q, off + 32 * cc, p.q_dtype, &x[8 * cc]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[8 * cc + j] = rvalid ? tq_load1(p.q, off + 32 * cc + j, p.q_dtype) : 0.f;
+            }
+        }
+        // x[8cc + j] is element 32cc + 8g + j: register bits = element bits 0-2 and 5-6
+        if (p.rot_q) tq_wht_row_g4(x, kWhtH);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qop[cc][j] = (_Float16)x[8 * cc + j];
+        if (KQJL) {
+            const int64_t offp = (int64_t)(q0 + (rvalid ? i : 0)) * p.qp_st + (int64_t)head * p.qp_sh + 8 * g;
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                if (rvalid && p.q_vec) {
+                    tq_load8(p.qp, offp + 32 * cc, p.q_dtype, &x[8 * cc]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        x[8 * cc + j] = rvalid ? tq_load1(p.qp, offp + 32 * cc + j, p.q_dtype) : 0.f;
+                }
+            }
+            if (p.rot_qp) tq_wht_row_g4(x, kWhtH);
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qpop[cc][j] = (_Float16)x[8 * cc + j];
+        } else {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) qpop[cc] = tq_half8{};
+        }
+    }
+
+    // ---- dequantisation of tile ti by this thread: token tt, dims 8pp .. 8pp + 7 ----
+    const int tt = tid >> 4;
+    const int pp = tid & 15;
+    const int32_t* bt_row = p.bt + (int64_t)s * p.bt_stride;
+    // block of tile ti (wave-uniform) and whether it is readable
+    auto tile_block = [&](int ti, int& nv) -> int64_t {
+        const int t0 = ti * 16;
+        int blk = bt_row[t0 / p.block_size];
+        nv = L - t0;
+        nv = nv < 16 ? nv : 16;
+        if (blk < 0 || (int64_t)blk >= p.num_blocks) {
+            blk = 0;
+            nv = 0;
+        }
+        return blk;
+    };
+    auto load_raw = [&](int ti, Raw& w) {
+        int nv;
+        const int64_t blk = tile_block(ti, nv);
+        const int r = (ti * 16) % p.block_size + tt;
+        auto at = [&](const tq_region& rg, int row) -> const uint8_t* {
+            return static_cast<const uint8_t*>(rg.ptr) + blk * rg.stride_block + (int64_t)kh * rg.stride_head +
+                   (int64_t)row * rg.stride_row;
+        };
+        load_fields(at(p.kidx, r), KB, pp, w.kw);
+        load_fields(at(p.vidx, r), VB, pp, w.vw);
+        if (KQJL) {
+            // natural order: the dword holding byte pp; permuted: the whole row
+            const uint32_t* sr = reinterpret_cast<const uint32_t*>(at(p.ksig, r));
+            if (!p.k_perm) {
+                w.sg0 = sr[pp >> 2];
+                w.sg1 = w.sg2 = w.sg3 = 0;
+            } else {
+                w.sg0 = sr[0];
+                w.sg1 = sr[1];
+                w.sg2 = sr[2];
+                w.sg3 = sr[3];
+            }
+        }
+        w.nrm = 0;
+        const int nr = (ti * 16) % p.block_size + (tid & 15);
+        if (tid < 16) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.knorm, nr));
+        else if (tid < 32 && KQJL) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.krnorm, nr));
+        else if (tid >= 32 && tid < 48) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.vnorm, nr));
+    };
+    auto store_tile = [&](int ti, const Raw& w, int buf) {
+        int nv;
+        tile_block(ti, nv);
+        uint8_t* b = s_lds + buf * kBuf;
+        const uint8_t* tab = s_lds + kOffTab;
+        {
+            const uint32_t f = fields(w.kw, KB, pp);
+            tq_u32x4 h;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t e = (f >> (2 * KB * k)) & ((1u << (2 * KB)) - 1u);
+                h[k] = *reinterpret_cast<const uint32_t*>(tab + 4 * e);
+            }
+            *reinterpret_cast<tq_u32x4*>(b + tt * kKRow + 16 * pp) = h;
+        }
+        if (KQJL) {
+            // sign of dim 8pp + j: natural bit 8pp + j; permuted (row bit 32c + k = dim 4k + c):
+            // bit 32 (j & 3) + 2pp + (j >> 2)
+            uint32_t bitsj = 0;
+            if (!p.k_perm) {
+                bitsj = (w.sg0 >> (8 * (pp & 3))) & 0xffu;
+            } else {
+                const uint32_t d[4] = {w.sg0, w.sg1, w.sg2, w.sg3};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bitsj |= ((d[j & 3] >> (2 * pp + (j >> 2))) & 1u) << j;
+            }
+            tq_u32x4 h;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // bit 1 -> +1 (0x3c00), bit 0 -> -1 (0xbc00)
+                const uint32_t lo = ((bitsj >> (2 * k)) & 1u) ? 0x3c00u : 0xbc00u;
+                const uint32_t hi = ((bitsj >> (2 * k + 1)) & 1u) ? 0x3c00u : 0xbc00u;
+                h[k] = lo | (hi << 16);
+            }
+            *reinterpret_cast<tq_u32x4*>(b + kOffS + tt * kKRow + 16 * pp) = h;
+        }
+        {
+            const uint32_t f = fields(w.vw, VB, pp);
+            const uint8_t* tv = tab + 1024;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t e = (f >> (2 * VB * k)) & ((1u << (2 * VB)) - 1u);
+                const uint32_t h2 = *reinterpret_cast<const uint32_t*>(tv + 4 * e);
+                const int d = 8 * pp + 2 * k;
+                *reinterpret_cast<uint16_t*>(b + kOffV + d * 32 + 2 * tt) = (uint16_t)h2;
+                *reinterpret_cast<uint16_t*>(b + kOffV + (d + 1) * 32 + 2 * tt) =
+                    (uint16_t)(h2 >> 16);
+            }
+        }
+        if (tid < 48) {
+            // norms of unusable tokens are zeroed bit-wise (their bits may be anything)
+            const int tok = tid & 15;
+            const float x = tok < nv ? tq_f16_to_f32(w.nrm) : 0.f;
+            const float scale = tid < 16 ? p.c1 : (tid < 32 ? p.c2 : 1.f);
+            reinterpret_cast<float*>(b + kOffN)[tid] = x * scale;
+        }
+    };
+
+    __syncthreads();  // pair tables
+    Raw raw;
+    if (ntiles > 0) {
+        load_raw(0, raw);
+        store_tile(0, raw, 0);
+    }
+    __syncthreads();
+
+    float m = kNegInf, lsum = 0.f;
+    tq_floatx4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int ti = 0; ti < ntiles; ++ti) {
+        const int buf = ti & 1;
+        if (ti + 1 < ntiles) load_raw(ti + 1, raw);
+        int nv;
+        tile_block(ti, nv);
+        const uint8_t* b = s_lds + buf * kBuf;
+        // scores^T: tokens 4g + r of row n
+        tq_floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const tq_half8 a = *reinterpret_cast<const tq_half8*>(
+                b + n * kKRow + 2 * (32 * cc + 8 * g));
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[cc], sc, 0, 0, 0);
+        }
+        tq_floatx4 tj = {0.f, 0.f, 0.f, 0.f};
+        if (KQJL) {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const tq_half8 a = *reinterpret_cast<const tq_half8*>(
+                    b + kOffS + n * kKRow + 2 * (32 * cc + 8 * g));
+                tj = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qpop[cc], tj, 0, 0, 0);
+            }
+        }
+        const tq_floatx4 kn1 = *reinterpret_cast<const tq_floatx4*>(b + kOffN + 16 * g);
+        const tq_floatx4 kr2 =
+            *reinterpret_cast<const tq_floatx4*>(b + kOffN + 64 + 16 * g);
+        const tq_floatx4 vn =
+            *reinterpret_cast<const tq_floatx4*>(b + kOffN + 128 + 16 * g);
+        float sv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = 4 * g + r;
+            const float v = __builtin_fmaf(kn1[r], sc[r], kr2[r] * tj[r]);
+            sv[r] = (tok < nv && ti * 16 + tok <= qpos) ? v : kNegInf;
+        }
+        float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        mt = max_over_groups(mt);
+        const float m_new = fmaxf(m, mt);
+        if (__builtin_amdgcn_ballot_w64(m_new > m)) {
+            const float alpha = m_new > m ? __builtin_amdgcn_exp2f(m - m_new) : 1.f;  // 0 while m = -inf
+            lsum *= alpha;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+        }
+        m = m_new;
+        const float nb = m_new == kNegInf ? 0.f : -m_new;
+        float pr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(sv[r] + nb);  // 0 for masked tokens
+        lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+        tq_half4v bop;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bop[r] = (_Float16)(pr[r] * vn[r]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const tq_half4v a = *reinterpret_cast<const tq_half4v*>(
+                b + kOffV + (16 * j + n) * 32 + 8 * g);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[j], 0, 0, 0);
+        }
+        if (ti + 1 < ntiles) store_tile(ti + 1, raw, buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- normalise, rotate, write ----
+    const float l = sum_over_groups(lsum);
+    const float inv = l > 0.f ? p.v_cinv / l : 0.f;
+    float o[32];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[4 * j + r] = acc[j][r] * inv;
+    // o[4j + r] is dim 16j + 4g + r: register bits = dim bits 0-1 and 4-6
+    if (p.rot_out) tq_wht_row_g4(o, kWhtH);
+    if (rvalid) {
+        const int64_t ob = (int64_t)(q0 + i) * p.out_st + (int64_t)head * p.out_sh + 4 * g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tq_store1(p.out, ob + 16 * j + r, p.out_dtype, o[4 * j + r]);
+    }
+}
+
+const void* prefill_kernel_ptr(int kb, bool kq, int vb) {
+#define TQ_PF(KB, KQ, VB) \
+    if (kb == KB && kq == KQ && vb == VB) return (const void*)prefill_kernel<KB, KQ, VB>;
+#define TQ_PF_V(KB, KQ) TQ_PF(KB, KQ, 2) TQ_PF(KB, KQ, 3) TQ_PF(KB, KQ, 4)
+    TQ_PF_V(2, false) TQ_PF_V(2, true) TQ_PF_V(3, false) TQ_PF_V(3, true) TQ_PF_V(4, false) TQ_PF_V(4, true)
+#undef TQ_PF_V
+#undef TQ_PF
+    return nullptr;
+}
+
+bool aligned(const void* ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
+
+int check_region(const tq_region& r, int align) {
+    if (!r.ptr) return TQ_ERR_INVALID_ARGUMENT;
+    if (!aligned(r.ptr, align) || r.stride_block % align || r.stride_head % align || r.stride_row % align)
+        return TQ_ERR_INVALID_ARGUMENT;
+    return TQ_OK;
+}
+
+bool q_vector_ok(const void* q, int dtype, int64_t st, int64_t sh) {
+    const uintptr_t a = dtype == TQ_F32 ? 32 : 16;
+    return aligned(q, a) && st % 8 == 0 && sh % 8 == 0;
+}
+
+}  // namespace
+
+extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, int64_t q_stride_head,
+                          const void* q_proj, int64_t qp_stride_token, int64_t qp_stride_head,
+                          const int32_t* cu_seqlens_q, int num_seqs, int max_q_len,
+                          int num_q_heads, int num_kv_heads, int head_dim,
+                          const tq_kv_view* k, const tq_kv_view* v,
+                          int block_size, int64_t num_blocks,
+                          const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                          const int32_t* seq_lens, float sm_scale, float corr_scale, int flags,
+                          void* out, int out_dtype, int64_t out_stride_token, int64_t out_stride_head,
+                          tq_stream_t stream) {
+    if (head_dim != TQ_HEAD_DIM) return TQ_ERR_HEAD_DIM;
+    if (!k || !v) return TQ_ERR_INVALID_ARGUMENT;
+    if (num_seqs < 0 || max_q_len < 0 || num_q_heads <= 0 || num_kv_heads <= 0) return TQ_ERR_INVALID_ARGUMENT;
+    if (num_q_heads % num_kv_heads) return TQ_ERR_GQA;
+    if (k->bits < 2 || k->bits > 4 || v->bits < 2 || v->bits > 4) return TQ_ERR_BITS;
+    if (v->qjl) return TQ_ERR_INVALID_ARGUMENT;
+    if (block_size <= 0 || block_size % 16) return TQ_ERR_BLOCK_SIZE;
+    if (q_dtype != TQ_F32 && q_dtype != TQ_F16 && q_dtype != TQ_BF16) return TQ_ERR_DTYPE;
+    if (out_dtype != TQ_F32 && out_dtype != TQ_F16 && out_dtype != TQ_BF16) return TQ_ERR_DTYPE;
+    if (flags & ~(TQ_PREFILL_CAUSAL | TQ_PREFILL_ROTATE)) return TQ_ERR_INVALID_ARGUMENT;
+    if (max_blocks_per_seq < 0 || num_blocks < 1) return TQ_ERR_INVALID_ARGUMENT;  // unreadable entries read block 0
+    if (num_seqs == 0 || max_q_len == 0) return TQ_OK;
+    if (!q || !cu_seqlens_q || !seq_lens || !block_tables || !out || !k->centroids || !v->centroids)
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (block_table_stride < max_blocks_per_seq) return TQ_ERR_INVALID_ARGUMENT;
+    int rc;
+    if ((rc = check_region(k->idx, 4))) return rc;
+    if ((rc = check_region(k->norm, 2))) return rc;
+    if ((rc = check_region(v->idx, 4))) return rc;
+    if ((rc = check_region(v->norm, 2))) return rc;
+    if (k->qjl) {
+        if ((rc = check_region(k->signs, 4))) return rc;
+        if ((rc = check_region(k->rnorm, 2))) return rc;
+    }
+    const int group = num_q_heads / num_kv_heads;
+    const int64_t rows = (int64_t)max_q_len * group;
+    const int64_t n_rb = (rows + kRowsPerWG - 1) / kRowsPerWG;
+    const int64_t grid = n_rb * num_seqs * num_kv_heads;
+    if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
+
+    PrefillParams p = {};
+    p.q = q;
+    p.q_st = q_stride_token;
+    p.q_sh = q_stride_head;
+    p.qp = q_proj ? q_proj : q;
+    p.qp_st = q_proj ? qp_stride_token : q_stride_token;
+    p.qp_sh = q_proj ? qp_stride_head : q_stride_head;
+    p.q_dtype = q_dtype;
+    p.q_vec = q_vector_ok(p.q, q_dtype, p.q_st, p.q_sh) && q_vector_ok(p.qp, q_dtype, p.qp_st, p.qp_sh);
+    p.cu_q = cu_seqlens_q;
+    p.num_seqs = num_seqs;
+    p.hq = num_q_heads;
+    p.hkv = num_kv_heads;
+    p.group = group;
+    p.n_rb = (int)n_rb;
+    p.kidx = k->idx;
+    p.ksig = k->qjl ? k->signs : k->idx;
+    p.knorm = k->norm;
+    p.krnorm = k->qjl ? k->rnorm : k->norm;
+    p.vidx = v->idx;
+    p.vnorm = v->norm;
+    p.k_cent = k->centroids;
+    p.v_cent = v->centroids;
+    p.k_perm = k->signs_permuted ? 1 : 0;
+    p.k_cs = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
+    p.v_cs = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
+    p.v_cinv = 1.f / p.v_cs;
+    p.block_size = block_size;
+    p.num_blocks = num_blocks;
+    p.bt = block_tables;
+    p.bt_stride = block_table_stride;
+    p.max_blocks = max_blocks_per_seq;
+    p.seq_lens = seq_lens;
+    p.c1 = sm_scale * kLog2e / p.k_cs;
+    p.c2 = sm_scale * kLog2e * corr_scale;
+    p.causal = (flags & TQ_PREFILL_CAUSAL) ? 1 : 0;
+    const int rot = (flags & TQ_PREFILL_ROTATE) ? 1 : 0;
+    p.rot_q = rot;
+    p.rot_qp = rot && !q_proj;
+    p.rot_out = rot;
+    p.out = out;
+    p.out_dtype = out_dtype;
+    p.out_st = out_stride_token;
+    p.out_sh = out_stride_head;
+    const void* kern = prefill_kernel_ptr(k->bits, k->qjl != 0, v->bits);
+    if (!kern) return TQ_ERR_BITS;
+    void* args[] = {&p};
+    hipError_t le = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(256), args, kLdsBytes, (hipStream_t)stream);
+    if (le != hipSuccess) return (int)le;
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TQ_OK : (int)e;
+}

@@ -96,6 +96,12 @@ SIGNATURES = {
          _f32, _f32, _f32, _i32, _vp, _sz, _vp, _i32, _i64, _i64, _vp, _vp],
     ),
     "tq_wht_rows": (_i32, [_vp, _i32, _i64, _i64, _i32, _i32, _i32, _vp, _i32, _i64, _i64, _vp]),
+    "tq_prefill": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32, _i32,
+         ctypes.POINTER(TQKVView), ctypes.POINTER(TQKVView), _i32, _i64, _vp, _i64, _i32, _vp,
+         _f32, _f32, _i32, _vp, _i32, _i64, _i64, _vp],
+    ),
     "tq_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "tq_decode_concurrent_units": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
     "tq_polarquant_compress_matrix": (

@@ -405,6 +405,98 @@ def decode_paged(
     )
 
 
+PREFILL_CAUSAL = 1
+PREFILL_ROTATE = 2
+
+
+def prefill_paged(
+    q: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    k_cache: torch.Tensor,
+    k_fmt: PagedKVFormat,
+    k_centroids: torch.Tensor,
+    v_cache: torch.Tensor,
+    v_fmt: PagedKVFormat,
+    v_centroids: torch.Tensor,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    corr_scale: Optional[float] = None,
+    q_proj: Optional[torch.Tensor] = None,
+    causal: bool = True,
+    rotate: bool = False,
+    max_q_len: Optional[int] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Prefill / extend attention of q [T, Hq, 128] over paged packed K/V caches (tq_prefill).
+
+    Sequence s owns query rows cu_seqlens_q[s] .. cu_seqlens_q[s+1] - 1 (int32 [S+1], device)
+    and seq_lens[s] cache tokens, the new tokens included (written by compress_paged first).
+    causal=True: query i of a sequence with n new tokens sits at position seq_lens - n + i and
+    sees cache tokens up to it; causal=False: every query sees the whole sequence (the
+    reference's Sq > 1 kernel, kernels/attention.py:146-196).  Scores and defaults as
+    decode_paged; rotate=True takes q and returns the output in the model basis.  max_q_len:
+    host-side bound of the per-sequence query counts (default: T).
+    """
+    dev = _lib.require_gpu("prefill_paged", q, cu_seqlens_q, k_cache, v_cache, block_tables, seq_lens,
+                           k_centroids, v_centroids)
+    if q.dim() != 3 or q.shape[2] != 128:
+        raise ValueError("q must be [T, Hq, 128]")
+    if k_fmt.block_size != v_fmt.block_size:
+        raise ValueError("K and V caches must share block_size")
+    if v_fmt.qjl:
+        raise ValueError("the V cache carries no QJL data")
+    _check_cache(k_cache, k_fmt, "prefill_paged(k)")
+    _check_cache(v_cache, v_fmt, "prefill_paged(v)")
+    if k_cache.shape[0] != v_cache.shape[0] or k_cache.shape[1] != v_cache.shape[1]:
+        raise ValueError("K and V caches must have the same [num_blocks, num_kv_heads]")
+    T, Hq, _ = q.shape
+    Hkv = k_cache.shape[1]
+    if Hq % Hkv:
+        raise ValueError(f"num_q_heads {Hq} must be a multiple of num_kv_heads {Hkv}")
+    if block_tables.dtype != torch.int32 or seq_lens.dtype != torch.int32 or cu_seqlens_q.dtype != torch.int32:
+        raise TypeError("block_tables, seq_lens and cu_seqlens_q must be int32")
+    S = seq_lens.shape[0]
+    if cu_seqlens_q.dim() != 1 or cu_seqlens_q.shape[0] != S + 1:
+        raise ValueError("cu_seqlens_q must be [num_seqs + 1]")
+    if block_tables.dim() != 2 or block_tables.shape[0] != S or block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be [S, max_blocks] with unit inner stride")
+    seq_lens = seq_lens.contiguous()
+    cu_seqlens_q = cu_seqlens_q.contiguous()
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    if q_proj is not None:
+        if q_proj.shape != q.shape:
+            raise ValueError("q_proj must have q's shape")
+        q_proj = q_proj.to(q.dtype)
+        if q_proj.stride(2) != 1:
+            q_proj = q_proj.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.stride(2) != 1:
+        raise ValueError("out must be [T, Hq, 128] with unit inner stride")
+    kc = k_centroids.to(device=dev, dtype=torch.float32).contiguous()
+    vc = v_centroids.to(device=dev, dtype=torch.float32).contiguous()
+    if kc.numel() != 2 ** k_fmt.bits or vc.numel() != 2 ** v_fmt.bits:
+        raise ValueError("centroid counts must match the formats' bit widths")
+    kv = paged_view(k_cache, k_fmt, kc)
+    vv = paged_view(v_cache, v_fmt, vc)
+    flags = (PREFILL_CAUSAL if causal else 0) | (PREFILL_ROTATE if rotate else 0)
+    mq = T if max_q_len is None else int(max_q_len)
+    rc = _lib.lib().tq_prefill(
+        q.data_ptr(), _lib.dtype_code(q), q.stride(0), q.stride(1),
+        _lib.ptr(q_proj), q_proj.stride(0) if q_proj is not None else 0, q_proj.stride(1) if q_proj is not None else 0,
+        cu_seqlens_q.data_ptr(), S, mq, Hq, Hkv, 128,
+        ctypes.byref(kv), ctypes.byref(vv), k_fmt.block_size, k_cache.shape[0],
+        block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1], seq_lens.data_ptr(),
+        float((1.0 / math.sqrt(128)) if sm_scale is None else sm_scale),
+        float((math.sqrt(math.pi / 2) / 128) if corr_scale is None else corr_scale), flags,
+        out.data_ptr(), _lib.dtype_code(out), out.stride(0), out.stride(1), _lib.stream_handle(dev),
+    )
+    _lib.check(rc, "tq_prefill")
+    return out
+
+
 # ---- conversion to and from the reference's array-of-slots layout ------------------------
 
 def _tile_fields(fmt: PagedKVFormat):
