@@ -189,6 +189,45 @@ def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, 
     return res, state
 
 
+def prefill_case(dev, steps, warmup, B=4, n=4096, Hq=48, Hkv=8, kb=3, kq=True, vb=3, bs=16, seed=7):
+    """Full causal prefill over the packed cache: B sequences of n new tokens each (already
+    compressed into the cache), one tq_prefill call per step."""
+    import torch
+    from turboquant.core import make_codebook
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, prefill_paged
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    nbl = math.ceil(n / bs)
+    nb = B * nbl + 8
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))
+    bt = perm[:B * nbl].view(B, nbl).to(torch.int32).to(dev)
+    lens_host = [n] * B
+    lens = torch.tensor(lens_host, dtype=torch.int32, device=dev)
+    kc, kbnd = make_codebook(D, kb, device=dev)
+    vc, vbnd = (kc, kbnd) if vb == kb else make_codebook(D, vb, device=dev)
+    k_cache = allocate_cache(nb, Hkv, kf, device=dev)
+    v_cache = allocate_cache(nb, Hkv, vf, device=dev)
+    fill_paged((k_cache, v_cache), (kf, vf), (kc, vc), (kbnd, vbnd), bt, lens_host, Hkv, gen, dev)
+    q = torch.randn((B * n, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    cu = torch.arange(0, B * n + 1, n, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+
+    def step():
+        prefill_paged(q, cu, k_cache, kf, kc, v_cache, vf, vc, bt, lens, causal=True, max_q_len=n, out=out)
+
+    ms = timed(step, steps, warmup)
+    # (query row, visible key) pairs x 3 products (q.k, qp.signs, p.v) x 2 x 128 flops
+    pairs = B * Hq * n * (n + 1) // 2
+    flops = pairs * (3 if kq else 2) * 2 * D
+    return {"workload": f"prefill: {B} x {n} new tokens (causal), Hq {Hq} / Hkv {Hkv}, "
+                        f"turbo{kb}{'+QJL' if kq else ''} K / turbo{vb} V, bs {bs}",
+            "us_per_layer": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
+            "frac_of_fp16_mfma": flops / (ms * 1e-3) / 1e12 / 2500.0,
+            "algorithmic_flops": flops}
+
+
 def compress_case(dev, steps, warmup):
     """K and V [16384, 8, 128] bf16 -> turbo4 paged blocks of 16 in 8192 blocks."""
     import torch
@@ -289,7 +328,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["config2", "config3", "config4", "config5"], default=None)
+    ap.add_argument("--only", choices=["config2", "config3", "config4", "config5", "prefill"], default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device-to-device copy (reference for rocprof byte counters)")
     args = ap.parse_args()
@@ -340,6 +379,10 @@ def main():
                             extra_compress=True)
         extra["config5"] = r5
         print(f"# config5 {r5['us_per_layer']:.1f} us/step", file=sys.stderr, flush=True)
+    if args.only in (None, "prefill"):
+        rp = prefill_case(dev, min(steps, 20), min(warmup, 5))
+        extra["prefill"] = rp
+        print(f"# prefill {rp['us_per_layer']:.1f} us/layer, {rp['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
     if args.only in (None, "config2"):
         r2 = compress_case(dev, steps, warmup)
         extra["config2"] = r2

@@ -184,6 +184,71 @@ def test_paged_backend_decode_step(dev):
             want[s, hs] = odec.decode_dense(q64[s, hs], q64[s, hs], k, sg, rn, v, impl.scale, cs) @ H64
     np.testing.assert_allclose(output.view(S, Hq, 128).float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
 
-    with pytest.raises(NotImplementedError):
-        impl.forward(None, q, None, None, kv, PagedDecodeMetadata(meta.block_tables, meta.seq_lens, 70, num_prefills=1),
-                     output=output)
+
+def test_paged_backend_mixed_batch(dev):
+    """A batch of two decode sequences followed by two extend sequences (vLLM order): the
+    decode rows equal decode_paged(rotate=True), the extend rows prefill_paged(rotate=True) -
+    bit for bit - and the extend rows match the oracle's causal prefill of q H rotated back."""
+    from turboquant.integration.paged_backend import (PagedDecodeMetadata, TurboQuantPagedImpl,
+                                                      TurboQuantPagedState)
+    from turboquant.kernels.paged import decode_paged, prefill_paged
+
+    Hq, Hkv, bs = 8, 2, 16
+    state = TurboQuantPagedState(128, device=dev, k_bits=3, v_bits=3, k_qjl=True, block_size=bs)
+    impl = TurboQuantPagedImpl(Hq, 128, 1 / math.sqrt(128), Hkv, state)
+    lens = [90, 17, 40, 129]
+    n_new = [1, 1, 40, 33]             # the third is a full prefill, the fourth an extend
+    S = len(lens)
+    g = torch.Generator().manual_seed(4)
+    nb = 40
+    perm = torch.randperm(nb, generator=g)
+    bt = torch.full((S, 9), -1, dtype=torch.int32)
+    o = 0
+    for s, L in enumerate(lens):
+        nbl = (L + bs - 1) // bs
+        bt[s, :nbl] = perm[o:o + nbl].int()
+        o += nbl
+    slots = torch.cat([torch.tensor([int(bt[s, t // bs]) * bs + t % bs for t in range(L)]) for s, L in enumerate(lens)])
+    key = torch.randn(slots.numel(), Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    value = torch.randn(slots.numel(), Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    kv = state.allocate_kv_cache(nb, Hkv)
+    impl.do_kv_cache_update(None, key, value, kv, slots.to(dev))
+    k_cache, v_cache = state.split_kv_cache(kv)
+
+    T = sum(n_new)
+    qsl = torch.tensor([0] + list(np.cumsum(n_new)), dtype=torch.int32, device=dev)
+    q = torch.randn(T + 3, Hq * 128, generator=g).to(torch.bfloat16).to(dev)  # 3 padding rows
+    output = torch.full((T + 3, Hq * 128), 7.0, dtype=torch.bfloat16, device=dev)
+    btd, lensd = bt.to(dev), torch.tensor(lens, dtype=torch.int32, device=dev)
+    md = PagedDecodeMetadata(btd, lensd, max(lens), seq_lens_host=lens, query_start_loc=qsl, num_decodes=2,
+                             max_query_len=40)
+    impl.forward(None, q, None, None, kv, md, output=output)
+    torch.cuda.synchronize()
+    dec = decode_paged(q[:2].view(2, Hq, 128), k_cache, state.k_format, state.k_centroids, v_cache, state.v_format,
+                       state.v_centroids, btd[:2], lensd[:2], sm_scale=impl.scale, max_seq_len=max(lens),
+                       seq_lens_host=lens[:2], rotate=True)
+    pre = prefill_paged(q[2:T].view(T - 2, Hq, 128), qsl[2:] - 2, k_cache, state.k_format, state.k_centroids,
+                        v_cache, state.v_format, state.v_centroids, btd[2:], lensd[2:], sm_scale=impl.scale,
+                        rotate=True)
+    torch.cuda.synchronize()
+    assert torch.equal(output[:2].view(2, Hq, 128), dec)
+    assert torch.equal(output[2:T].view(T - 2, Hq, 128), pre)
+    assert torch.all(output[T:] == 7.0)            # padding rows untouched
+
+    kc64 = state.k_centroids.double().cpu().numpy()
+    kn, vn = k_cache.cpu().numpy(), v_cache.cpu().numpy()
+    G = Hq // Hkv
+    cs = math.sqrt(math.pi / 2) / 128
+    qn = q[:T].view(T, Hq, 128).float().cpu().numpy().astype(np.float64) @ H64
+    got = output[:T].view(T, Hq, 128).float().cpu().numpy()
+    for s in (2, 3):
+        L, n = lens[s], n_new[s]
+        r0 = int(sum(n_new[:s]))
+        for h in range(Hkv):
+            kp = opaged.gather_sequence(kn, bt[s].numpy(), L, h, bs, 3, True)
+            vp = opaged.gather_sequence(vn, bt[s].numpy(), L, h, bs, 3, False)
+            k, sg, rn = odec.dequant_keys(kp, kc64, 3, True)
+            v = odec.dequant_values(vp, kc64, 3)
+            hs = slice(h * G, (h + 1) * G)
+            want = odec.prefill_dense(qn[r0:r0 + n, hs], qn[r0:r0 + n, hs], k, sg, rn, v, impl.scale, cs) @ H64
+            np.testing.assert_allclose(got[r0:r0 + n, hs], want, rtol=RTOL, atol=ATOL)

@@ -9,11 +9,13 @@
 // (new token i, query head of the GQA group) pair, rows ordered token-major, so a workgroup
 // serves 64 / G tokens with all G heads of the group and each K/V tile is dequantised once for
 // all of them.  The cache is walked in 16-token tiles (a tile never spans two blocks).  Per
-// tile the 256 threads dequantise into one of two LDS buffers (thread t: token t / 16, dims
-// 8 (t % 16) .. + 7) while the waves compute on the other:
+// tile the 256 threads dequantise into one of two LDS buffers (thread t: token t % 16, dims
+// 8 (t / 16) .. + 7) while the waves compute on the other:
 //   Khat [16 tok][128] fp16 = c[idx] * cscale       row stride 272 B (16 B pad: no bank clash)
 //   Shat [16 tok][128] fp16 = +-1                    QJL keys only
-//   VhatT [128 dim][16 tok] fp16 = c[vidx] * cscale  transposed: the PV A operand
+//   VhatT [128 dim][16 tok] fp16 = c[vidx] * cscale  transposed: the PV A operand; row stride
+//                                                    40 B, so the 4 dim rows a wave writes at
+//                                                    once start 16 banks apart
 //   kn1, kr2, vn [16] f32 = norm * c1, rnorm * c2, vnorm (c1, c2 below)
 // Each wave computes for its 16 rows (MFMA layout: lane l, n = l % 16, g = l / 16):
 //   S^T [16 tok x 16 rows] = Khat . Q^T     4 x mfma_f32_16x16x32_f16 (B: q row n in registers)
@@ -36,8 +38,9 @@ constexpr float kWhtH = 0.08838834764831845f;  // 1 / sqrt(128)
 constexpr int kRowsPerWG = 64;
 constexpr int kKRow = 272;                       // bytes per token row of Khat / Shat
 constexpr int kOffS = 16 * kKRow;                // Shat
-constexpr int kOffV = 2 * 16 * kKRow;            // VhatT: 128 rows of 32 bytes
-constexpr int kOffN = kOffV + 128 * 32;          // kn1[16], kr2[16], vn[16]
+constexpr int kVRow = 40;                        // bytes per dim row of VhatT (16 tokens + pad)
+constexpr int kOffV = 2 * 16 * kKRow;            // VhatT: 128 rows
+constexpr int kOffN = kOffV + 128 * kVRow;       // kn1[16], kr2[16], vn[16]
 constexpr int kBuf = kOffN + 3 * 16 * 4;         // one tile buffer
 constexpr int kOffTab = 2 * kBuf;                // pair tables: K then V, 256 x 4 bytes each
 constexpr int kLdsBytes = kOffTab + 2 * 1024;
@@ -90,6 +93,7 @@ struct Raw {
     uint32_t kw[2], vw[2];   // dwords holding the 8 index fields (funnel-shifted by the byte offset)
     uint32_t sg0, sg1, sg2, sg3;  // sign bits (QJL keys): sg0 = dword of byte pp, or the whole row if permuted
     uint32_t nrm;            // fp16 norm bits (threads 0-47: K norm, K residual norm, V norm)
+    int nv;                  // usable rows of the tile (0: unreadable block)
 };
 
 // The 8 index fields of dims 8pp..8pp+7: bytes bits*pp .. of the token's index row, read as
@@ -108,7 +112,7 @@ __device__ __forceinline__ uint32_t fields(const uint32_t (&w)[2], int bits, int
 }
 
 template <int KB, bool KQJL, int VB>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -198,8 +202,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     }
 
     // ---- dequantisation of tile ti by this thread: token tt, dims 8pp .. 8pp + 7 ----
-    const int tt = tid >> 4;
-    const int pp = tid & 15;
+    const int tt = tid & 15;
+    const int pp = tid >> 4;
     const int32_t* bt_row = p.bt + (int64_t)s * p.bt_stride;
     // block of tile ti (wave-uniform) and whether it is readable
     auto tile_block = [&](int ti, int& nv) -> int64_t {
@@ -214,8 +218,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
         return blk;
     };
     auto load_raw = [&](int ti, Raw& w) {
-        int nv;
-        const int64_t blk = tile_block(ti, nv);
+        const int64_t blk = tile_block(ti, w.nv);
         const int r = (ti * 16) % p.block_size + tt;
         auto at = [&](const tq_region& rg, int row) -> const uint8_t* {
             return static_cast<const uint8_t*>(rg.ptr) + blk * rg.stride_block + (int64_t)kh * rg.stride_head +
@@ -243,8 +246,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
         else if (tid >= 32 && tid < 48) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.vnorm, nr));
     };
     auto store_tile = [&](int ti, const Raw& w, int buf) {
-        int nv;
-        tile_block(ti, nv);
+        const int nv = w.nv;
         uint8_t* b = s_lds + buf * kBuf;
         const uint8_t* tab = s_lds + kOffTab;
         {
@@ -286,9 +288,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
                 const uint32_t e = (f >> (2 * VB * k)) & ((1u << (2 * VB)) - 1u);
                 const uint32_t h2 = *reinterpret_cast<const uint32_t*>(tv + 4 * e);
                 const int d = 8 * pp + 2 * k;
-                *reinterpret_cast<uint16_t*>(b + kOffV + d * 32 + 2 * tt) = (uint16_t)h2;
-                *reinterpret_cast<uint16_t*>(b + kOffV + (d + 1) * 32 + 2 * tt) =
-                    (uint16_t)(h2 >> 16);
+                *reinterpret_cast<uint16_t*>(b + kOffV + d * kVRow + 2 * tt) = (uint16_t)h2;
+                *reinterpret_cast<uint16_t*>(b + kOffV + (d + 1) * kVRow + 2 * tt) = (uint16_t)(h2 >> 16);
             }
         }
         if (tid < 48) {
@@ -301,11 +302,14 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     };
 
     __syncthreads();  // pair tables
-    Raw raw;
+    // Raw data runs two tiles ahead of the compute (two register sets; tile t + 2 is loaded
+    // while tile t is computed and tile t + 1 is dequantised).
+    Raw rawA, rawB;
     if (ntiles > 0) {
-        load_raw(0, raw);
-        store_tile(0, raw, 0);
+        load_raw(0, rawA);
+        store_tile(0, rawA, 0);
     }
+    if (ntiles > 1) load_raw(1, rawB);
     __syncthreads();
 
     float m = kNegInf, lsum = 0.f;
@@ -313,11 +317,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
 
-    for (int ti = 0; ti < ntiles; ++ti) {
+    // One tile: ld holds tile ti's raw data (already in LDS) and receives tile ti + 2's; nx holds
+    // tile ti + 1's, dequantised into the other buffer at the end.
+    auto step = [&](int ti, Raw& ld, const Raw& nx) {
         const int buf = ti & 1;
-        if (ti + 1 < ntiles) load_raw(ti + 1, raw);
-        int nv;
-        tile_block(ti, nv);
+        const int nv = ld.nv;  // tile ti
+        if (ti + 2 < ntiles) load_raw(ti + 2, ld);
         const uint8_t* b = s_lds + buf * kBuf;
         // scores^T: tokens 4g + r of row n
         tq_floatx4 sc = {0.f, 0.f, 0.f, 0.f};
@@ -369,11 +374,16 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const tq_half4v a = *reinterpret_cast<const tq_half4v*>(
-                b + kOffV + (16 * j + n) * 32 + 8 * g);
+                b + kOffV + (16 * j + n) * kVRow + 8 * g);
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[j], 0, 0, 0);
         }
-        if (ti + 1 < ntiles) store_tile(ti + 1, raw, buf ^ 1);
+        if (ti + 1 < ntiles) store_tile(ti + 1, nx, buf ^ 1);
         __syncthreads();
+    };
+    for (int ti = 0; ti < ntiles; ti += 2) {
+        step(ti, rawA, rawB);
+        if (ti + 1 >= ntiles) break;
+        step(ti + 1, rawB, rawA);
     }
 
     // ---- normalise, rotate, write ----

@@ -15,12 +15,14 @@ the hot path is here, in the shapes the reference's backends use:
   last `num_protected_layers` layers are not compressed (get_state returns None and the caller
   keeps its own attention for them, as the reference does), or, with `protected_bits`, get a
   4-bit (or other) packed format of their own.
-- TurboQuantPagedImpl: the decode half of an attention implementation in vLLM's shape
+- TurboQuantPagedImpl: an attention implementation in vLLM's shape
   (TurboQuantFP4Impl.do_kv_cache_update / forward and TurboQuantFP4Backend.get_kv_cache_shape,
   integration/tq_fp4_backend.py:389-735).  One uint8 tensor [num_blocks, num_kv_heads,
   k_tile + v_tile] holds both caches: each (block, KV head) has its K tile followed by its V
-  tile.  Prefill / extend over the packed cache is not part of this build: forward accepts
-  decode tokens only (one query token per sequence).
+  tile.  forward runs the decode sequences (one new token each, first in the batch, as vLLM
+  orders them) through the split-K decode kernels and the prefill / extend sequences through
+  the tiled prefill kernel, both reading the packed cache (the reference FP4 backend falls back
+  to dequantised attention for extends, tq_fp4_backend.py:558-601).
 """
 
 from __future__ import annotations
@@ -31,7 +33,7 @@ from typing import Optional, Sequence
 import torch
 
 from turboquant.core import make_codebook, make_wht_matrix
-from turboquant.kernels.paged import PagedKVFormat, compress_paged, decode_paged
+from turboquant.kernels.paged import PagedKVFormat, compress_paged, decode_paged, prefill_paged
 from turboquant.kernels.rotation import wht_rows
 
 
@@ -118,6 +120,16 @@ class TurboQuantPagedState:
                             tokens_per_chunk=tokens_per_chunk, workspace=workspace,
                             rotate=not self.weights_fused)
 
+    def prefill(self, q: torch.Tensor, cu_seqlens_q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                block_tables: torch.Tensor, seq_lens: torch.Tensor, sm_scale: Optional[float] = None,
+                max_q_len: Optional[int] = None, out: Optional[torch.Tensor] = None,
+                causal: bool = True) -> torch.Tensor:
+        """Prefill / extend attention of q [T, Hq, 128] (new tokens of each sequence, already in
+        the cache) in the model's basis."""
+        return prefill_paged(q, cu_seqlens_q, k_cache, self.k_format, self.k_centroids, v_cache, self.v_format,
+                             self.v_centroids, block_tables, seq_lens, sm_scale=sm_scale, causal=causal,
+                             rotate=not self.weights_fused, max_q_len=max_q_len, out=out)
+
 
 class TurboQuantPagedConfig:
     """Which layers are compressed, and with which formats.
@@ -194,13 +206,20 @@ def reset_tq_paged_config() -> None:
 
 @dataclass
 class PagedDecodeMetadata:
-    """What forward needs of the framework's attention metadata (decode batch)."""
+    """What forward needs of the framework's attention metadata.
+
+    Without query_start_loc every sequence is a decode (one query token).  With it (int32
+    [num_seqs + 1], vLLM's query_start_loc), the first num_decodes sequences are decodes and the
+    rest prefill / extend sequences whose new tokens are the last ones of seq_lens.
+    """
 
     block_tables: torch.Tensor                   # int32 [num_seqs, max_blocks]
-    seq_lens: torch.Tensor                       # int32 [num_seqs], including the new token
+    seq_lens: torch.Tensor                       # int32 [num_seqs], including the new tokens
     max_seq_len: int                             # host-side upper bound of seq_lens
     seq_lens_host: Optional[Sequence[int]] = None
-    num_prefills: int = 0                        # prefill / extend tokens are not supported
+    query_start_loc: Optional[torch.Tensor] = None
+    num_decodes: Optional[int] = None            # default: all sequences when query_start_loc is None
+    max_query_len: Optional[int] = None          # host-side bound of the prefill query counts
 
 
 class TurboQuantPagedImpl:
@@ -252,21 +271,33 @@ class TurboQuantPagedImpl:
                 attn_metadata: Optional[PagedDecodeMetadata], output: Optional[torch.Tensor] = None,
                 output_scale: Optional[torch.Tensor] = None,
                 output_block_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Decode: query [num_seqs, num_heads, head_size] -> output of the same shape."""
+        """query [num_tokens, num_heads * head_size] (or [num_tokens, num_heads, head_size]) ->
+        output of the same shape: decode tokens first (one per sequence), then the new tokens of
+        the prefill / extend sequences."""
         if output is None:
             raise ValueError("Output tensor must be provided.")
         if output_scale is not None or output_block_scale is not None:
             raise NotImplementedError("fused output quantization is not supported")
         if attn_metadata is None:
             return output.fill_(0)
-        if attn_metadata.num_prefills:
-            raise NotImplementedError("prefill / extend over the packed cache is not part of this build")
-        n = attn_metadata.seq_lens.shape[0]
-        q = query[:n].view(n, self.num_heads, self.head_size)
-        out = output[:n].view(n, self.num_heads, self.head_size)
+        md = attn_metadata
+        S = md.seq_lens.shape[0]
+        nd = S if md.query_start_loc is None else (md.num_decodes if md.num_decodes is not None else 0)
         k_cache, v_cache = self.state.split_kv_cache(kv_cache)
-        self.state.decode(q, k_cache, v_cache, attn_metadata.block_tables, attn_metadata.seq_lens,
-                          sm_scale=self.scale, sparse_threshold=self.sparse_threshold,
-                          max_seq_len=attn_metadata.max_seq_len, seq_lens_host=attn_metadata.seq_lens_host,
-                          out=out)
+        if nd:
+            q = query[:nd].view(nd, self.num_heads, self.head_size)
+            out = output[:nd].view(nd, self.num_heads, self.head_size)
+            lens_host = md.seq_lens_host[:nd] if md.seq_lens_host is not None else None
+            self.state.decode(q, k_cache, v_cache, md.block_tables[:nd], md.seq_lens[:nd],
+                              sm_scale=self.scale, sparse_threshold=self.sparse_threshold,
+                              max_seq_len=md.max_seq_len, seq_lens_host=lens_host, out=out)
+        if nd < S:
+            qsl = md.query_start_loc
+            t0 = nd  # decode tokens come first, one per sequence
+            cu = (qsl[nd:] - t0).to(torch.int32)
+            tp = query.shape[0] - t0
+            q = query[t0:].view(tp, self.num_heads, self.head_size)
+            out = output[t0:].view(tp, self.num_heads, self.head_size)
+            self.state.prefill(q, cu, k_cache, v_cache, md.block_tables[nd:], md.seq_lens[nd:], sm_scale=self.scale,
+                               max_q_len=md.max_query_len, out=out)
         return output
