@@ -96,17 +96,9 @@ struct Raw {
     int nv;                  // usable rows of the tile (0: unreadable block)
 };
 
-// The 8 index fields of dims 8pp..8pp+7: bytes bits*pp .. of the token's index row, read as
-// the two aligned dwords around them (the second one clamped to the row: a field that ends in
-// the row's last dword lies entirely in it).
-__device__ __forceinline__ void load_fields(const uint8_t* row, int bits, int pp, uint32_t (&w)[2]) {
-    const int o = bits * pp;
-    const int w0 = o >> 2;
-    const int w1 = (w0 + 1 < 4 * bits) ? w0 + 1 : w0;
-    const uint32_t* r32 = reinterpret_cast<const uint32_t*>(row);
-    w[0] = r32[w0];
-    w[1] = r32[w1];
-}
+// The 8 index fields of dims 8pp..8pp+7 start at byte bits*pp of the token's index row; the
+// thread loads the two aligned dwords around them (the second one clamped to the row: a field
+// that ends in the row's last dword lies entirely in it) and shifts the window down.
 __device__ __forceinline__ uint32_t fields(const uint32_t (&w)[2], int bits, int pp) {
     return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)((bits * pp) & 3) * 8u);
 }
@@ -217,33 +209,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         }
         return blk;
     };
+    // Loop-invariant byte offsets of this thread's data inside a 16-row tile (rows are less than
+    // 2^31 / 16 bytes apart: checked on the host), added to the tile's wave-uniform base address.
+    auto field_off = [&](const tq_region& rg, int bits, int second) -> uint32_t {
+        const int w0 = (bits * pp) >> 2;
+        const int w1 = (w0 + 1 < 4 * bits) ? w0 + 1 : w0;
+        return (uint32_t)(tt * rg.stride_row) + 4u * (uint32_t)(second ? w1 : w0);
+    };
+    const uint32_t o_k0 = field_off(p.kidx, KB, 0), o_k1 = field_off(p.kidx, KB, 1);
+    const uint32_t o_v0 = field_off(p.vidx, VB, 0), o_v1 = field_off(p.vidx, VB, 1);
+    const uint32_t o_sg = (uint32_t)(tt * p.ksig.stride_row) + (p.k_perm ? 0u : 4u * (uint32_t)(pp >> 2));
+    const int ntok = tid & 15;  // token of the norm threads (0-47)
+    const tq_region& nreg = tid < 16 ? p.knorm : (tid < 32 ? p.krnorm : p.vnorm);
+    const uint32_t o_nm = (uint32_t)(ntok * nreg.stride_row);
     auto load_raw = [&](int ti, Raw& w) {
         const int64_t blk = tile_block(ti, w.nv);
-        const int r = (ti * 16) % p.block_size + tt;
-        auto at = [&](const tq_region& rg, int row) -> const uint8_t* {
+        const int row0 = (ti * 16) % p.block_size;
+        auto base = [&](const tq_region& rg) -> const uint8_t* {  // wave-uniform
             return static_cast<const uint8_t*>(rg.ptr) + blk * rg.stride_block + (int64_t)kh * rg.stride_head +
-                   (int64_t)row * rg.stride_row;
+                   (int64_t)row0 * rg.stride_row;
         };
-        load_fields(at(p.kidx, r), KB, pp, w.kw);
-        load_fields(at(p.vidx, r), VB, pp, w.vw);
+        auto ld32 = [](const uint8_t* b, uint32_t o) { return *reinterpret_cast<const uint32_t*>(b + (uint64_t)o); };
+        const uint8_t* bk = base(p.kidx);
+        w.kw[0] = ld32(bk, o_k0);
+        w.kw[1] = ld32(bk, o_k1);
+        const uint8_t* bv = base(p.vidx);
+        w.vw[0] = ld32(bv, o_v0);
+        w.vw[1] = ld32(bv, o_v1);
         if (KQJL) {
             // natural order: the dword holding byte pp; permuted: the whole row
-            const uint32_t* sr = reinterpret_cast<const uint32_t*>(at(p.ksig, r));
+            const uint8_t* bs = base(p.ksig);
+            w.sg0 = ld32(bs, o_sg);
             if (!p.k_perm) {
-                w.sg0 = sr[pp >> 2];
                 w.sg1 = w.sg2 = w.sg3 = 0;
             } else {
-                w.sg0 = sr[0];
-                w.sg1 = sr[1];
-                w.sg2 = sr[2];
-                w.sg3 = sr[3];
+                w.sg1 = ld32(bs, o_sg + 4);
+                w.sg2 = ld32(bs, o_sg + 8);
+                w.sg3 = ld32(bs, o_sg + 12);
             }
         }
         w.nrm = 0;
-        const int nr = (ti * 16) % p.block_size + (tid & 15);
-        if (tid < 16) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.knorm, nr));
-        else if (tid < 32 && KQJL) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.krnorm, nr));
-        else if (tid >= 32 && tid < 48) w.nrm = *reinterpret_cast<const uint16_t*>(at(p.vnorm, nr));
+        if (tid < 16) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.knorm) + (uint64_t)o_nm);
+        else if (tid < 32 && KQJL) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.krnorm) + (uint64_t)o_nm);
+        else if (tid >= 32 && tid < 48) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.vnorm) + (uint64_t)o_nm);
     };
     auto store_tile = [&](int ti, const Raw& w, int buf) {
         const int nv = w.nv;
@@ -346,12 +354,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             *reinterpret_cast<const tq_floatx4*>(b + kOffN + 64 + 16 * g);
         const tq_floatx4 vn =
             *reinterpret_cast<const tq_floatx4*>(b + kOffN + 128 + 16 * g);
+        // tokens 4g + r below lim are usable and visible to the row (lim: one compare per token)
+        int lim = qpos - ti * 16 + 1 - 4 * g;
+        lim = lim < nv - 4 * g ? lim : nv - 4 * g;
         float sv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int tok = 4 * g + r;
             const float v = __builtin_fmaf(kn1[r], sc[r], kr2[r] * tj[r]);
-            sv[r] = (tok < nv && ti * 16 + tok <= qpos) ? v : kNegInf;
+            sv[r] = r < lim ? v : kNegInf;
         }
         float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
         mt = max_over_groups(mt);
@@ -465,6 +475,10 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
         if ((rc = check_region(k->signs, 4))) return rc;
         if ((rc = check_region(k->rnorm, 2))) return rc;
     }
+    // per-thread offsets inside a tile are 32-bit: 16 rows of any region below 2^31 bytes
+    const tq_region* regs[6] = {&k->idx, &k->norm, &v->idx, &v->norm, &k->signs, &k->rnorm};
+    for (int r = 0; r < (k->qjl ? 6 : 4); ++r)
+        if (regs[r]->stride_row < 0 || regs[r]->stride_row >= (1ll << 26)) return TQ_ERR_INVALID_ARGUMENT;
     const int group = num_q_heads / num_kv_heads;
     const int64_t rows = (int64_t)max_q_len * group;
     const int64_t n_rb = (rows + kRowsPerWG - 1) / kRowsPerWG;
