@@ -112,7 +112,7 @@ def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, 
 
     gen = torch.Generator(device=dev).manual_seed(seed)
     kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout="values")
     blocks_per = [math.ceil(L / bs) for L in lens_host]
     maxb = max(blocks_per)
     nb = sum(blocks_per) + 64
@@ -198,7 +198,7 @@ def prefill_case(dev, steps, warmup, B=4, n=4096, Hq=48, Hkv=8, kb=3, kq=True, v
 
     gen = torch.Generator(device=dev).manual_seed(seed)
     kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout="values")
     nbl = math.ceil(n / bs)
     nb = B * nbl + 8
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(seed))
@@ -240,13 +240,14 @@ def compress_case(dev, steps, warmup):
     perm = torch.randperm(nb, generator=torch.Generator().manual_seed(2))
     slots = (perm[torch.arange(T) // bs] * bs + torch.arange(T) % bs).to(torch.int32).to(dev)
     fmt = PagedKVFormat(bits=4, qjl=False, block_size=bs)
+    vfmt = PagedKVFormat(bits=4, qjl=False, block_size=bs, layout="values")
     c, b = make_codebook(D, 4, device=dev)
     kc = allocate_cache(nb, H, fmt, device=dev)
-    vc = allocate_cache(nb, H, fmt, device=dev)
+    vc = allocate_cache(nb, H, vfmt, device=dev)
 
     def step():
         compress_paged(k, slots, kc, fmt, c, b)
-        compress_paged(v, slots, vc, fmt, c, b)
+        compress_paged(v, slots, vc, vfmt, c, b)
 
     ms = timed(step, steps, warmup)
     alg = 2 * (T * H * D * 2 + T * H * fmt.token_bytes) + T * 4
@@ -280,9 +281,11 @@ def cpu_baseline_decode(state, max_seconds=20.0):
     except ImportError:  # pragma: no cover
         threadpool_limits = None
     threads = min(os.cpu_count() or 1, 16)
+    from turboquant.kernels.paged import to_rows_layout
     kf, vf = state["kf"], state["vf"]
-    kc_np = state["k_cache"].cpu().numpy()
-    vc_np = state["v_cache"].cpu().numpy()
+    # the payload in row form (index rows, then sign rows): what _gather_tiles reads
+    kc_np = to_rows_layout(state["k_cache"], kf).cpu().numpy()
+    vc_np = to_rows_layout(state["v_cache"], vf).cpu().numpy()
     bt = state["bt"].cpu().numpy()
     q = state["q"].float().cpu().numpy().astype(np.float64)
     kcb = state["kc"].double().cpu().numpy()

@@ -112,15 +112,36 @@ int tq_compress_packed(const void* x, int x_dtype, int64_t x_row_stride, int64_t
                        tq_stream_t stream);
 
 /*
+ * Paged tile layouts (tile_layout of tq_compress_paged, layout of tq_kv_view).  A tile holds
+ * the block_size tokens of one (physical block, KV head): a payload region of block_size * P
+ * bytes, P = 16*bits (+ 16 with QJL signs), then [block_size fp16 norms][block_size fp16
+ * residual norms, QJL only].  Per token the bytes are the reference's: the index fields as a
+ * little-endian bit stream (16*bits bytes), the 16 sign bytes (bit d = dim d), fp16 norms.  The
+ * payload is stored per 16-token sub-tile j (rows 16j..16j+15, 16*P bytes at j*16*P):
+ *   TQ_TILE_ROWS   the index rows of all block_size tokens (16*bits bytes each), then their
+ *                  sign rows (16 bytes each), at the offsets tq_tile_offsets returns (no
+ *                  sub-tile split);
+ *   TQ_TILE_KEYS   chunk (4n + g) of C = 4*bits (+ 4) bytes for row n (0..15) and dim quarter
+ *                  g (dims 32g..32g+31): the 4*bits index bytes of those dims, then their 4
+ *                  sign bytes (QJL) - what one lane of the decode kernel reads for one key;
+ *   TQ_TILE_VALUES chunk (16g + n) of 4*bits bytes for row group g (rows 4g..4g+3) and dim
+ *                  group n (dims 8n..8n+7): the bits bytes of those 8 dims of row 4g + r at
+ *                  r*bits (no QJL) - what one lane reads for the value product.
+ * The lane-grouped layouts let a decode lane fetch its key data and its value data for a
+ * 16-token tile with one load each.
+ */
+#define TQ_TILE_ROWS   0
+#define TQ_TILE_KEYS   1
+#define TQ_TILE_VALUES 2
+
+/*
  * Fused paged compression: x [num_tokens, num_heads, 128] -> packed rows written into the
  * paged cache at slot_mapping[t] (block = slot / block_size, row = slot % block_size).
  * Negative slots are skipped (the reference clamps them to 0, integration/vllm_backend.py:223-230).
  * Math as tq_polarquant_compress; stored: index bits, fp16 norm and, with use_qjl, sign bits
- * and fp16 residual norm.
- * Cache: one tile per (physical block, KV head) at cache + block*stride_block + head*stride_head;
- * a tile is the SoA layout returned by tq_tile_bytes()/tq_tile_offsets():
- *   [block_size rows x 16*bits idx bytes][block_size x 16 sign bytes, QJL only]
- *   [block_size fp16 norms][block_size fp16 residual norms, QJL only].
+ * and fp16 residual norm, in the tile layout tile_layout (TQ_TILE_VALUES: no QJL).
+ * Cache: one tile per (physical block, KV head) at cache + block*stride_block + head*stride_head,
+ * tq_tile_bytes() bytes.
  * Requirements: cache, strides 16-byte aligned; block_size multiple of 16; bits 2..4.
  * Slots >= num_blocks*block_size are skipped.
  * Replaces turbo4_fp8_compress_and_scatter (integration/vllm_backend.py:179-230) and the
@@ -131,11 +152,13 @@ int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_token, int64_
                       const void* slot_mapping, int slot_dtype,
                       void* cache, int64_t cache_stride_block, int64_t cache_stride_head,
                       int64_t num_blocks, int block_size,
-                      int bits, int use_qjl, int rotate, float wht_scale,
+                      int bits, int use_qjl, int tile_layout, int rotate, float wht_scale,
                       const float* centroids, const float* boundaries,
                       tq_stream_t stream);
 
-/* Bytes of one (block, KV head) tile and the byte offsets of its regions. */
+/* Bytes of one (block, KV head) tile (any layout) and the byte offsets of its regions in the
+ * TQ_TILE_ROWS layout (the lane-grouped layouts keep off_idx = 0, off_norm and off_rnorm; their
+ * signs are inside the payload). */
 int64_t tq_tile_bytes(int block_size, int bits, int use_qjl);
 int tq_tile_offsets(int block_size, int bits, int use_qjl,
                     int64_t* off_idx, int64_t* off_signs, int64_t* off_norm, int64_t* off_rnorm);
@@ -167,6 +190,10 @@ typedef struct tq_kv_view {
                                 scale back out in fp32; a scale in [1,2) chosen so every scaled
                                 centroid is nearly exact in fp16 removes the table's rounding.
                                 0 means 1. */
+    int32_t layout;          /* TQ_TILE_ROWS: the regions above.  TQ_TILE_KEYS / TQ_TILE_VALUES
+                                (paged only): idx describes the payload region of the lane-grouped
+                                tiles (stride_row = P bytes per token, the sub-tile of row r at
+                                (r & ~15) * P), signs is unused, norm / rnorm as above. */
 } tq_kv_view;
 
 /*

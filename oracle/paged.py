@@ -1,9 +1,16 @@
 """Paged-cache oracle (test infrastructure only), numpy.
 
-Per-token payload -> tile layout of the paged cache, written token by token:
-  tile (block, head) = [bs x 16*bits idx][bs x 16 signs]? [bs x fp16 norm][bs x fp16 rnorm]?
-(signs/rnorm for QJL keys only), token at slot s -> block s // bs, row s % bs
-(integration/vllm_backend.py:223-230), negative or out-of-range slots dropped.
+Per-token payload -> tile of the paged cache, token at slot s -> block s // bs, row s % bs
+(integration/vllm_backend.py:223-230), negative or out-of-range slots dropped.  A tile is
+[payload: bs x (16*bits idx + 16 signs?) bytes][bs x fp16 norm][bs x fp16 rnorm]? (signs and
+rnorm for QJL keys only).  The payload order is the layout:
+  "rows"  : all idx rows (16*bits bytes each), then all sign rows (16 bytes each);
+  "keys"  : per 16-row sub-tile, for row n = 0..15 and dim quarter g = 0..3, one chunk: the
+            idx bytes of dims 32g..32g+31 of row n, then (QJL) their 4 sign bytes;
+  "values": per 16-row sub-tile, for row group g = 0..3 and dim group n = 0..15, one chunk:
+            the idx bytes of dims 8n..8n+7 of rows 4g, 4g+1, 4g+2, 4g+3 in turn.
+Here the sub-tiles are assembled chunk by chunk (build_subtile / split_subtile) rather than
+through byte-position formulas.
 Reference array-of-slots layout [num_blocks, bs, Hkv, slot] (kernels/sparse_v.py:293-304):
 per token idx bytes, [signs], fp16 norm, [fp16 rnorm], zero padding.
 """
@@ -14,6 +21,7 @@ import numpy as np
 
 
 def tile_offsets(block_size: int, bits: int, qjl: bool):
+    """(idx row bytes, sign rows offset ("rows" layout), norm offset, rnorm offset, tile bytes)."""
     idx_row = 16 * bits
     off_signs = block_size * idx_row
     off_norm = block_size * (idx_row + (16 if qjl else 0))
@@ -22,13 +30,87 @@ def tile_offsets(block_size: int, bits: int, qjl: bool):
     return idx_row, off_signs, off_norm, off_rnorm, tile
 
 
+def build_subtile(idx: np.ndarray, signs: np.ndarray | None, bits: int, layout: str) -> bytes:
+    """Payload bytes of 16 rows (idx [16, 16*bits], signs [16, 16] or None) in a lane-grouped
+    layout, assembled chunk by chunk."""
+    out = bytearray()
+    if layout == "keys":
+        for n in range(16):
+            for g in range(4):
+                out += bytes(idx[n, 4 * bits * g: 4 * bits * (g + 1)])
+                if signs is not None:
+                    out += bytes(signs[n, 4 * g: 4 * g + 4])
+    elif layout == "values":
+        assert signs is None
+        for g in range(4):
+            for n in range(16):
+                for r in range(4):
+                    out += bytes(idx[4 * g + r, bits * n: bits * (n + 1)])
+    else:
+        raise ValueError(layout)
+    return bytes(out)
+
+
+def split_subtile(buf: bytes, bits: int, qjl: bool, layout: str):
+    """Inverse of build_subtile: (idx [16, 16*bits], signs [16, 16] or None)."""
+    idx = np.zeros((16, 16 * bits), np.uint8)
+    signs = np.zeros((16, 16), np.uint8) if qjl else None
+    it = iter(buf)
+    take = lambda k: np.array([next(it) for _ in range(k)], np.uint8)  # noqa: E731
+    if layout == "keys":
+        for n in range(16):
+            for g in range(4):
+                idx[n, 4 * bits * g: 4 * bits * (g + 1)] = take(4 * bits)
+                if qjl:
+                    signs[n, 4 * g: 4 * g + 4] = take(4)
+    else:
+        for g in range(4):
+            for n in range(16):
+                for r in range(4):
+                    idx[4 * g + r, bits * n: bits * (n + 1)] = take(bits)
+    return idx, signs
+
+
+def _tile_rows(tile: np.ndarray, block_size: int, bits: int, qjl: bool, layout: str):
+    """(idx [bs, 16*bits], signs [bs, 16] or None) of one tile in any layout."""
+    idx_row, off_signs, _, _, _ = tile_offsets(block_size, bits, qjl)
+    if layout == "rows":
+        idx = tile[:block_size * idx_row].reshape(block_size, idx_row).copy()
+        signs = tile[off_signs:off_signs + 16 * block_size].reshape(block_size, 16).copy() if qjl else None
+        return idx, signs
+    P = idx_row + (16 if qjl else 0)
+    idx = np.zeros((block_size, idx_row), np.uint8)
+    signs = np.zeros((block_size, 16), np.uint8) if qjl else None
+    for j in range(block_size // 16):
+        i_, s_ = split_subtile(tile[16 * P * j: 16 * P * (j + 1)].tobytes(), bits, qjl, layout)
+        idx[16 * j:16 * j + 16] = i_
+        if qjl:
+            signs[16 * j:16 * j + 16] = s_
+    return idx, signs
+
+
+def _set_tile_rows(tile: np.ndarray, idx: np.ndarray, signs, block_size: int, bits: int, qjl: bool, layout: str):
+    idx_row, off_signs, _, _, _ = tile_offsets(block_size, bits, qjl)
+    if layout == "rows":
+        tile[:block_size * idx_row] = idx.reshape(-1)
+        if qjl:
+            tile[off_signs:off_signs + 16 * block_size] = signs.reshape(-1)
+        return
+    P = idx_row + (16 if qjl else 0)
+    for j in range(block_size // 16):
+        b = build_subtile(idx[16 * j:16 * j + 16], signs[16 * j:16 * j + 16] if qjl else None, bits, layout)
+        tile[16 * P * j: 16 * P * (j + 1)] = np.frombuffer(b, np.uint8)
+
+
 def scatter_tokens(payload: dict, slot_mapping: np.ndarray, num_blocks: int, num_heads: int,
-                   block_size: int, bits: int, qjl: bool, cache: np.ndarray | None = None) -> np.ndarray:
-    """payload[name]: per (token, head) arrays — idx [T,H,16b] u8, signs [T,H,16] u8,
+                   block_size: int, bits: int, qjl: bool, cache: np.ndarray | None = None,
+                   layout: str = "rows") -> np.ndarray:
+    """payload[name]: per (token, head) arrays - idx [T,H,16b] u8, signs [T,H,16] u8,
     norm [T,H] u16 bits, rnorm [T,H] u16 bits.  Returns uint8 [num_blocks, H, tile]."""
     idx_row, off_signs, off_norm, off_rnorm, tile = tile_offsets(block_size, bits, qjl)
     if cache is None:
         cache = np.zeros((num_blocks, num_heads, tile), dtype=np.uint8)
+    touched = {}
     T = len(slot_mapping)
     for t in range(T):
         s = int(slot_mapping[t])
@@ -37,37 +119,46 @@ def scatter_tokens(payload: dict, slot_mapping: np.ndarray, num_blocks: int, num
         blk, row = divmod(s, block_size)
         for h in range(num_heads):
             c = cache[blk, h]
-            c[row * idx_row:(row + 1) * idx_row] = payload["idx"][t, h]
+            if (blk, h) not in touched:
+                touched[(blk, h)] = _tile_rows(c, block_size, bits, qjl, layout)
+            rows_idx, rows_sg = touched[(blk, h)]
+            rows_idx[row] = payload["idx"][t, h]
             c[off_norm + 2 * row: off_norm + 2 * row + 2] = np.array(
                 [payload["norm"][t, h] & 0xFF, payload["norm"][t, h] >> 8], dtype=np.uint8)
             if qjl:
-                c[off_signs + 16 * row: off_signs + 16 * row + 16] = payload["signs"][t, h]
+                rows_sg[row] = payload["signs"][t, h]
                 c[off_rnorm + 2 * row: off_rnorm + 2 * row + 2] = np.array(
                     [payload["rnorm"][t, h] & 0xFF, payload["rnorm"][t, h] >> 8], dtype=np.uint8)
+    for (blk, h), (rows_idx, rows_sg) in touched.items():
+        _set_tile_rows(cache[blk, h], rows_idx, rows_sg, block_size, bits, qjl, layout)
     return cache
 
 
 def gather_sequence(cache: np.ndarray, block_table: np.ndarray, seq_len: int, head: int,
-                    block_size: int, bits: int, qjl: bool) -> dict:
+                    block_size: int, bits: int, qjl: bool, layout: str = "rows") -> dict:
     """Per-token payload of one (sequence, head) read back through the block table."""
     idx_row, off_signs, off_norm, off_rnorm, _ = tile_offsets(block_size, bits, qjl)
     out = {"idx": np.zeros((seq_len, idx_row), np.uint8), "norm": np.zeros(seq_len, np.uint16)}
     if qjl:
         out["signs"] = np.zeros((seq_len, 16), np.uint8)
         out["rnorm"] = np.zeros(seq_len, np.uint16)
+    rows = {}
     for t in range(seq_len):
         blk = int(block_table[t // block_size])
         row = t % block_size
         c = cache[blk, head]
-        out["idx"][t] = c[row * idx_row:(row + 1) * idx_row]
+        if blk not in rows:
+            rows[blk] = _tile_rows(c, block_size, bits, qjl, layout)
+        out["idx"][t] = rows[blk][0][row]
         out["norm"][t] = int(c[off_norm + 2 * row]) | (int(c[off_norm + 2 * row + 1]) << 8)
         if qjl:
-            out["signs"][t] = c[off_signs + 16 * row: off_signs + 16 * row + 16]
+            out["signs"][t] = rows[blk][1][row]
             out["rnorm"][t] = int(c[off_rnorm + 2 * row]) | (int(c[off_rnorm + 2 * row + 1]) << 8)
     return out
 
 
-def to_slots(cache: np.ndarray, block_size: int, bits: int, qjl: bool, slot_bytes: int) -> np.ndarray:
+def to_slots(cache: np.ndarray, block_size: int, bits: int, qjl: bool, slot_bytes: int,
+             layout: str = "rows") -> np.ndarray:
     """Tile layout -> reference array-of-slots [num_blocks, bs, H, slot_bytes], per token."""
     nb, H, _ = cache.shape
     idx_row, off_signs, off_norm, off_rnorm, _ = tile_offsets(block_size, bits, qjl)
@@ -75,10 +166,11 @@ def to_slots(cache: np.ndarray, block_size: int, bits: int, qjl: bool, slot_byte
     for b in range(nb):
         for h in range(H):
             c = cache[b, h]
+            ridx, rsg = _tile_rows(c, block_size, bits, qjl, layout)
             for r in range(block_size):
-                parts = [c[r * idx_row:(r + 1) * idx_row]]
+                parts = [ridx[r]]
                 if qjl:
-                    parts.append(c[off_signs + 16 * r: off_signs + 16 * r + 16])
+                    parts.append(rsg[r])
                 parts.append(c[off_norm + 2 * r: off_norm + 2 * r + 2])
                 if qjl:
                     parts.append(c[off_rnorm + 2 * r: off_rnorm + 2 * r + 2])

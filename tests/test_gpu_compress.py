@@ -241,7 +241,10 @@ def _payload_from_oracle(ref, bits, qjl, T, H):
 
 @pytest.mark.parametrize("bits,qjl", [(2, False), (2, True), (3, False), (3, True), (4, False), (4, True)])
 @pytest.mark.parametrize("block_size", [16, 32])
-def test_compress_paged_bytes(dev, bits, qjl, block_size):
+@pytest.mark.parametrize("layout", ["keys", "values", "rows"])
+def test_compress_paged_bytes(dev, bits, qjl, block_size, layout):
+    if layout == "values" and qjl:
+        pytest.skip("the values layout carries no QJL data")
     from turboquant.core import make_wht_matrix
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
     T, H, nb = 203, 3, 20
@@ -251,30 +254,34 @@ def test_compress_paged_bytes(dev, bits, qjl, block_size):
     perm[5] = -1                       # padding token: skipped
     perm[6] = nb * block_size + 3      # out of range: skipped
     slots = perm.to(torch.int32)
-    fmt = PagedKVFormat(bits=bits, qjl=qjl, block_size=block_size)
+    fmt = PagedKVFormat(bits=bits, qjl=qjl, block_size=block_size, layout=layout)
     cent, bnd = _codebook(bits)
     cache = allocate_cache(nb, H, fmt, device=dev)
     compress_paged(x.to(dev), slots.to(dev), cache, fmt, cent.to(dev), bnd.to(dev))
     got = cache.cpu().numpy()
     ref = ocomp.polarquant_compress(x.float().reshape(T * H, 128), cent, bnd, 2 ** bits, qjl, make_wht_matrix(128))
     pl = _payload_from_oracle(ref, bits, qjl, T, H)
-    want = opaged.scatter_tokens(pl, perm.numpy(), nb, H, block_size, bits, qjl)
+    want = opaged.scatter_tokens(pl, perm.numpy(), nb, H, block_size, bits, qjl, layout=layout)
     if np.array_equal(got, want):
         return
-    # Differences must come only from boundary-band indices / fp16 norm rounding of the same tokens.
+    # Differences must come only from boundary-band indices / fp16 norm rounding of the same
+    # tokens; compared per token in row form (the oracle reads any layout back into rows).
     xn = ref["x_normalized"].reshape(T, H, 128)
+    _, _, off_norm, off_rnorm, _ = opaged.tile_offsets(block_size, bits, qjl)
     for t in range(T):
         s = int(perm[t])
         if s < 0 or s >= nb * block_size:
             continue
+        blk, row = divmod(s, block_size)
         for h in range(H):
-            one = {k: v[t:t + 1, h:h + 1] for k, v in pl.items()}
-            w = opaged.scatter_tokens(one, np.array([s]), nb, 1, block_size, bits, qjl)[s // block_size, 0]
-            gt = got[s // block_size, h]
-            if np.array_equal(gt[w != 0], w[w != 0]) and np.array_equal(np.nonzero(gt)[0], np.nonzero(w)[0]):
+            gi, gs = opaged._tile_rows(got[blk, h], block_size, bits, qjl, layout)
+            wi, ws = opaged._tile_rows(want[blk, h], block_size, bits, qjl, layout)
+            same_norms = np.array_equal(got[blk, h, off_norm + 2 * row: off_norm + 2 * row + 2],
+                                        want[blk, h, off_norm + 2 * row: off_norm + 2 * row + 2])
+            if np.array_equal(gi[row], wi[row]) and (not qjl or np.array_equal(gs[row], ws[row])) and same_norms:
                 continue
-            iw = opack.unpack_indices(w[(s % block_size) * 16 * bits:(s % block_size + 1) * 16 * bits][None], bits)
-            ig = opack.unpack_indices(gt[(s % block_size) * 16 * bits:(s % block_size + 1) * 16 * bits][None], bits)
+            ig = opack.unpack_indices(gi[row][None], bits)
+            iw = opack.unpack_indices(wi[row][None], bits)
             st = ocomp.classify_index_mismatch(torch.from_numpy(ig), torch.from_numpy(iw), xn[t, h][None], bnd, BAND_ULPS)
             assert st[2] == 0, f"token {t} head {h}: out-of-band index mismatch"
     # untouched blocks stay zero
@@ -296,7 +303,7 @@ def test_config2_full_size_roundtrip(dev):
     x = (torch.randn(T, H, 128, generator=g) * scale).to(torch.bfloat16)
     perm = torch.randperm(nb, generator=g)
     slots = (perm[torch.arange(T) // bs] * bs + torch.arange(T) % bs).to(torch.int32)
-    fmt = PagedKVFormat(bits=4, qjl=False, block_size=bs)
+    fmt = PagedKVFormat(bits=4, qjl=False, block_size=bs, layout="values")
     cent, bnd = _codebook(4)
     cache = allocate_cache(nb, H, fmt, device=dev)
     compress_paged(x.to(dev), slots.to(dev), cache, fmt, cent.to(dev), bnd.to(dev))

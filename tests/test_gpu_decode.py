@@ -34,7 +34,7 @@ def random_payload(rng, n, bits, qjl, norm_scale=10.0):
     return pl
 
 
-def build_case(seed, S, Hq, Hkv, seq_lens, kb, kq, vb, bs, extra_blocks=3):
+def build_case(seed, S, Hq, Hkv, seq_lens, kb, kq, vb, bs, extra_blocks=3, layouts=("keys", "values")):
     rng = np.random.default_rng(seed)
     maxb = max(1, max(math.ceil(L / bs) for L in seq_lens))
     nb = S * maxb + extra_blocks
@@ -53,12 +53,12 @@ def build_case(seed, S, Hq, Hkv, seq_lens, kb, kq, vb, bs, extra_blocks=3):
         vp = random_payload(rng, L * Hkv, vb, False)
         kp3 = {k: v.reshape(L, Hkv, *v.shape[1:]) for k, v in kp.items()}
         vp3 = {k: v.reshape(L, Hkv, *v.shape[1:]) for k, v in vp.items()}
-        opaged.scatter_tokens(kp3, slots, nb, Hkv, bs, kb, kq, k_cache)
-        opaged.scatter_tokens(vp3, slots, nb, Hkv, bs, vb, False, v_cache)
+        opaged.scatter_tokens(kp3, slots, nb, Hkv, bs, kb, kq, k_cache, layout=layouts[0])
+        opaged.scatter_tokens(vp3, slots, nb, Hkv, bs, vb, False, v_cache, layout=layouts[1])
         k_tok[s], v_tok[s] = kp3, vp3
     q = rng.standard_normal((S, Hq, 128)).astype(np.float32)
     return dict(q=q, bt=bt, nb=nb, k_cache=k_cache, v_cache=v_cache, k_tok=k_tok, v_tok=v_tok,
-                seq_lens=np.array(seq_lens, np.int32))
+                seq_lens=np.array(seq_lens, np.int32), layouts=layouts)
 
 
 def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.0, q_round=None):
@@ -91,8 +91,8 @@ def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.
 
 def run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, dtype=torch.bfloat16, chunk=None, thresh=0.0, stats=False):
     from turboquant.kernels.paged import PagedKVFormat, decode_paged
-    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs, layout=case["layouts"][0])
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=case["layouts"][1])
     q = torch.from_numpy(case["q"]).to(dtype).to(dev)
     st = torch.zeros(2, dtype=torch.int64, device=dev) if stats else None
     out = decode_paged(q, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
@@ -110,6 +110,20 @@ def test_decode_bit_widths(dev, kb, kq, vb):
     S, Hq, Hkv, bs = 3, 8, 2, 16
     lens = [37, 1, 300]
     case = build_case(11 + kb * 7 + vb, S, Hq, Hkv, lens, kb, kq, vb, bs)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk=64)
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=qr)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,kq,vb", [(4, False, 4), (3, True, 3), (2, True, 2), (3, False, 2)])
+@pytest.mark.parametrize("layouts", [("rows", "rows"), ("keys", "rows"), ("rows", "values")])
+def test_decode_row_major_paged_tiles(dev, kb, kq, vb, layouts):
+    """Paged caches with row-major tiles (or one row-major and one lane-grouped) run the general
+    kernel; the results match the oracle like the lane-grouped fast path's."""
+    S, Hq, Hkv, bs = 3, 8, 2, 16
+    lens = [37, 1, 300]
+    case = build_case(71 + kb * 5 + vb, S, Hq, Hkv, lens, kb, kq, vb, bs, layouts=layouts)
     sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
     got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk=64)
     want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=qr)
@@ -175,7 +189,7 @@ def test_decode_workspace_reuse(dev):
     for rep, (lens, chunk) in enumerate([([300, 17, 64], 32), ([300, 17, 64], 32), ([1000, 0, 5, 77], 48)]):
         S, Hq, Hkv = len(lens), 8, 2
         case = build_case(40 + rep, S, Hq, Hkv, lens, 3, True, 3, 16)
-        kf, vf = PagedKVFormat(bits=3, qjl=True), PagedKVFormat(bits=3)
+        kf, vf = PagedKVFormat(bits=3, qjl=True), PagedKVFormat(bits=3, layout="values")
         cb = _cb(3).to(dev)
         q = torch.from_numpy(case["q"]).to(torch.bfloat16).to(dev)
         msl = max(lens)
@@ -279,7 +293,7 @@ def test_decode_constant_values_full_size(dev):
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged
     B, Hq, Hkv, ctx, bs = 64, 48, 8, 32768, 16
     kf = PagedKVFormat(bits=3, qjl=True, block_size=bs)
-    vf = PagedKVFormat(bits=3, qjl=False, block_size=bs)
+    vf = PagedKVFormat(bits=3, qjl=False, block_size=bs, layout="values")
     nb = B * ctx // bs
     g = torch.Generator(device=dev).manual_seed(4)
     k_cache = torch.randint(0, 256, (nb, Hkv, kf.tile_bytes), dtype=torch.uint8, device=dev, generator=g)
@@ -311,8 +325,8 @@ def test_decode_constant_values_full_size(dev):
     qr = q[0].float().cpu().numpy().astype(np.float64)
     G = Hq // Hkv
     for kh in range(Hkv):
-        kp = opaged.gather_sequence(kc_np, bt0, ctx, kh, bs, 3, True)
-        vp = opaged.gather_sequence(vc_np, bt0, ctx, kh, bs, 3, False)
+        kp = opaged.gather_sequence(kc_np, bt0, ctx, kh, bs, 3, True, layout="keys")
+        vp = opaged.gather_sequence(vc_np, bt0, ctx, kh, bs, 3, False, layout="values")
         k, sg, rn = odec.dequant_keys(kp, cb.double().numpy(), 3, True)
         v = odec.dequant_values(vp, cb.double().numpy(), 3)
         hs = slice(kh * G, (kh + 1) * G)

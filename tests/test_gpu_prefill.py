@@ -48,8 +48,8 @@ def oracle_prefill(case, q, cu, Hq, Hkv, kb, kq, vb, sm, cs, causal=True, qp=Non
 def run_prefill(dev, case, q, cu, kb, kq, vb, bs, sm, cs, causal=True, rotate=False, qp=None,
                 dtype=torch.bfloat16, out_dtype=None, max_q_len=None):
     from turboquant.kernels.paged import PagedKVFormat, prefill_paged
-    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs, layout=case["layouts"][0])
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=case["layouts"][1])
     qt = torch.from_numpy(q).to(dtype).to(dev)
     qpt = torch.from_numpy(qp).to(dtype).to(dev) if qp is not None else None
     out = None
@@ -82,6 +82,20 @@ def test_prefill_bit_widths_and_groups(dev, kb, kq, vb, G, causal):
     q, cu = make_queries(rng, n_new, Hq)
     got, qr, _ = run_prefill(dev, case, q, cu, kb, kq, vb, bs, SM, CS, causal=causal)
     want = oracle_prefill(case, qr, cu, Hq, Hkv, kb, kq, vb, SM, CS, causal=causal)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,kq,vb", [(3, True, 3), (2, False, 4)])
+def test_prefill_row_major_paged_tiles(dev, kb, kq, vb):
+    """Row-major tiles are read as well as the lane-grouped ones."""
+    Hq, Hkv, bs = 8, 2, 32
+    lens = [100, 37]
+    n_new = [20, 37]
+    case = build_case(31 + kb, len(lens), Hq, Hkv, lens, kb, kq, vb, bs, layouts=("rows", "rows"))
+    rng = np.random.default_rng(kb)
+    q, cu = make_queries(rng, n_new, Hq)
+    got, qr, _ = run_prefill(dev, case, q, cu, kb, kq, vb, bs, SM, CS)
+    want = oracle_prefill(case, qr, cu, Hq, Hkv, kb, kq, vb, SM, CS)
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
@@ -151,7 +165,7 @@ def test_prefill_last_row_is_a_decode_step(dev):
     q, cu = make_queries(rng, [1000], Hq)
     got, qr, _ = run_prefill(dev, case, q, cu, kb, kq, vb, bs, SM, CS)
     kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout="values")
     qlast = torch.from_numpy(qr[-1:]).to(torch.bfloat16).to(dev)
     dec = decode_paged(qlast, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
                        torch.from_numpy(case["v_cache"]).to(dev), vf, _cb(vb).to(dev),

@@ -63,7 +63,7 @@ def test_wht_rows_layouts_and_involution(dev):
 def _decode(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk, rotate, q=None, q_proj=None):
     from turboquant.kernels.paged import PagedKVFormat, decode_paged
     kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout="values")
     if q is None:
         q = torch.from_numpy(case["q"]).to(torch.bfloat16).to(dev)
     out = decode_paged(q, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
@@ -176,8 +176,8 @@ def test_paged_backend_decode_step(dev):
     want = np.zeros((S, Hq, 128))
     for s, L in enumerate(lens):
         for h in range(Hkv):
-            kp = opaged.gather_sequence(kn, bt[s].numpy(), L, h, bs, kb, True)
-            vp = opaged.gather_sequence(vn, bt[s].numpy(), L, h, bs, vb, False)
+            kp = opaged.gather_sequence(kn, bt[s].numpy(), L, h, bs, kb, True, layout="keys")
+            vp = opaged.gather_sequence(vn, bt[s].numpy(), L, h, bs, vb, False, layout="values")
             k, sg, rn = odec.dequant_keys(kp, kc64, kb, True)
             v = odec.dequant_values(vp, vc64, vb)
             hs = slice(h * G, (h + 1) * G)
@@ -245,8 +245,8 @@ def test_paged_backend_mixed_batch(dev):
         L, n = lens[s], n_new[s]
         r0 = int(sum(n_new[:s]))
         for h in range(Hkv):
-            kp = opaged.gather_sequence(kn, bt[s].numpy(), L, h, bs, 3, True)
-            vp = opaged.gather_sequence(vn, bt[s].numpy(), L, h, bs, 3, False)
+            kp = opaged.gather_sequence(kn, bt[s].numpy(), L, h, bs, 3, True, layout="keys")
+            vp = opaged.gather_sequence(vn, bt[s].numpy(), L, h, bs, 3, False, layout="values")
             k, sg, rn = odec.dequant_keys(kp, kc64, 3, True)
             v = odec.dequant_values(vp, kc64, 3)
             hs = slice(h * G, (h + 1) * G)

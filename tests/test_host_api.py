@@ -214,9 +214,14 @@ def test_host_side_argument_rejection():
     assert L.tq_polarquant_compress(fake, 9, 128, 4, 128, 1, 0.1, fake, fake, 3, 1, fake, fake, fake, fake, fake, None) == -7
     assert L.tq_polarquant_compress(fake, 0, 128, 0, 128, 1, 0.1, fake, fake, 3, 1, fake, fake, fake, fake, fake, None) == 0
     assert L.tq_compress_paged(fake, 2, 1024, 128, 10, 8, 128, fake, 3, fake, 1056, 8448, 10, 24,
-                               4, 0, 1, 0.1, fake, fake, None) == -8
+                               4, 0, 1, 1, 0.1, fake, fake, None) == -8
     assert L.tq_compress_paged(fake, 2, 1024, 128, 10, 8, 128, fake, 7, fake, 1056, 8448, 10, 16,
-                               4, 0, 1, 0.1, fake, fake, None) == -7
+                               4, 0, 1, 1, 0.1, fake, fake, None) == -7
+    # tile layouts: unknown code, and QJL signs in the values layout
+    assert L.tq_compress_paged(fake, 2, 1024, 128, 10, 8, 128, fake, 3, fake, 1056, 8448, 10, 16,
+                               4, 0, 3, 1, 0.1, fake, fake, None) == -1
+    assert L.tq_compress_paged(fake, 2, 1024, 128, 10, 8, 128, fake, 3, fake, 1088, 8704, 10, 16,
+                               3, 1, 2, 1, 0.1, fake, fake, None) == -1
     assert L.tq_tile_bytes(16, 3, 1) == 1088 and L.tq_tile_bytes(24, 3, 1) == -1
     off = [ctypes.c_int64() for _ in range(4)]
     assert L.tq_tile_offsets(16, 3, 1, *[ctypes.byref(o) for o in off]) == 0

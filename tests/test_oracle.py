@@ -256,9 +256,13 @@ def test_permute_signs_brute_force():
 
 
 # ---------------------------------------------------------------- paged
-def test_paged_scatter_gather_roundtrip():
+@pytest.mark.parametrize("layout", ["rows", "keys", "values"])
+def test_paged_scatter_gather_roundtrip(layout):
     rng = np.random.default_rng(1)
-    for bits, qjl, bs in [(4, False, 16), (3, True, 32), (2, True, 16)]:
+    cases = [(4, False, 16), (3, True, 32), (2, True, 16), (3, False, 32)]
+    for bits, qjl, bs in cases:
+        if layout == "values" and qjl:
+            continue
         T, H, nb = 70, 3, 9
         pl = {"idx": rng.integers(0, 256, (T, H, 16 * bits), dtype=np.uint8),
               "norm": rng.integers(0, 65536, (T, H)).astype(np.uint16)}
@@ -266,23 +270,63 @@ def test_paged_scatter_gather_roundtrip():
             pl["signs"] = rng.integers(0, 256, (T, H, 16), dtype=np.uint8)
             pl["rnorm"] = rng.integers(0, 65536, (T, H)).astype(np.uint16)
         perm = rng.permutation(nb * bs)[:T]
-        cache = opaged.scatter_tokens(pl, perm, nb, H, bs, bits, qjl)
+        cache = opaged.scatter_tokens(pl, perm, nb, H, bs, bits, qjl, layout=layout)
         # a block table listing, for a sequence made of the tokens in slot order
         order = np.argsort(perm)
         slots_sorted = perm[order]
         for h in range(H):
             for t_i, t in enumerate(order):
                 blk, row = divmod(int(perm[t]), bs)
-                got = opaged.gather_sequence(cache, np.array([blk]), row + 1, h, bs, bits, qjl)
+                got = opaged.gather_sequence(cache, np.array([blk]), row + 1, h, bs, bits, qjl, layout=layout)
                 assert np.array_equal(got["idx"][row], pl["idx"][t, h])
                 assert got["norm"][row] == pl["norm"][t, h]
                 if qjl:
                     assert np.array_equal(got["signs"][row], pl["signs"][t, h])
                     assert got["rnorm"][row] == pl["rnorm"][t, h]
         assert len(slots_sorted) == T
-        slots = opaged.to_slots(cache, bs, bits, qjl, 16 * bits + (20 if qjl else 2))
+        slots = opaged.to_slots(cache, bs, bits, qjl, 16 * bits + (20 if qjl else 2), layout=layout)
         blk, row = divmod(int(perm[0]), bs)
         assert np.array_equal(slots[blk, row, 0, :16 * bits], pl["idx"][0, 0])
+
+
+@pytest.mark.parametrize("bits,qjl", [(2, False), (2, True), (3, False), (3, True), (4, False), (4, True)])
+def test_lane_grouped_layouts_one_chunk_per_lane(bits, qjl):
+    """The property the lane-grouped layouts exist for, checked on byte provenance: in a
+    16-row sub-tile, decode lane (n, g) needs the index bytes of row n, dims 32g..32g+31, and
+    their sign bytes (keys), or the index bytes of dims 8n..8n+7 of rows 4g..4g+3 (values); each
+    such set must be one contiguous run of bytes, the runs tiling the payload in lane order."""
+    bs = 32
+    # tag every payload byte with (kind, row, byte index): kind 0 index, 1 sign
+    idx = np.arange(bs * 16 * bits).reshape(bs, 16 * bits)
+    sg = 100000 + np.arange(bs * 16).reshape(bs, 16)
+    for layout in ("keys", "values"):
+        if layout == "values" and qjl:
+            continue
+        P = 16 * bits + (16 if qjl else 0)
+        # payload built through the oracle with 16-bit tags split over two byte planes
+        planes = []
+        for shift in (0, 8, 16):
+            tile = np.zeros(bs * P + 64 * bs, np.uint8)
+            opaged._set_tile_rows(tile, ((idx >> shift) & 0xFF).astype(np.uint8),
+                                  ((sg >> shift) & 0xFF).astype(np.uint8) if qjl else None, bs, bits, qjl, layout)
+            planes.append(tile[:bs * P].astype(np.int64) << shift)
+        tag = planes[0] | planes[1] | planes[2]
+        for j in range(bs // 16):
+            sub = tag[16 * P * j:16 * P * (j + 1)]
+            pos = 0
+            for a in range(4 if layout == "values" else 16):
+                for b in range(16 if layout == "values" else 4):
+                    if layout == "keys":
+                        n, g = a, b
+                        want = list(idx[16 * j + n, 4 * bits * g:4 * bits * (g + 1)])
+                        if qjl:
+                            want += list(sg[16 * j + n, 4 * g:4 * g + 4])
+                    else:
+                        g, n = a, b
+                        want = [int(x) for r in range(4) for x in idx[16 * j + 4 * g + r, bits * n:bits * (n + 1)]]
+                    assert list(sub[pos:pos + len(want)]) == want, (layout, j, a, b)
+                    pos += len(want)
+            assert pos == 16 * P
 
 
 def test_paged_layout_matches_product_format():
@@ -302,11 +346,13 @@ def test_reference_slot_converters_roundtrip():
     sys.path.insert(0, str(pathlib.Path(__file__).parents[1] / "turboquant-amd_amd"))
     from turboquant.kernels.paged import PagedKVFormat, from_reference_slots, to_reference_slots
     rng = np.random.default_rng(5)
-    for bits, qjl in [(4, False), (3, True)]:
-        f = PagedKVFormat(bits=bits, qjl=qjl, block_size=16)
+    for bits, qjl, layout, bs in [(4, False, "rows", 16), (3, True, "rows", 16), (3, True, "keys", 32),
+                                  (2, False, "keys", 16), (4, True, "keys", 16), (3, False, "values", 32),
+                                  (2, False, "values", 16), (4, False, "values", 16)]:
+        f = PagedKVFormat(bits=bits, qjl=qjl, block_size=bs, layout=layout)
         cache = torch.from_numpy(rng.integers(0, 256, (4, 2, f.tile_bytes), dtype=np.uint8))
         slots = to_reference_slots(cache, f, slot_bytes=f.slot_bytes + 6)
-        assert np.array_equal(slots.numpy(), opaged.to_slots(cache.numpy(), 16, bits, qjl, f.slot_bytes + 6))
+        assert np.array_equal(slots.numpy(), opaged.to_slots(cache.numpy(), bs, bits, qjl, f.slot_bytes + 6, layout=layout))
         assert torch.equal(from_reference_slots(slots, f), cache)
 
 

@@ -32,6 +32,7 @@ struct CompressParams {
     int64_t stride_block, stride_head, num_blocks;
     int block_size;
     int idx32;  // rows and slots below 2^31: 32-bit index arithmetic
+    int tile_layout;  // TQ_TILE_ROWS / TQ_TILE_KEYS / TQ_TILE_VALUES
     int64_t off_signs, off_norm, off_rnorm;
     // unpacked output
     int64_t* indices;
@@ -296,11 +297,35 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
                 w[wi] |= (uint32_t)idx[k] << sh;
                 if (sh + BITS > 32) w[wi + 1] |= (uint32_t)idx[k] >> (32 - sh);
             }
-            uint32_t* irow = reinterpret_cast<uint32_t*>(tile + r_in_blk * (16 * BITS) + 4 * BITS * q);
             if (write) {
+                if (p.tile_layout == TQ_TILE_KEYS) {
+                    // chunk (4n + q) of the row's 16-row sub-tile: index bytes, then sign bytes
+                    constexpr int P = 16 * BITS + (QJL ? 16 : 0), C = 4 * BITS + (QJL ? 4 : 0);
+                    uint32_t* ch = reinterpret_cast<uint32_t*>(tile + (r_in_blk & ~(int64_t)15) * P +
+                                                               (4 * (r_in_blk & 15) + q) * C);
 #pragma unroll
-                for (int j = 0; j < BITS; ++j) irow[j] = w[j];
-                if (QJL) *reinterpret_cast<uint32_t*>(tile + p.off_signs + r_in_blk * 16 + 4 * q) = sbits;
+                    for (int j = 0; j < BITS; ++j) ch[j] = w[j];
+                    if (QJL) ch[BITS] = sbits;
+                } else if (p.tile_layout == TQ_TILE_VALUES) {
+                    // dims 8n..8n+7 (n = 4q + i) of row 4g + r go to chunk (16g + n) at byte r * BITS
+                    uint8_t* st = tile + (r_in_blk & ~(int64_t)15) * (16 * BITS);
+                    const int t16 = (int)(r_in_blk & 15), g = t16 >> 2, r = t16 & 3;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        uint8_t* d = st + (16 * g + 4 * q + i) * (4 * BITS) + r * BITS;
+                        // bytes BITS*i .. BITS*i + BITS - 1 of the lane's stream
+#pragma unroll
+                        for (int k = 0; k < BITS; ++k) {
+                            const int byte = BITS * i + k;
+                            d[k] = (uint8_t)(w[byte >> 2] >> (8 * (byte & 3)));
+                        }
+                    }
+                } else {
+                    uint32_t* irow = reinterpret_cast<uint32_t*>(tile + r_in_blk * (16 * BITS) + 4 * BITS * q);
+#pragma unroll
+                    for (int j = 0; j < BITS; ++j) irow[j] = w[j];
+                    if (QJL) *reinterpret_cast<uint32_t*>(tile + p.off_signs + r_in_blk * 16 + 4 * q) = sbits;
+                }
                 if (q == 0) {
                     reinterpret_cast<uint16_t*>(tile + p.off_norm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(norm);
                     if (QJL)
@@ -408,7 +433,7 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
                                  const void* slot_mapping, int slot_dtype,
                                  void* cache, int64_t cache_stride_block, int64_t cache_stride_head,
                                  int64_t num_blocks, int block_size,
-                                 int bits, int use_qjl, int rotate, float wht_scale,
+                                 int bits, int use_qjl, int tile_layout, int rotate, float wht_scale,
                                  const float* centroids, const float* boundaries,
                                  tq_stream_t stream) {
     if (head_dim != TQ_HEAD_DIM) return TQ_ERR_HEAD_DIM;
@@ -416,6 +441,9 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
     if (block_size <= 0 || block_size % 16) return TQ_ERR_BLOCK_SIZE;
     if (num_tokens < 0 || num_heads <= 0 || num_blocks < 0) return TQ_ERR_INVALID_ARGUMENT;
     if (slot_dtype != TQ_I32 && slot_dtype != TQ_I64) return TQ_ERR_DTYPE;
+    if (tile_layout != TQ_TILE_ROWS && tile_layout != TQ_TILE_KEYS && tile_layout != TQ_TILE_VALUES)
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (tile_layout == TQ_TILE_VALUES && use_qjl) return TQ_ERR_INVALID_ARGUMENT;
     if (num_tokens == 0 || num_blocks == 0) return TQ_OK;
     if (!x || !slot_mapping || !cache || !centroids || !boundaries) return TQ_ERR_INVALID_ARGUMENT;
     int rc = check_x(x, x_dtype);
@@ -443,6 +471,7 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
     p.stride_head = cache_stride_head;
     p.num_blocks = num_blocks;
     p.block_size = block_size;
+    p.tile_layout = tile_layout;
     p.off_signs = g.off_signs;
     p.off_norm = g.off_norm;
     p.off_rnorm = g.off_rnorm;

@@ -79,6 +79,8 @@ struct DecodeParams {
     int64_t out_ss, out_sh;
     int rot_q, rot_qp, rot_out;  // rotate q / q_proj by H on load, the output by H on the write
     float wht_h;                 // 1 / sqrt(128)
+    int k_lg, v_lg;              // lane-grouped key / value tiles
+    int32_t vstep;               // bytes from value row 4g + r to 4g + r + 1 in the lane's stream
 };
 
 // nrec = 0 turns every load through the descriptor into a zero read (unreadable block).
@@ -153,7 +155,7 @@ struct Tile {
 // rows read as zero; the row offsets then go into the vector offset, which the range check sees.
 template <int KB, bool KQJL, int VB, bool NV, bool MASKED>
 __device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB, NV>& t, const Tile& tl, const LaneOff& o,
-                                          const int32_t* rrow) {
+                                          const int32_t* rrow, int32_t vstep, int v_lg) {
     auto nrec = [&](int r) -> uint32_t { return MASKED ? (uint32_t)(tl.nvalid * rrow[r]) : tl.nrec; };
     {
         auto r = make_rsrc(tl.base[R_KIDX], nrec(R_KIDX));
@@ -207,12 +209,23 @@ __device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB, NV>& t, const Ti
     auto rv = make_rsrc(tl.base[R_VIDX], nrec(R_VIDX));
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const uint32_t off = MASKED ? o.vidx + r * rrow[R_VIDX] : o.vidx;
-        const int soff = MASKED ? 0 : sgpr(r * rrow[R_VIDX]);
+        const uint32_t off = MASKED ? o.vidx + r * vstep : o.vidx;
         if (VB == 3) {
+            // lane-grouped: row r's 3 bytes at 3r of the chunk, read as the aligned 8-byte
+            // window at (3r & ~3) and shifted down by (3r & 3) bytes (then selected as bytes 0..2)
+            const int soff = MASKED ? 0 : sgpr(v_lg ? ((3 * r) & ~3) : r * vstep);
             tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, soff, 0);
-            t.vw[r][0] = w[0]; t.vw[r][VB == 3 ? 1 : 0] = w[1];
-        } else if (VB == 4) {
+            if (v_lg) {
+                t.vw[r][0] = __builtin_amdgcn_alignbit(w[1], w[0], 8 * ((3 * r) & 3));
+                t.vw[r][VB == 3 ? 1 : 0] = 0;
+            } else {
+                t.vw[r][0] = w[0];
+                t.vw[r][VB == 3 ? 1 : 0] = w[1];
+            }
+            continue;
+        }
+        const int soff = MASKED ? 0 : sgpr(r * vstep);
+        if (VB == 4) {
             t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, soff, 0);
         } else {
             t.vw[r][0] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, soff, 0);
@@ -500,12 +513,24 @@ void decode_kernel(DecodeParams p) {
 
     // ---- loop-invariant per-lane byte offsets inside a tile ----
     LaneOff o;
-    o.kidx = (uint32_t)(n * p.rrow[R_KIDX] + 4 * KB * g);
-    o.ksig = (uint32_t)(n * p.rrow[R_KSIG] + 4 * g);
+    // (lane-grouped tiles always have their norm rows 2 bytes apart: NV instances only)
+    if (NV && p.k_lg) {
+        // chunk (4n + g) of the 16-row sub-tile: index dwords, then the sign dword
+        o.kidx = (uint32_t)((4 * n + g) * (4 * KB + (KQJL ? 4 : 0)));
+        o.ksig = o.kidx + 4u * KB;
+    } else {
+        o.kidx = (uint32_t)(n * p.rrow[R_KIDX] + 4 * KB * g);
+        o.ksig = (uint32_t)(n * p.rrow[R_KSIG] + 4 * g);
+    }
     o.kn = (uint32_t)(4 * g * p.rrow[R_KNORM]);
     o.krn = (uint32_t)(4 * g * p.rrow[R_KRNORM]);
     o.vn = (uint32_t)(4 * g * p.rrow[R_VNORM]);
-    {
+    if (NV && p.v_lg) {
+        // chunk (16g + n) of the 16-row sub-tile, row 4g + r at r * VB (vstep); a 3-bit field is
+        // shifted to bytes 0..2 at load time
+        o.vidx = (uint32_t)((16 * g + n) * 4 * VB);
+        o.vsel = 0x0c020100u;
+    } else {
         int start = VB * n;
         o.vsel = 0;
         if (VB == 3) {
@@ -569,7 +594,7 @@ void decode_kernel(DecodeParams p) {
         Tile tl;
         locate(t0, live, tl);
         nvalid = tl.nvalid;
-        load_tile<KB, KQJL, VB, NV, false>(raw, tl, o, p.rrow);
+        load_tile<KB, KQJL, VB, NV, false>(raw, tl, o, p.rrow, p.vstep, NV && p.v_lg);
     };
 
     // Tiles 0..nfull-1 are complete.  A paged cache allocates whole blocks, so its partial last
@@ -619,7 +644,7 @@ void decode_kernel(DecodeParams p) {
             Tile tl;
             locate(t_begin + 16 * nfull, true, tl);
             tv = tl.nvalid;
-            load_tile<KB, KQJL, VB, NV, true>(tr, tl, o, p.rrow);
+            load_tile<KB, KQJL, VB, NV, true>(tr, tl, o, p.rrow, p.vstep, NV && p.v_lg);
         }
         if (tv)
             compute_tile<KB, KQJL, VB, NV, QCOLS, false>(tr, tv, sm, qop, qlo, qpop, kbank, vbank, one, o, g, hmask,
@@ -848,12 +873,13 @@ bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block
         return d >= 0 && d + rows_bytes < (1ll << 30);
     };
     const int64_t bs = block_size;
-    if (k->idx.stride_row != 16 * k->bits || k->norm.stride_row != 2 || !same(k->idx, k->norm)) return false;
+    if (k->layout != TQ_TILE_KEYS || v->layout != TQ_TILE_VALUES) return false;
+    if (k->idx.stride_row != 16 * k->bits + (k->qjl ? 16 : 0) || k->norm.stride_row != 2 || !same(k->idx, k->norm))
+        return false;
     if (!delta_ok(k->idx, k->norm, 2 * bs)) return false;
     if (k->qjl) {
-        if (k->signs.stride_row != 16 || k->rnorm.stride_row != 2 || !same(k->idx, k->signs) || !same(k->idx, k->rnorm))
-            return false;
-        if (!delta_ok(k->idx, k->signs, 16 * bs) || !delta_ok(k->idx, k->rnorm, 2 * bs)) return false;
+        if (k->rnorm.stride_row != 2 || !same(k->idx, k->rnorm)) return false;
+        if (!delta_ok(k->idx, k->rnorm, 2 * bs)) return false;
     }
     if (v->idx.stride_row != 16 * v->bits || v->norm.stride_row != 2 || !same(v->idx, v->norm)) return false;
     if (!delta_ok(v->idx, v->norm, 2 * bs)) return false;
@@ -930,16 +956,26 @@ int decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, in
     if (num_seqs == 0) return TQ_OK;
     if (!q || !seq_lens || !out || !k->centroids || !v->centroids) return TQ_ERR_INVALID_ARGUMENT;
     if (block_tables && block_table_stride < max_blocks_per_seq) return TQ_ERR_INVALID_ARGUMENT;
+    // lane-grouped tiles: keys as TQ_TILE_KEYS, values as TQ_TILE_VALUES, paged, natural sign
+    // order, the payload region's row stride = payload bytes per token
+    const bool k_lg = k->layout == TQ_TILE_KEYS, v_lg = v->layout == TQ_TILE_VALUES;
+    if ((k->layout != TQ_TILE_ROWS && !k_lg) || (v->layout != TQ_TILE_ROWS && !v_lg)) return TQ_ERR_INVALID_ARGUMENT;
+    if (k_lg && (!block_tables || k->signs_permuted || k->idx.stride_row != 16 * k->bits + (k->qjl ? 16 : 0)))
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (v_lg && (!block_tables || v->idx.stride_row != 16 * v->bits)) return TQ_ERR_INVALID_ARGUMENT;
+    // the kernels read lane-grouped tiles only with every norm stream at 2 bytes per row
+    if ((k_lg || v_lg) && (k->norm.stride_row != 2 || v->norm.stride_row != 2 || (k->qjl && k->rnorm.stride_row != 2)))
+        return TQ_ERR_INVALID_ARGUMENT;
     int rc;
     if ((rc = check_region(k->idx, 4))) return rc;
     if ((rc = check_region(k->norm, 2))) return rc;
     if ((rc = check_region(v->idx, 4))) return rc;
     if ((rc = check_region(v->norm, 2))) return rc;
     if (k->qjl) {
-        if ((rc = check_region(k->signs, 4))) return rc;
+        if (!k_lg && (rc = check_region(k->signs, 4))) return rc;
         if ((rc = check_region(k->rnorm, 2))) return rc;
     }
-    const tq_region* regs[R_COUNT] = {&k->idx, k->qjl ? &k->signs : &k->idx, &k->norm,
+    const tq_region* regs[R_COUNT] = {&k->idx, (k->qjl && !k_lg) ? &k->signs : &k->idx, &k->norm,
                                       k->qjl ? &k->rnorm : &k->norm, &v->idx, &v->norm};
     int64_t max_row = 0;
     for (int r = 0; r < R_COUNT; ++r) max_row = regs[r]->stride_row > max_row ? regs[r]->stride_row : max_row;
@@ -983,10 +1019,7 @@ int decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, in
         f.k_sh = k->idx.stride_head;
         f.k_sb = (uint32_t)k->idx.stride_block;
         f.d_kn = (uint32_t)(static_cast<const uint8_t*>(k->norm.ptr) - kb);
-        if (k->qjl) {
-            f.d_ksig = (uint32_t)(static_cast<const uint8_t*>(k->signs.ptr) - kb);
-            f.d_krn = (uint32_t)(static_cast<const uint8_t*>(k->rnorm.ptr) - kb);
-        }
+        if (k->qjl) f.d_krn = (uint32_t)(static_cast<const uint8_t*>(k->rnorm.ptr) - kb);
         const uint8_t* vb = static_cast<const uint8_t*>(v->idx.ptr);
         f.vbase = vb;
         f.v_sh = v->idx.stride_head;
@@ -1092,6 +1125,9 @@ int decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, in
     p.rot_qp = rotate && !q_proj;
     p.rot_out = rotate;
     p.wht_h = kWhtH;
+    p.k_lg = k_lg ? 1 : 0;
+    p.v_lg = v_lg ? 1 : 0;
+    p.vstep = v_lg ? v->bits : (int32_t)v->idx.stride_row;
 
     const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
     const int64_t grid = (units + 3) / 4;

@@ -27,10 +27,13 @@
 // fp16 without scaling (exact for bf16/fp16 queries) and the softmax scale is applied in the
 // exponent: p = exp2(c * (s - m)), c = sm_scale * log2(e) / centroid_scale.
 //
-// Memory: the K and V buffer descriptors are loop invariant (base = cache + head offset); a
-// tile is addressed by scalar offsets (block * block_stride + region offset), which needs the
-// cache to span less than 2 GiB (checked on the host; larger caches use decode_kernel).  The
-// norm streams are read once per pair: lanes of tile A and tile B differ in their vector offset.
+// Memory: the caches are in the lane-grouped tile layouts (TQ_TILE_KEYS / TQ_TILE_VALUES):
+// per 16-row sub-tile a lane reads its key data (index dwords + sign dword) with one load and
+// its value data (4 rows x 8 dims) with one load.  The K and V buffer descriptors are loop
+// invariant (base = cache + head offset); a tile is addressed by scalar offsets (block *
+// block_stride + region offset), which needs the cache to span less than 2 GiB (checked on the
+// host; larger caches use decode_kernel).  The norm streams are read once per pair: lanes of
+// tile A and tile B differ in their vector offset.
 // Block-table entries of the next pair come through the scalar cache (a vector load would cost
 // the texture data path a whole wave of lanes for 8 bytes).  Loads run one pair ahead.
 //
@@ -532,12 +535,11 @@ void decode_fast_kernel(FastDecodeParams p) {
     }
 
     // ---- loop-invariant lane offsets inside a tile ----
-    const uint32_t o_kidx = (uint32_t)(n * 16 * KB + 4 * KB * g);
-    const uint32_t o_ksig = (uint32_t)(16 * n + 4 * g);
+    // lane-grouped tiles: the lane's key chunk (row n, dims 32g..) and value chunk (rows
+    // 4g..4g+3, dims 8n..8n+7) inside a 16-row sub-tile
+    const uint32_t o_kch = (uint32_t)((4 * n + g) * (4 * KB + (KQJL ? 4 : 0)));
+    const uint32_t o_vch = (uint32_t)((16 * g + n) * 4 * VB);
     const uint32_t o_norm = (uint32_t)(8 * g);  // tokens 4g..4g+3, 2 bytes each
-    // V: dims 8n..8n+7 of token 4g+r start at byte VB*n of its row; one dword per token, read at
-    // that (for VB = 3 unaligned) byte offset, holds them in bits 0 .. 8*VB-1
-    const uint32_t o_vidx = (uint32_t)(4 * g * 16 * VB + VB * n);
     const auto rk = rsrc(p.kbase + (int64_t)kh * p.k_sh);
     const auto rv = rsrc(p.vbase + (int64_t)kh * p.v_sh);
     const uint64_t hi8 = 0xff00ff00ff00ff00ull;
@@ -603,31 +605,30 @@ void decode_fast_kernel(FastDecodeParams p) {
         info.vbB = (uint32_t)blk[1] * p.v_sb;
         info.r0A = r0[0];
         info.r0B = r0[1];
-        auto load_kw = [&](uint32_t (&kw)[KB], uint32_t soff) {
-            if (KB == 2) {
-                tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, o_kidx, soff, 0);
-                kw[0] = v[0];
-                kw[1 % KB] = v[1];
-            } else if (KB == 3) {
+        // One load per tile: chunk (4n + g) of the 16-row sub-tile holds the lane's index
+        // dwords and, with QJL, the sign dword after them (4 * (KB + QJL) bytes).
+        auto load_k = [&](uint32_t (&kw)[KB], uint32_t& ks, uint32_t soff) {
+            constexpr int C = 4 * KB + (KQJL ? 4 : 0);
+            uint32_t d[5];
+            if (C == 8) {
+                tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, o_kch, soff, 0);
+                d[0] = v[0]; d[1] = v[1];
+            } else if (C == 12) {
                 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-                u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rk, o_kidx, soff, 0);
-                kw[0] = v[0];
-                kw[1 % KB] = v[1];
-                kw[2 % KB] = v[2];
+                u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rk, o_kch, soff, 0);
+                d[0] = v[0]; d[1] = v[1]; d[2] = v[2];
             } else {
-                tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, o_kidx, soff, 0);
-                kw[0] = v[0];
-                kw[1 % KB] = v[1];
-                kw[2 % KB] = v[2];
-                kw[3 % KB] = v[3];
+                tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, o_kch, soff, 0);
+                d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
+                if (C == 20) d[4] = __builtin_amdgcn_raw_buffer_load_b32(rk, o_kch + 16u, soff, 0);
             }
+#pragma unroll
+            for (int j = 0; j < KB; ++j) kw[j] = d[j];
+            ks = KQJL ? d[KB] : 0u;
         };
-        load_kw(kr.kwA, kb[0] + r0[0] * (uint32_t)(16 * KB));
-        load_kw(kr.kwB, kb[1] + r0[1] * (uint32_t)(16 * KB));
-        if (KQJL) {
-            kr.ksA = __builtin_amdgcn_raw_buffer_load_b32(rk, o_ksig, kb[0] + p.d_ksig + r0[0] * 16u, 0);
-            kr.ksB = __builtin_amdgcn_raw_buffer_load_b32(rk, o_ksig, kb[1] + p.d_ksig + r0[1] * 16u, 0);
-        }
+        constexpr uint32_t P = 16 * KB + (KQJL ? 16 : 0);  // payload bytes per row
+        load_k(kr.kwA, kr.ksA, kb[0] + r0[0] * P);
+        load_k(kr.kwB, kr.ksB, kb[1] + r0[1] * P);
         const NormAddr na = norm_addr(kb[0] + 2u * r0[0], kb[1] + 2u * r0[1]);
         tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_kn, 0);
         kr.kn[0] = a[0];
@@ -639,19 +640,26 @@ void decode_fast_kernel(FastDecodeParams p) {
         }
     };
     auto load_v = [&](const PairInfo& info, VRaw& vr) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t off = o_vidx + (uint32_t)(r * 16 * VB);
-            const uint32_t sA = info.vbA + info.r0A * (uint32_t)(16 * VB);
-            const uint32_t sB = info.vbB + info.r0B * (uint32_t)(16 * VB);
+        // One load per tile: chunk (16g + n) of the 16-row sub-tile holds dims 8n..8n+7 of rows
+        // 4g..4g+3, VB bytes each; row r's fields go to bits 0 .. 8*VB-1 of vw[r].
+        auto load1 = [&](uint32_t (&vw)[4], uint32_t soff) {
             if (VB == 2) {
-                vr.vwA[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, sA, 0);
-                vr.vwB[r] = __builtin_amdgcn_raw_buffer_load_b16(rv, off, sB, 0);
+                tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, o_vch, soff, 0);
+                vw[0] = a[0]; vw[1] = a[0] >> 16; vw[2] = a[1]; vw[3] = a[1] >> 16;
+            } else if (VB == 3) {
+                typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+                u32x3 a = __builtin_amdgcn_raw_buffer_load_b96(rv, o_vch, soff, 0);
+                vw[0] = a[0];
+                vw[1] = __builtin_amdgcn_alignbit(a[1], a[0], 24);
+                vw[2] = __builtin_amdgcn_alignbit(a[2], a[1], 16);
+                vw[3] = a[2] >> 8;
             } else {
-                vr.vwA[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, sA, 0);
-                vr.vwB[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, off, sB, 0);
+                tq_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rv, o_vch, soff, 0);
+                vw[0] = a[0]; vw[1] = a[1]; vw[2] = a[2]; vw[3] = a[3];
             }
-        }
+        };
+        load1(vr.vwA, info.vbA + info.r0A * (uint32_t)(16 * VB));
+        load1(vr.vwB, info.vbB + info.r0B * (uint32_t)(16 * VB));
         // norm of row j of a tile at row0 of its block: d_vn + 2 (row0 + j)
         const NormAddr na = norm_addr(info.vbA + 2u * info.r0A, info.vbB + 2u * info.r0B);
         tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, na.vo, na.so + p.d_vn, 0);

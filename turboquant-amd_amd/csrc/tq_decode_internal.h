@@ -19,7 +19,7 @@ struct FastDecodeParams {
     const uint8_t* kbase;
     int64_t k_sh;
     uint32_t k_sb;
-    uint32_t d_ksig, d_kn, d_krn;
+    uint32_t d_kn, d_krn;  // norm regions (the signs sit in the lane-grouped payload)
     const uint8_t* vbase;
     int64_t v_sh;
     uint32_t v_sb;

@@ -57,6 +57,7 @@ struct PrefillParams {
     const float* k_cent;
     const float* v_cent;
     int k_perm;
+    int k_lg, v_lg;  // lane-grouped key / value tiles (TQ_TILE_KEYS / TQ_TILE_VALUES)
     float k_cs, v_cs, v_cinv;
     int block_size;
     int64_t num_blocks;
@@ -95,13 +96,6 @@ struct Raw {
     uint32_t nrm;            // fp16 norm bits (threads 0-47: K norm, K residual norm, V norm)
     int nv;                  // usable rows of the tile (0: unreadable block)
 };
-
-// The 8 index fields of dims 8pp..8pp+7 start at byte bits*pp of the token's index row; the
-// thread loads the two aligned dwords around them (the second one clamped to the row: a field
-// that ends in the row's last dword lies entirely in it) and shifts the window down.
-__device__ __forceinline__ uint32_t fields(const uint32_t (&w)[2], int bits, int pp) {
-    return __builtin_amdgcn_alignbit(w[1], w[0], (uint32_t)((bits * pp) & 3) * 8u);
-}
 
 template <int KB, bool KQJL, int VB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void prefill_kernel(PrefillParams p) {
@@ -211,14 +205,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     };
     // Loop-invariant byte offsets of this thread's data inside a 16-row tile (rows are less than
     // 2^31 / 16 bytes apart: checked on the host), added to the tile's wave-uniform base address.
-    auto field_off = [&](const tq_region& rg, int bits, int second) -> uint32_t {
-        const int w0 = (bits * pp) >> 2;
-        const int w1 = (w0 + 1 < 4 * bits) ? w0 + 1 : w0;
-        return (uint32_t)(tt * rg.stride_row) + 4u * (uint32_t)(second ? w1 : w0);
+    // Byte offsets of the thread's index fields (K, V) and of its sign dword in a 16-row
+    // sub-tile, for the row-major and the lane-grouped tile layouts.
+    uint32_t ok, ov, o_sg;
+    if (p.k_lg) {
+        const int c = 4 * tt + (pp >> 2);  // chunk: row tt, dim quarter pp / 4
+        constexpr int C = 4 * KB + (KQJL ? 4 : 0);
+        ok = (uint32_t)(c * C + (pp & 3) * KB);
+        o_sg = (uint32_t)(c * C + 4 * KB);  // byte pp & 3 of it: dims 8pp..8pp+7
+    } else {
+        ok = (uint32_t)(tt * p.kidx.stride_row + KB * pp);
+        o_sg = (uint32_t)(tt * p.ksig.stride_row) + (p.k_perm ? 0u : 4u * (uint32_t)(pp >> 2));
+    }
+    if (p.v_lg) {
+        ov = (uint32_t)((16 * (tt >> 2) + pp) * 4 * VB + (tt & 3) * VB);  // chunk: rows 4(tt/4).., dims 8pp..
+    } else {
+        ov = (uint32_t)(tt * p.vidx.stride_row + VB * pp);
+    }
+    // the aligned dword holding the first field and the next one; in a row-major row the next
+    // one is clamped to the row (a field ending in the row's last dword lies entirely in it), in
+    // a lane-grouped tile it is always inside the tile (chunks or the norm region follow)
+    auto second = [](uint32_t o, bool lg, uint32_t row_start, int row_dwords) -> uint32_t {
+        const uint32_t w0 = o & ~3u;
+        if (lg) return w0 + 4u;
+        return (w0 + 4u < row_start + 4u * (uint32_t)row_dwords) ? w0 + 4u : w0;
     };
-    const uint32_t o_k0 = field_off(p.kidx, KB, 0), o_k1 = field_off(p.kidx, KB, 1);
-    const uint32_t o_v0 = field_off(p.vidx, VB, 0), o_v1 = field_off(p.vidx, VB, 1);
-    const uint32_t o_sg = (uint32_t)(tt * p.ksig.stride_row) + (p.k_perm ? 0u : 4u * (uint32_t)(pp >> 2));
+    const uint32_t o_k0 = ok & ~3u, o_k1 = second(ok, p.k_lg, (uint32_t)(tt * p.kidx.stride_row), 4 * KB);
+    const uint32_t o_v0 = ov & ~3u, o_v1 = second(ov, p.v_lg, (uint32_t)(tt * p.vidx.stride_row), 4 * VB);
+    const uint32_t sh_k = (ok & 3u) * 8u, sh_v = (ov & 3u) * 8u;
     const int ntok = tid & 15;  // token of the norm threads (0-47)
     const tq_region& nreg = tid < 16 ? p.knorm : (tid < 32 ? p.krnorm : p.vnorm);
     const uint32_t o_nm = (uint32_t)(ntok * nreg.stride_row);
@@ -258,7 +272,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         uint8_t* b = s_lds + buf * kBuf;
         const uint8_t* tab = s_lds + kOffTab;
         {
-            const uint32_t f = fields(w.kw, KB, pp);
+            const uint32_t f = __builtin_amdgcn_alignbit(w.kw[1], w.kw[0], sh_k);
             tq_u32x4 h;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -289,7 +303,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             *reinterpret_cast<tq_u32x4*>(b + kOffS + tt * kKRow + 16 * pp) = h;
         }
         {
-            const uint32_t f = fields(w.vw, VB, pp);
+            const uint32_t f = __builtin_amdgcn_alignbit(w.vw[1], w.vw[0], sh_v);
             const uint8_t* tv = tab + 1024;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -466,17 +480,22 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
     if (!q || !cu_seqlens_q || !seq_lens || !block_tables || !out || !k->centroids || !v->centroids)
         return TQ_ERR_INVALID_ARGUMENT;
     if (block_table_stride < max_blocks_per_seq) return TQ_ERR_INVALID_ARGUMENT;
+    const bool k_lg = k->layout == TQ_TILE_KEYS, v_lg = v->layout == TQ_TILE_VALUES;
+    if ((k->layout != TQ_TILE_ROWS && !k_lg) || (v->layout != TQ_TILE_ROWS && !v_lg)) return TQ_ERR_INVALID_ARGUMENT;
+    if (k_lg && (k->signs_permuted || k->idx.stride_row != 16 * k->bits + (k->qjl ? 16 : 0)))
+        return TQ_ERR_INVALID_ARGUMENT;
+    if (v_lg && v->idx.stride_row != 16 * v->bits) return TQ_ERR_INVALID_ARGUMENT;
     int rc;
     if ((rc = check_region(k->idx, 4))) return rc;
     if ((rc = check_region(k->norm, 2))) return rc;
     if ((rc = check_region(v->idx, 4))) return rc;
     if ((rc = check_region(v->norm, 2))) return rc;
     if (k->qjl) {
-        if ((rc = check_region(k->signs, 4))) return rc;
+        if (!k_lg && (rc = check_region(k->signs, 4))) return rc;
         if ((rc = check_region(k->rnorm, 2))) return rc;
     }
     // per-thread offsets inside a tile are 32-bit: 16 rows of any region below 2^31 bytes
-    const tq_region* regs[6] = {&k->idx, &k->norm, &v->idx, &v->norm, &k->signs, &k->rnorm};
+    const tq_region* regs[6] = {&k->idx, &k->norm, &v->idx, &v->norm, &k->rnorm, k_lg ? &k->idx : &k->signs};
     for (int r = 0; r < (k->qjl ? 6 : 4); ++r)
         if (regs[r]->stride_row < 0 || regs[r]->stride_row >= (1ll << 26)) return TQ_ERR_INVALID_ARGUMENT;
     const int group = num_q_heads / num_kv_heads;
@@ -501,7 +520,7 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
     p.group = group;
     p.n_rb = (int)n_rb;
     p.kidx = k->idx;
-    p.ksig = k->qjl ? k->signs : k->idx;
+    p.ksig = (k->qjl && !k_lg) ? k->signs : k->idx;
     p.knorm = k->norm;
     p.krnorm = k->qjl ? k->rnorm : k->norm;
     p.vidx = v->idx;
@@ -509,6 +528,8 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
     p.k_cent = k->centroids;
     p.v_cent = v->centroids;
     p.k_perm = k->signs_permuted ? 1 : 0;
+    p.k_lg = k_lg ? 1 : 0;
+    p.v_lg = v_lg ? 1 : 0;
     p.k_cs = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
     p.v_cs = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
     p.v_cinv = 1.f / p.v_cs;

@@ -18,7 +18,7 @@ import torch
 
 LIB_NAME = "libturboquant_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / "lib" / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 HEAD_DIM = 128
 
 TQ_F32, TQ_F16, TQ_BF16, TQ_I32, TQ_I64 = 0, 1, 2, 3, 4
@@ -56,7 +56,11 @@ class TQKVView(ctypes.Structure):
         ("qjl", ctypes.c_int32),
         ("signs_permuted", ctypes.c_int32),
         ("centroid_scale", ctypes.c_float),
+        ("layout", ctypes.c_int32),
     ]
+
+
+TILE_ROWS, TILE_KEYS, TILE_VALUES = 0, 1, 2
 
 
 _vp = ctypes.c_void_p
@@ -76,7 +80,7 @@ SIGNATURES = {
     "tq_compress_paged": (
         _i32,
         [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _i32,
-         _i32, _i32, _i32, _f32, _vp, _vp, _vp],
+         _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp],
     ),
     "tq_tile_bytes": (_i64, [_i32, _i32, _i32]),
     "tq_tile_offsets": (

@@ -59,7 +59,7 @@ class TurboQuantPagedState:
         self.block_size = block_size
         self.weights_fused = bool(weights_fused)
         self.k_format = PagedKVFormat(bits=self.k_bits, qjl=self.k_qjl, block_size=block_size)
-        self.v_format = PagedKVFormat(bits=self.v_bits, qjl=False, block_size=block_size)
+        self.v_format = PagedKVFormat(bits=self.v_bits, qjl=False, block_size=block_size, layout="values")
         self.wht = make_wht_matrix(head_size, self.device)
         self.k_centroids, self.k_boundaries = make_codebook(head_size, self.k_bits, device=self.device)
         if self.v_bits == self.k_bits:
@@ -257,7 +257,8 @@ class TurboQuantPagedImpl:
         if head_size != 128:
             raise ValueError("head_size must be 128")
         kf = PagedKVFormat(bits=k_bits, qjl=k_qjl, block_size=block_size)
-        vf = PagedKVFormat(bits=v_bits if v_bits is not None else k_bits, qjl=False, block_size=block_size)
+        vf = PagedKVFormat(bits=v_bits if v_bits is not None else k_bits, qjl=False, block_size=block_size,
+                           layout="values")
         return (num_blocks, num_kv_heads, kf.tile_bytes + vf.tile_bytes)
 
     def do_kv_cache_update(self, layer, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,

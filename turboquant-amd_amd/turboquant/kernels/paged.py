@@ -33,14 +33,27 @@ from turboquant.core.rotation import wht_scale
 MI355X_CUS = 256
 
 
+_LAYOUTS = {"rows": 0, "keys": 1, "values": 2}
+
+
 @dataclass(frozen=True)
 class PagedKVFormat:
-    """Geometry of one paged cache (K or V)."""
+    """Geometry of one paged cache (K or V).
+
+    layout: how the payload (index bytes and QJL sign bytes) of a tile is ordered -
+      "keys"   (default): per 16-token sub-tile, chunk (4n + g) holds the index bytes and then
+               the sign bytes of row n, dims 32g..32g+31 - one load per decode lane for a key;
+      "values": per 16-token sub-tile, chunk (16g + n) holds dims 8n..8n+7 of rows 4g..4g+3 -
+               one load per decode lane for the value product (no QJL);
+      "rows"   : all index rows, then all sign rows (row-major; read by the general kernel).
+    A V cache uses layout="values"; decode_paged checks the roles.
+    """
 
     bits: int = 4
     qjl: bool = False
     block_size: int = 16
     head_dim: int = 128
+    layout: str = "keys"
 
     def __post_init__(self):
         if self.bits not in (2, 3, 4):
@@ -49,6 +62,27 @@ class PagedKVFormat:
             raise ValueError(f"block_size must be a positive multiple of 16, got {self.block_size}")
         if self.head_dim != 128:
             raise ValueError("head_dim must be 128")
+        if self.layout not in _LAYOUTS:
+            raise ValueError(f"layout must be one of {sorted(_LAYOUTS)}, got {self.layout!r}")
+        if self.layout == "values" and self.qjl:
+            raise ValueError("the values layout carries no QJL data")
+
+    @classmethod
+    def for_keys(cls, bits: int, qjl: bool = False, block_size: int = 16) -> "PagedKVFormat":
+        return cls(bits=bits, qjl=qjl, block_size=block_size, layout="keys")
+
+    @classmethod
+    def for_values(cls, bits: int, block_size: int = 16) -> "PagedKVFormat":
+        return cls(bits=bits, qjl=False, block_size=block_size, layout="values")
+
+    @property
+    def layout_code(self) -> int:
+        return _LAYOUTS[self.layout]
+
+    @property
+    def payload_bytes(self) -> int:
+        """Index + sign bytes per token (the payload region's row stride)."""
+        return self.idx_bytes + (16 if self.qjl else 0)
 
     @property
     def idx_bytes(self) -> int:
@@ -56,6 +90,7 @@ class PagedKVFormat:
 
     @property
     def off_signs(self) -> int:
+        """Sign rows of the "rows" layout (the lane-grouped layouts interleave them)."""
         return self.block_size * self.idx_bytes
 
     @property
@@ -84,6 +119,15 @@ class PagedKVFormat:
 def allocate_cache(num_blocks: int, num_kv_heads: int, fmt: PagedKVFormat, device=None) -> torch.Tensor:
     """Zeroed uint8 cache [num_blocks, num_kv_heads, fmt.tile_bytes]."""
     return torch.zeros((num_blocks, num_kv_heads, fmt.tile_bytes), dtype=torch.uint8, device=device)
+
+
+def _check_roles(k_fmt: PagedKVFormat, v_fmt: PagedKVFormat) -> None:
+    if v_fmt.qjl:
+        raise ValueError("the V cache carries no QJL data")
+    if k_fmt.layout == "values":
+        raise ValueError("the K cache format uses layout='values'; keys use 'keys' (or 'rows')")
+    if v_fmt.layout == "keys":
+        raise ValueError("the V cache format uses layout='keys'; values use 'values' (or 'rows')")
 
 
 def _check_cache(cache: torch.Tensor, fmt: PagedKVFormat, what: str) -> None:
@@ -129,7 +173,7 @@ def compress_paged(
         x.data_ptr(), _lib.dtype_code(x), x.stride(0), x.stride(1), T, H, fmt.head_dim,
         slot_mapping.data_ptr(), _lib.dtype_code(slot_mapping),
         cache.data_ptr(), cache.stride(0), cache.stride(1), cache.shape[0], fmt.block_size,
-        fmt.bits, int(fmt.qjl), int(bool(rotate)), wht_scale(fmt.head_dim),
+        fmt.bits, int(fmt.qjl), fmt.layout_code, int(bool(rotate)), wht_scale(fmt.head_dim),
         cent.data_ptr(), bnd.data_ptr(), _lib.stream_handle(dev),
     )
     _lib.check(rc, "tq_compress_paged")
@@ -241,13 +285,18 @@ def _region(ptr: int, stride_block: int, stride_head: int, stride_row: int, stri
 
 
 def paged_view(cache: torch.Tensor, fmt: PagedKVFormat, centroids: torch.Tensor) -> _lib.TQKVView:
-    """TQKVView over a cache tensor in this module's tile layout."""
+    """TQKVView over a cache tensor in this module's tile layouts."""
     base = cache.data_ptr()
     sb, sh = cache.stride(0), cache.stride(1)
     view = _lib.TQKVView()
-    view.idx = _region(base, sb, sh, fmt.idx_bytes)
+    view.layout = fmt.layout_code
+    if fmt.layout == "rows":
+        view.idx = _region(base, sb, sh, fmt.idx_bytes)
+        if fmt.qjl:
+            view.signs = _region(base + fmt.off_signs, sb, sh, 16)
+    else:
+        view.idx = _region(base, sb, sh, fmt.payload_bytes)  # payload region; signs inside it
     if fmt.qjl:
-        view.signs = _region(base + fmt.off_signs, sb, sh, 16)
         view.rnorm = _region(base + fmt.off_rnorm, sb, sh, 2)
     view.norm = _region(base + fmt.off_norm, sb, sh, 2)
     view.centroids = centroids.data_ptr()
@@ -358,8 +407,7 @@ def decode_paged(
         raise ValueError("q must be [S, Hq, 128]")
     if k_fmt.block_size != v_fmt.block_size:
         raise ValueError("K and V caches must share block_size")
-    if v_fmt.qjl:
-        raise ValueError("the V cache carries no QJL data")
+    _check_roles(k_fmt, v_fmt)
     _check_cache(k_cache, k_fmt, "decode_paged(k)")
     _check_cache(v_cache, v_fmt, "decode_paged(v)")
     if k_cache.shape[0] != v_cache.shape[0] or k_cache.shape[1] != v_cache.shape[1]:
@@ -444,8 +492,7 @@ def prefill_paged(
         raise ValueError("q must be [T, Hq, 128]")
     if k_fmt.block_size != v_fmt.block_size:
         raise ValueError("K and V caches must share block_size")
-    if v_fmt.qjl:
-        raise ValueError("the V cache carries no QJL data")
+    _check_roles(k_fmt, v_fmt)
     _check_cache(k_cache, k_fmt, "prefill_paged(k)")
     _check_cache(v_cache, v_fmt, "prefill_paged(v)")
     if k_cache.shape[0] != v_cache.shape[0] or k_cache.shape[1] != v_cache.shape[1]:
@@ -510,9 +557,52 @@ def _tile_fields(fmt: PagedKVFormat):
     return fields
 
 
+@functools.lru_cache(maxsize=None)
+def _rows_positions(fmt: PagedKVFormat) -> Optional[torch.Tensor]:
+    """pos[j] = byte of fmt's tile that holds byte j of the same tile in the "rows" layout
+    (None for the rows layout itself).  Norm regions coincide."""
+    if fmt.layout == "rows":
+        return None
+    bs, b, q = fmt.block_size, fmt.bits, fmt.qjl
+    P = fmt.payload_bytes
+    pos = torch.arange(fmt.tile_bytes, dtype=torch.int64)
+    R = torch.arange(bs).view(bs, 1)
+    sub, t16 = (R // 16) * 16 * P, R % 16
+    k = torch.arange(16 * b).view(1, -1)                    # index byte of the token
+    if fmt.layout == "keys":
+        C = 4 * b + (4 if q else 0)
+        pos[:bs * 16 * b] = (sub + (4 * t16 + k // (4 * b)) * C + k % (4 * b)).reshape(-1)
+        if q:
+            ks = torch.arange(16).view(1, -1)               # sign byte of the token
+            pos[fmt.off_signs:fmt.off_signs + bs * 16] = (sub + (4 * t16 + ks // 4) * C + 4 * b + ks % 4).reshape(-1)
+    else:
+        g, r = t16 // 4, t16 % 4
+        pos[:bs * 16 * b] = (sub + (16 * g + k // b) * (4 * b) + r * b + k % b).reshape(-1)
+    return pos
+
+
+def to_rows_layout(cache: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
+    """The same tiles in the "rows" layout (a copy)."""
+    pos = _rows_positions(fmt)
+    if pos is None:
+        return cache.clone()
+    return cache[..., :fmt.tile_bytes].index_select(2, pos.to(cache.device))
+
+
+def from_rows_layout(rows: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
+    """Inverse of to_rows_layout."""
+    pos = _rows_positions(fmt)
+    if pos is None:
+        return rows.clone()
+    out = torch.zeros(rows.shape[:2] + (fmt.tile_bytes,), dtype=torch.uint8, device=rows.device)
+    out[..., pos.to(rows.device)] = rows[..., :fmt.tile_bytes]
+    return out
+
+
 def to_reference_slots(cache: torch.Tensor, fmt: PagedKVFormat, slot_bytes: Optional[int] = None) -> torch.Tensor:
     """Tile layout -> [num_blocks, block_size, Hkv, slot_bytes] slots holding, per token,
     index bytes, [sign bytes], fp16 norm, [fp16 residual norm], then zero padding."""
+    cache = to_rows_layout(cache, fmt)
     nb, h, _ = cache.shape
     bs = fmt.block_size
     sb = slot_bytes or fmt.slot_bytes
@@ -538,4 +628,4 @@ def from_reference_slots(slots: torch.Tensor, fmt: PagedKVFormat) -> torch.Tenso
         part = slots[..., pos: pos + width].permute(0, 2, 1, 3).reshape(nb, h, bs * width)
         cache[:, :, off: off + bs * width] = part
         pos += width
-    return cache
+    return from_rows_layout(cache, fmt)
