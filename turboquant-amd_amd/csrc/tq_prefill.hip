@@ -9,8 +9,8 @@
 // (new token i, query head of the GQA group) pair, rows ordered token-major, so a workgroup
 // serves 64 / G tokens with all G heads of the group and each K/V tile is dequantised once for
 // all of them.  The cache is walked in 16-token tiles (a tile never spans two blocks).  Per
-// tile the 256 threads dequantise into one of two LDS buffers (thread t: token t % 16, dims
-// 8 (t / 16) .. + 7) while the waves compute on the other:
+// tile the 256 threads dequantise into one of two LDS buffers (8 dims of one token per thread,
+// for the keys and for the values; mappings in the kernel) while the waves compute on the other:
 //   Khat [16 tok][128] fp16 = c[idx] * cscale       row stride 272 B (16 B pad: no bank clash)
 //   Shat [16 tok][128] fp16 = +-1                    QJL keys only
 //   VhatT [128 dim][16 tok] fp16 = c[vidx] * cscale  transposed: the PV A operand; row stride
@@ -56,7 +56,6 @@ struct PrefillParams {
     tq_region kidx, ksig, knorm, krnorm, vidx, vnorm;
     const float* k_cent;
     const float* v_cent;
-    int k_perm;
     int k_lg, v_lg;  // lane-grouped key / value tiles (TQ_TILE_KEYS / TQ_TILE_VALUES)
     float k_cs, v_cs, v_cinv;
     int block_size;
@@ -92,7 +91,7 @@ __device__ __forceinline__ float sum_over_groups(float x) {
 // Raw packed data one thread dequantises for a tile.
 struct Raw {
     uint32_t kw[2], vw[2];   // dwords holding the 8 index fields (funnel-shifted by the byte offset)
-    uint32_t sg0, sg1, sg2, sg3;  // sign bits (QJL keys): sg0 = dword of byte pp, or the whole row if permuted
+    uint32_t sg0;            // sign bits (QJL keys): the dword holding byte pk of the sign row
     uint32_t nrm;            // fp16 norm bits (threads 0-47: K norm, K residual norm, V norm)
     int nv;                  // usable rows of the tile (0: unreadable block)
 };
@@ -187,7 +186,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         }
     }
 
-    // ---- dequantisation of tile ti by this thread: token tt, dims 8pp .. 8pp + 7 ----
+    // ---- dequantisation of tile ti by this thread: keys and signs of token tk, dims 8pk..8pk+7,
+    // values of token tt, dims 8pp..8pp+7.  Keys: each wave takes 4 whole rows (4w..4w+3), so a
+    // wave's key loads cover consecutive bytes; values: each wave takes dims 32w..32w+31 of all
+    // 16 rows, so its transposed LDS writes hit 4 dim rows 16 banks apart.
+    const int tk = 4 * (tid >> 6) + ((tid >> 4) & 3);
+    const int pk = tid & 15;
     const int tt = tid & 15;
     const int pp = tid >> 4;
     const int32_t* bt_row = p.bt + (int64_t)s * p.bt_stride;
@@ -209,13 +213,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     // sub-tile, for the row-major and the lane-grouped tile layouts.
     uint32_t ok, ov, o_sg;
     if (p.k_lg) {
-        const int c = 4 * tt + (pp >> 2);  // chunk: row tt, dim quarter pp / 4
+        const int c = 4 * tk + (pk >> 2);  // chunk: row tk, dim quarter pk / 4
         constexpr int C = 4 * KB + (KQJL ? 4 : 0);
-        ok = (uint32_t)(c * C + (pp & 3) * KB);
-        o_sg = (uint32_t)(c * C + 4 * KB);  // byte pp & 3 of it: dims 8pp..8pp+7
+        ok = (uint32_t)(c * C + (pk & 3) * KB);
+        o_sg = (uint32_t)(c * C + 4 * KB);  // byte pk & 3 of it: dims 8pk..8pk+7
     } else {
-        ok = (uint32_t)(tt * p.kidx.stride_row + KB * pp);
-        o_sg = (uint32_t)(tt * p.ksig.stride_row) + (p.k_perm ? 0u : 4u * (uint32_t)(pp >> 2));
+        ok = (uint32_t)(tk * p.kidx.stride_row + KB * pk);
+        o_sg = (uint32_t)(tk * p.ksig.stride_row) + 4u * (uint32_t)(pk >> 2);
     }
     if (p.v_lg) {
         ov = (uint32_t)((16 * (tt >> 2) + pp) * 4 * VB + (tt & 3) * VB);  // chunk: rows 4(tt/4).., dims 8pp..
@@ -230,7 +234,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         if (lg) return w0 + 4u;
         return (w0 + 4u < row_start + 4u * (uint32_t)row_dwords) ? w0 + 4u : w0;
     };
-    const uint32_t o_k0 = ok & ~3u, o_k1 = second(ok, p.k_lg, (uint32_t)(tt * p.kidx.stride_row), 4 * KB);
+    const uint32_t o_k0 = ok & ~3u, o_k1 = second(ok, p.k_lg, (uint32_t)(tk * p.kidx.stride_row), 4 * KB);
     const uint32_t o_v0 = ov & ~3u, o_v1 = second(ov, p.v_lg, (uint32_t)(tt * p.vidx.stride_row), 4 * VB);
     const uint32_t sh_k = (ok & 3u) * 8u, sh_v = (ov & 3u) * 8u;
     const int ntok = tid & 15;  // token of the norm threads (0-47)
@@ -251,16 +255,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         w.vw[0] = ld32(bv, o_v0);
         w.vw[1] = ld32(bv, o_v1);
         if (KQJL) {
-            // natural order: the dword holding byte pp; permuted: the whole row
-            const uint8_t* bs = base(p.ksig);
-            w.sg0 = ld32(bs, o_sg);
-            if (!p.k_perm) {
-                w.sg1 = w.sg2 = w.sg3 = 0;
-            } else {
-                w.sg1 = ld32(bs, o_sg + 4);
-                w.sg2 = ld32(bs, o_sg + 8);
-                w.sg3 = ld32(bs, o_sg + 12);
-            }
+            w.sg0 = ld32(base(p.ksig), o_sg);
         }
         w.nrm = 0;
         if (tid < 16) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.knorm) + (uint64_t)o_nm);
@@ -279,19 +274,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                 const uint32_t e = (f >> (2 * KB * k)) & ((1u << (2 * KB)) - 1u);
                 h[k] = *reinterpret_cast<const uint32_t*>(tab + 4 * e);
             }
-            *reinterpret_cast<tq_u32x4*>(b + tt * kKRow + 16 * pp) = h;
+            *reinterpret_cast<tq_u32x4*>(b + tk * kKRow + 16 * pk) = h;
         }
         if (KQJL) {
-            // sign of dim 8pp + j: natural bit 8pp + j; permuted (row bit 32c + k = dim 4k + c):
-            // bit 32 (j & 3) + 2pp + (j >> 2)
-            uint32_t bitsj = 0;
-            if (!p.k_perm) {
-                bitsj = (w.sg0 >> (8 * (pp & 3))) & 0xffu;
-            } else {
-                const uint32_t d[4] = {w.sg0, w.sg1, w.sg2, w.sg3};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) bitsj |= ((d[j & 3] >> (2 * pp + (j >> 2))) & 1u) << j;
-            }
+            // sign of dim 8pk + j: bit j of byte pk & 3 of the dword (natural bit order)
+            const uint32_t bitsj = (w.sg0 >> (8 * (pk & 3))) & 0xffu;
             tq_u32x4 h;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -300,7 +287,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
                 const uint32_t hi = ((bitsj >> (2 * k + 1)) & 1u) ? 0x3c00u : 0xbc00u;
                 h[k] = lo | (hi << 16);
             }
-            *reinterpret_cast<tq_u32x4*>(b + kOffS + tt * kKRow + 16 * pp) = h;
+            *reinterpret_cast<tq_u32x4*>(b + kOffS + tk * kKRow + 16 * pk) = h;
         }
         {
             const uint32_t f = __builtin_amdgcn_alignbit(w.vw[1], w.vw[0], sh_v);
@@ -475,6 +462,7 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
     if (q_dtype != TQ_F32 && q_dtype != TQ_F16 && q_dtype != TQ_BF16) return TQ_ERR_DTYPE;
     if (out_dtype != TQ_F32 && out_dtype != TQ_F16 && out_dtype != TQ_BF16) return TQ_ERR_DTYPE;
     if (flags & ~(TQ_PREFILL_CAUSAL | TQ_PREFILL_ROTATE)) return TQ_ERR_INVALID_ARGUMENT;
+    if (k->qjl && k->signs_permuted) return TQ_ERR_INVALID_ARGUMENT;  // paged caches: natural sign order
     if (max_blocks_per_seq < 0 || num_blocks < 1) return TQ_ERR_INVALID_ARGUMENT;  // unreadable entries read block 0
     if (num_seqs == 0 || max_q_len == 0) return TQ_OK;
     if (!q || !cu_seqlens_q || !seq_lens || !block_tables || !out || !k->centroids || !v->centroids)
@@ -482,7 +470,7 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
     if (block_table_stride < max_blocks_per_seq) return TQ_ERR_INVALID_ARGUMENT;
     const bool k_lg = k->layout == TQ_TILE_KEYS, v_lg = v->layout == TQ_TILE_VALUES;
     if ((k->layout != TQ_TILE_ROWS && !k_lg) || (v->layout != TQ_TILE_ROWS && !v_lg)) return TQ_ERR_INVALID_ARGUMENT;
-    if (k_lg && (k->signs_permuted || k->idx.stride_row != 16 * k->bits + (k->qjl ? 16 : 0)))
+    if (k_lg && k->idx.stride_row != 16 * k->bits + (k->qjl ? 16 : 0))
         return TQ_ERR_INVALID_ARGUMENT;
     if (v_lg && v->idx.stride_row != 16 * v->bits) return TQ_ERR_INVALID_ARGUMENT;
     int rc;
@@ -527,7 +515,6 @@ extern "C" int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, in
     p.vnorm = v->norm;
     p.k_cent = k->centroids;
     p.v_cent = v->centroids;
-    p.k_perm = k->signs_permuted ? 1 : 0;
     p.k_lg = k_lg ? 1 : 0;
     p.v_lg = v_lg ? 1 : 0;
     p.k_cs = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
