@@ -72,6 +72,18 @@ def timed(fn, steps, warmup):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+def read_stream_reference(dev, nbytes=1 << 31, steps=20, warmup=3):
+    """A practical read ceiling of the GPU the bench runs on: torch's amax over a 2 GiB int64
+    tensor (a library streaming reduction), timed like the workloads."""
+    import torch
+    x = torch.ones(nbytes // 8, dtype=torch.int64, device=dev)
+    ms = timed(lambda: torch.amax(x), steps, warmup)
+    del x
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"op": "torch.amax over a 2 GiB int64 tensor", "read_gbs": round(gbs, 1),
+            "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_lens_host, Hkv, gen, dev, chunk_tokens=1 << 20):
     """Compress synthetic K and V for every sequence into the caches (untimed setup)."""
     import torch
@@ -394,6 +406,8 @@ def main():
     if head is None:
         key = next(iter(extra))
         head = extra.pop(key)
+    stream_ref = read_stream_reference(dev)
+    print(f"# read stream reference {stream_ref['read_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     cpu = None
     if state4 is not None and not args.no_cpu_baseline:
         cpu = cpu_baseline_decode(state4)
@@ -423,7 +437,7 @@ def main():
             "traffic_source": traffic_src,
         },
         "cpu_baseline": cpu,
-        "details": {"headline": head, **extra,
+        "details": {"headline": head, **extra, "read_stream_reference": stream_ref,
                     "reference_published_us_per_layer": {"turbo3_v12_sparse_v": 843, "turbo4": 797,
                                                           "note": "MI355X Triton, shape unstated (README.md:102-103)"}},
     }
