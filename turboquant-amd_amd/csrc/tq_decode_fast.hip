@@ -83,8 +83,10 @@ __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
 #define TQ_FAST_QUAD 1
 #endif
 // 2- and 3-bit indices are looked up four at a time (a 4B-bit field -> 4 fp16 centroids, one
-// 8-byte entry) instead of in pairs.  3 bits: 4096 entries, not replicated (32 KB); 2 bits: 256
-// entries x 16 bank replicas, entry stride 128 bytes (32 KB).
+// 8-byte entry) instead of in pairs.  3 bits: 4096 entries (32 KB); 2 bits: 256 entries (2 KB);
+// neither replicated.  A K quad table sits at LDS address 0 and a 2-bit V quad table at
+// v2_quad_base<KB>(), so that a 2-bit lookup address is the index byte times 8 (one SDWA shift)
+// plus a constant that goes into the ds_read offset.
 template <int B>
 constexpr bool quad_table() {
     return TQ_FAST_QUAD && (B == 3 || B == 2);
@@ -92,7 +94,13 @@ constexpr bool quad_table() {
 // Bit position of the field in a quad table address (log2 of the entry stride).
 template <int B>
 constexpr int quad_shift() {
-    return B == 2 ? 7 : 3;
+    return 3;
+}
+// LDS address of a 2-bit V quad table: after the K table at 0 (2-bit quads: 2 KB; 3-bit quads
+// and 4-bit pair tables: 32 KB).
+template <int KB>
+constexpr uint32_t v2_quad_base() {
+    return KB == 2 ? 2048u : 32768u;
 }
 // Replicas of the fp4 sign table (fewer when a quad table takes the LDS).
 template <int KB, int VB>
@@ -163,7 +171,7 @@ struct LaneCtx {
     tq_i32x8 qph, qpl;          // q_proj * corr * cscale * 2^b in fp8: hi, (x - hi) * 16
     int sc_hi, sc_lo;           // E8M0 scales undoing 2^b and 2^(b+4)
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
-    uint32_t vquad;                // V quad table base (+ replica offset; a 3-bit K quad table is at address 0)
+    uint32_t vquad;                // 3-bit V quad table base (a 3-bit K quad table is at address 0)
     uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
     uint64_t hmask;             // lanes of real heads
     bool lo8;                   // column < 8: tile A
@@ -176,11 +184,10 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
     for (int cc = 0; cc < 4; ++cc) {
         tq_u32x4 a;
         if (quad_table<KB>()) {
-            // dims 8cc..8cc+7 of the lane's 32: two quads
-            // a 3-bit K quad table sits at LDS address 0: the address is the field times 8
-            const uint32_t base = KB == 3 ? 0u : c.kbank;
-            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc), base));
-            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc + 1), base));
+            // dims 8cc..8cc+7 of the lane's 32: two quads; the K quad table sits at LDS address 0,
+            // so the address is the field times 8
+            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc), 0u));
+            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc + 1), 0u));
             a[0] = lo[0];
             a[1] = lo[1];
             a[2] = hi[0];
@@ -330,8 +337,11 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
-                const tq_u32x2 xa = lds_read2(entry_addr<4 * VB, 1, quad_shift<VB>()>(wa, 4 * VB * qh, c.vquad));
-                const tq_u32x2 xb = lds_read2(entry_addr<4 * VB, 1, quad_shift<VB>()>(wb, 4 * VB * qh, c.vquad));
+                // 2 bits: a fixed table address, which goes into the ds_read offset
+                const uint32_t fa = entry_addr<4 * VB, 1, quad_shift<VB>()>(wa, 4 * VB * qh, VB == 2 ? 0u : c.vquad);
+                const uint32_t fb = entry_addr<4 * VB, 1, quad_shift<VB>()>(wb, 4 * VB * qh, VB == 2 ? 0u : c.vquad);
+                const tq_u32x2 xa = lds_read2(VB == 2 ? fa + v2_quad_base<KB>() : fa);
+                const tq_u32x2 xb = lds_read2(VB == 2 ? fb + v2_quad_base<KB>() : fb);
                 la[0][r] = xa[0];
                 la[1][r] = xa[1];
                 lb[0][r] = xb[0];
@@ -396,13 +406,11 @@ void decode_fast_kernel(FastDecodeParams p) {
             for (int e = tid; e < 4096; e += 256)
                 reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{pr[e & 63], pr[e >> 6]};
         } else if (quad) {
-            // 256 entries, one per thread: 16 replicas x 8 bytes
+            // 256 entries of 8 bytes, one per thread
             const int e = tid;
             const uint32_t lo = tq_pack_half2(cent[e & 3] * cs, cent[(e >> 2) & 3] * cs);
             const uint32_t hi = tq_pack_half2(cent[(e >> 4) & 3] * cs, cent[(e >> 6) & 3] * cs);
-            tq_u32x4* d = reinterpret_cast<tq_u32x4*>(t) + e * 8;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) d[r] = tq_u32x4{lo, hi, lo, hi};
+            reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{lo, hi};
         } else {
             // 2^(2 bits) entries (16, 64 or 256), 32 replicas x 4 bytes
             const int ent = 1 << (2 * bits);
@@ -432,15 +440,14 @@ void decode_fast_kernel(FastDecodeParams p) {
     c.lo8 = n < 8;
     const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
-    const uint32_t bank8 = 8u * (uint32_t)(lane & 15);  // 2-bit quad tables: 16 replicas of 8 bytes
-    c.kbank = lds0 + p.lds_k + (KB == 2 && quad_table<KB>() ? bank8 : bank4);
+    c.kbank = lds0 + p.lds_k + bank4;
     c.vbank = lds0 + p.lds_v + bank4;
     c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
-    // V quad table: address 0 when it is the K quad table, else its base from a VGPR (a VALU
-    // op takes one scalar operand, and the field mask is one)
+    // 3-bit V quad table: address 0 when it is the K quad table, else its base from a VGPR (a
+    // VALU op takes one scalar operand, and the field mask is one)
     c.vquad = lds0 + p.lds_v;
-    if (VB == 2) c.vquad += bank8;
-    else if (!(quad_table<KB>() && KB == 3 && p.lds_v == 0)) asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
+    if (VB == 3 && !(quad_table<KB>() && KB == 3 && p.lds_v == 0))
+        asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
     c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -749,17 +756,48 @@ const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count) {
 
 void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
                                uint32_t* lds_v, uint32_t* lds_scratch, size_t* total) {
-    // Tables at offsets that are multiples of their sizes: largest first.
+    // Each table at a multiple of its size (pair tables are addressed by OR).  Fixed addresses
+    // first: a K quad table at 0 (and any K table when a 2-bit V quad table follows it), a 2-bit
+    // V quad table right after the K table (its own copy even when K and V share a codebook);
+    // then the others, largest first, at the lowest free multiple of their size.
+    const bool kquad = TQ_FAST_QUAD && (kb == 3 || kb == 2), vquad = TQ_FAST_QUAD && (vb == 3 || vb == 2);
+    const bool v2 = vquad && vb == 2;
+    const size_t ks = kquad ? (kb == 3 ? (size_t)4096 * 8 : (size_t)256 * 8) : ((size_t)1 << (2 * kb)) * 128;
+    const size_t vs = vquad ? (vb == 3 ? (size_t)4096 * 8 : (size_t)256 * 8) : ((size_t)1 << (2 * vb)) * 128;
+    const size_t ss = kq ? (size_t)256 * 4 * ((kquad || vquad) ? 16 : 32) : 0;
+    struct Used {
+        size_t off, size;
+    } used[4];
+    int nu = 0;
+    size_t end = 0;
+    auto take = [&](uint32_t* o, size_t off, size_t size) {
+        *o = (uint32_t)off;
+        used[nu++] = {off, size};
+        end = off + size > end ? off + size : end;
+    };
+    auto place = [&](uint32_t* o, size_t size) {
+        for (size_t off = 0;; off += size) {
+            bool ok = true;
+            for (int i = 0; i < nu; ++i)
+                if (off < used[i].off + used[i].size && used[i].off < off + size) ok = false;
+            if (ok) {
+                take(o, off, size);
+                return;
+            }
+        }
+    };
+    const bool kfixed = kquad || v2;
+    if (kfixed) take(lds_k, 0, ks);
+    if (v2) take(lds_v, kb == 2 ? 2048 : 32768, vs);  // v2_quad_base<KB>() in the kernel
     struct T {
         size_t size;
         uint32_t* off;
     } t[3];
     int n = 0;
-    uint32_t dummy = 0;
-    const bool kquad = TQ_FAST_QUAD && (kb == 3 || kb == 2), vquad = TQ_FAST_QUAD && (vb == 3 || vb == 2);
-    t[n++] = {kq ? (size_t)256 * 4 * ((kquad || vquad) ? 16 : 32) : 0, lds_sign};
-    t[n++] = {kquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * kb)) * 128, lds_k};
-    t[n++] = {share ? 0 : (vquad ? (size_t)4096 * 8 : ((size_t)1 << (2 * vb)) * 128), share ? &dummy : lds_v};
+    if (ss) t[n++] = {ss, lds_sign};
+    else *lds_sign = 0;
+    if (!kfixed) t[n++] = {ks, lds_k};
+    if (!v2 && !share) t[n++] = {vs, lds_v};
     for (int i = 0; i < n; ++i)
         for (int j = i + 1; j < n; ++j)
             if (t[j].size > t[i].size) {
@@ -767,24 +805,10 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
                 t[i] = t[j];
                 t[j] = x;
             }
-    // A 3-bit K quad table goes first: the kernel addresses it from LDS address 0.
-    if (kquad && kb == 3)
-        for (int i = 1; i < n; ++i)
-            if (t[i].off == lds_k) {
-                T x = t[0];
-                t[0] = t[i];
-                t[i] = x;
-            }
-    size_t off = 0;
-    for (int i = 0; i < n; ++i) {
-        // each table at a multiple of its size (pair tables are addressed by OR)
-        if (t[i].size) off = (off + t[i].size - 1) / t[i].size * t[i].size;
-        *t[i].off = (uint32_t)off;
-        off += t[i].size;
-    }
-    if (share) *lds_v = *lds_k;
-    *lds_scratch = (uint32_t)off;  // 512 bytes: pairs of 3-bit fields while the quad tables are built
-    *total = off + 512;
+    for (int i = 0; i < n; ++i) place(t[i].off, t[i].size);
+    if (share && !v2) *lds_v = *lds_k;
+    *lds_scratch = (uint32_t)end;  // 512 bytes: pairs of 3-bit fields while the quad tables are built
+    *total = end + 512;
 }
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
