@@ -61,12 +61,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint8_t* base) {
 __device__ __forceinline__ uint32_t lds_read(uint32_t addr) { return *(lds_u32*)(uintptr_t)addr; }
 
 // LDS address of the table entry held in bits [pos, pos + W) of the word array w: the field is
-// moved to bit 7 (one shift or funnel shift) and merged with the lane's replica address (one
-// and-or).  Tables sit at LDS offsets that are multiples of their size.
+// moved to bit P, the log2 of the entry stride (one shift or funnel shift), and merged with the
+// table base plus the lane's replica offset (one and-or).  Tables sit at LDS offsets that are
+// multiples of their size.
 template <int W, int N, int P = 7>
 __device__ __forceinline__ uint32_t entry_addr(const uint32_t (&w)[N], int pos, uint32_t bank_addr) {
     const int wi = pos >> 5, sh = pos & 31;
     uint32_t f;
+    if (W == 8 && P == 3 && sh == 0) {
+        // byte 0 times 8 in one SDWA shift (the compiler turns the mask-and-shift into two ops;
+        // bytes 1-3 it selects by itself)
+        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(f)
+            : "v"(3u), "v"(w[wi]));
+        return f | bank_addr;
+    }
     if (sh + W <= 32 || wi + 1 >= N)
         f = sh >= P ? (w[wi] >> (sh - P)) : (w[wi] << (P - sh));
     else
@@ -148,7 +157,8 @@ struct KRaw {
     uint32_t kn[2], krn[2];     // fp16 norms of tokens 4g..4g+3 of the lane's tile
 };
 struct VRaw {
-    uint32_t vwA[4], vwB[4];    // index bits of dims 8n..8n+7 of tokens 4g..4g+3 (bits 0 .. 8*VB-1)
+    uint32_t vwA[4], vwB[4];    // index bits of dims 8n..8n+7 of tokens 4g..4g+3 (bits 0 .. 8*VB-1;
+                                // 2-bit quad tables: odd tokens at bits 16-31)
     uint32_t vn[2];             // fp16 norms of tokens 4g..4g+3 of the lane's tile
 };
 // Wave-uniform description of a pair.
@@ -338,8 +348,9 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
             for (int r = 0; r < 4; ++r) {
                 const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
                 // 2 bits: a fixed table address, which goes into the ds_read offset
-                const uint32_t fa = entry_addr<4 * VB, 1, quad_shift<VB>()>(wa, 4 * VB * qh, VB == 2 ? 0u : c.vquad);
-                const uint32_t fb = entry_addr<4 * VB, 1, quad_shift<VB>()>(wb, 4 * VB * qh, VB == 2 ? 0u : c.vquad);
+                const int pos = 4 * VB * qh + (VB == 2 ? 16 * (r & 1) : 0);
+                const uint32_t fa = entry_addr<4 * VB, 1, quad_shift<VB>()>(wa, pos, VB == 2 ? 0u : c.vquad);
+                const uint32_t fb = entry_addr<4 * VB, 1, quad_shift<VB>()>(wb, pos, VB == 2 ? 0u : c.vquad);
                 const tq_u32x2 xa = lds_read2(VB == 2 ? fa + v2_quad_base<KB>() : fa);
                 const tq_u32x2 xb = lds_read2(VB == 2 ? fb + v2_quad_base<KB>() : fb);
                 la[0][r] = xa[0];
@@ -651,8 +662,10 @@ void decode_fast_kernel(FastDecodeParams p) {
         // 4g..4g+3, VB bytes each; row r's fields go to bits 0 .. 8*VB-1 of vw[r].
         auto load1 = [&](uint32_t (&vw)[4], uint32_t soff) {
             if (VB == 2) {
+                // a quad table reads the odd rows' bytes in place (bits 16-31)
                 tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, o_vch, soff, 0);
-                vw[0] = a[0]; vw[1] = a[0] >> 16; vw[2] = a[1]; vw[3] = a[1] >> 16;
+                vw[0] = a[0]; vw[1] = quad_table<VB>() ? a[0] : a[0] >> 16;
+                vw[2] = a[1]; vw[3] = quad_table<VB>() ? a[1] : a[1] >> 16;
             } else if (VB == 3) {
                 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
                 u32x3 a = __builtin_amdgcn_raw_buffer_load_b96(rv, o_vch, soff, 0);
