@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the TurboQuant packed-KV hot path on one MI355X.
 
-Prints ONE JSON line.  Headline (`value`): BASELINE config 4 — Sparse-V split-K decode, turbo3
+Prints ONE JSON line.  Headline (`value`): benchmark config 4 — Sparse-V split-K decode, turbo3
 + QJL keys / turbo3 values, batch 64 x context 32768, 48 query / 8 KV heads, block 16,
 threshold 1e-4 — in us per layer (one tq_decode call = one layer's decode for the batch).
 The same line carries configs 2 (turbo4 paged compress), 3 (turbo4 decode) and 5 (turbo2 + QJL
@@ -32,7 +32,7 @@ D = 128
 
 
 def outlier_kv(T, H, gen, device, dtype):
-    """N(0,1) x per-channel log-normal(0, 0.5) scale, 2% of channels x8."""
+    """N(0,1) x per-channel log-normal(0, 0.5) scale, 2% of channels x8 (benchmark config 2)."""
     import torch
     scale = torch.exp(torch.randn(H, D, generator=gen, device=device) * 0.5)
     out = torch.rand(H, D, generator=gen, device=device) < 0.02
@@ -241,7 +241,7 @@ def prefill_case(dev, steps, warmup, B=4, n=4096, Hq=48, Hkv=8, kb=3, kq=True, v
 
 
 def compress_case(dev, steps, warmup):
-    """K and V [16384, 8, 128] bf16 -> turbo4 paged blocks of 16 in 8192 blocks."""
+    """Benchmark config 2: K and V [16384, 8, 128] bf16 -> turbo4 paged blocks of 16 in 8192 blocks."""
     import torch
     from turboquant.core import make_codebook
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged

@@ -2,7 +2,7 @@
 
   codebooks.json      make_codebook values (d = 128, bits 1..4) from the restated QUADPACK
                       iteration, cross-checked against the closed-form iteration before writing.
-  config1_oracle.npz  BASELINE config 1 (torch.manual_seed(0); randn(1024, 128); bits 3; QJL;
+  config1_oracle.npz  benchmark config 1 (torch.manual_seed(0); randn(1024, 128); bits 3; QJL;
                       WHT): packed indices / signs, norms, residual norms, and a checksum of the
                       input so a change of RNG or torch build is detected.
 

@@ -1,6 +1,6 @@
 """GPU parity: compression kernels vs the CPU oracle.
 
-Bar: packed indices / sign bits / bytes bit-exact except elements whose
+Bar (the path's parity target): packed indices / sign bits / bytes bit-exact except elements whose
 oracle value lies within a rounding band of a codebook boundary (counted and reported);
 norms within rtol 1e-2 / atol 1e-3.  The band is BAND_ULPS fp32 ulps at the coordinate scale
 1/sqrt(128) (2^-27): the WHT butterfly and the oracle's sgemm sum the same 128 terms in
@@ -61,7 +61,7 @@ def check_against_oracle(res, ref, cent, bnd, bits, use_qjl, name, band_ulps=BAN
 
 
 def test_config1_polarquant_compress(dev):
-    """K [1024,128] N(0,1) seed 0, bits=3, QJL, WHT."""
+    """Benchmark config 1: K [1024,128] N(0,1) seed 0, bits=3, QJL, WHT."""
     from turboquant.core import PolarQuantConfig, make_wht_matrix, polarquant_compress
     torch.manual_seed(0)
     K = torch.randn(1024, 128)
@@ -292,7 +292,7 @@ def test_compress_paged_bytes(dev, bits, qjl, block_size, layout):
 
 
 def test_config2_full_size_roundtrip(dev):
-    """BASELINE config 2 at full size: 16384 tokens x 8 heads bf16 turbo4 into 8192 blocks."""
+    """Benchmark config 2 at full size: 16384 tokens x 8 heads bf16 turbo4 into 8192 blocks."""
     from turboquant.core import make_wht_matrix
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged, to_reference_slots
     T, H, nb, bs = 16384, 8, 8192, 16

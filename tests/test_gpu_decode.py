@@ -1,6 +1,6 @@
 """GPU parity: decode attention kernels vs the float64 CPU oracle.
 
-Bar: attention outputs within rtol 1e-2 / atol 1e-3 of the reference
+Bar (the path's parity target): attention outputs within rtol 1e-2 / atol 1e-3 of the reference
 path (attention_unpacked_ref semantics with the correct split combine).  The kernel computes
 Q and the dequantized K/V in fp16 with fp32 accumulation.
 """
@@ -287,7 +287,7 @@ def test_sparse_v_reference_slot_layout(dev):
 
 
 def test_decode_constant_values_full_size(dev):
-    """BASELINE config 4 shape (B=64, ctx 32768, Hq 48 / Hkv 8): with every V token equal,
+    """Benchmark config 4 shape (B=64, ctx 32768, Hq 48 / Hkv 8): with every V token equal,
     the output equals that vector whatever the scores (size-independent property), dense and
     Sparse-V; plus one sequence checked against the oracle in full."""
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged
