@@ -89,14 +89,17 @@ def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.
     return out, skipped, total
 
 
-def run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, dtype=torch.bfloat16, chunk=None, thresh=0.0, stats=False):
+def run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, dtype=torch.bfloat16, chunk=None, thresh=0.0, stats=False,
+            share_codebook=False):
     from turboquant.kernels.paged import PagedKVFormat, decode_paged
     kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs, layout=case["layouts"][0])
     vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=case["layouts"][1])
     q = torch.from_numpy(case["q"]).to(dtype).to(dev)
     st = torch.zeros(2, dtype=torch.int64, device=dev) if stats else None
-    out = decode_paged(q, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
-                       torch.from_numpy(case["v_cache"]).to(dev), vf, _cb(vb).to(dev),
+    kc = _cb(kb).to(dev)
+    vc = kc if share_codebook else _cb(vb).to(dev)
+    out = decode_paged(q, torch.from_numpy(case["k_cache"]).to(dev), kf, kc,
+                       torch.from_numpy(case["v_cache"]).to(dev), vf, vc,
                        torch.from_numpy(case["bt"]).to(dev), torch.from_numpy(case["seq_lens"]).to(dev),
                        sm_scale=sm, corr_scale=cs, sparse_threshold=thresh, tokens_per_chunk=chunk, skip_stats=st)
     torch.cuda.synchronize()
@@ -113,6 +116,19 @@ def test_decode_bit_widths(dev, kb, kq, vb):
     sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
     got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk=64)
     want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=qr)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,kq", [(2, True), (2, False), (3, True), (4, False)])
+def test_decode_shared_codebook(dev, kb, kq):
+    """One centroid tensor for K and V (as a serving stack holds it): the kernel builds one
+    shared table, or, for 2-bit values, its own V table at the fixed address."""
+    S, Hq, Hkv, bs = 3, 12, 2, 16
+    lens = [200, 17, 64]
+    case = build_case(5 + kb, S, Hq, Hkv, lens, kb, kq, kb, bs)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, kq, kb, bs, sm, cs, chunk=96, share_codebook=True)
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, kb, sm, cs, q_round=qr)
     np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
