@@ -5,11 +5,18 @@ Prints ONE JSON line.  Headline (`value`): benchmark config 4 — Sparse-V split
 + QJL keys / turbo3 values, batch 64 x context 32768, 48 query / 8 KV heads, block 16,
 threshold 1e-4 — in us per layer (one tq_decode call = one layer's decode for the batch).
 The same line carries configs 2 (turbo4 paged compress), 3 (turbo4 decode) and 5 (turbo2 + QJL
-compress + decode step), the roofline of the headline kernel and a CPU baseline.
+compress + decode step), the shapes the reference publishes numbers for, the roofline of the
+headline kernel and a CPU baseline.
 
-Inputs are synthetic (seeded) and resident in HBM before the timed region; timing uses HIP
-events on the stream the kernels run on (torch's current stream), W untimed warmup steps, then
-exactly K timed steps bracketed by torch.cuda.synchronize().
+Inputs are synthetic (seeded) and resident in HBM before the timed region.  Each workload
+first runs an untimed, reported settle phase (its own step, repeated for a fixed wall time:
+the GPU's clocks ramp over the first tens of milliseconds of work), then W untimed warmup
+steps, then exactly K timed steps bracketed by torch.cuda.synchronize().  HIP events on the
+stream the kernels run on (torch's current stream) mark every step; `value` is the median
+step, the mean is reported beside it.
+
+The workload builders (WORKLOADS, build_decode_workload, compress workload) are shared with the
+GPU parity tests, which check exactly the inputs timed here.
 """
 
 from __future__ import annotations
@@ -18,7 +25,9 @@ import argparse
 import json
 import math
 import os
-import platform
+import random
+import re
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -28,7 +37,9 @@ sys.path.insert(0, str(ROOT / "turboquant-amd_amd"))
 
 METRIC = "packed-KV decode attn μs/layer + HBM GB/s (% roofline); compress GB/s"
 HBM_PEAK_GBS = 8000.0
+FP16_MFMA_TFLOPS = 2500.0
 D = 128
+SETTLE_S = 0.25
 
 
 def outlier_kv(T, H, gen, device, dtype):
@@ -40,56 +51,35 @@ def outlier_kv(T, H, gen, device, dtype):
     return (torch.randn(T, H, D, generator=gen, device=device) * scale).to(dtype)
 
 
-def profiled_traffic(head):
-    """HBM bytes per launch of the headline decode kernel from the committed rocprof summary.
-
-    profiles/decode_fast_kernel_config4_pmc.md holds FETCH_SIZE and WRITE_SIZE of the kernel (two
-    rocprofv3 --pmc runs of this script with --copy-calibration), scaled by what the same
-    counters read for two kernels of known traffic.  Returned only for the config 4 headline.
-    """
-    import re
-    path = ROOT / "profiles" / "decode_fast_kernel_config4_pmc.md"
-    if not head.get("workload", "").startswith("config4") or not path.exists():
-        return None, None
-    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", path.read_text(), re.M)
-    if not m:
-        return None, None
-    return int(m.group(1)), "profiles/decode_fast_kernel_config4_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)"
+def _lens3():
+    rng = random.Random(3)  # one generator per workload: any subset gives the same lengths
+    return [rng.randint(1024, 8192) for _ in range(32)]
 
 
-def timed(fn, steps, warmup):
-    import torch
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        fn()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps  # ms per step
+def _lens5():
+    rng = random.Random(5)
+    return [int(round(math.exp(rng.uniform(math.log(2048), math.log(131072))))) for _ in range(64)]
 
 
-def read_stream_reference(dev, nbytes=1 << 31, steps=20, warmup=3):
-    """A practical read ceiling of the GPU the bench runs on: torch's amax over a 2 GiB int64
-    tensor (a library streaming reduction), timed like the workloads."""
-    import torch
-    x = torch.ones(nbytes // 8, dtype=torch.int64, device=dev)
-    ms = timed(lambda: torch.amax(x), steps, warmup)
-    del x
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"op": "torch.amax over a 2 GiB int64 tensor", "read_gbs": round(gbs, 1),
-            "frac_of_8tbs": round(gbs / HBM_PEAK_GBS, 4)}
+# Benchmark configs 3-5; `lens` gives the per-sequence context lengths.
+WORKLOADS = {
+    "config3": dict(name="config3: turbo4 decode, B=32, Hq 32 / Hkv 8, ctx U[1K,8K], bs 16",
+                    B=32, Hq=32, Hkv=8, lens=_lens3, kb=4, kq=False, vb=4, thresh=0.0, bs=16, seed=3),
+    "config4": dict(name="config4: Sparse-V split-K decode, turbo3+QJL K / turbo3 V, B=64 x ctx 32768, "
+                         "Hq 48 / Hkv 8, bs 16, T=1e-4",
+                    B=64, Hq=48, Hkv=8, lens=lambda: [32768] * 64, kb=3, kq=True, vb=3, thresh=1e-4, bs=16, seed=4),
+    "config5": dict(name="config5: turbo2+QJL compress 64 new tokens + decode, B=64, Hq 64 / Hkv 8, "
+                         "ctx log-U[2K,128K], bs 16",
+                    B=64, Hq=64, Hkv=8, lens=_lens5, kb=2, kq=True, vb=2, thresh=0.0, bs=16, seed=5, new_tokens=True),
+}
 
 
-def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_lens_host, Hkv, gen, dev, chunk_tokens=1 << 20):
+def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_lens_host, Hkv, gen, dev,
+               chunk_tokens=1 << 20):
     """Compress synthetic K and V for every sequence into the caches (untimed setup)."""
     import torch
     from turboquant.kernels.paged import compress_paged
     bs = fmts[0].block_size
-    S = len(seq_lens_host)
     toks, slots = [], []
     pending = 0
     bt_host = block_tables.cpu()
@@ -105,7 +95,7 @@ def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_len
             compress_paged(x, slot, kv_cache_pair[which], fmts[which], centroids[which], boundaries[which])
         toks, slots, pending = [], [], 0
 
-    for s in range(S):
+    for s in range(len(seq_lens_host)):
         L = int(seq_lens_host[s])
         t = torch.arange(L)
         slots.append((bt_host[s, t // bs].long() * bs + t % bs).to(torch.int32))
@@ -116,15 +106,21 @@ def fill_paged(kv_cache_pair, fmts, centroids, boundaries, block_tables, seq_len
     flush()
 
 
-def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, steps, warmup, extra_compress=None,
-                time_rotated=False):
+def build_decode_workload(key, dev, lens=None):
+    """Inputs of benchmark workload `key` on `dev`: caches filled by compress_paged from the
+    outlier-channel distribution, random-permutation block tables, bf16 N(0,1) queries, the
+    split-K chunk from the planner, the workspace; config 5 also its 64 new tokens and slots."""
     import torch
+    from turboquant import _lib
     from turboquant.core import make_codebook
-    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged, plan_tokens_per_chunk
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, plan_tokens_per_chunk
 
+    w = WORKLOADS[key]
+    B, Hq, Hkv, bs, seed = w["B"], w["Hq"], w["Hkv"], w["bs"], w["seed"]
+    lens_host = list(lens if lens is not None else w["lens"]())
     gen = torch.Generator(device=dev).manual_seed(seed)
-    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
-    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout="values")
+    kf = PagedKVFormat(bits=w["kb"], qjl=w["kq"], block_size=bs)
+    vf = PagedKVFormat(bits=w["vb"], qjl=False, block_size=bs, layout="values")
     blocks_per = [math.ceil(L / bs) for L in lens_host]
     maxb = max(blocks_per)
     nb = sum(blocks_per) + 64
@@ -135,70 +131,113 @@ def decode_case(name, B, Hq, Hkv, lens_host, kb, kq, vb, thresh, bs, seed, dev, 
         bt[s, :n] = perm[o:o + n].to(torch.int32)
         o += n
     bt = bt.to(dev)
-    lens = torch.tensor(lens_host, dtype=torch.int32, device=dev)
-    kc, kbnd = make_codebook(D, kb, device=dev)
+    lens_t = torch.tensor(lens_host, dtype=torch.int32, device=dev)
+    kc, kbnd = make_codebook(D, w["kb"], device=dev)
     # one codebook tensor per bit width, shared by K and V as a serving stack holds it
-    vc, vbnd = (kc, kbnd) if vb == kb else make_codebook(D, vb, device=dev)
+    vc, vbnd = (kc, kbnd) if w["vb"] == w["kb"] else make_codebook(D, w["vb"], device=dev)
     k_cache = allocate_cache(nb, Hkv, kf, device=dev)
     v_cache = allocate_cache(nb, Hkv, vf, device=dev)
     fill_paged((k_cache, v_cache), (kf, vf), (kc, vc), (kbnd, vbnd), bt, lens_host, Hkv, gen, dev)
     q = torch.randn((B, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
-    out = torch.empty_like(q)
     msl = max(lens_host)
     chunk = plan_tokens_per_chunk(dev, B, Hq, Hkv, msl, kf, vf, kc is vc, lens_host)
-    from turboquant import _lib
     ws = torch.empty(_lib.lib().tq_decode_workspace_bytes(B, Hq, msl, chunk), dtype=torch.uint8, device=dev)
-    stats = torch.zeros(2, dtype=torch.int64, device=dev)
-
-    def step():
-        decode_paged(q, k_cache, kf, kc, v_cache, vf, vc, bt, lens, sparse_threshold=thresh,
-                     max_seq_len=msl, tokens_per_chunk=chunk, out=out, workspace=ws)
-
-    if extra_compress is not None:
-        step_inner = step
-        newk = outlier_kv(B, Hkv, gen, dev, torch.bfloat16)
-        newv = outlier_kv(B, Hkv, gen, dev, torch.bfloat16)
-        # one new token per sequence goes into the last slot of its context
+    st = dict(key=key, name=w["name"], B=B, Hq=Hq, Hkv=Hkv, q=q, out=torch.empty_like(q), k_cache=k_cache,
+              v_cache=v_cache, kf=kf, vf=vf, kc=kc, vc=vc, kbnd=kbnd, vbnd=vbnd, bt=bt, lens=lens_t,
+              lens_host=lens_host, msl=msl, chunk=chunk, ws=ws, thresh=w["thresh"], new_tokens=None)
+    if w.get("new_tokens"):
+        # one new token per sequence, written into the last slot of its context
         last = torch.tensor([L - 1 for L in lens_host])
         slot_new = (bt.cpu()[torch.arange(B), last // bs].long() * bs + last % bs).to(torch.int32).to(dev)
-        from turboquant.kernels.paged import compress_paged
+        st["new_tokens"] = (outlier_kv(B, Hkv, gen, dev, torch.bfloat16), outlier_kv(B, Hkv, gen, dev, torch.bfloat16),
+                            slot_new)
+    return st
 
-        def step():  # noqa: F811
-            compress_paged(newk, slot_new, k_cache, kf, kc, kbnd)
-            compress_paged(newv, slot_new, v_cache, vf, vc, vbnd)
-            step_inner()
 
-    ms = timed(step, steps, warmup)
-    ms_rot = None
+def decode_step(st, rotate=False, skip_stats=None):
+    """One benchmark step of a decode workload: [compress the new tokens,] decode the batch."""
+    from turboquant.kernels.paged import compress_paged, decode_paged
+
+    def step():
+        if st["new_tokens"] is not None:
+            newk, newv, slot_new = st["new_tokens"]
+            compress_paged(newk, slot_new, st["k_cache"], st["kf"], st["kc"], st["kbnd"])
+            compress_paged(newv, slot_new, st["v_cache"], st["vf"], st["vc"], st["vbnd"])
+        return decode_paged(st["q"], st["k_cache"], st["kf"], st["kc"], st["v_cache"], st["vf"], st["vc"], st["bt"],
+                            st["lens"], sparse_threshold=st["thresh"], max_seq_len=st["msl"],
+                            tokens_per_chunk=st["chunk"], out=st["out"], workspace=st["ws"], rotate=rotate,
+                            skip_stats=skip_stats)
+    return step
+
+
+def settle(fn, seconds=SETTLE_S):
+    """Untimed: run fn back to back for a fixed wall time; returns the milliseconds spent."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        for _ in range(8):
+            fn()
+        n += 8
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            break
+    return round((time.perf_counter() - t0) * 1e3, 1), n
+
+
+def timed(fn, steps, warmup, settle_s=SETTLE_S):
+    """Settle, W warmup steps, then K steps each bracketed by HIP events on the current stream.
+    Returns dict(median_ms, mean_ms, steps_ms, settle_ms)."""
+    import torch
+    settle_ms, settle_n = settle(fn, settle_s) if settle_s > 0 else (0.0, 0)
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return {"median_ms": statistics.median(per), "mean_ms": ev[0].elapsed_time(ev[-1]) / steps,
+            "steps_ms": per, "settle_ms": settle_ms, "settle_steps": settle_n}
+
+
+def decode_case(key, dev, steps, warmup, time_rotated=False):
+    import torch
+    st = build_decode_workload(key, dev)
+    t = timed(decode_step(st), steps, warmup)
+    ms = t["median_ms"]
+    res = {"workload": st["name"], "us_per_layer": ms * 1e3, "mean_us": t["mean_ms"] * 1e3,
+           "settle_ms": t["settle_ms"]}
     if time_rotated:
         # the same decode with q and the output in the model basis (rotations fused)
-        def step_rot():
-            decode_paged(q, k_cache, kf, kc, v_cache, vf, vc, bt, lens, sparse_threshold=thresh,
-                         max_seq_len=msl, tokens_per_chunk=chunk, out=out, workspace=ws, rotate=True)
-        ms_rot = timed(step_rot, steps, warmup)
-    skip_frac = None
-    if thresh > 0:
-        decode_paged(q, k_cache, kf, kc, v_cache, vf, vc, bt, lens, sparse_threshold=thresh,
-                     max_seq_len=msl, tokens_per_chunk=chunk, out=out, workspace=ws, skip_stats=stats)
+        res["rotated_us_per_layer"] = timed(decode_step(st, rotate=True), steps, warmup, settle_s=0.05)["median_ms"] * 1e3
+    tokens = sum(st["lens_host"])
+    kf, vf, Hkv = st["kf"], st["vf"], st["Hkv"]
+    kv_bytes = tokens * Hkv * (kf.token_bytes + vf.token_bytes)
+    io_bytes = 2 * st["B"] * st["Hq"] * D * 2 + st["bt"].numel() * 4 + st["B"] * 4
+    alg = kv_bytes + io_bytes
+    if st["new_tokens"] is not None:
+        # the compress step: bf16 K and V in, the packed rows out
+        alg += 2 * st["B"] * Hkv * D * 2 + st["B"] * Hkv * (kf.token_bytes + vf.token_bytes) + st["B"] * 4
+    res.update(algorithmic_bytes=alg, kv_bytes=kv_bytes, hbm_gbs=alg / (ms * 1e-3) / 1e9,
+               frac_of_8tbs=alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, tokens_per_chunk=st["chunk"],
+               mean_ctx=tokens / st["B"])
+    if st["thresh"] > 0:
+        stats = torch.zeros(2, dtype=torch.int64, device=dev)
+        decode_step(st, skip_stats=stats)()
         torch.cuda.synchronize()
         sk, tot = stats.tolist()
-        skip_frac = sk / max(tot, 1)
-    tokens = sum(lens_host)
-    kv_bytes = tokens * Hkv * (kf.token_bytes + vf.token_bytes)
-    io_bytes = 2 * B * Hq * D * 2 + bt.numel() * 4 + B * 4
-    alg_bytes = kv_bytes + io_bytes
-    res = {
-        "workload": name, "us_per_layer": ms * 1e3, "algorithmic_bytes": alg_bytes, "kv_bytes": kv_bytes,
-        "hbm_gbs": alg_bytes / (ms * 1e-3) / 1e9, "frac_of_8tbs": alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "tokens_per_chunk": chunk, "mean_ctx": tokens / B,
-    }
-    if skip_frac is not None:
-        res["sparse_v_skip_fraction"] = skip_frac
-    if ms_rot is not None:
-        res["rotated_us_per_layer"] = ms_rot * 1e3
-    state = dict(q=q, k_cache=k_cache, v_cache=v_cache, kf=kf, vf=vf, kc=kc, vc=vc, bt=bt, lens=lens,
-                 lens_host=lens_host, Hkv=Hkv, chunk=chunk)
-    return res, state
+        frac = sk / max(tot, 1)
+        res["sparse_v_skip_fraction"] = frac
+        # V tiles are fetched whole (the skip test needs the scores of a pair, which arrive
+        # after its loads were issued): skipped tokens save PV work, not bytes
+        res["bytes_fetched"] = alg
+        res["v_bytes_of_skipped_tokens"] = int(sk * vf.token_bytes)
+    return res, st
 
 
 def prefill_case(dev, steps, warmup, B=4, n=4096, Hq=48, Hkv=8, kb=3, kq=True, vb=3, bs=16, seed=7):
@@ -229,23 +268,27 @@ def prefill_case(dev, steps, warmup, B=4, n=4096, Hq=48, Hkv=8, kb=3, kq=True, v
     def step():
         prefill_paged(q, cu, k_cache, kf, kc, v_cache, vf, vc, bt, lens, causal=True, max_q_len=n, out=out)
 
-    ms = timed(step, steps, warmup)
+    ms = timed(step, steps, warmup, settle_s=0.1)["median_ms"]
     # (query row, visible key) pairs x 3 products (q.k, qp.signs, p.v) x 2 x 128 flops
     pairs = B * Hq * n * (n + 1) // 2
     flops = pairs * (3 if kq else 2) * 2 * D
     return {"workload": f"prefill: {B} x {n} new tokens (causal), Hq {Hq} / Hkv {Hkv}, "
                         f"turbo{kb}{'+QJL' if kq else ''} K / turbo{vb} V, bs {bs}",
             "us_per_layer": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
-            "frac_of_fp16_mfma": flops / (ms * 1e-3) / 1e12 / 2500.0,
+            "frac_of_fp16_mfma": flops / (ms * 1e-3) / 1e12 / FP16_MFMA_TFLOPS,
             "algorithmic_flops": flops}
 
 
-def compress_case(dev, steps, warmup):
-    """Benchmark config 2: K and V [16384, 8, 128] bf16 -> turbo4 paged blocks of 16 in 8192 blocks."""
+COMPRESS_T, COMPRESS_H, COMPRESS_NB, COMPRESS_BS = 16384, 8, 8192, 16
+
+
+def build_compress_workload(dev):
+    """Benchmark config 2 inputs: K and V [16384, 8, 128] bf16 (outlier channels), slots of a
+    seeded permutation of 8192 blocks of 16, turbo4 formats and codebook, zeroed caches."""
     import torch
     from turboquant.core import make_codebook
-    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
-    T, H, nb, bs = 16384, 8, 8192, 16
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache
+    T, H, nb, bs = COMPRESS_T, COMPRESS_H, COMPRESS_NB, COMPRESS_BS
     gen = torch.Generator(device=dev).manual_seed(2)
     k = outlier_kv(T, H, gen, dev, torch.bfloat16)
     v = outlier_kv(T, H, gen, dev, torch.bfloat16)
@@ -254,96 +297,198 @@ def compress_case(dev, steps, warmup):
     fmt = PagedKVFormat(bits=4, qjl=False, block_size=bs)
     vfmt = PagedKVFormat(bits=4, qjl=False, block_size=bs, layout="values")
     c, b = make_codebook(D, 4, device=dev)
-    kc = allocate_cache(nb, H, fmt, device=dev)
-    vc = allocate_cache(nb, H, vfmt, device=dev)
+    return dict(k=k, v=v, slots=slots, fmt=fmt, vfmt=vfmt, c=c, b=b,
+                kc=allocate_cache(nb, H, fmt, device=dev), vc=allocate_cache(nb, H, vfmt, device=dev))
+
+
+def compress_case(dev, steps, warmup):
+    """Benchmark config 2: K and V [16384, 8, 128] bf16 -> turbo4 paged blocks of 16 in 8192 blocks."""
+    from turboquant.kernels.paged import compress_paged
+    w = build_compress_workload(dev)
 
     def step():
-        compress_paged(k, slots, kc, fmt, c, b)
-        compress_paged(v, slots, vc, vfmt, c, b)
+        compress_paged(w["k"], w["slots"], w["kc"], w["fmt"], w["c"], w["b"])
+        compress_paged(w["v"], w["slots"], w["vc"], w["vfmt"], w["c"], w["b"])
 
-    ms = timed(step, steps, warmup)
-    alg = 2 * (T * H * D * 2 + T * H * fmt.token_bytes) + T * 4
+    t = timed(step, steps, warmup, settle_s=0.1)
+    ms = t["median_ms"]
+    T, H = COMPRESS_T, COMPRESS_H
+    alg = 2 * (T * H * D * 2 + T * H * w["fmt"].token_bytes) + T * 4
     return {"workload": "config2: turbo4 paged compress K+V, 16384 tok x 8 heads bf16, bs 16",
-            "us_per_layer": ms * 1e3, "algorithmic_bytes": alg, "compress_gbs": alg / (ms * 1e-3) / 1e9,
-            "frac_of_8tbs": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            "us_per_layer": ms * 1e3, "mean_us": t["mean_ms"] * 1e3, "algorithmic_bytes": alg,
+            "compress_gbs": alg / (ms * 1e-3) / 1e9, "frac_of_8tbs": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def _gather_tiles(cache_np, blocks, kh, fmt, L):
-    """Vectorized read of one (sequence, KV head) through its block table -> per-token payload."""
-    import numpy as np
-    bs = fmt.block_size
-    tiles = cache_np[blocks, kh]                                   # [nblk, tile]
-    nblk = tiles.shape[0]
-    out = {"idx": tiles[:, : bs * fmt.idx_bytes].reshape(nblk * bs, fmt.idx_bytes)[:L],
-           "norm": tiles[:, fmt.off_norm: fmt.off_norm + 2 * bs].copy().view(np.uint16).reshape(-1)[:L]}
-    if fmt.qjl:
-        out["signs"] = tiles[:, fmt.off_signs: fmt.off_signs + 16 * bs].reshape(nblk * bs, 16)[:L]
-        out["rnorm"] = tiles[:, fmt.off_rnorm: fmt.off_rnorm + 2 * bs].copy().view(np.uint16).reshape(-1)[:L]
+def published_shapes(dev, steps, warmup):
+    """The shapes the reference publishes MI355X numbers for (docs/BLOG_NOTES.md): the v7
+    packed_attention API at BH 8/32/64 x Sk 32768 (turbo2 + QJL keys, turbo2 values), the
+    end-to-end compress_k + compress_v + packed_attention pipeline at those shapes
+    (:167-171: 1.41 / 5.33 / 10.84 ms) and compress_k at N = 2K..524K vectors (:66-71:
+    0.050 / 0.059 / 0.098 / 0.271 ms)."""
+    import torch
+    from turboquant.kernels.packed_attention import packed_attention
+    from turboquant.kernels.packed_compress import compress_k, compress_k_permuted, compress_v, solve_codebook
+    out = {"attention": [], "pipeline": [], "compress_k": []}
+    gen = torch.Generator(device=dev).manual_seed(11)
+    cb = solve_codebook(D, 2).to(dev)
+    bnd = (cb[:-1] + cb[1:]) / 2
+    g64 = torch.Generator().manual_seed(12)
+    Pi, _ = torch.linalg.qr(torch.randn(D, D, generator=g64, dtype=torch.float64))
+    S = torch.randn(D, D, generator=g64, dtype=torch.float64)
+    PiT = Pi.T.contiguous().float().to(dev)
+    PiST = (Pi @ S.T).contiguous().float().to(dev)
+    cs = math.sqrt(math.pi / 2) / D
+    pub = {8: 1.41, 32: 5.33, 64: 10.84}
+    for BH in (8, 32, 64):
+        Sk = 32768
+        K = torch.randn(BH * Sk, D, generator=gen, device=dev)
+        V = torch.randn(BH * Sk, D, generator=gen, device=dev)
+        Q = (torch.randn(BH, D, generator=gen, device=dev) * 0.1).half()
+        Qp = (torch.randn(BH, D, generator=gen, device=dev) * 0.1).half()
+        ki, ks, kr, kn = compress_k_permuted(K, PiT, PiST, cb, bnd)
+        vi, vn = compress_v(V, PiT, cb, bnd)
+        ki, ks, vi = ki.view(BH, Sk, -1), ks.view(BH, Sk, -1), vi.view(BH, Sk, -1)
+        kr, kn, vn = kr.view(BH, Sk), kn.view(BH, Sk), vn.view(BH, Sk)
+
+        def attend():
+            return packed_attention(Q, Qp, ki, ks, kr, kn, vi, vn, cb, cs)
+
+        ms = timed(attend, steps, warmup, settle_s=0.05)["median_ms"]
+        nbytes = BH * Sk * (32 + 16 + 2 + 2 + 32 + 2) + 2 * BH * D * 2
+        out["attention"].append({"BH": BH, "Sk": Sk, "us": ms * 1e3, "hbm_gbs": nbytes / (ms * 1e-3) / 1e9})
+
+        def pipeline():
+            a = compress_k_permuted(K, PiT, PiST, cb, bnd)
+            b = compress_v(V, PiT, cb, bnd)
+            return packed_attention(Q, Qp, a[0].view(BH, Sk, -1), a[1].view(BH, Sk, -1), a[2].view(BH, Sk),
+                                    a[3].view(BH, Sk), b[0].view(BH, Sk, -1), b[1].view(BH, Sk), cb, cs)
+
+        ms = timed(pipeline, max(3, steps // 4), 2, settle_s=0.05)["median_ms"]
+        out["pipeline"].append({"BH": BH, "Sk": Sk, "us": ms * 1e3, "reference_published_us": pub[BH] * 1e3})
+        del K, V, ki, ks, kr, kn, vi, vn
+    pubk = {2048: 50, 32768: 59, 131072: 98, 524288: 271}
+    for N in (2048, 32768, 131072, 524288):
+        K = torch.randn(N, D, generator=gen, device=dev)
+        ms = timed(lambda: compress_k(K, PiT, PiST, cb, bnd), steps, warmup, settle_s=0.05)["median_ms"]
+        # two 128 x 128 fp32 products per row (rotation, sign projection)
+        out["compress_k"].append({"N": N, "us": ms * 1e3, "reference_published_us": pubk[N],
+                                  "fp32_tflops": N * 2 * 2 * D * D / (ms * 1e-3) / 1e12})
+        del K
     return out
 
 
-def cpu_baseline_decode(state, max_seconds=20.0):
-    """The oracle's float64 decode (a CPU restatement of the reference's PyTorch path:
-    dequantize, scores, softmax, weighted sum, with the Sparse-V chunk walk) on whole sequences
-    of the headline workload, scaled by tokens to the full batch."""
-    import numpy as np
-    from oracle import decode as odec
+def profile_value(name, key):
+    """A `key: value` line of a committed rocprof summary under profiles/ (None if absent)."""
+    path = ROOT / "profiles" / name
+    if not path.exists():
+        return None
+    m = re.search(rf"^{re.escape(key)}:\s*([-+0-9.eE]+)", path.read_text(), re.M)
+    return None if m is None else float(m.group(1))
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the headline decode kernel (two rocprofv3 --pmc runs of this script
+    with --copy-calibration, FETCH_SIZE and WRITE_SIZE scaled by two kernels of known traffic)."""
+    v = profile_value("decode_fast_kernel_config4_pmc.md", "traffic_bytes_per_launch")
+    return (int(v), "profiles/decode_fast_kernel_config4_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)") \
+        if v is not None else (None, None)
+
+
+def parity_counts():
+    """Compress index mismatches of configs 1 and 2 against the oracle, by distance from the
+    nearest codebook boundary, as the GPU parity tests last recorded them."""
+    path = ROOT / "profiles" / "compress_parity_config1_config2.md"
+    if not path.exists():
+        return None
+    m = re.search(r"```json\n(.*?)\n```", path.read_text(), re.S)
+    return json.loads(m.group(1)) if m else None
+
+
+def cpu_info():
+    model = None
     try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    threads = min(os.cpu_count() or 1, 16)
-    from turboquant.kernels.paged import to_rows_layout
-    kf, vf = state["kf"], state["vf"]
-    # the payload in row form (index rows, then sign rows): what _gather_tiles reads
-    kc_np = to_rows_layout(state["k_cache"], kf).cpu().numpy()
-    vc_np = to_rows_layout(state["v_cache"], vf).cpu().numpy()
-    bt = state["bt"].cpu().numpy()
-    q = state["q"].float().cpu().numpy().astype(np.float64)
-    kcb = state["kc"].double().cpu().numpy()
-    vcb = state["vc"].double().cpu().numpy()
-    Hkv = state["Hkv"]
-    G = q.shape[1] // Hkv
-    limiter = threadpool_limits(limits=threads) if threadpool_limits is not None else None
-    t0 = time.perf_counter()
-    done_tokens = 0
-    seqs = 0
-    for s in range(len(state["lens_host"])):
-        L = state["lens_host"][s]
-        blocks = bt[s, : math.ceil(L / kf.block_size)]
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    import torch
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "torch_num_threads": torch.get_num_threads()}
+
+
+def cpu_baseline_decode(st, max_seconds=20.0):
+    """The reference's PyTorch path in fp32 on the host cores (oracle/torch_ref.py: paged gather,
+    dequantisation by table gather, bmm scores with the QJL term, softmax with the split-aware
+    Sparse-V rule, bmm with V) on whole sequences of the headline workload, timed until
+    max_seconds, scaled by tokens to the full batch."""
+    import numpy as np
+    import torch
+    from oracle import paged as opaged
+    from oracle import torch_ref
+    kf, vf = st["kf"], st["vf"]
+    bs, Hkv, G = kf.block_size, st["Hkv"], st["Hq"] // st["Hkv"]
+    q = st["q"].float().cpu()
+    kcb, vcb = st["kc"].float().cpu(), st["vc"].float().cpu()
+    sm, cs = 1 / math.sqrt(D), math.sqrt(math.pi / 2) / D
+    info = cpu_info()
+    el = 0.0
+    done_tokens = seqs = 0
+    for s in range(st["B"]):
+        L = st["lens_host"][s]
+        nbl = math.ceil(L / bs)
+        blocks = st["bt"][s, :nbl].long()
+        # host copy of the sequence's tiles, in the row-major tile layout (untimed preparation)
+        kt = st["k_cache"].index_select(0, blocks).cpu().numpy()
+        vt = st["v_cache"].index_select(0, blocks).cpu().numpy()
+        krows = torch.from_numpy(np.stack([_rows_tiles(kt[:, h], kf, opaged) for h in range(Hkv)], axis=1))
+        vrows = torch.from_numpy(np.stack([_rows_tiles(vt[:, h], vf, opaged) for h in range(Hkv)], axis=1))
+        local_bt = torch.arange(nbl, dtype=torch.int32)
+        t0 = time.perf_counter()
         for kh in range(Hkv):
-            kp = _gather_tiles(kc_np, blocks, kh, kf, L)
-            vp = _gather_tiles(vc_np, blocks, kh, vf, L)
-            k, sg, rn = odec.dequant_keys(kp, kcb, kf.bits, kf.qjl)
-            v = odec.dequant_values(vp, vcb, vf.bits)
-            hs = slice(kh * G, (kh + 1) * G)
-            odec.decode_chunked(q[s, hs], q[s, hs], k, sg, rn, v, 1 / math.sqrt(D),
-                                math.sqrt(math.pi / 2) / D, state["chunk"], 1e-4)
+            kp = torch_ref.gather_rows(krows, local_bt, L, kh, bs, kf.idx_bytes, kf.qjl)
+            vp = torch_ref.gather_rows(vrows, local_bt, L, kh, bs, vf.idx_bytes, False)
+            k, sg, rn = torch_ref.dequant(kp, kcb, kf.bits, kf.qjl)
+            v, _, _ = torch_ref.dequant(vp, vcb, vf.bits, False)
+            qs = q[s, kh * G:(kh + 1) * G]
+            torch_ref.decode(qs, qs, k, sg, rn, v, sm, cs, st["chunk"], st["thresh"])
+        el += time.perf_counter() - t0
         done_tokens += L
         seqs += 1
-        if time.perf_counter() - t0 > max_seconds:
+        if el > max_seconds:
             break
-    el = time.perf_counter() - t0
-    if limiter is not None:
-        limiter.restore_original_limits()
-    total = sum(state["lens_host"])
-    us_full = el / done_tokens * total * 1e6
-    return {"value": round(us_full, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"{seqs} of {len(state['lens_host'])} sequences (all {Hkv} KV heads, {done_tokens} tokens), "
-                      f"numpy float64 oracle incl. paged gather + dequant, {el:.1f} s, scaled linearly by tokens",
-            "cpu_model": platform.processor() or platform.machine()}
+    total = sum(st["lens_host"])
+    return {"value": round(el / done_tokens * total * 1e6, 1), "unit": "us/layer", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{seqs} of {st['B']} sequences (all {Hkv} KV heads, {done_tokens} tokens), torch fp32 on the "
+                      f"host (paged gather, dequant, bmm scores + QJL, split-aware Sparse-V softmax, bmm V), "
+                      f"{el:.1f} s, scaled linearly by tokens",
+            **info}
+
+
+def _rows_tiles(tiles, fmt, opaged):
+    """Tiles [n, tile_bytes] in fmt's layout -> the same tiles in the row-major layout."""
+    import numpy as np
+    tok = opaged.tiles_to_tokens(tiles, fmt.block_size, fmt.bits, fmt.qjl, fmt.layout)
+    n, bs = tiles.shape[0], fmt.block_size
+    parts = [tok["idx"].reshape(n, -1)]
+    if fmt.qjl:
+        parts.append(tok["signs"].reshape(n, -1))
+    parts.append(tok["norm"].view(np.uint8).reshape(n, -1))
+    if fmt.qjl:
+        parts.append(tok["rnorm"].view(np.uint8).reshape(n, -1))
+    return np.ascontiguousarray(np.concatenate(parts, axis=1))
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # 100 + 100 by default: the first tens of milliseconds after the (host-side) set-up run
-    # ~12 % slower on MI355X (measured: 530 us/layer for a 30-step window after 5 warm-up steps,
-    # 463-471 us when re-timed right after), so the warm-up covers that ramp.
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["config2", "config3", "config4", "config5", "prefill"], default=None)
+    ap.add_argument("--no-published", action="store_true", help="skip the reference-published shapes")
+    ap.add_argument("--only", choices=["config2", "config3", "config4", "config5", "prefill", "published"],
+                    default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device-to-device copy (reference for rocprof byte counters)")
     args = ap.parse_args()
@@ -370,49 +515,55 @@ def main():
               "written each", file=sys.stderr, flush=True)
         del src, dst
     extra = {}
-    import random
+
+    def want(k):
+        return args.only in (None, k)
 
     head = None
-    state4 = None
-    if args.only in (None, "config4"):
-        head, state4 = decode_case(
-            "config4: Sparse-V split-K decode, turbo3+QJL K / turbo3 V, B=64 x ctx 32768, Hq 48 / Hkv 8, bs 16, T=1e-4",
-            64, 48, 8, [32768] * 64, 3, True, 3, 1e-4, 16, 4, dev, steps, warmup, time_rotated=True)
-        print(f"# config4 {head['us_per_layer']:.1f} us/layer, {head['hbm_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
-    if args.only in (None, "config3"):
-        rng = random.Random(3)  # one generator per workload: --only gives the same lengths
-        lens3 = [rng.randint(1024, 8192) for _ in range(32)]
-        r3, _ = decode_case("config3: turbo4 decode, B=32, Hq 32 / Hkv 8, ctx U[1K,8K], bs 16",
-                            32, 32, 8, lens3, 4, False, 4, 0.0, 16, 3, dev, steps, warmup)
-        extra["config3"] = r3
-        print(f"# config3 {r3['us_per_layer']:.1f} us/layer", file=sys.stderr, flush=True)
-    if args.only in (None, "config5"):
-        rng = random.Random(5)
-        lens5 = [int(round(math.exp(rng.uniform(math.log(2048), math.log(131072))))) for _ in range(64)]
-        r5, _ = decode_case("config5: turbo2+QJL compress 64 new tokens + decode, B=64, Hq 64 / Hkv 8, "
-                            "ctx log-U[2K,128K], bs 16", 64, 64, 8, lens5, 2, True, 2, 0.0, 16, 5, dev, steps, warmup,
-                            extra_compress=True)
-        extra["config5"] = r5
-        print(f"# config5 {r5['us_per_layer']:.1f} us/step", file=sys.stderr, flush=True)
-    if args.only in (None, "prefill"):
+    cpu = None
+    if want("config4"):
+        head, state4 = decode_case("config4", dev, steps, warmup, time_rotated=True)
+        print(f"# config4 {head['us_per_layer']:.1f} us/layer (mean {head['mean_us']:.1f}), {head['hbm_gbs']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+        if not args.no_cpu_baseline:
+            cpu = cpu_baseline_decode(state4)
+            print(f"# cpu baseline {cpu['value']:.0f} us/layer ({cpu['cores']} threads)", file=sys.stderr, flush=True)
+        del state4
+        torch.cuda.empty_cache()
+    for key in ("config3", "config5"):
+        if want(key):
+            r, _ = decode_case(key, dev, steps, warmup)
+            extra[key] = r
+            print(f"# {key} {r['us_per_layer']:.1f} us (mean {r['mean_us']:.1f})", file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
+    if want("prefill"):
         rp = prefill_case(dev, min(steps, 20), min(warmup, 5))
         extra["prefill"] = rp
         print(f"# prefill {rp['us_per_layer']:.1f} us/layer, {rp['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
-    if args.only in (None, "config2"):
+    if want("config2"):
         r2 = compress_case(dev, steps, warmup)
         extra["config2"] = r2
         print(f"# config2 {r2['us_per_layer']:.1f} us, {r2['compress_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    if (args.only == "published") or (args.only is None and not args.no_published):
+        extra["reference_published_shapes"] = published_shapes(dev, steps, warmup)
+        print("# published shapes done", file=sys.stderr, flush=True)
 
     if head is None:
         key = next(iter(extra))
         head = extra.pop(key)
-    stream_ref = read_stream_reference(dev)
-    print(f"# read stream reference {stream_ref['read_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
-    cpu = None
-    if state4 is not None and not args.no_cpu_baseline:
-        cpu = cpu_baseline_decode(state4)
     us = head["us_per_layer"]
-    traffic, traffic_src = profiled_traffic(head)
+    traffic, traffic_src = profiled_traffic() if head["workload"].startswith("config4") else (None, None)
+    mfma = profile_value("decode_fast_kernel_config4_pmc.md", "mfma_busy_fraction")
+    details = {"headline": head, **extra,
+               "timing": "median of K per-step HIP-event intervals after a settle phase (settle_ms, untimed) "
+                         "and W warmup steps; mean_us = total of the K steps / K",
+               "reference_published_us_per_layer": {"turbo3_v12_sparse_v": 843, "turbo4": 797,
+                                                    "note": "MI355X Triton, shape unstated (README.md:102-103)"}}
+    if mfma is not None:
+        details["mfma_busy_fraction_headline"] = mfma
+    par = parity_counts()
+    if par is not None:
+        details["parity"] = par
     line = {
         "metric": METRIC,
         "value": round(us, 3),
@@ -437,9 +588,7 @@ def main():
             "traffic_source": traffic_src,
         },
         "cpu_baseline": cpu,
-        "details": {"headline": head, **extra, "read_stream_reference": stream_ref,
-                    "reference_published_us_per_layer": {"turbo3_v12_sparse_v": 843, "turbo4": 797,
-                                                          "note": "MI355X Triton, shape unstated (README.md:102-103)"}},
+        "details": details,
     }
     print(json.dumps(line))
 

@@ -69,11 +69,14 @@ def polarquant_compress(x: torch.Tensor, centroids: torch.Tensor, boundaries: to
 
 
 def polarquant_compress_fp64(x: torch.Tensor, centroids: torch.Tensor, boundaries: torch.Tensor,
-                             use_qjl: bool, rotate: bool):
-    """float64 shadow: x_n = (x @ H) / (|x @ H| + 1e-8) with H = +-h exactly; idx = #{b < x_n}."""
+                             use_qjl: bool, rotate: bool, matrix: torch.Tensor | None = None):
+    """float64 shadow: x_n = (x @ H) / (|x @ H| + 1e-8) with H = +-h exactly (or the given
+    matrix, its fp32 entries taken exactly); idx = #{b < x_n}."""
     x64 = x.detach().cpu().double().reshape(-1, x.shape[-1])
     D = x64.shape[1]
-    if rotate:
+    if matrix is not None:
+        x_rot = x64 @ matrix.detach().cpu().double()
+    elif rotate:
         h = float(wht_matrix(D)[0, 0])
         H = torch.from_numpy(wht_closed_form(D, h))
         x_rot = x64 @ H
@@ -146,3 +149,50 @@ def compress_packed(x: np.ndarray, pit: np.ndarray, pist: np.ndarray | None, cen
         out.update(resid=resid, rnorm=np.sqrt((resid * resid).sum(axis=1)), proj=proj,
                    sign=(proj >= 0).astype(np.uint8), proj_scale=np.abs(resid) @ np.abs(P))
     return out
+
+
+def ulp32(v) -> np.ndarray:
+    """Spacing of float32 at |v| (the fp32 ulp of each value), float64."""
+    a = np.abs(np.asarray(v, dtype=np.float64)).astype(np.float32)
+    return np.spacing(a).astype(np.float64)
+
+
+def classify_strict(idx_test, idx_ref, x_ref, boundaries, idx_fp64):
+    """Index mismatches of a test computation against the fp32 reference restatement, under the
+    contract "bit-exact except elements within 1 ulp of a codebook boundary".
+
+    For each mismatch, the boundary between the two indices is b[min(i, j)] (left searchsorted:
+    idx = #{b < x}); its distance from the reference value is counted in fp32 ulps of
+    max(|x_ref|, |b|).  A mismatch within 1 ulp is accepted; one further out is accepted only
+    when the test index equals the float64 shadow's (the reference's fp32 rounding put it on the
+    wrong side).  Returns a dict of counts; `failures` must be 0."""
+    t = np.asarray(idx_test, dtype=np.int64).reshape(-1)
+    r = np.asarray(idx_ref, dtype=np.int64).reshape(-1)
+    f = np.asarray(idx_fp64, dtype=np.int64).reshape(-1)
+    x = np.asarray(x_ref, dtype=np.float64).reshape(-1)
+    b = np.asarray(boundaries, dtype=np.float64).reshape(-1)
+    mism = np.nonzero(t != r)[0]
+    out = {"elements": int(t.size), "mismatches": int(mism.size), "within_1ulp": 0, "ulp_1_to_8": 0,
+           "ulp_over_8": 0, "beyond_1ulp_test_equals_fp64": 0, "failures": 0, "ref_differs_from_fp64": int((r != f).sum())}
+    if mism.size == 0:
+        return out
+    adjacent = np.abs(t[mism] - r[mism]) == 1
+    k = np.clip(np.minimum(t[mism], r[mism]), 0, max(b.size - 1, 0))
+    bb = b[k] if b.size else np.zeros(mism.size)
+    d = np.abs(x[mism] - bb) / np.maximum(ulp32(np.maximum(np.abs(x[mism]), np.abs(bb))), 1e-300)
+    d = np.where(adjacent, d, np.inf)
+    le1 = d <= 1.0
+    out["within_1ulp"] = int(le1.sum())
+    out["ulp_1_to_8"] = int(((d > 1.0) & (d <= 8.0)).sum())
+    out["ulp_over_8"] = int((d > 8.0).sum())
+    eq64 = t[mism] == f[mism]
+    out["beyond_1ulp_test_equals_fp64"] = int((~le1 & eq64).sum())
+    out["failures"] = int((~le1 & ~eq64).sum())
+    return out
+
+
+def classify_strict_fp64(idx_test, idx_fp64, x_fp64, boundaries):
+    """classify_strict when the reference itself is the float64 restatement (compress_k /
+    compress_v, whose fp16 tl.dot products are not a target): a mismatch is accepted only within
+    1 fp32 ulp of the boundary."""
+    return classify_strict(idx_test, idx_fp64, x_fp64, boundaries, idx_fp64)

@@ -99,6 +99,23 @@ def decode_chunked(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, chunk: i
     return num / den[:, None], skipped, L
 
 
+def sparse_v_margins(q, qp, k_mse, signs, rnorm, sm_scale, corr_scale, chunk: int, tile: int = 16):
+    """Per token t: max_h (s_h,t - m_h,t) in natural-log units, m_h,t being the running max of
+    head h through t's tile inside t's chunk (the quantity decode_chunked compares with
+    log(threshold)); [L]."""
+    L = k_mse.shape[0]
+    s_all = scores(q, qp, k_mse, signs, rnorm, sm_scale, corr_scale)
+    out = np.empty(L)
+    for c0 in range(0, L, chunk):
+        c1 = min(c0 + chunk, L)
+        m = np.full(q.shape[0], -np.inf)
+        for t0 in range(c0, c1, tile):
+            t1 = min(t0 + tile, c1)
+            m = np.maximum(m, s_all[:, t0:t1].max(axis=1))
+            out[t0:t1] = (s_all[:, t0:t1] - m[:, None]).max(axis=0)
+    return out
+
+
 def prefill_dense(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, causal: bool = True):
     """n query tokens [n, G, 128] (qp likewise, or None) over one KV head's L tokens, the new
     tokens being the last n of them -> out [n, G, 128].

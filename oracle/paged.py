@@ -177,3 +177,43 @@ def to_slots(cache: np.ndarray, block_size: int, bits: int, qjl: bool, slot_byte
                 p = np.concatenate(parts)
                 out[b, r, h, :len(p)] = p
     return out
+
+
+def subtile_row_positions(bits: int, qjl: bool, layout: str) -> np.ndarray:
+    """pos[j] = byte of the row-major 16-row payload ([16 idx rows][16 sign rows]) that byte j
+    of the lane-grouped sub-tile holds.  Derived by running build_subtile on byte ids (low and
+    high byte planes separately: build_subtile only moves bytes), not by a second formula."""
+    idx_row = 16 * bits
+    ids_idx = np.arange(16 * idx_row, dtype=np.int64).reshape(16, idx_row)
+    ids_sg = (16 * idx_row + np.arange(256, dtype=np.int64)).reshape(16, 16) if qjl else None
+    planes = []
+    for shift in (0, 8):
+        i8 = ((ids_idx >> shift) & 0xFF).astype(np.uint8)
+        s8 = ((ids_sg >> shift) & 0xFF).astype(np.uint8) if qjl else None
+        planes.append(np.frombuffer(build_subtile(i8, s8, bits, layout), np.uint8).astype(np.int64))
+    return planes[0] | (planes[1] << 8)
+
+
+def tiles_to_tokens(tiles: np.ndarray, block_size: int, bits: int, qjl: bool, layout: str) -> dict:
+    """Whole tiles [n, tile_bytes] (any layout) -> per-token payload of their n * block_size rows
+    (idx [.., 16*bits] u8, signs [.., 16] u8, norm / rnorm [..] u16), vectorised."""
+    tiles = np.ascontiguousarray(tiles)
+    n = tiles.shape[0]
+    idx_row, off_signs, off_norm, off_rnorm, _ = tile_offsets(block_size, bits, qjl)
+    P = idx_row + (16 if qjl else 0)
+    if layout == "rows":
+        idx = tiles[:, :block_size * idx_row].reshape(n * block_size, idx_row)
+        signs = tiles[:, off_signs:off_signs + 16 * block_size].reshape(n * block_size, 16) if qjl else None
+    else:
+        pos = subtile_row_positions(bits, qjl, layout)
+        sub = tiles[:, :block_size * P].reshape(n * (block_size // 16), 16 * P)
+        rows = np.empty_like(sub)
+        rows[:, pos] = sub
+        idx = rows[:, :16 * idx_row].reshape(-1, idx_row)
+        signs = rows[:, 16 * idx_row:].reshape(-1, 16) if qjl else None
+    out = {"idx": idx,
+           "norm": np.ascontiguousarray(tiles[:, off_norm:off_norm + 2 * block_size]).view(np.uint16).reshape(-1)}
+    if qjl:
+        out["signs"] = signs
+        out["rnorm"] = np.ascontiguousarray(tiles[:, off_rnorm:off_rnorm + 2 * block_size]).view(np.uint16).reshape(-1)
+    return out

@@ -1,5 +1,7 @@
 """Test configuration: import paths, the `gpu` marker, shared helpers."""
 
+import json
+import os
 import pathlib
 import sys
 
@@ -29,3 +31,20 @@ def pytest_collection_modifyitems(config, items):
 @pytest.fixture(scope="session")
 def dev():
     return torch.device("cuda:0")
+
+
+# Compress parity counts (index mismatches by distance from the boundary) recorded by the GPU
+# tests; written as JSON to $TQ_PARITY_OUT at the end of the session when that is set.
+_PARITY: dict = {}
+
+
+@pytest.fixture(scope="session")
+def parity_log():
+    return _PARITY
+
+
+def pytest_sessionfinish(session, exitstatus):
+    path = os.environ.get("TQ_PARITY_OUT")
+    if path and _PARITY:
+        pathlib.Path(path).parent.mkdir(parents=True, exist_ok=True)
+        pathlib.Path(path).write_text(json.dumps(_PARITY, indent=1, sort_keys=True))

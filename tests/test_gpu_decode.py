@@ -348,3 +348,68 @@ def test_decode_constant_values_full_size(dev):
         hs = slice(kh * G, (kh + 1) * G)
         want = odec.decode_dense(qr[hs], qr[hs], k, sg, rn, v, 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128)
         np.testing.assert_allclose(out[0, hs].float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,vb", [(3, 3), (2, 2), (4, 4)])
+@pytest.mark.parametrize("layouts", [("keys", "values"), ("rows", "rows")])
+def test_decode_per_head_query_scales(dev, kb, vb, layouts):
+    """Query magnitudes spanning 1e-2 .. 1e2 across the heads of one GQA group (q_proj = q, so
+    the QJL operand spans the same range): every head against the fp64 oracle at the contract
+    tolerance.  Fast kernel (lane-grouped tiles) and general kernel (row-major tiles)."""
+    S, Hkv, G, bs = 2, 2, 8, 16
+    Hq = Hkv * G
+    case = build_case(620 + kb, S, Hq, Hkv, [300, 77], kb, True, vb, bs, layouts=layouts)
+    scales = 10.0 ** np.linspace(-2.0, 2.0, G)
+    case["q"] = (case["q"] * scales[np.arange(Hq) % G][None, :, None]).astype(np.float32)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, True, vb, bs, sm, cs, chunk=64)
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, True, vb, sm, cs, q_round=qr)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,vb", [(3, 3), (2, 2), (4, 4)])
+@pytest.mark.parametrize("layouts", [("keys", "values"), ("rows", "rows")])
+def test_decode_qjl_small_heads_beside_large(dev, kb, vb, layouts):
+    """Explicit q_proj with magnitudes 1e-2 .. 1e2 across one GQA group, the key norms zero so
+    the score is the QJL term alone, residual norms ~1e4 so the smallest head (1e-2) gets a
+    softmax spread of ~1 log unit: precision its QJL operand would lose to a block scale shared
+    with the head 1e4 larger (its elements would fall to the bottom of fp8's range) shows in its
+    output.  That head is checked against the fp64 oracle at the contract tolerance; the larger
+    ones only share the group: their logits span 4 to 1e4 log units, where the fast kernel's
+    fp8 hi + lo operand (2^-8 relative on the QJL term, a small correction of realistic scores)
+    and the oracle's own ties decide the one-hot softmax."""
+    from turboquant.kernels.paged import PagedKVFormat, decode_paged
+    S, Hkv, G, bs = 2, 2, 8, 16
+    Hq = Hkv * G
+    lens = [300, 77]
+    case = build_case(600 + kb, S, Hq, Hkv, lens, kb, True, vb, bs, layouts=layouts)
+    rng = np.random.default_rng(601 + kb)
+    nb = case["nb"]
+    _, _, off_norm, off_rnorm, _ = opaged.tile_offsets(bs, kb, True)
+    case["k_cache"][:, :, off_norm:off_norm + 2 * bs] = 0
+    rn = (rng.uniform(0.5, 1.5, (nb, Hkv, bs)) * 1e4).astype(np.float16)
+    case["k_cache"][:, :, off_rnorm:off_rnorm + 2 * bs] = rn.view(np.uint8).reshape(nb, Hkv, 2 * bs)
+    for s, L in enumerate(lens):
+        t = np.arange(L)
+        blk, row = case["bt"][s, t // bs], t % bs
+        case["k_tok"][s]["norm"][:] = 0
+        case["k_tok"][s]["rnorm"][:] = rn[blk, :, row].view(np.uint16)
+    scales = 10.0 ** np.linspace(-2.0, 2.0, G)
+    qp = (rng.standard_normal((S, Hq, 128)) * scales[np.arange(Hq) % G][None, :, None]).astype(np.float32)
+    kf = PagedKVFormat(bits=kb, qjl=True, block_size=bs, layout=layouts[0])
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=layouts[1])
+    q_t = torch.from_numpy(case["q"]).to(torch.bfloat16).to(dev)
+    qp_t = torch.from_numpy(qp).to(torch.bfloat16).to(dev)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    out = decode_paged(q_t, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
+                       torch.from_numpy(case["v_cache"]).to(dev), vf, _cb(vb).to(dev),
+                       torch.from_numpy(case["bt"]).to(dev), torch.from_numpy(case["seq_lens"]).to(dev),
+                       sm_scale=sm, corr_scale=cs, q_proj=qp_t, tokens_per_chunk=64)
+    torch.cuda.synchronize()
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, True, vb, sm, cs,
+                            qp=qp_t.float().cpu().numpy().astype(np.float64),
+                            q_round=q_t.float().cpu().numpy().astype(np.float64))
+    small = np.nonzero(scales[np.arange(Hq) % G] <= 0.011)[0]
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got[:, small], want[:, small], rtol=RTOL, atol=ATOL)

@@ -502,3 +502,74 @@ def test_permuted_sign_dequant_matches_natural():
     kp2 = dict(kp, signs=opack.permute_signs(kp["signs"]))
     _, s_perm, _ = odec.dequant_keys(kp2, kc, 2, True, signs_permuted=True)
     assert np.array_equal(s_nat, s_perm)
+
+
+@pytest.mark.parametrize("bits,qjl,layout", [(3, True, "keys"), (2, True, "keys"), (4, False, "keys"),
+                                             (3, False, "values"), (2, False, "values"), (4, False, "values"),
+                                             (3, True, "rows")])
+@pytest.mark.parametrize("bs", [16, 32])
+def test_tiles_to_tokens_matches_per_token_gather(bits, qjl, layout, bs):
+    """The vectorised tile reader (a permutation derived from build_subtile) equals the per-token,
+    chunk-by-chunk gather_sequence on random caches."""
+    rng = np.random.default_rng(bits * 10 + bs + int(qjl))
+    tb = opaged.tile_offsets(bs, bits, qjl)[4]
+    cache = rng.integers(0, 256, (6, 2, tb), dtype=np.uint8)
+    bt = np.array([3, 1, 4, 0, 2])
+    L = bs * 5 - 3
+    for h in range(2):
+        slow = opaged.gather_sequence(cache, bt, L, h, bs, bits, qjl, layout)
+        fast = opaged.tiles_to_tokens(cache[bt, h], bs, bits, qjl, layout)
+        for k in slow:
+            np.testing.assert_array_equal(slow[k], fast[k][:L])
+
+
+def test_sparse_v_margins_decide_like_decode_chunked():
+    """A token is dropped by decode_chunked exactly when its margin is <= log(threshold)."""
+    rng = np.random.default_rng(5)
+    G, L = 6, 300
+    q = rng.standard_normal((G, 128)) * 8
+    k = rng.standard_normal((L, 128))
+    v = rng.standard_normal((L, 128))
+    for thr in (1e-4, 1e-2):
+        _, sk, _ = odec.decode_chunked(q, None, k, None, None, v, 0.1, 0.0, 96, thr)
+        m = odec.sparse_v_margins(q, None, k, None, None, 0.1, 0.0, 96)
+        assert sk == int((m <= math.log(thr)).sum()) and sk > 0
+
+
+@pytest.mark.parametrize("kb,kq,vb", [(3, True, 3), (2, True, 2), (4, False, 4)])
+def test_torch_reference_path_matches_oracle(kb, kq, vb):
+    """oracle/torch_ref.py (the fp32 torch formulation bench.py times as the CPU baseline) against
+    the float64 numpy oracle: dequantisation exact, outputs and Sparse-V skip counts equal (run in
+    float64), and within 1e-5 in float32."""
+    from oracle import torch_ref
+    rng = np.random.default_rng(kb * 3 + vb)
+    L, G, bs = 700, 6, 16
+    kp = {"idx": rng.integers(0, 256, (L, 16 * kb), dtype=np.uint8),
+          "norm": (rng.uniform(5, 15, L)).astype(np.float16).view(np.uint16)}
+    if kq:
+        kp["signs"] = rng.integers(0, 256, (L, 16), dtype=np.uint8)
+        kp["rnorm"] = (rng.uniform(0, 3, L)).astype(np.float16).view(np.uint16)
+    vp = {"idx": rng.integers(0, 256, (L, 16 * vb), dtype=np.uint8),
+          "norm": (rng.uniform(5, 15, L)).astype(np.float16).view(np.uint16)}
+    kc = (np.sort(rng.standard_normal(2 ** kb)) * 0.1).astype(np.float32).astype(np.float64)
+    vc = (np.sort(rng.standard_normal(2 ** vb)) * 0.1).astype(np.float32).astype(np.float64)
+    k, sg, rn = odec.dequant_keys(kp, kc, kb, kq)
+    v = odec.dequant_values(vp, vc, vb)
+    tp = lambda pl: {n: torch.from_numpy(a.copy().view(np.uint8).reshape(L, -1)) for n, a in pl.items()}  # noqa: E731
+    tk, tsg, trn = torch_ref.dequant(tp(kp), torch.from_numpy(kc), kb, kq)
+    tv, _, _ = torch_ref.dequant(tp(vp), torch.from_numpy(vc), vb, False)
+    np.testing.assert_array_equal(tk.double().numpy(), k.astype(np.float32).astype(np.float64))
+    np.testing.assert_array_equal(tv.double().numpy(), v.astype(np.float32).astype(np.float64))
+    if kq:
+        np.testing.assert_array_equal(tsg.numpy(), sg)
+    q = rng.standard_normal((G, 128)) * 4
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    for chunk, thr in ((None, 0.0), (256, 1e-4), (96, 1e-2)):
+        want, sk, _ = odec.decode_chunked(q, q, k, sg, rn, v, sm, cs, chunk or L, thr)
+        t64 = lambda a: None if a is None else torch.from_numpy(np.asarray(a, np.float64))  # noqa: E731
+        got, tsk = torch_ref.decode(t64(q), t64(q), t64(k), t64(sg), t64(rn), t64(v), sm, cs, chunk, thr)
+        np.testing.assert_allclose(got.numpy(), want, rtol=1e-12, atol=1e-12)
+        assert tsk == sk
+        got32, _ = torch_ref.decode(torch.from_numpy(q).float(), torch.from_numpy(q).float(), tk,
+                                    tsg, trn, tv, sm, cs, chunk, thr)
+        np.testing.assert_allclose(got32.double().numpy(), want, rtol=1e-4, atol=1e-5)

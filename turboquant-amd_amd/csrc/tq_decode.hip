@@ -259,7 +259,7 @@ __device__ __forceinline__ float sum_over_groups(float x) {
 template <int KB, bool KQJL, int VB, bool NV, bool QCOLS, bool FULL>
 __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cur, int nvalid, SoftmaxState& st,
                                              const tq_half8 (&qop)[4], const tq_half8 (&qlo)[QCOLS ? 1 : 4],
-                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], uint32_t kbank, uint32_t vbank,
+                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], float qpm, uint32_t kbank, uint32_t vbank,
                                              uint32_t one, const LaneOff& o, int g, uint64_t hmask,
                                              uint64_t gmask, const DecodeParams& p, bool sparse, bool count) {
     // ---------------- QK products ----------------
@@ -304,13 +304,13 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cu
     }
 
     // ---------------- online softmax ----------------
-    // score = norm * S (+ rnorm * QJL; corr_scale is folded into the QJL operand)
+    // score = norm * S (+ rnorm * qpm * QJL: corr_scale and the operand scale 2^-e in qpm)
     float sc[4];
     float mt = kNegInf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         float v = norm_at<NV>(cur.kn, r) * s1v[r];
-        if (KQJL) v = __builtin_fmaf(norm_at<NV>(cur.krn, r), s2v[r], v);
+        if (KQJL) v = __builtin_fmaf(norm_at<NV>(cur.krn, r) * qpm, s2v[r], v);
         sc[r] = (FULL || 4 * g + r < nvalid) ? v : kNegInf;
         mt = fmaxf(mt, sc[r]);
     }
@@ -463,6 +463,7 @@ void decode_kernel(DecodeParams p) {
     tq_half8 qop[4];
     tq_half8 qlo[QCOLS ? 1 : 4];
     tq_half8 qpop[KQJL ? 4 : 1];
+    float qpm = 0.f;  // QJL products of this lane's head -> log2 units (undoes the operand scale)
     {
         float qv[32], qpv[32];
         const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
@@ -489,6 +490,19 @@ void decode_kernel(DecodeParams p) {
         // q x H: elements 32g + i (or, for permuted signs, 4i + g) over lane groups g
         if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);
         if (KQJL && p.rot_qp) tq_wht_row_g4(qpv, p.wht_h);
+        // The QJL operand is q_proj * 2^e in fp16, e per head (column) so that the head's largest
+        // |q_proj| lands in [2^12, 2^13): a head with a small q_proj stays out of the fp16
+        // subnormals.  sm_scale * log2(e) * corr_scale * 2^-e is applied to the fp32 products.
+        int qpe = 0;
+        if (KQJL) {
+            float amax = 0.f;
+#pragma unroll
+            for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(qpv[k]));
+            amax = max_over_groups(amax);  // lanes (n, g), g = 0..3: the four quarters of head n
+            if (amax > 0.f && amax < __builtin_huge_valf()) qpe = 12 - ilogbf(amax);
+            qpe = qpe < -100 ? -100 : (qpe > 100 ? 100 : qpe);
+            qpm = ldexpf(p.qp_scale * p.corr_scale, -qpe);
+        }
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
 #pragma unroll
@@ -505,7 +519,7 @@ void decode_kernel(DecodeParams p) {
                 if (KQJL) {
                     // sign operand slot j of MFMA cc holds bit 4cc + j/2 + 16(j&1) of the lane's 32
                     const int bit = 4 * cc + (j >> 1) + 16 * (j & 1);
-                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)(-qpv[bit] * p.qp_scale * p.corr_scale);
+                    qpop[cc % (KQJL ? 4 : 1)][j] = (_Float16)(-ldexpf(qpv[bit], qpe));
                 }
             }
         }
@@ -622,7 +636,7 @@ void decode_kernel(DecodeParams p) {
             const int ahead = t + D - 1;
             fetch(t_begin + 16 * ahead, ahead < nload, ring[(k + D - 1) % D], nv[(k + D - 1) % D]);
             if (nv[k])
-                compute_tile<KB, KQJL, VB, NV, QCOLS, true>(ring[k], nv[k], sm, qop, qlo, qpop, kbank, vbank, one, o,
+                compute_tile<KB, KQJL, VB, NV, QCOLS, true>(ring[k], nv[k], sm, qop, qlo, qpop, qpm, kbank, vbank, one, o,
                                                             g, hmask, gmask, p, sparse, count);
         }
         if (done) break;
@@ -647,7 +661,7 @@ void decode_kernel(DecodeParams p) {
             load_tile<KB, KQJL, VB, NV, true>(tr, tl, o, p.rrow, p.vstep, NV && p.v_lg);
         }
         if (tv)
-            compute_tile<KB, KQJL, VB, NV, QCOLS, false>(tr, tv, sm, qop, qlo, qpop, kbank, vbank, one, o, g, hmask,
+            compute_tile<KB, KQJL, VB, NV, QCOLS, false>(tr, tv, sm, qop, qlo, qpop, qpm, kbank, vbank, one, o, g, hmask,
                                                          gmask, p, sparse, count);
     }
 
@@ -924,10 +938,9 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     return TQ_OK;
 }
 
-namespace {
-
 // rotate: q (and q_proj when it is q) enter as q x H, the output leaves as out x H.
-int decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+// Shared by tq_decode, tq_decode_rotated and the fixed-scratch variant (tq_decode_internal.h).
+int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
                 const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
                 int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
                 const tq_kv_view* k, const tq_kv_view* v,
@@ -1149,8 +1162,6 @@ int decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, in
                          rotate, st);
 }
 
-}  // namespace
-
 extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
                          const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
                          int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
@@ -1164,7 +1175,7 @@ extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64
                          void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
                          unsigned long long* skip_stats,
                          tq_stream_t stream) {
-    return decode_impl(0, q, q_dtype, q_stride_seq, q_stride_head, q_proj, qp_stride_seq, qp_stride_head, num_seqs, num_q_heads,
+    return tq_decode_impl(0, q, q_dtype, q_stride_seq, q_stride_head, q_proj, qp_stride_seq, qp_stride_head, num_seqs, num_q_heads,
                        num_kv_heads, head_dim, k, v, block_size, num_blocks, block_tables, block_table_stride,
                        max_blocks_per_seq, seq_lens, max_seq_len, sm_scale, corr_scale, sparse_threshold,
                        tokens_per_chunk, workspace, workspace_bytes, out, out_dtype, out_stride_seq, out_stride_head,
@@ -1184,7 +1195,7 @@ extern "C" int tq_decode_rotated(const void* q, int q_dtype, int64_t q_stride_se
                                  void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
                                  unsigned long long* skip_stats,
                                  tq_stream_t stream) {
-    return decode_impl(1, q, q_dtype, q_stride_seq, q_stride_head, q_proj, qp_stride_seq, qp_stride_head, num_seqs, num_q_heads,
+    return tq_decode_impl(1, q, q_dtype, q_stride_seq, q_stride_head, q_proj, qp_stride_seq, qp_stride_head, num_seqs, num_q_heads,
                        num_kv_heads, head_dim, k, v, block_size, num_blocks, block_tables, block_table_stride,
                        max_blocks_per_seq, seq_lens, max_seq_len, sm_scale, corr_scale, sparse_threshold,
                        tokens_per_chunk, workspace, workspace_bytes, out, out_dtype, out_stride_seq, out_stride_head,

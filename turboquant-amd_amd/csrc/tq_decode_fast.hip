@@ -518,15 +518,18 @@ void decode_fast_kernel(FastDecodeParams p) {
         // q x H: x[i] is element 16g + (i & 15) + 64 (i >> 4), so register bits 0-3 and 4 are
         // element bits 0-3 and 6, lane bits 4-5 element bits 4-5
         if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);
+        // One E8M0 scale per column (query head): a lane's 32 fp8 elements straddle two of the
+        // instruction's 32-wide scale blocks (dims 16g.. and 64 + 16g..), so the scale is uniform
+        // over the column's four lane groups; a head whose q_proj is orders of magnitude below
+        // its group's largest still gets its own exponent and keeps its precision.
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             x[i] *= p.qp_mul;
             amax = fmaxf(amax, fabsf(x[i]));
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-        // 2^b brings the largest magnitude into [128, 256): inside the fp8 e4m3 normal range
+        amax = max_over_groups(amax);  // lanes col, col ^ 16, col ^ 32, col ^ 48
+        // 2^b brings the head's largest magnitude into [128, 256): inside the fp8 e4m3 normal range
         int b = 0;
         if (amax > 0.f && amax < __builtin_huge_valf()) b = 7 - ilogbf(amax);
         b = b < -100 ? -100 : (b > 100 ? 100 : b);

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "turboquant_hip.h"
+
 struct FastDecodeParams {
     const void* q;
     int64_t q_ss, q_sh;
@@ -62,3 +64,19 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
 // Launch decode_fast_kernel (grid of 256-thread workgroups, 4 work units each).
 int tq_decode_fast_launch(const FastDecodeParams& p, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream);
+
+// The implementation behind tq_decode (rotate = 0) and tq_decode_rotated (rotate = 1): the
+// same arguments, checks and launches.
+int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+                   const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+                   int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                   const tq_kv_view* k, const tq_kv_view* v,
+                   int block_size, int64_t num_blocks,
+                   const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                   const int32_t* seq_lens, int max_seq_len,
+                   float sm_scale, float corr_scale, float sparse_threshold,
+                   int tokens_per_chunk,
+                   void* workspace, size_t workspace_bytes,
+                   void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+                   unsigned long long* skip_stats,
+                   tq_stream_t stream);
