@@ -5,7 +5,8 @@
  * Every entry point:
  *   - takes plain device pointers, sizes and byte strides (no framework types);
  *   - launches asynchronously on the given stream and never allocates device memory
- *     (outputs and workspaces are caller-owned);
+ *     (outputs and workspaces are caller-owned; tq_decode_noalloc uses a fixed array of the
+ *     library instead of a workspace);
  *   - returns TQ_OK, a negative TQ_ERR_* code for an argument rejected on the host
  *     before any launch, or a positive hipError_t reported by the launch.
  *
@@ -44,6 +45,7 @@ typedef struct ihipStream_t* tq_stream_t; /* == hipStream_t */
 #define TQ_ERR_DTYPE            (-7)
 #define TQ_ERR_BLOCK_SIZE       (-8)  /* block_size not a positive multiple of 16 */
 #define TQ_ERR_CHUNK            (-9)  /* tokens_per_chunk not a positive multiple of 16 */
+#define TQ_ERR_SCRATCH_LIMIT    (-10) /* tq_decode_noalloc: the call needs more than the fixed scratch */
 
 /* ---- dtype codes ------------------------------------------------------------- */
 #define TQ_F32  0
@@ -298,6 +300,32 @@ int tq_prefill(const void* q, int q_dtype, int64_t q_stride_token, int64_t q_str
                tq_stream_t stream);
 
 size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk);
+
+/*
+ * tq_decode without a caller workspace and without any device allocation: the split-K partial
+ * results go to a fixed array of TQ_NOALLOC_SCRATCH_BYTES inside this library (one copy per
+ * GPU, held from the library's load on that GPU until the process ends; its device address is
+ * looked up once per device on the first call there).  Same arguments (minus the workspace),
+ * checks, kernels and results as tq_decode.  Returns TQ_ERR_SCRATCH_LIMIT, before any launch,
+ * when tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk) exceeds
+ * TQ_NOALLOC_SCRATCH_BYTES (choose a larger tokens_per_chunk).  Calls that overlap in time on
+ * one GPU share its array and race; nothing is carried between calls.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ */
+#define TQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int tq_decode_noalloc(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,
+                      const void* q_proj, int64_t qp_stride_seq, int64_t qp_stride_head,
+                      int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                      const tq_kv_view* k, const tq_kv_view* v,
+                      int block_size, int64_t num_blocks,
+                      const int32_t* block_tables, int64_t block_table_stride, int max_blocks_per_seq,
+                      const int32_t* seq_lens, int max_seq_len,
+                      float sm_scale, float corr_scale, float sparse_threshold,
+                      int tokens_per_chunk,
+                      void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
+                      unsigned long long* skip_stats,
+                      tq_stream_t stream);
 
 /* Work units (one per sequence, KV head and chunk of tokens_per_chunk tokens) that tq_decode
  * can run at once on the current device for this configuration: resident waves per compute

@@ -107,6 +107,9 @@ extern "C" const char* tq_status_string(int status) {
         case TQ_ERR_DTYPE: return "unsupported dtype";
         case TQ_ERR_BLOCK_SIZE: return "block_size must be a positive multiple of 16";
         case TQ_ERR_CHUNK: return "tokens_per_chunk must be a positive multiple of 16";
+        case TQ_ERR_SCRATCH_LIMIT:
+            return "the call needs more split-K scratch than tq_decode_noalloc's fixed array "
+                   "(TQ_NOALLOC_SCRATCH_BYTES): use a larger tokens_per_chunk";
         default: break;
     }
     if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -61,6 +61,7 @@ class TQKVView(ctypes.Structure):
 
 
 TILE_ROWS, TILE_KEYS, TILE_VALUES = 0, 1, 2
+NOALLOC_SCRATCH_BYTES = 64 << 20  # TQ_NOALLOC_SCRATCH_BYTES
 
 
 _vp = ctypes.c_void_p
@@ -107,6 +108,12 @@ SIGNATURES = {
          _f32, _f32, _i32, _vp, _i32, _i64, _i64, _vp],
     ),
     "tq_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "tq_decode_noalloc": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _vp, _i64, _i64, _i32, _i32, _i32, _i32,
+         ctypes.POINTER(TQKVView), ctypes.POINTER(TQKVView), _i32, _i64, _vp, _i64, _i32, _vp, _i32,
+         _f32, _f32, _f32, _i32, _vp, _i32, _i64, _i64, _vp, _vp],
+    ),
     "tq_decode_concurrent_units": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
     "tq_polarquant_compress_matrix": (
         _i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
