@@ -548,6 +548,9 @@ def main():
         extra["reference_published_shapes"] = published_shapes(dev, steps, warmup)
         print("# published shapes done", file=sys.stderr, flush=True)
 
+    if head is None and args.only == "published":
+        print(json.dumps({"reference_published_shapes": extra["reference_published_shapes"]}))
+        return
     if head is None:
         key = next(iter(extra))
         head = extra.pop(key)

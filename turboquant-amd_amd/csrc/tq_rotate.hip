@@ -1,26 +1,19 @@
-// Compression with a general rotation matrix (fp32), for the entry points that take an arbitrary
-// rotation_matrix or the PiT / PiST pair instead of the Walsh-Hadamard transform.
+// polarquant_compress with a general rotation matrix (fp32), for the entry point that takes an
+// arbitrary rotation_matrix instead of the Walsh-Hadamard transform (core/quantizer.py:135-183):
+//   x_rot = x @ R; norm = |x_rot|; x_n = x_rot / (norm + 1e-8); idx = #{b < x_n};
+//   k_mse = c[idx] * norm; QJL: r = (x_n - c[idx]) * norm, rnorm = |r|, sign = r >= 0 ? +1 : -1.
+// The product is fp32 FMAs summed over d = 0..127 in order.
 //
-// Two orders of operations, as in the reference:
-//   POLARQUANT (core/quantizer.py:135-183): x_rot = x @ R; norm = |x_rot|;
-//     x_n = x_rot / (norm + 1e-8); idx = #{b < x_n}; k_mse = c[idx] * norm;
-//     QJL: r = (x_n - c[idx]) * norm, rnorm = |r|, sign = r >= 0 ? +1 : -1.
-//   PACKED (kernels/packed_compress.py:44-142): norm = |x|; x_n = x * (1 / (norm + 1e-8));
-//     rot = x_n @ PiT; idx = #{b <= rot}; resid = (rot - c[idx]) * norm; rnorm = |resid|;
-//     proj = resid @ PiST; sign bit = proj >= 0; indices packed as a little-endian bit stream
-//     (2 bits: byte j = sum_c idx[4j+c] << 2c), sign bits LSB-first, norms fp16.
-// The reference computes the products with fp16 dot products; here they are fp32 FMAs summed
-// over d = 0..127 in order.
-//
-// Layout: the matrices (128 x 128 f32, row d holds R[d][0..127]) are staged in LDS once per
+// Layout: the matrix (128 x 128 f32, row d holds R[d][0..127]) is staged in LDS once per
 // workgroup; each wave handles 4 rows per pass, lane l owns output columns 2l and 2l+1, and the
-// 4 input rows are broadcast from LDS.  The products are VALU work (32K FMAs per row and
-// matrix), not on the paged hot path.
+// 4 input rows are broadcast from LDS.  VALU work (32K FMAs per row), off the paged hot path.
+//
+// The packed entry point (compress_k / compress_v with PiT and PiST) runs on the matrix cores:
+// tq_packed.hip.
 #include "tq_common.h"
 
 namespace {
 
-enum { ROT_POLARQUANT = 0, ROT_PACKED = 1 };
 constexpr int kRows = 4;     // rows per wave per pass
 constexpr int kD = TQ_HEAD_DIM;
 
@@ -30,20 +23,13 @@ struct RotParams {
     int64_t x_stride;
     int64_t n_rows;
     const float* rot;
-    const float* proj;
     const float* centroids;
     const float* boundaries;
-    // POLARQUANT outputs
     int64_t* indices;
     float* norms;
     float* k_mse;
     float* signs;
     float* rnorm;
-    // PACKED outputs
-    uint8_t* idx_out;     // [n_rows][16 * bits]
-    uint8_t* signs_out;   // [n_rows][16]
-    uint16_t* rnorm_out;  // fp16 [n_rows]
-    uint16_t* norm_out;   // fp16 [n_rows]
 };
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -73,21 +59,15 @@ __device__ __forceinline__ void rows_times_matrix(const float* rows, const float
     }
 }
 
-template <int BITS, bool QJL, int MODE>
+template <int BITS, bool QJL>
 __global__ __launch_bounds__(256) void rotate_compress_kernel(RotParams p) {
     constexpr int NC = 1 << BITS;
     constexpr int NB = NC - 1;
-    constexpr bool PROJ = MODE == ROT_PACKED && QJL;
     extern __shared__ float s_mem[];
     float* s_rot = s_mem;
-    float* s_proj = s_mem + kD * kD;                               // PROJ only
-    float* s_rows = s_mem + (PROJ ? 2 : 1) * kD * kD;              // [4 waves][kRows][128]
-    uint8_t* s_bytes = reinterpret_cast<uint8_t*>(s_rows + 4 * kRows * kD);  // [4][2][kRows][128]
+    float* s_rows = s_mem + kD * kD;  // [4 waves][kRows][128]
 
-    for (int i = threadIdx.x; i < kD * kD; i += 256) {
-        s_rot[i] = p.rot[i];
-        if (PROJ) s_proj[i] = p.proj[i];
-    }
+    for (int i = threadIdx.x; i < kD * kD; i += 256) s_rot[i] = p.rot[i];
     __shared__ float s_cent[NC], s_bnd[NB > 0 ? NB : 1];
     if (threadIdx.x < NC) s_cent[threadIdx.x] = p.centroids[threadIdx.x];
     if (threadIdx.x < NB) s_bnd[threadIdx.x] = p.boundaries[threadIdx.x];
@@ -96,8 +76,6 @@ __global__ __launch_bounds__(256) void rotate_compress_kernel(RotParams p) {
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     float* rows = s_rows + wave * kRows * kD;
-    uint8_t* bidx = s_bytes + wave * 2 * kRows * kD;
-    uint8_t* bsgn = bidx + kRows * kD;
     const int64_t ngroups = (p.n_rows + kRows - 1) / kRows;
 
     // Every wave of the workgroup runs the same number of passes (barriers inside).
@@ -114,126 +92,44 @@ __global__ __launch_bounds__(256) void rotate_compress_kernel(RotParams p) {
                 xv[r] = make_float2(tq_load1(p.x, o, p.x_dtype), tq_load1(p.x, o + 1, p.x_dtype));
             }
         }
-        float norm[kRows];
-        if (MODE == ROT_PACKED) {
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                norm[r] = __builtin_sqrtf(wave_sum(__builtin_fmaf(xv[r].x, xv[r].x, xv[r].y * xv[r].y)));
-                const float inv = 1.0f / (norm[r] + 1e-8f);
-                xv[r].x *= inv;
-                xv[r].y *= inv;
-            }
-        }
 #pragma unroll
         for (int r = 0; r < kRows; ++r) *reinterpret_cast<float2*>(rows + r * kD + 2 * lane) = xv[r];
         __syncthreads();
         float2 rot[kRows];
         rows_times_matrix(rows, s_rot, lane, rot);
-        __syncthreads();  // rows is rewritten below
+        __syncthreads();  // rows is rewritten by the next pass
 
-        if (MODE == ROT_POLARQUANT) {
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const float nrm = __builtin_sqrtf(wave_sum(__builtin_fmaf(rot[r].x, rot[r].x, rot[r].y * rot[r].y)));
-                const float den = nrm + 1e-8f;
-                const float xn[2] = {rot[r].x / den, rot[r].y / den};
-                float rr[2];
-                int idx[2];
+        for (int r = 0; r < kRows; ++r) {
+            const float nrm = __builtin_sqrtf(wave_sum(__builtin_fmaf(rot[r].x, rot[r].x, rot[r].y * rot[r].y)));
+            const float den = nrm + 1e-8f;
+            const float xn[2] = {rot[r].x / den, rot[r].y / den};
+            float rr[2];
+            int idx[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                int k = 0;
+#pragma unroll
+                for (int b = 0; b < NB; ++b) k += s_bnd[b] < xn[e] ? 1 : 0;
+                idx[e] = xn[e] != xn[e] ? NB : k;  // searchsorted puts NaN last
+                rr[e] = (xn[e] - s_cent[idx[e]]) * nrm;
+            }
+            float rn = 0.f;
+            if (QJL) rn = __builtin_sqrtf(wave_sum(__builtin_fmaf(rr[0], rr[0], rr[1] * rr[1])));
+            if (live[r]) {
+                const int64_t row = row0 + r;
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
-                    int k = 0;
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) k += s_bnd[b] < xn[e] ? 1 : 0;
-                    idx[e] = xn[e] != xn[e] ? NB : k;  // searchsorted puts NaN last
-                    rr[e] = (xn[e] - s_cent[idx[e]]) * nrm;
+                    const int64_t o = row * kD + 2 * lane + e;
+                    p.indices[o] = idx[e];
+                    p.k_mse[o] = s_cent[idx[e]] * nrm;
+                    if (QJL) p.signs[o] = rr[e] >= 0.f ? 1.f : -1.f;
                 }
-                float rn = 0.f;
-                if (QJL) rn = __builtin_sqrtf(wave_sum(__builtin_fmaf(rr[0], rr[0], rr[1] * rr[1])));
-                if (live[r]) {
-                    const int64_t row = row0 + r;
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        const int64_t o = row * kD + 2 * lane + e;
-                        p.indices[o] = idx[e];
-                        p.k_mse[o] = s_cent[idx[e]] * nrm;
-                        if (QJL) p.signs[o] = rr[e] >= 0.f ? 1.f : -1.f;
-                    }
-                    if (lane == 0) {
-                        p.norms[row] = nrm;
-                        if (QJL) p.rnorm[row] = rn;
-                    }
+                if (lane == 0) {
+                    p.norms[row] = nrm;
+                    if (QJL) p.rnorm[row] = rn;
                 }
             }
-        } else {
-            float2 resid[kRows];
-            float rn[kRows];
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const float rv[2] = {rot[r].x, rot[r].y};
-                float re[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    int k = 0;
-#pragma unroll
-                    for (int b = 0; b < NB; ++b) k += s_bnd[b] <= rv[e] ? 1 : 0;
-                    bidx[r * kD + 2 * lane + e] = (uint8_t)k;
-                    re[e] = (rv[e] - s_cent[k]) * norm[r];
-                }
-                resid[r] = make_float2(re[0], re[1]);
-                rn[r] = QJL ? __builtin_sqrtf(wave_sum(__builtin_fmaf(re[0], re[0], re[1] * re[1]))) : 0.f;
-            }
-            if (PROJ) {
-#pragma unroll
-                for (int r = 0; r < kRows; ++r) *reinterpret_cast<float2*>(rows + r * kD + 2 * lane) = resid[r];
-                __syncthreads();
-                float2 pj[kRows];
-                rows_times_matrix(rows, s_proj, lane, pj);
-#pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    bsgn[r * kD + 2 * lane] = pj[r].x >= 0.f ? 1 : 0;
-                    bsgn[r * kD + 2 * lane + 1] = pj[r].y >= 0.f ? 1 : 0;
-                }
-            }
-            __syncthreads();
-            // Pack: lane t < kRows * 4 * BITS builds index dword t % (4 BITS) of row t / (4 BITS);
-            // lanes 0..15 build the sign dwords (4 per row).
-            constexpr int IW = 4 * BITS;
-            if (lane < kRows * IW) {
-                const int r = lane / IW, w = lane % IW;
-                if (live[0] && row0 + r < p.n_rows) {
-                    uint32_t word = 0;
-                    const int d0 = (32 * w) / BITS;
-                    const int d1 = (32 * w + 31) / BITS;
-                    for (int d = d0; d <= d1 && d < kD; ++d) {
-                        const int sh = BITS * d - 32 * w;
-                        const uint32_t v = bidx[r * kD + d];
-                        word |= sh >= 0 ? (v << sh) : (v >> -sh);
-                    }
-                    reinterpret_cast<uint32_t*>(p.idx_out + (row0 + r) * (16 * BITS))[w] = word;
-                }
-            }
-            if (PROJ && lane < kRows * 4) {
-                const int r = lane / 4, w = lane % 4;
-                if (live[0] && row0 + r < p.n_rows) {
-                    uint32_t word = 0;
-#pragma unroll
-                    for (int b = 0; b < 32; ++b) word |= (uint32_t)bsgn[r * kD + 32 * w + b] << b;
-                    reinterpret_cast<uint32_t*>(p.signs_out + (row0 + r) * 16)[w] = word;
-                }
-            }
-            if (lane < kRows && row0 + lane < p.n_rows) {
-                // lane r writes row r's norms (every lane holds all kRows values)
-                float nv = norm[0], rv = rn[0];
-#pragma unroll
-                for (int r = 1; r < kRows; ++r)
-                    if (lane == r) {
-                        nv = norm[r];
-                        rv = rn[r];
-                    }
-                p.norm_out[row0 + lane] = (uint16_t)tq_f32_to_f16_bits(nv);
-                if (QJL) p.rnorm_out[row0 + lane] = (uint16_t)tq_f32_to_f16_bits(rv);
-            }
-            __syncthreads();  // byte staging is rewritten by the next pass
         }
     }
 }
@@ -244,18 +140,13 @@ int check_x(const void* x, int dtype) {
     return TQ_OK;
 }
 
-size_t rot_lds_bytes(bool proj) {
-    return (size_t)(proj ? 2 : 1) * kD * kD * 4 + 4 * kRows * kD * 4 + 4 * 2 * kRows * kD;
-}
+size_t rot_lds_bytes() { return (size_t)kD * kD * 4 + 4 * kRows * kD * 4; }
 
-template <int MODE>
 int launch_rotate(const RotParams& p, int bits, bool qjl, hipStream_t st) {
-    const bool proj = MODE == ROT_PACKED && qjl;
-    const size_t lds = rot_lds_bytes(proj);
+    const size_t lds = rot_lds_bytes();
     const void* kern = nullptr;
 #define TQ_RK(B)                                                                                       \
-    if (bits == B) kern = qjl ? (const void*)rotate_compress_kernel<B, true, MODE>                      \
-                              : (const void*)rotate_compress_kernel<B, false, MODE>;
+    if (bits == B) kern = qjl ? (const void*)rotate_compress_kernel<B, true> : (const void*)rotate_compress_kernel<B, false>;
     TQ_RK(1) TQ_RK(2) TQ_RK(3) TQ_RK(4)
 #undef TQ_RK
     if (!kern) return TQ_ERR_BITS;
@@ -264,12 +155,12 @@ int launch_rotate(const RotParams& p, int bits, bool qjl, hipStream_t st) {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return (int)e;
-    if ((size_t)max_lds < lds) return TQ_ERR_WORKSPACE;  // device cannot stage the matrices in LDS
+    if ((size_t)max_lds < lds) return TQ_ERR_WORKSPACE;  // device cannot stage the matrix in LDS
     e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     const int64_t groups = (p.n_rows + kRows - 1) / kRows;
     int64_t grid = (groups + 3) / 4;
-    const int64_t cap = (int64_t)cus * (proj ? 1 : 2);  // resident workgroups (LDS-limited)
+    const int64_t cap = (int64_t)cus * 2;  // resident workgroups (LDS-limited)
     grid = grid < cap ? grid : cap;
     void* args[] = {const_cast<RotParams*>(&p)};
     e = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(256), args, lds, st);
@@ -279,6 +170,13 @@ int launch_rotate(const RotParams& p, int bits, bool qjl, hipStream_t st) {
 }
 
 }  // namespace
+
+// tq_packed.hip
+size_t tq_packed_mfma_lds_bytes(bool proj);
+int tq_packed_mfma_launch(const void* x, int x_dtype, int64_t x_stride, int64_t n_rows, const float* pit,
+                          const float* pist, const float* centroids, const float* boundaries, int bits,
+                          uint8_t* idx_out, uint8_t* signs_out, uint16_t* rnorm_out, uint16_t* norm_out,
+                          hipStream_t st);
 
 extern "C" int tq_polarquant_compress_matrix(const void* x, int x_dtype, int64_t x_row_stride, int64_t n_rows,
                                              int head_dim, const float* rotation,
@@ -306,7 +204,7 @@ extern "C" int tq_polarquant_compress_matrix(const void* x, int x_dtype, int64_t
     p.k_mse = k_mse;
     p.signs = signs;
     p.rnorm = rnorm;
-    return launch_rotate<ROT_POLARQUANT>(p, bits, use_qjl != 0, (hipStream_t)stream);
+    return launch_rotate(p, bits, use_qjl != 0, (hipStream_t)stream);
 }
 
 extern "C" int tq_compress_packed(const void* x, int x_dtype, int64_t x_row_stride, int64_t n_rows, int head_dim,
@@ -321,22 +219,11 @@ extern "C" int tq_compress_packed(const void* x, int x_dtype, int64_t x_row_stri
     const bool qjl = pist != nullptr;
     if (qjl && (!signs_out || !rnorm_out)) return TQ_ERR_INVALID_ARGUMENT;
     if ((reinterpret_cast<uintptr_t>(idx_out) & 3) || (qjl && (reinterpret_cast<uintptr_t>(signs_out) & 3)) ||
-        (reinterpret_cast<uintptr_t>(norm_out) & 1) || (qjl && (reinterpret_cast<uintptr_t>(rnorm_out) & 1)))
+        (reinterpret_cast<uintptr_t>(norm_out) & 1) || (qjl && (reinterpret_cast<uintptr_t>(rnorm_out) & 1)) ||
+        (reinterpret_cast<uintptr_t>(pit) & 15) || (qjl && (reinterpret_cast<uintptr_t>(pist) & 15)))
         return TQ_ERR_ALIGNMENT;
     int rc = check_x(x, x_dtype);
     if (rc) return rc;
-    RotParams p = {};
-    p.x = x;
-    p.x_dtype = x_dtype;
-    p.x_stride = x_row_stride;
-    p.n_rows = n_rows;
-    p.rot = pit;
-    p.proj = pist;
-    p.centroids = centroids;
-    p.boundaries = boundaries;
-    p.idx_out = idx_out;
-    p.signs_out = signs_out;
-    p.rnorm_out = rnorm_out;
-    p.norm_out = norm_out;
-    return launch_rotate<ROT_PACKED>(p, bits, qjl, (hipStream_t)stream);
+    return tq_packed_mfma_launch(x, x_dtype, x_row_stride, n_rows, pit, pist, centroids, boundaries, bits, idx_out,
+                                 signs_out, rnorm_out, norm_out, (hipStream_t)stream);
 }
