@@ -215,6 +215,18 @@ def decode_case(key, dev, steps, warmup, time_rotated=False):
     if time_rotated:
         # the same decode with q and the output in the model basis (rotations fused)
         res["rotated_us_per_layer"] = timed(decode_step(st, rotate=True), steps, warmup, settle_s=0.05)["median_ms"] * 1e3
+        # the same tiles in a K cache spanning more than 2 GiB (a serving pool), the blocks moved
+        # past 2 GiB: the kernel's 64-bit per-tile addressing
+        kc = st["k_cache"]
+        shift = (3 << 30) // (kc.shape[1] * kc.shape[2]) + 1 - kc.shape[0] // 2
+        big = torch.zeros((kc.shape[0] + shift,) + tuple(kc.shape[1:]), dtype=torch.uint8, device=dev)
+        big[shift:] = kc
+        bt_big = torch.where(st["bt"] >= 0, st["bt"] + shift, st["bt"])
+        vbig = torch.zeros((big.shape[0],) + tuple(st["v_cache"].shape[1:]), dtype=torch.uint8, device=dev)
+        vbig[shift:] = st["v_cache"]
+        stb = dict(st, k_cache=big, v_cache=vbig, bt=bt_big, out=torch.empty_like(st["q"]))
+        res["k_cache_beyond_2gib_us_per_layer"] = timed(decode_step(stb), steps, warmup, settle_s=0.05)["median_ms"] * 1e3
+        del big, vbig, stb
     tokens = sum(st["lens_host"])
     kf, vf, Hkv = st["kf"], st["vf"], st["Hkv"]
     kv_bytes = tokens * Hkv * (kf.token_bytes + vf.token_bytes)

@@ -413,3 +413,44 @@ def test_decode_qjl_small_heads_beside_large(dev, kb, vb, layouts):
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got[:, small], want[:, small], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,kq,vb", [(3, True, 3), (4, False, 4), (2, True, 2)])
+def test_decode_cache_beyond_2gib(dev, kb, kq, vb):
+    """Caches spanning more than 2 GiB (the 64-bit per-tile addressing of the fast kernel): the
+    sequences' blocks sit at both ends of a ~3 GiB K cache.  The output equals the same tiles'
+    decode from a compact cache bit for bit, and the oracle at the contract tolerance."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, decode_paged
+    S, Hkv, G, bs = 3, 2, 6, 16
+    Hq = Hkv * G
+    lens = [300, 1000, 45]
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout="values")
+    nb_big = (3 << 30) // (Hkv * kf.tile_bytes) + 1
+    small = build_case(700 + kb, S, Hq, Hkv, lens, kb, kq, vb, bs)
+    nbs = small["nb"]
+    # compact block b -> big block: the first half near the start, the rest past 2 GiB
+    remap = np.where(np.arange(nbs) < nbs // 2, np.arange(nbs), nb_big - nbs + np.arange(nbs))
+    assert int(remap.max()) * Hkv * kf.tile_bytes > (2 << 30)
+    k_big = allocate_cache(nb_big, Hkv, kf, device=dev)
+    v_big = allocate_cache(nb_big, Hkv, vf, device=dev)
+    rm = torch.from_numpy(remap).to(dev)
+    k_big[rm] = torch.from_numpy(small["k_cache"]).to(dev)
+    v_big[rm] = torch.from_numpy(small["v_cache"]).to(dev)
+    bt_small = small["bt"]
+    bt_big = np.where(bt_small >= 0, remap[np.maximum(bt_small, 0)], -1).astype(np.int32)
+    q = torch.from_numpy(small["q"]).to(torch.bfloat16).to(dev)
+    lens_t = torch.from_numpy(small["seq_lens"]).to(dev)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    outs = []
+    for kc, vc, bt in ((k_big, v_big, bt_big), (torch.from_numpy(small["k_cache"]).to(dev),
+                                                   torch.from_numpy(small["v_cache"]).to(dev), bt_small)):
+        outs.append(decode_paged(q, kc, kf, _cb(kb).to(dev), vc, vf, _cb(vb).to(dev), torch.from_numpy(bt).to(dev),
+                                 lens_t, sm_scale=sm, corr_scale=cs, tokens_per_chunk=128, sparse_threshold=1e-4))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    want, _, _ = oracle_out(small, Hq, Hkv, kb, kq, vb, sm, cs, chunk=128, thresh=1e-4,
+                            q_round=q.float().cpu().numpy().astype(np.float64))
+    np.testing.assert_allclose(outs[0].float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+    del k_big, v_big
+    torch.cuda.empty_cache()

@@ -386,18 +386,13 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cu
 
 // QCOLS: the GQA group fits in 8 heads, so the 16 columns of the QK product carry q (hi part,
 // columns 0..7) and q - hi (lo part, columns 8..15); a lane swizzle merges them.
-#ifndef TQ_DECODE_DEPTH
-#define TQ_DECODE_DEPTH 2
-#endif
-#ifndef TQ_DECODE_WAVES
-#define TQ_DECODE_WAVES 3
-#endif
-// Tiles in flight per wave (register ring) and waves per SIMD.
-constexpr int kDepth = TQ_DECODE_DEPTH;
+// Tiles in flight per wave (register ring) and waves per SIMD (2 for the 16-column variants
+// with QJL keys and 3-bit values, whose registers do not fit 3).
+constexpr int kDepth = 2;
 
 template <int KB, bool KQJL, int VB, bool QCOLS>
 constexpr int decode_waves() {
-    return (TQ_DECODE_WAVES == 3 && !QCOLS && KQJL && VB == 3 && KB >= 3) ? 2 : TQ_DECODE_WAVES;
+    return (!QCOLS && KQJL && VB == 3 && KB >= 3) ? 2 : 3;
 }
 
 template <int KB, bool KQJL, int VB, bool QCOLS, bool NV>
@@ -862,22 +857,14 @@ int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num
     return e == hipSuccess ? TQ_OK : (int)e;
 }
 
-bool fast_path_enabled() {
-    static const bool on = [] {
-        const char* e = std::getenv("TQ_DECODE_FAST");
-        return !(e && e[0] == '0');
-    }();
-    return on;
-}
-
 // The fast kernel reads this library's tile layout: per cache one block stride and one head
 // stride for all regions, rows of 16*bits index bytes, 16 sign bytes and 2-byte norms, the
-// other regions after the index region of the same tile, and every tile reachable with 31-bit
-// offsets from the head's base.
+// other regions after the index region of the same tile.  *big: some tile lies 2 GiB or more
+// from its head's base (64-bit per-tile addressing).
 bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block_size, int64_t num_blocks,
-                  const int32_t* block_tables) {
+                  const int32_t* block_tables, bool* big) {
     // num_blocks >= 1: unreadable table entries are redirected to block 0 and masked
-    if (!fast_path_enabled() || !block_tables || num_blocks < 1 || group > 8 || k->signs_permuted) return false;
+    if (!block_tables || num_blocks < 1 || group > 8 || k->signs_permuted) return false;
     if (block_size & (block_size - 1)) return false;  // 16 << tile_shift
     auto same = [](const tq_region& a, const tq_region& b) {
         return a.stride_block == b.stride_block && a.stride_head == b.stride_head;
@@ -897,10 +884,11 @@ bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block
     }
     if (v->idx.stride_row != 16 * v->bits || v->norm.stride_row != 2 || !same(v->idx, v->norm)) return false;
     if (!delta_ok(v->idx, v->norm, 2 * bs)) return false;
-    auto span_ok = [&](const tq_region& r) {
-        return r.stride_block > 0 && r.stride_block < (1ll << 30) && num_blocks * r.stride_block < (1ll << 31) - (1ll << 16);
-    };
-    return span_ok(k->idx) && span_ok(v->idx);
+    auto stride_ok = [&](const tq_region& r) { return r.stride_block > 0 && r.stride_block < (1ll << 30); };
+    if (!stride_ok(k->idx) || !stride_ok(v->idx)) return false;
+    auto small = [&](const tq_region& r) { return num_blocks * r.stride_block < (1ll << 31) - (1ll << 16); };
+    *big = !(small(k->idx) && small(v->idx));
+    return true;
 }
 
 }  // namespace
@@ -923,7 +911,7 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     if (!kern) return TQ_ERR_BITS;
     const int share = (share_codebook && k_bits == v_bits) ? 1 : 0;
     size_t lds = lds_bytes(k_bits, v_bits, share);
-    if (norm_row_bytes == 2 && group <= 8 && fast_path_enabled()) {
+    if (norm_row_bytes == 2 && group <= 8) {
         // the paged fast path (library tile layout)
         kern = tq_decode_fast_kernel_ptr(k_bits, k_qjl != 0, v_bits);
         uint32_t a, b, c, d;
@@ -1013,8 +1001,10 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     const float k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
     const float v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
     const bool share = k->centroids == v->centroids && k->bits == v->bits && k_cscale == v_cscale;
-    if (fast_path_ok(k, v, group, block_size, num_blocks, block_tables)) {
+    bool big = false;
+    if (fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &big)) {
         FastDecodeParams f = {};
+        f.big = big ? 1 : 0;
         f.q = q;
         f.q_ss = q_stride_seq;
         f.q_sh = q_stride_head;

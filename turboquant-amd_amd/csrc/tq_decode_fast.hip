@@ -30,10 +30,11 @@
 // Memory: the caches are in the lane-grouped tile layouts (TQ_TILE_KEYS / TQ_TILE_VALUES):
 // per 16-row sub-tile a lane reads its key data (index dwords + sign dword) with one load and
 // its value data (4 rows x 8 dims) with one load.  The K and V buffer descriptors are loop
-// invariant (base = cache + head offset); a tile is addressed by scalar offsets (block *
-// block_stride + region offset), which needs the cache to span less than 2 GiB (checked on the
-// host; larger caches use decode_kernel).  The norm streams are read once per pair: lanes of
-// tile A and tile B differ in their vector offset.
+// invariant (base = cache + head offset) and a tile is addressed by scalar offsets (block *
+// block_stride + region offset) when the cache spans less than 2 GiB; the norm streams are then
+// read once per pair (lanes of tile A and tile B differ in their vector offset).  A larger cache
+// (the BIG instances, picked on the host) gets one descriptor per tile from a 64-bit base and
+// reads each tile's norms with the lanes of that tile.
 // Block-table entries of the next pair come through the scalar cache (a vector load would cost
 // the texture data path a whole wave of lanes for 8 bytes).  Loads run one pair ahead.
 //
@@ -46,10 +47,6 @@
 namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
-
-#ifndef TQ_FAST_WAVES
-#define TQ_FAST_WAVES 0
-#endif
 
 typedef int tq_i32x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) const uint32_t lds_u32;
@@ -88,9 +85,6 @@ __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
     return *(lds_u32x2*)(uintptr_t)addr;
 }
 
-#ifndef TQ_FAST_QUAD
-#define TQ_FAST_QUAD 1
-#endif
 // 2- and 3-bit indices are looked up four at a time (a 4B-bit field -> 4 fp16 centroids, one
 // 8-byte entry) instead of in pairs.  3 bits: 4096 entries (32 KB); 2 bits: 256 entries (2 KB);
 // neither replicated.  A K quad table sits at LDS address 0 and a 2-bit V quad table at
@@ -98,7 +92,7 @@ __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
 // plus a constant that goes into the ds_read offset.
 template <int B>
 constexpr bool quad_table() {
-    return TQ_FAST_QUAD && (B == 3 || B == 2);
+    return B == 3 || B == 2;
 }
 // Bit position of the field in a quad table address (log2 of the entry stride).
 template <int B>
@@ -163,7 +157,8 @@ struct VRaw {
 };
 // Wave-uniform description of a pair.
 struct PairInfo {
-    uint32_t vbA, vbB;          // scalar byte offsets of the tiles' blocks in the V cache
+    uint32_t vbA, vbB;          // scalar byte offsets of the tiles' blocks in the V cache (BIG:
+                                // the block numbers)
     uint32_t r0A, r0B;          // first row of each tile inside its block
     int nvA, nvB;               // valid rows (0: past the end or unreadable block)
 };
@@ -379,12 +374,13 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
 // Waves per SIMD (register budget 512 / waves): QJL keys need the fp8 q_proj operands.
 template <int KB, bool KQJL, int VB>
 constexpr int fast_waves() {
-    return TQ_FAST_WAVES > 0 ? TQ_FAST_WAVES : (KQJL ? 3 : 4);
+    return KQJL ? 3 : 4;
 }
 
 // COUNT: Sparse-V skip statistics requested (a separate instance keeps the counting off the
 // common path).
-template <int KB, bool KQJL, int VB, bool COUNT>
+// BIG: a cache spanning 2 GiB or more (tiles addressed from 64-bit per-tile bases).
+template <int KB, bool KQJL, int VB, bool COUNT, bool BIG>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
                                                                      fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
@@ -561,8 +557,12 @@ void decode_fast_kernel(FastDecodeParams p) {
     const uint32_t o_kch = (uint32_t)((4 * n + g) * (4 * KB + (KQJL ? 4 : 0)));
     const uint32_t o_vch = (uint32_t)((16 * g + n) * 4 * VB);
     const uint32_t o_norm = (uint32_t)(8 * g);  // tokens 4g..4g+3, 2 bytes each
-    const auto rk = rsrc(p.kbase + (int64_t)kh * p.k_sh);
-    const auto rv = rsrc(p.vbase + (int64_t)kh * p.v_sh);
+    // One descriptor per head (tiles at 32-bit scalar offsets from it), or, for a cache spanning
+    // 2 GiB or more (BIG), one per tile from a 64-bit base.
+    const uint8_t* kunit = p.kbase + (int64_t)kh * p.k_sh;
+    const uint8_t* vunit = p.vbase + (int64_t)kh * p.v_sh;
+    const auto rk = rsrc(kunit);
+    const auto rv = rsrc(vunit);
     const uint64_t hi8 = 0xff00ff00ff00ff00ull;
 
     // ---- tile walk ----
@@ -618,17 +618,18 @@ void decode_fast_kernel(FastDecodeParams p) {
             blk[x] = bk;
             nv[x] = nvr;
             r0[x] = (uint32_t)(((tile0 + i) & tmask) << 4);
-            kb[x] = (uint32_t)bk * p.k_sb;
+            kb[x] = BIG ? 0u : (uint32_t)bk * p.k_sb;
         }
         info.nvA = nv[0];
         info.nvB = nv[1];
-        info.vbA = (uint32_t)blk[0] * p.v_sb;
-        info.vbB = (uint32_t)blk[1] * p.v_sb;
+        // BIG: the block numbers themselves
+        info.vbA = BIG ? (uint32_t)blk[0] : (uint32_t)blk[0] * p.v_sb;
+        info.vbB = BIG ? (uint32_t)blk[1] : (uint32_t)blk[1] * p.v_sb;
         info.r0A = r0[0];
         info.r0B = r0[1];
         // One load per tile: chunk (4n + g) of the 16-row sub-tile holds the lane's index
         // dwords and, with QJL, the sign dword after them (4 * (KB + QJL) bytes).
-        auto load_k = [&](uint32_t (&kw)[KB], uint32_t& ks, uint32_t soff) {
+        auto load_k = [&](uint32_t (&kw)[KB], uint32_t& ks, __amdgpu_buffer_rsrc_t rk, uint32_t soff) {
             constexpr int C = 4 * KB + (KQJL ? 4 : 0);
             uint32_t d[5];
             if (C == 8) {
@@ -648,8 +649,28 @@ void decode_fast_kernel(FastDecodeParams p) {
             ks = KQJL ? d[KB] : 0u;
         };
         constexpr uint32_t P = 16 * KB + (KQJL ? 16 : 0);  // payload bytes per row
-        load_k(kr.kwA, kr.ksA, kb[0] + r0[0] * P);
-        load_k(kr.kwB, kr.ksB, kb[1] + r0[1] * P);
+        if (BIG) {
+            const auto rkA = rsrc(kunit + (int64_t)blk[0] * p.k_sb);
+            const auto rkB = rsrc(kunit + (int64_t)blk[1] * p.k_sb);
+            load_k(kr.kwA, kr.ksA, rkA, r0[0] * P);
+            load_k(kr.kwB, kr.ksB, rkB, r0[1] * P);
+            // lanes with col < 8 read tile A's norms, the others tile B's
+            tq_u32x2 a, bb = {0u, 0u};
+            if (c.lo8) {
+                a = __builtin_amdgcn_raw_buffer_load_b64(rkA, o_norm, 2u * r0[0] + p.d_kn, 0);
+                if (KQJL) bb = __builtin_amdgcn_raw_buffer_load_b64(rkA, o_norm, 2u * r0[0] + p.d_krn, 0);
+            } else {
+                a = __builtin_amdgcn_raw_buffer_load_b64(rkB, o_norm, 2u * r0[1] + p.d_kn, 0);
+                if (KQJL) bb = __builtin_amdgcn_raw_buffer_load_b64(rkB, o_norm, 2u * r0[1] + p.d_krn, 0);
+            }
+            kr.kn[0] = a[0];
+            kr.kn[1] = a[1];
+            kr.krn[0] = bb[0];
+            kr.krn[1] = bb[1];
+            return;
+        }
+        load_k(kr.kwA, kr.ksA, rk, kb[0] + r0[0] * P);
+        load_k(kr.kwB, kr.ksB, rk, kb[1] + r0[1] * P);
         const NormAddr na = norm_addr(kb[0] + 2u * r0[0], kb[1] + 2u * r0[1]);
         tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_kn, 0);
         kr.kn[0] = a[0];
@@ -663,7 +684,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     auto load_v = [&](const PairInfo& info, VRaw& vr) {
         // One load per tile: chunk (16g + n) of the 16-row sub-tile holds dims 8n..8n+7 of rows
         // 4g..4g+3, VB bytes each; row r's fields go to bits 0 .. 8*VB-1 of vw[r].
-        auto load1 = [&](uint32_t (&vw)[4], uint32_t soff) {
+        auto load1 = [&](uint32_t (&vw)[4], __amdgpu_buffer_rsrc_t rv, uint32_t soff) {
             if (VB == 2) {
                 // a quad table reads the odd rows' bytes in place (bits 16-31)
                 tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, o_vch, soff, 0);
@@ -681,8 +702,20 @@ void decode_fast_kernel(FastDecodeParams p) {
                 vw[0] = a[0]; vw[1] = a[1]; vw[2] = a[2]; vw[3] = a[3];
             }
         };
-        load1(vr.vwA, info.vbA + info.r0A * (uint32_t)(16 * VB));
-        load1(vr.vwB, info.vbB + info.r0B * (uint32_t)(16 * VB));
+        if (BIG) {
+            const auto rvA = rsrc(vunit + (int64_t)info.vbA * p.v_sb);
+            const auto rvB = rsrc(vunit + (int64_t)info.vbB * p.v_sb);
+            load1(vr.vwA, rvA, info.r0A * (uint32_t)(16 * VB));
+            load1(vr.vwB, rvB, info.r0B * (uint32_t)(16 * VB));
+            tq_u32x2 a;
+            if (c.lo8) a = __builtin_amdgcn_raw_buffer_load_b64(rvA, o_norm, 2u * info.r0A + p.d_vn, 0);
+            else a = __builtin_amdgcn_raw_buffer_load_b64(rvB, o_norm, 2u * info.r0B + p.d_vn, 0);
+            vr.vn[0] = a[0];
+            vr.vn[1] = a[1];
+            return;
+        }
+        load1(vr.vwA, rv, info.vbA + info.r0A * (uint32_t)(16 * VB));
+        load1(vr.vwB, rv, info.vbB + info.r0B * (uint32_t)(16 * VB));
         // norm of row j of a tile at row0 of its block: d_vn + 2 (row0 + j)
         const NormAddr na = norm_addr(info.vbA + 2u * info.r0A, info.vbB + 2u * info.r0B);
         tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, na.vo, na.so + p.d_vn, 0);
@@ -759,10 +792,13 @@ void decode_fast_kernel(FastDecodeParams p) {
 
 }  // namespace
 
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count) {
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count, bool big) {
 #define TQ_FP(KB, KQ, VB)                                                                              \
     if (kb == KB && kq == KQ && vb == VB)                                                              \
-        return count ? (const void*)decode_fast_kernel<KB, KQ, VB, true> : (const void*)decode_fast_kernel<KB, KQ, VB, false>;
+        return big ? (count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, true>                  \
+                            : (const void*)decode_fast_kernel<KB, KQ, VB, false, true>)                \
+                   : (count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, false>                 \
+                            : (const void*)decode_fast_kernel<KB, KQ, VB, false, false>);
 #define TQ_FP_V(KB, KQ) TQ_FP(KB, KQ, 2) TQ_FP(KB, KQ, 3) TQ_FP(KB, KQ, 4)
     TQ_FP_V(2, false) TQ_FP_V(2, true) TQ_FP_V(3, false) TQ_FP_V(3, true) TQ_FP_V(4, false) TQ_FP_V(4, true)
 #undef TQ_FP_V
@@ -776,7 +812,7 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
     // first: a K quad table at 0 (and any K table when a 2-bit V quad table follows it), a 2-bit
     // V quad table right after the K table (its own copy even when K and V share a codebook);
     // then the others, largest first, at the lowest free multiple of their size.
-    const bool kquad = TQ_FAST_QUAD && (kb == 3 || kb == 2), vquad = TQ_FAST_QUAD && (vb == 3 || vb == 2);
+    const bool kquad = kb == 3 || kb == 2, vquad = vb == 3 || vb == 2;
     const bool v2 = vquad && vb == 2;
     const size_t ks = kquad ? (kb == 3 ? (size_t)4096 * 8 : (size_t)256 * 8) : ((size_t)1 << (2 * kb)) * 128;
     const size_t vs = vquad ? (vb == 3 ? (size_t)4096 * 8 : (size_t)256 * 8) : ((size_t)1 << (2 * vb)) * 128;
@@ -829,7 +865,7 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream) {
-    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats);
+    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats, prm.big != 0);
     if (!kern) return TQ_ERR_BITS;
     FastDecodeParams p = prm;
     void* args[] = {&p};

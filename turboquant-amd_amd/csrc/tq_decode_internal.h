@@ -51,10 +51,11 @@ struct FastDecodeParams {
     int64_t out_ss, out_sh;
     int rot_q, rot_qp, rot_out;  // rotate q / q_proj by H on load, the output by H on the write
     float wht_h;                 // 1 / sqrt(128)
+    int big;                     // a cache spans 2 GiB or more: 64-bit per-tile addressing
 };
 
-// decode_fast_kernel<kb, kq, vb, count> (nullptr: unsupported bit widths).
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false);
+// decode_fast_kernel<kb, kq, vb, count, big> (nullptr: unsupported bit widths).
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false, bool big = false);
 
 // LDS byte offsets of the fp4 sign table, the K and the V tables, a 512-byte scratch, and the
 // total.
