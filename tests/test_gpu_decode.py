@@ -61,7 +61,10 @@ def build_case(seed, S, Hq, Hkv, seq_lens, kb, kq, vb, bs, extra_blocks=3, layou
                 seq_lens=np.array(seq_lens, np.int32), layouts=layouts)
 
 
-def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.0, q_round=None):
+def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.0, q_round=None, tile=16,
+               margins=None):
+    """Oracle outputs (and Sparse-V skip totals) of a case; margins: a list that receives, per
+    (sequence, KV head), the tokens' keep margins (oracle.decode.sparse_v_margins)."""
     G = Hq // Hkv
     kc, vc = _cb(kb).double().numpy(), _cb(vb).double().numpy()
     S = len(case["seq_lens"])
@@ -82,7 +85,9 @@ def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.
             if chunk is None:
                 out[s, hs] = odec.decode_dense(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs)
             else:
-                o, sk, tt = odec.decode_chunked(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs, chunk, thresh)
+                o, sk, tt = odec.decode_chunked(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs, chunk, thresh, tile=tile)
+                if margins is not None:
+                    margins.append(odec.sparse_v_margins(q[s, hs], qpv[s, hs], k, sg, rn, sm, cs, chunk, tile=tile))
                 out[s, hs] = o
                 skipped += sk
                 total += tt
@@ -264,8 +269,18 @@ def test_packed_attention_v7_api(dev):
             np.testing.assert_allclose(got[h], want[0], rtol=RTOL, atol=ATOL)
 
 
+def _skip_allowance(margins, thresh, delta=2e-3):
+    """Tokens whose keep margin lies within delta (natural-log units, well above the kernels'
+    score rounding) of log(threshold): either decision is within rounding."""
+    return int(sum((np.abs(m - math.log(thresh)) < delta).sum() for m in margins))
+
+
 def test_sparse_v_reference_slot_layout(dev):
-    """tq_v11 / tq_v12_sparse_v read the reference's [NB, 2, BS, Hkv, 128] slot cache in place."""
+    """tq_v11 / tq_v12_sparse_v read the reference's [NB, 2, BS, Hkv, 128] slot cache in place
+    (block 32, GQA 6, the reference's own benchmark shape, kernels/sparse_v.py:270-274).  Dense
+    against the oracle; Sparse-V (T = 1e-6, the reference's threshold) against the oracle's
+    chunk walk with the running max updated once per 32-token KV block, outputs at the contract
+    tolerance and skip counts equal up to the tokens within rounding of the threshold."""
     from turboquant.kernels.sparse_v import tq_v11, tq_v12_sparse_v
     rng = np.random.default_rng(8)
     Hkv, G, bs, S = 4, 6, 32, 3
@@ -277,15 +292,20 @@ def test_sparse_v_reference_slot_layout(dev):
     norms = (rng.uniform(5, 15, (nb, 2, bs, Hkv))).astype(np.float16)
     cache[..., 48:50] = norms.view(np.uint8).reshape(nb, 2, bs, Hkv, 2)
     bt = rng.permutation(nb)[: S * maxb].reshape(S, maxb).astype(np.int32)
-    q = rng.standard_normal((S, Hq, 128)).astype(np.float16)
+    q = (rng.standard_normal((S, Hq, 128)) * 6).astype(np.float16)
     cent = _cb(3)
-    t = lambda a: torch.from_numpy(a).to(dev)
+    t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
     sm = 1 / math.sqrt(128)
+    chunk, thresh = 256, 1e-6
     out11 = torch.empty((S, Hq, 128), dtype=torch.float16, device=dev)
     out12 = torch.empty_like(out11)
-    tq_v11(out11, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm)
-    tq_v12_sparse_v(out12, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm)
+    st = torch.zeros(2, dtype=torch.int64, device=dev)
+    tq_v11(out11, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm, tokens_per_chunk=chunk)
+    tq_v12_sparse_v(out12, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm, thresh,
+                    tokens_per_chunk=chunk, skip_stats=st)
     torch.cuda.synchronize()
+    skipped = total = 0
+    margins = []
     for s, L in enumerate(lens):
         for kh in range(Hkv):
             blks = bt[s, np.arange(L) // bs]
@@ -297,9 +317,46 @@ def test_sparse_v_reference_slot_layout(dev):
             k, _, _ = odec.dequant_keys(kp, cent.double().numpy(), 3, False)
             v = odec.dequant_values(vp, cent.double().numpy(), 3)
             hs = slice(kh * G, (kh + 1) * G)
-            want = odec.decode_dense(q[s, hs].astype(np.float64), None, k, None, None, v, sm, 0.0)
+            qs = q[s, hs].astype(np.float64)
+            want = odec.decode_dense(qs, None, k, None, None, v, sm, 0.0)
             np.testing.assert_allclose(out11[s, hs].float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
-            np.testing.assert_allclose(out12[s, hs].float().cpu().numpy(), want, rtol=RTOL, atol=5 * ATOL)
+            want12, sk, tot = odec.decode_chunked(qs, None, k, None, None, v, sm, 0.0, chunk, thresh, tile=32)
+            margins.append(odec.sparse_v_margins(qs, None, k, None, None, sm, 0.0, chunk, tile=32))
+            np.testing.assert_allclose(out12[s, hs].float().cpu().numpy(), want12, rtol=RTOL, atol=ATOL)
+            skipped += sk
+            total += tot
+    gsk, gtot = st.tolist()
+    allow = _skip_allowance(margins, thresh)
+    print(f"tq_v12_sparse_v: skipped gpu {gsk} oracle {skipped} of {total} (within rounding {allow})")
+    assert gtot == total and skipped > 0
+    assert abs(gsk - skipped) <= allow
+
+
+@pytest.mark.parametrize("layouts", [("keys", "values"), ("rows", "rows")])
+@pytest.mark.parametrize("chunk", [256, 240])
+def test_decode_sparse_v_block32(dev, layouts, chunk):
+    """Block size 32 with Sparse-V on the fast (lane-grouped) and general (row-major) kernels:
+    the running max the skip test uses is updated once per 32-token KV block; a chunk that is
+    not a multiple of 32 is rounded up to one.  Against decode_chunked(tile=32) with skip
+    counts."""
+    S, Hq, Hkv, bs = 2, 12, 2, 32
+    lens = [700, 1500]
+    case = build_case(79, S, Hq, Hkv, lens, 3, True, 3, bs, layouts=layouts)
+    case["q"] *= 4.0
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    eff = chunk + 16 if chunk % 32 else chunk
+    for thresh in (1e-4, 1e-2):
+        got, st, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=chunk, thresh=thresh, stats=True)
+        margins = []
+        want, sk, tot = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, chunk=eff, thresh=thresh, q_round=qr, tile=32,
+                                   margins=margins)
+        vmax = float(_cb(3).abs().max()) * 15.0
+        flip_tol = 0.0 if thresh < 1e-3 else 2 * thresh * vmax
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL + flip_tol)
+        allow = _skip_allowance(margins, thresh)
+        print(f"block 32, chunk {chunk}, thresh {thresh}: skipped gpu {int(st[0])} oracle {sk} of {tot} ({allow})")
+        assert int(st[1]) == tot and sk > 0
+        assert abs(int(st[0]) - sk) <= allow
 
 
 def test_decode_constant_values_full_size(dev):

@@ -68,6 +68,8 @@ struct DecodeParams {
     float qp_scale;    // sm_scale * log2(e)             (QJL operand)
     float corr_scale;
     float thresh;      // > 0: Sparse-V on
+    float log2_thresh;
+    int sparse_pair;   // Sparse-V running max per 32-token KV block (two tiles) instead of per tile
     int chunk;
     int n_chunks;      // chunks per (seq, head) slot in the workspace
     float* ws_acc;     // [num_seqs][hq][n_chunks][128]
@@ -254,14 +256,14 @@ __device__ __forceinline__ float sum_over_groups(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// FULL: all 16 rows valid (no masking).  kbank/vbank: LDS byte address of the lane's bank
-// replica in the K / V pair table; one = 0x3C003C00 (half2 of 1.0) held in a vector register.
+// Scores of one tile (log2 units; rows at or past nvalid are -inf) and their max over the
+// lane's head column.  kbank: LDS byte address of the lane's bank replica in the K pair table;
+// one = 0x3C003C00 (half2 of 1.0) held in a vector register.
 template <int KB, bool KQJL, int VB, bool NV, bool QCOLS, bool FULL>
-__device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cur, int nvalid, SoftmaxState& st,
+__device__ __forceinline__ float tile_scores(const TileRaw<KB, KQJL, VB, NV>& cur, int nvalid,
                                              const tq_half8 (&qop)[4], const tq_half8 (&qlo)[QCOLS ? 1 : 4],
-                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], float qpm, uint32_t kbank, uint32_t vbank,
-                                             uint32_t one, const LaneOff& o, int g, uint64_t hmask,
-                                             uint64_t gmask, const DecodeParams& p, bool sparse, bool count) {
+                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], float qpm, uint32_t kbank,
+                                             uint32_t one, int g, float (&sc)[4]) {
     // ---------------- QK products ----------------
     tq_floatx4 s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -303,9 +305,7 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cu
             s1v[r] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s1v[r]), 0x128, 0xf, 0xf, true));
     }
 
-    // ---------------- online softmax ----------------
     // score = norm * S (+ rnorm * qpm * QJL: corr_scale and the operand scale 2^-e in qpm)
-    float sc[4];
     float mt = kNegInf;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -314,7 +314,22 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cu
         sc[r] = (FULL || 4 * g + r < nvalid) ? v : kNegInf;
         mt = fmaxf(mt, sc[r]);
     }
-    mt = max_over_groups(mt);
+    return max_over_groups(mt);
+}
+
+// One tile: scores, online softmax, Sparse-V, PV.  FULL: all 16 rows valid (no masking).
+// vbank: LDS byte address of the lane's bank replica in the V pair table.  m_blk (> -inf when
+// the KV block spans two tiles): the running max through the end of the tile's block, which the
+// Sparse-V test then uses instead of the max through this tile.
+template <int KB, bool KQJL, int VB, bool NV, bool QCOLS, bool FULL>
+__device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cur, int nvalid, SoftmaxState& st,
+                                             const tq_half8 (&qop)[4], const tq_half8 (&qlo)[QCOLS ? 1 : 4],
+                                             const tq_half8 (&qpop)[KQJL ? 4 : 1], float qpm, uint32_t kbank, uint32_t vbank,
+                                             uint32_t one, const LaneOff& o, int g, uint64_t hmask,
+                                             uint64_t gmask, const DecodeParams& p, bool sparse, bool count, float m_blk) {
+    // ---------------- online softmax ----------------
+    float sc[4];
+    const float mt = tile_scores<KB, KQJL, VB, NV, QCOLS, FULL>(cur, nvalid, qop, qlo, qpop, qpm, kbank, one, g, sc);
     const float m_new = fmaxf(st.m, mt);
     const float mref = m_new == kNegInf ? 0.f : m_new;
     float pr[4];
@@ -348,7 +363,8 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cu
         uint32_t nsig = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint64_t bal = __builtin_amdgcn_ballot_w64(pr[r] > p.thresh) & hmask;
+            const bool pass = p.sparse_pair ? sc[r] > m_blk + p.log2_thresh : pr[r] > p.thresh;
+            const uint64_t bal = __builtin_amdgcn_ballot_w64(pass) & hmask;
             orall |= bal;
             const bool keep = (bal & gmask) != 0;
             pv[r] = keep ? pv[r] : 0.f;
@@ -612,6 +628,9 @@ void decode_kernel(DecodeParams p) {
     // Loads run kDepth - 1 tiles ahead of the compute through a ring of kDepth register tiles;
     // tile T lives in slot T % kDepth.
     constexpr int D = kDepth;
+    static_assert(D == 2, "the KV-block max look-ahead reads the next tile from the other ring slot");
+    const bool blk2 = sparse && p.sparse_pair;  // (paged: the partial last tile is in the ring)
+    float m_blk = kNegInf;
     const int ntiles = (t_end - t_begin + 15) >> 4;
     const int nfull = (t_end - t_begin) >> 4;
     const int nload = paged ? ntiles : nfull;
@@ -630,9 +649,19 @@ void decode_kernel(DecodeParams p) {
             }
             const int ahead = t + D - 1;
             fetch(t_begin + 16 * ahead, ahead < nload, ring[(k + D - 1) % D], nv[(k + D - 1) % D]);
+            if (blk2 && k == 0) {
+                // first tile of a 32-token KV block: the block's max from this tile and the next
+                // (already fetched into the other ring slot; a tile past the end scores -inf)
+                float sc[4];
+                const float ma = tile_scores<KB, KQJL, VB, NV, QCOLS, true>(ring[0], nv[0], qop, qlo, qpop, qpm, kbank,
+                                                                            one, g, sc);
+                const float mb = tile_scores<KB, KQJL, VB, NV, QCOLS, false>(ring[1 % D], t + 1 < ntiles ? nv[1 % D] : 0,
+                                                                             qop, qlo, qpop, qpm, kbank, one, g, sc);
+                m_blk = fmaxf(sm.m, fmaxf(nv[0] ? ma : kNegInf, mb));
+            }
             if (nv[k])
                 compute_tile<KB, KQJL, VB, NV, QCOLS, true>(ring[k], nv[k], sm, qop, qlo, qpop, qpm, kbank, vbank, one, o,
-                                                            g, hmask, gmask, p, sparse, count);
+                                                            g, hmask, gmask, p, sparse, count, m_blk);
         }
         if (done) break;
     }
@@ -655,9 +684,14 @@ void decode_kernel(DecodeParams p) {
             tv = tl.nvalid;
             load_tile<KB, KQJL, VB, NV, true>(tr, tl, o, p.rrow, p.vstep, NV && p.v_lg);
         }
+        if (blk2 && (nfull & 1) == 0) {
+            // a partial tile that starts a KV block ends it too
+            float sc[4];
+            m_blk = fmaxf(sm.m, tile_scores<KB, KQJL, VB, NV, QCOLS, false>(tr, tv, qop, qlo, qpop, qpm, kbank, one, g, sc));
+        }
         if (tv)
             compute_tile<KB, KQJL, VB, NV, QCOLS, false>(tr, tv, sm, qop, qlo, qpop, qpm, kbank, vbank, one, o, g, hmask,
-                                                         gmask, p, sparse, count);
+                                                         gmask, p, sparse, count, m_blk);
     }
 
     const float lsum = sum_over_groups(sm.lsum);
@@ -992,6 +1026,12 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
             if (regs[r]->stride_block != 16 * regs[r]->stride_row) return TQ_ERR_INVALID_ARGUMENT;
         if ((int64_t)(max_blocks_per_seq + 1) * block_size * max_row >= (1ll << 30)) return TQ_ERR_INVALID_ARGUMENT;
     }
+    // Sparse-V over KV blocks of 32 tokens or more: the running max the skip test uses is updated
+    // once per 32-token block (once per KV block for block_size 32, kernels/sparse_v.py:70-123),
+    // so chunks start on such a block (tokens_per_chunk rounded up to a multiple of 32; the
+    // workspace this needs is never larger).
+    const bool sparse_pair = sparse_threshold > 0.f && block_size >= 32 && block_tables;
+    if (sparse_pair && tokens_per_chunk % 32) tokens_per_chunk += 16;
     const int n_chunks = n_chunks_for(max_seq_len, tokens_per_chunk);
     const size_t need = tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return TQ_ERR_WORKSPACE;
@@ -1047,6 +1087,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.seq_lens = seq_lens;
         f.c_exp = sm_scale * kLog2e / k_cscale;
         f.sparse = sparse_threshold > 0.f ? 1 : 0;
+        f.sparse_pair = sparse_pair ? 1 : 0;
         f.thr_log = f.sparse ? std::log2(sparse_threshold) / f.c_exp : 0.f;
         f.qp_mul = corr_scale * k_cscale;
         f.chunk = tokens_per_chunk;
@@ -1114,6 +1155,8 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     p.q_scale = p.qp_scale / p.k_cscale;
     p.corr_scale = corr_scale;
     p.thresh = sparse_threshold > 0.f ? sparse_threshold : 0.f;
+    p.log2_thresh = sparse_threshold > 0.f ? std::log2(sparse_threshold) : 0.f;
+    p.sparse_pair = sparse_pair ? 1 : 0;
     p.chunk = tokens_per_chunk;
     p.n_chunks = n_chunks;
     p.ws_acc = ws_acc;

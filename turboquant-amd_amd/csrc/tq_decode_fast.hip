@@ -296,13 +296,17 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
     // ---------------- Sparse-V ----------------
+    // The skip test uses the running max through the token's KV block: through its own tile for
+    // 16-token blocks, through the pair (a 32-token block) otherwise.
     if (p.sparse) {
-        const float m_skip = c.lo8 ? fmaxf(m_old, mt) : m_new;
+        const float m_skip = (c.lo8 && !p.sparse_pair) ? fmaxf(m_old, mt) : m_new;
         const float thr = m_skip + p.thr_log;
         uint32_t kept = 0;
+        uint64_t any = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint64_t bal = __builtin_amdgcn_ballot_w64(sc[r] > thr) & c.hmask;
+            any |= bal;
             // some head of this lane's 8-lane group (its tile's token 4g + r) passes
             const bool keep = (uint32_t)((bal << c.shl8) >> 32) >= (1u << 24);
             pr[r] = keep ? pr[r] : 0.f;
@@ -312,6 +316,7 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
             st.n_tot += (uint32_t)(pi.nvA + pi.nvB);
             st.n_kept += kept;
         }
+        if (!any) return;  // every token of the pair dropped: no PV products
     }
 
     // ---------------- PV ----------------

@@ -40,6 +40,7 @@ struct FastDecodeParams {
     float c_exp;     // sm_scale * log2(e) / k_cscale: raw score units -> log2 units
     float thr_log;   // log2(threshold) / c_exp
     int sparse;
+    int sparse_pair; // Sparse-V running max per 32-token pair (block_size >= 32) instead of per tile
     float qp_mul;    // corr_scale * k_cscale
     int chunk, n_chunks;
     float* ws_acc;   // [num_seqs][hq][n_chunks][128]

@@ -8,9 +8,12 @@ cache written for the reference is read in place.  block_size is taken from the 
 shape (docs/MI355X_BLOCKSIZE_FIX.md:18-21).
 
 Sparse-V rule (kernels/sparse_v.py:108-149): with a running max m over the tokens processed
-so far in the work unit (updated per 16-token tile), token t's V is skipped when
-max over the GQA group of exp(score - m) <= threshold; skipped tokens still count in the
-softmax denominator.  The work unit here is a chunk of tokens_per_chunk tokens.
+so far in the work unit, updated once per KV block (block_size tokens, as the reference's
+KV_BLK_SZ = block_size loop does, for block sizes 16 and 32; every 32 tokens for larger
+blocks), token t's V is skipped when max over the GQA group of exp(score - m) <= threshold;
+skipped tokens still count in the softmax denominator.  The work unit here is a chunk of
+tokens_per_chunk tokens (rounded up to a multiple of 32 for block sizes of 32 or more); with
+tokens_per_chunk >= the sequence length it is the reference's single pass.
 """
 
 from __future__ import annotations
