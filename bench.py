@@ -156,13 +156,13 @@ def build_decode_workload(key, dev, lens=None):
 
 def decode_step(st, rotate=False, skip_stats=None):
     """One benchmark step of a decode workload: [compress the new tokens,] decode the batch."""
-    from turboquant.kernels.paged import compress_paged, decode_paged
+    from turboquant.kernels.paged import compress_paged_kv, decode_paged
 
     def step():
         if st["new_tokens"] is not None:
             newk, newv, slot_new = st["new_tokens"]
-            compress_paged(newk, slot_new, st["k_cache"], st["kf"], st["kc"], st["kbnd"])
-            compress_paged(newv, slot_new, st["v_cache"], st["vf"], st["vc"], st["vbnd"])
+            compress_paged_kv(newk, newv, slot_new, st["k_cache"], st["v_cache"], st["kf"], st["vf"],
+                              (st["kc"], st["kbnd"]), (st["vc"], st["vbnd"]))
         return decode_paged(st["q"], st["k_cache"], st["kf"], st["kc"], st["v_cache"], st["vf"], st["vc"], st["bt"],
                             st["lens"], sparse_threshold=st["thresh"], max_seq_len=st["msl"],
                             tokens_per_chunk=st["chunk"], out=st["out"], workspace=st["ws"], rotate=rotate,
@@ -315,12 +315,13 @@ def build_compress_workload(dev):
 
 def compress_case(dev, steps, warmup):
     """Benchmark config 2: K and V [16384, 8, 128] bf16 -> turbo4 paged blocks of 16 in 8192 blocks."""
-    from turboquant.kernels.paged import compress_paged
+    from turboquant.kernels.paged import compress_paged_kv
     w = build_compress_workload(dev)
 
     def step():
-        compress_paged(w["k"], w["slots"], w["kc"], w["fmt"], w["c"], w["b"])
-        compress_paged(w["v"], w["slots"], w["vc"], w["vfmt"], w["c"], w["b"])
+        # the layer's K + V cache update: one launch (tq_compress_paged_kv)
+        compress_paged_kv(w["k"], w["v"], w["slots"], w["kc"], w["vc"], w["fmt"], w["vfmt"], (w["c"], w["b"]),
+                          (w["c"], w["b"]))
 
     t = timed(step, steps, warmup, settle_s=0.1)
     ms = t["median_ms"]

@@ -162,6 +162,28 @@ int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_token, int64_
                       const float* centroids, const float* boundaries,
                       tq_stream_t stream);
 
+/* One tensor of a K + V cache update: its rows x[token, head, :] (dtype and strides as in
+ * tq_compress_paged), its paged cache and format, and its codebook. */
+typedef struct tq_paged_target {
+    const void* x;
+    int64_t x_stride_token, x_stride_head;   /* elements */
+    void* cache;
+    int64_t cache_stride_block, cache_stride_head;
+    int bits, use_qjl, tile_layout;
+    const float* centroids;
+    const float* boundaries;
+} tq_paged_target;
+
+/* tq_compress_paged of K and of V for the same tokens and slots, in one launch when K and V have
+ * the same bits and V has no QJL (otherwise two launches, same results).  Each target follows the
+ * rules of tq_compress_paged; num_blocks and block_size are shared.
+ * Replaces the pair of turbo4_fp8_compress_and_scatter calls of one attention layer (kv_idx 0
+ * and 1, integration/vllm_backend.py:179-230). */
+int tq_compress_paged_kv(const tq_paged_target* k, const tq_paged_target* v, int x_dtype,
+                         int64_t num_tokens, int num_heads, int head_dim,
+                         const void* slot_mapping, int slot_dtype, int64_t num_blocks, int block_size,
+                         int rotate, float wht_scale, tq_stream_t stream);
+
 /* Bytes of one (block, KV head) tile (any layout) and the byte offsets of its regions in the
  * TQ_TILE_ROWS layout (the lane-grouped layouts keep off_idx = 0, off_norm and off_rnorm; their
  * signs are inside the payload). */

@@ -173,7 +173,8 @@ def classify_strict(idx_test, idx_ref, x_ref, boundaries, idx_fp64):
     b = np.asarray(boundaries, dtype=np.float64).reshape(-1)
     mism = np.nonzero(t != r)[0]
     out = {"elements": int(t.size), "mismatches": int(mism.size), "within_1ulp": 0, "ulp_1_to_8": 0,
-           "ulp_over_8": 0, "beyond_1ulp_test_equals_fp64": 0, "failures": 0, "ref_differs_from_fp64": int((r != f).sum())}
+           "ulp_over_8": 0, "beyond_1ulp_test_equals_fp64": 0, "failures": 0, "ref_differs_from_fp64": int((r != f).sum()),
+           "test_differs_from_fp64": int((t != f).sum())}
     if mism.size == 0:
         return out
     adjacent = np.abs(t[mism] - r[mism]) == 1

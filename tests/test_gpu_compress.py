@@ -254,6 +254,206 @@ def _payload_from_oracle(ref, bits, qjl, T, H):
     return pl
 
 
+def compare_paged(cache, x, slots, fmt, cent, bnd, rotate=True, name=None, parity_log=None):
+    """The paged cache written by compress_paged(x, slots) against the oracle, token by token
+    (read back from any layout): indices under the 1-ulp / fp64 rule, sign bits under the same
+    rule around the centroid, fp16 norms (NaN where the oracle's is NaN), residual norms of rows
+    whose indices all match, and every block no slot points at still zero."""
+    from turboquant.core import make_wht_matrix
+    got = cache.cpu().numpy()
+    nb, H = got.shape[0], got.shape[1]
+    bs, bits, qjl = fmt.block_size, fmt.bits, fmt.qjl
+    T = x.shape[0]
+    slots = np.asarray(slots, np.int64)
+    xf = x.float().cpu().reshape(T * H, 128)
+    ref = ocomp.polarquant_compress(xf, cent, bnd, 2 ** bits, qjl, make_wht_matrix(128) if rotate else None)
+    ref64 = ocomp.polarquant_compress_fp64(xf, cent, bnd, qjl, rotate)
+    live = (slots >= 0) & (slots < nb * bs)
+    # a slot written twice keeps one of its writers: only slots written once are compared
+    uniq, counts = np.unique(slots[live], return_counts=True)
+    once = np.isin(slots, uniq[counts == 1]) & live
+    tok = np.nonzero(once)[0]
+    sel = slots[tok]
+    xn = ref["x_normalized"].reshape(T, H, 128).numpy()
+    stats_all = None
+    for h in range(H):
+        pl = opaged.tiles_to_tokens(got[:, h], bs, bits, qjl, fmt.layout)
+        gi = opack.unpack_indices(pl["idx"][sel], bits)
+        ri = ref["indices"].reshape(T, H, 128)[tok, h].numpy()
+        i64 = ref64["indices"].reshape(T, H, 128)[tok, h].numpy()
+        st = ocomp.classify_strict(gi, ri, xn[tok, h], bnd.numpy(), i64)
+        assert st["failures"] == 0, f"{name} head {h}: index mismatches beyond 1 ulp: {st}"
+        stats_all = st if stats_all is None else {k: stats_all[k] + st[k] for k in st}
+        gn = pl["norm"][sel].view(np.float16).astype(np.float32)
+        rn = ref["norms"].reshape(T, H)[tok, h].numpy().astype(np.float16).astype(np.float32)
+        np.testing.assert_array_equal(np.isnan(gn), np.isnan(rn))
+        fin = ~np.isnan(rn)
+        np.testing.assert_allclose(gn[fin], rn[fin], rtol=NORM_RTOL, atol=NORM_ATOL)
+        if qjl:
+            gs = opack.unpack_signs(pl["signs"][sel])
+            rsg = (ref["signs"].reshape(T, H, 128)[tok, h].numpy() > 0).astype(gs.dtype)
+            s64 = (ref64["signs"].reshape(T, H, 128)[tok, h].numpy() > 0).astype(gs.dtype)
+            c = cent.double().numpy()[ri]
+            xr = xn[tok, h].astype(np.float64)
+            cdist = np.abs(xr - c) / np.maximum(ocomp.ulp32(np.maximum(np.abs(xr), np.abs(c))), 1e-300)
+            ok = (gi != ri) | (cdist <= 1.0) | (gs == s64) | np.isnan(xr)
+            assert not ((gs != rsg) & ~ok).any(), f"{name} head {h}: sign flips away from centroids"
+            clean = (gi == ri).all(axis=1) & fin
+            grn = pl["rnorm"][sel].view(np.float16).astype(np.float32)[clean]
+            rrn = ref["rot_residual_norm"].reshape(T, H)[tok, h].numpy().astype(np.float16).astype(np.float32)[clean]
+            np.testing.assert_allclose(grn, rrn, rtol=NORM_RTOL, atol=NORM_ATOL)
+    if name is not None:
+        _log(parity_log, name, stats_all)
+    written = np.zeros(nb, bool)
+    written[slots[live] // bs] = True
+    assert not got[~written].any(), "blocks no slot points at were written"
+    return stats_all
+
+
+def block_order_slots(T, nb, bs, seed):
+    """Token t -> slot perm[t // bs] * bs + t % bs for a seeded permutation of the blocks (how a
+    prefill fills whole blocks)."""
+    perm = np.random.default_rng(seed).permutation(nb)
+    t = np.arange(T)
+    return perm[t // bs] * bs + t % bs
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rotate", [True, False])
+@pytest.mark.parametrize("bits,qjl", [(4, False), (3, True), (2, True), (2, False)])
+@pytest.mark.parametrize("layout", ["keys", "values", "rows"])
+def test_compress_paged_16bit(dev, dtype, rotate, bits, qjl, layout, parity_log):
+    """bf16 / fp16 rows (the matrix-core path): block-ordered slots (whole quads of rows land on
+    consecutive slots), one padding slot inside a quad and an odd token count (a partial last
+    group), with and without the rotation, every layout."""
+    if layout == "values" and qjl:
+        pytest.skip("the values layout carries no QJL data")
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
+    T, H, bs = 203, 3, 16
+    nb = 20
+    g = torch.Generator().manual_seed(11 + bits)
+    x = (torch.randn(T, H, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 0.5)).to(dtype)
+    slots = block_order_slots(T, nb, bs, 3)
+    slots[37] = -1
+    fmt = PagedKVFormat(bits=bits, qjl=qjl, block_size=bs, layout=layout)
+    cent, bnd = _codebook(bits)
+    cache = allocate_cache(nb, H, fmt, device=dev)
+    compress_paged(x.to(dev), torch.from_numpy(slots).to(dev), cache, fmt, cent.to(dev), bnd.to(dev), rotate=rotate)
+    torch.cuda.synchronize()
+    compare_paged(cache, x, slots, fmt, cent, bnd, rotate, f"paged16 {dtype} rot{int(rotate)} b{bits} q{int(qjl)} {layout}",
+                  parity_log)
+
+
+@pytest.mark.parametrize("rotate", [True, False])
+@pytest.mark.parametrize("layout", ["keys", "values"])
+def test_compress_paged_16bit_edge_rows(dev, rotate, layout):
+    """A NaN row (every index past the last boundary, NaN norm), a zero row, a row whose sum of
+    squares overflows (norm inf: x / inf = 0 for every element), a basis row, among ordinary
+    rows; int64 slots."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
+    T, H, bs, nb = 48, 2, 16, 6
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(T, H, 128, generator=g)
+    x[3, 0, 7] = float("nan")
+    x[4, 1] = 0.0
+    x[5, 0] = 3e19
+    x[6, 1] = 0.0
+    x[6, 1, 9] = 2.5
+    x = x.to(torch.bfloat16)
+    qjl = layout == "keys"
+    slots = block_order_slots(T, nb, bs, 8)
+    fmt = PagedKVFormat(bits=3, qjl=qjl, block_size=bs, layout=layout)
+    cent, bnd = _codebook(3)
+    cache = allocate_cache(nb, H, fmt, device=dev)
+    compress_paged(x.to(dev), torch.from_numpy(slots).to(dev), cache, fmt, cent.to(dev), bnd.to(dev), rotate=rotate)
+    torch.cuda.synchronize()
+    compare_paged(cache, x, slots, fmt, cent, bnd, rotate)
+    # the NaN row: every index 7, NaN norm; the overflowing row: inf norm, indices of 0
+    pl = opaged.tiles_to_tokens(cache[:, 0].cpu().numpy(), bs, 3, qjl, layout)
+    nan_idx = opack.unpack_indices(pl["idx"][slots[3]][None], 3)[0]
+    assert (nan_idx == 7).all()
+    assert np.isnan(pl["norm"][slots[3]].view(np.float16))
+    big = opack.unpack_indices(pl["idx"][slots[5]][None], 3)[0]
+    assert (big == int(np.searchsorted(bnd.numpy(), 0.0))).all()
+    assert np.isinf(pl["norm"][slots[5]].view(np.float16))
+
+
+def test_compress_paged_16bit_close_boundaries(dev):
+    """A codebook with two boundaries 1e-4 apart (inside one lookup cell) runs the linear count
+    of the matrix-core kernel; the probe rows put values on and next to every boundary."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
+    bnd = torch.tensor([-0.3, -0.05, 0.0, 1e-4, 0.02, 0.1, 0.4], dtype=torch.float32)
+    cent = torch.tensor([-0.5, -0.2, -0.02, 5e-5, 0.01, 0.05, 0.2, 0.6], dtype=torch.float32)
+    T, H, bs, nb = 64, 2, 16, 8
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(T, H, 128, generator=g) * 0.3).to(torch.bfloat16)
+    slots = block_order_slots(T, nb, bs, 1)
+    for layout, qjl in (("keys", True), ("values", False)):
+        fmt = PagedKVFormat(bits=3, qjl=qjl, block_size=bs, layout=layout)
+        cache = allocate_cache(nb, H, fmt, device=dev)
+        compress_paged(x.to(dev), torch.from_numpy(slots).to(dev), cache, fmt, cent.to(dev), bnd.to(dev), rotate=False)
+        torch.cuda.synchronize()
+        compare_paged(cache, x, slots, fmt, cent, bnd, False)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("kb,kq,vb,klayout,vlayout", [
+    (4, False, 4, "keys", "values"),     # one launch, turbo4 K and V
+    (3, True, 3, "keys", "values"),      # one launch, QJL signs in the K half only
+    (2, True, 2, "rows", "rows"),        # one launch, row layout for both
+    (4, True, 2, "keys", "values"),      # different bits: two launches behind the same call
+])
+def test_compress_paged_kv_matches_two_launches(dev, dtype, kb, kq, vb, klayout, vlayout):
+    """compress_paged_kv writes byte-for-byte what compress_paged(K) then compress_paged(V) write,
+    with padding and out-of-range slots, int64 slots and a second, shorter call into the same caches."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged, compress_paged_kv
+    T, H, bs, nb = 203, 4, 16, 20
+    g = torch.Generator().manual_seed(17 + kb + 5 * vb)
+    k = (torch.randn(T, H, 128, generator=g) * 2.0).to(dtype).to(dev)
+    v = torch.randn(T, H, 128, generator=g).to(dtype).to(dev)
+    slots = torch.from_numpy(block_order_slots(T, nb, bs, 4)).to(torch.int64)
+    slots[11] = -1
+    slots[12] = nb * bs + 7
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs, layout=klayout)
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=vlayout)
+    kcb = tuple(t.to(dev) for t in _codebook(kb))
+    vcb = tuple(t.to(dev) for t in _codebook(vb))
+    want_k = allocate_cache(nb, H, kf, device=dev)
+    want_v = allocate_cache(nb, H, vf, device=dev)
+    got_k = allocate_cache(nb, H, kf, device=dev)
+    got_v = allocate_cache(nb, H, vf, device=dev)
+    for n in (T, 61):
+        s = slots[:n].to(dev)
+        compress_paged(k[:n], s, want_k, kf, *kcb)
+        compress_paged(v[:n], s, want_v, vf, *vcb)
+        compress_paged_kv(k[:n], v[:n], s, got_k, got_v, kf, vf, kcb, vcb)
+        torch.cuda.synchronize()
+        assert torch.equal(got_k, want_k), f"K cache differs after a call over {n} tokens"
+        assert torch.equal(got_v, want_v), f"V cache differs after a call over {n} tokens"
+        k, v = k.flip(0).contiguous(), v.flip(0).contiguous()
+
+
+def test_compress_paged_kv_rejections(dev):
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged_kv
+    T, H, bs, nb = 8, 2, 16, 2
+    k = torch.zeros(T, H, 128, dtype=torch.bfloat16, device=dev)
+    slots = torch.arange(T, dtype=torch.int32, device=dev)
+    kf = PagedKVFormat(bits=3, qjl=True, block_size=bs, layout="keys")
+    vf = PagedKVFormat(bits=3, qjl=False, block_size=bs, layout="values")
+    cb = tuple(t.to(dev) for t in _codebook(3))
+    kc, vc = allocate_cache(nb, H, kf, device=dev), allocate_cache(nb, H, vf, device=dev)
+    with pytest.raises(ValueError):   # V with QJL
+        compress_paged_kv(k, k, slots, kc, vc, kf, PagedKVFormat(bits=3, qjl=True, block_size=bs, layout="rows"), cb, cb)
+    with pytest.raises(ValueError):   # K in the values layout
+        compress_paged_kv(k, k, slots, vc, vc, vf, vf, cb, cb)
+    with pytest.raises(TypeError):    # dtypes differ
+        compress_paged_kv(k, k.float(), slots, kc, vc, kf, vf, cb, cb)
+    with pytest.raises(ValueError):   # shapes differ
+        compress_paged_kv(k, k[:4], slots, kc, vc, kf, vf, cb, cb)
+    with pytest.raises(ValueError):   # wrong codebook size
+        compress_paged_kv(k, k, slots, kc, vc, kf, vf, cb, tuple(t.to(dev) for t in _codebook(2)))
+
+
 @pytest.mark.parametrize("bits,qjl", [(2, False), (2, True), (3, False), (3, True), (4, False), (4, True)])
 @pytest.mark.parametrize("block_size", [16, 32])
 @pytest.mark.parametrize("layout", ["keys", "values", "rows"])

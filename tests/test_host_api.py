@@ -252,6 +252,16 @@ def test_host_side_argument_rejection():
     assert L.tq_wht_rows(fake, 2, 128, 128, 0, 1, 128, fake, 2, 128, 128, None) == 0
     assert L.tq_permute_signs(fake, fake, 4, 64, None) == -2
     assert L.tq_unpack_bits(fake, fake, 4, 128, 0, None) == -3
+    # fused K + V compress: a missing target, then a V target in the values layout with QJL,
+    # then a block size the tiles do not support (checked for K before V)
+    tk = _lib.TQPagedTarget(0x1000, 1024, 128, 0x1000, 1056, 8448, 4, 0, 1, 0x1000, 0x1000)
+    tv = _lib.TQPagedTarget(0x1000, 1024, 128, 0x1000, 1056, 8448, 4, 1, 2, 0x1000, 0x1000)
+    kvc = lambda a, b, bs: L.tq_compress_paged_kv(a, b, 2, 10, 8, 128, fake, 3, 10, bs, 1, 0.1, None)  # noqa: E731
+    assert kvc(None, ctypes.byref(tv), 16) == -1
+    assert kvc(ctypes.byref(tk), ctypes.byref(tv), 16) == -1
+    assert kvc(ctypes.byref(tk), ctypes.byref(tk), 24) == -8
+    assert L.tq_compress_paged_kv(ctypes.byref(tk), ctypes.byref(tk), 2, 0, 8, 128, fake, 3, 10, 16, 1, 0.1,
+                                  None) == 0   # no tokens: nothing to launch
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

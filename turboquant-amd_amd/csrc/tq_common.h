@@ -92,11 +92,35 @@ __device__ __forceinline__ uint32_t tq_field(const uint32_t (&w)[N], int pos, in
     return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & mask;
 }
 
+// ---- division by a runtime divisor as a multiply-high and a shift ---------------------------
+// For 2 <= d < 2^31 with l = ceil(log2 d) and m = ceil(2^(31 + l) / d) (which fits 32 bits),
+// floor(n / d) = floor(n m / 2^(31 + l)) for every n < 2^31: m = 2^(31 + l) / d + e with
+// 0 <= e < 1, so the excess n e / 2^(31 + l) stays below 1 / d because 2^(31 + l) / d >= 2^31 > n.
+// d = 1 is m = 0 (q = n).
+struct tq_udiv {
+    uint32_t m;
+    int32_t sh;  // l - 1
+};
+inline tq_udiv tq_make_udiv(uint32_t d) {
+    tq_udiv v = {0u, 0};
+    if (d <= 1) return v;
+    int l = 0;
+    while ((1ull << l) < d) ++l;
+    v.m = (uint32_t)(((1ull << (31 + l)) + d - 1) / d);
+    v.sh = l - 1;
+    return v;
+}
+__device__ __forceinline__ uint32_t tq_udiv_apply(uint32_t n, tq_udiv v) {
+    return v.m ? (__umulhi(n, v.m) >> v.sh) : n;
+}
+
 // ---- correctly rounded quotient by a per-row divisor ------------------------------
 // q = RN(x / d) given rcp = RN(1/d): one residual correction of the product (Markstein).
+// The residual uses d clamped to FLT_MAX, so d = inf gives x * 0 = 0 for finite x (as x / inf
+// does) instead of NaN; the clamp is the same for every x of a row and is computed once.
 __device__ __forceinline__ float tq_div_rn(float x, float d, float rcp) {
     float q0 = x * rcp;
-    float e = __builtin_fmaf(-q0, d, x);
+    float e = __builtin_fmaf(-q0, __builtin_fminf(d, 3.40282347e38f), x);
     return __builtin_fmaf(e, rcp, q0);
 }
 

@@ -32,6 +32,7 @@ struct CompressParams {
     int64_t stride_block, stride_head, num_blocks;
     int block_size;
     int idx32;  // rows and slots below 2^31: 32-bit index arithmetic
+    tq_udiv tok_div, blk_div;  // by num_tokens and block_size (32-bit index arithmetic)
     int tile_layout;  // TQ_TILE_ROWS / TQ_TILE_KEYS / TQ_TILE_VALUES
     int64_t off_signs, off_norm, off_rnorm;
     // unpacked output
@@ -46,6 +47,10 @@ struct CompressParams {
 // a wave works on 16 rows and a 256-thread workgroup on 64.  Five Hadamard stages (dims bits
 // 0-4) run in registers, two (dims bits 5, 6 = lane bits 0, 1) through DPP quad_perm.
 constexpr int kRowsPerWG = 64;
+// Grid cap of the grid-stride compress launches: 256 CUs x 5 resident 256-thread workgroups
+// (89 VGPRs allow 5 waves per SIMD).  Measured on config-2 shapes (131,072 rows): 1280 beats
+// 2048 (one group per workgroup) and 512 / 768; the fused K + V launch is best near 2 x 1024.
+constexpr int kCompressGrid = 1280;
 constexpr int kDppXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
 template <int CTRL>
@@ -168,8 +173,39 @@ __device__ __forceinline__ int quant_linear(float x, const float (&bd)[NB]) {
     return x != x ? NB : cnt;
 }
 
+// Paged mode: round-to-nearest cells and decisions on y itself.  Cell k (0..256) covers
+// 128 x + 128 in [k - 1/2, k + 1/2] and holds c0 = #{b < lo_k - eps} and the one boundary inside
+// [lo_k - eps, hi_k + eps] (or +inf); the cell of x = y / den is the low mantissa bits of
+// fl(y (128 / den) + 128 + 1.5 * 2^23) (one fma; a tie lands in either neighbour, both cover it,
+// and the approximate 128 / den moves x by far less than eps).  The decision b < y / den is the
+// sign of b den - y, one fma of the exact product (den > 0): exact for this y, with no rounded
+// quotient in between.
+constexpr float kCellMagic = 12583040.f;          // 1.5 * 2^23 + 128
+constexpr uint32_t kCellMagicBase = 0x4B400000u;  // bits of 1.5 * 2^23
+template <int NB>
+__device__ __forceinline__ void build_cells_rn(const float (&bd)[NB], const float* boundaries, uint2* tab, int* bad) {
+    constexpr float eps = 1e-5f;
+    for (int k = threadIdx.x; k < kCells; k += blockDim.x) {
+        const float lo = ((float)k - 128.5f) * (1.f / 128.f) - eps, hi = ((float)k - 127.5f) * (1.f / 128.f) + eps;
+        int c0 = 0, c1 = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            c0 += bd[i] < lo ? 1 : 0;
+            c1 += bd[i] <= hi ? 1 : 0;
+        }
+        if (c1 - c0 > 1) atomicOr(bad, 1);
+        const float b = c1 > c0 ? boundaries[c0] : __builtin_huge_valf();
+        tab[k] = make_uint2(__float_as_uint(b), (uint32_t)c0);
+    }
+}
+__device__ __forceinline__ int quant_cell_y(float y, float den, float r128, const uint2* tab) {
+    const uint2 e = tab[__float_as_uint(__builtin_fmaf(y, r128, kCellMagic)) - kCellMagicBase];
+    return (int)e.y + (__builtin_fmaf(__uint_as_float(e.x), den, -y) < 0.f ? 1 : 0);
+}
+
+// The body of the compression kernels: workgroup wg of nwg takes 64-row groups wg, wg + nwg, ...
 template <int BITS, bool QJL, int MODE, int DT>
-__global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
+__device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, int nwg) {
     constexpr int NC = 1 << BITS;
     constexpr int NB = NC - 1;
     __shared__ float s_cent[NC];
@@ -182,14 +218,15 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) bd[i] = p.boundaries[i];
     __syncthreads();
-    build_cells<NB>(bd, p.boundaries, s_cells, &s_bad);
+    if (MODE == MODE_PAGED) build_cells_rn<NB>(bd, p.boundaries, s_cells, &s_bad);
+    else build_cells<NB>(bd, p.boundaries, s_cells, &s_bad);
     __syncthreads();
     const bool cells = s_bad == 0;
 
     const int q = threadIdx.x & 3;              // dims 32q..32q+31
     const int row_in_wg = threadIdx.x >> 2;     // 0..63
 
-    for (int64_t row0 = (int64_t)blockIdx.x * kRowsPerWG; row0 < p.n_rows; row0 += (int64_t)gridDim.x * kRowsPerWG) {
+    for (int64_t row0 = (int64_t)wg * kRowsPerWG; row0 < p.n_rows; row0 += (int64_t)nwg * kRowsPerWG) {
         const int64_t row = row0 + row_in_wg;
         const bool row_ok = row < p.n_rows;
         // Paged rows are head-major so that a workgroup's rows are consecutive tokens.
@@ -197,7 +234,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
         if (MODE == MODE_PAGED) {
             if (p.idx32) {
                 const uint32_t r = row_ok ? (uint32_t)row : 0u, nt = (uint32_t)p.num_tokens;
-                const uint32_t h = r / nt;
+                const uint32_t h = tq_udiv_apply(r, p.tok_div);
                 head = h;
                 tok = r - h * nt;
             } else {
@@ -225,29 +262,47 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
         const float norm = __builtin_sqrtf(row_sumsq(v));
         const float den = norm + 1e-8f;
         const float rcp = 1.0f / den;
-#pragma unroll
-        for (int k = 0; k < 32; ++k) v[k] = tq_div_rn(v[k], den, rcp);  // x / (norm + 1e-8)
+        // |x| <= 1 unless the norm is not finite (then x may be NaN: searchsorted puts it last)
+        const bool fast = cells && !__builtin_amdgcn_ballot_w64(!(norm < __builtin_huge_valf()));
 
         int idx[32];
-        // |x| <= 1 unless the norm is not finite (then x may be NaN: searchsorted puts it last)
-        if (cells && !__builtin_amdgcn_ballot_w64(!(norm < __builtin_huge_valf()))) {
-#pragma unroll
-            for (int k = 0; k < 32; ++k) idx[k] = quant_cell(v[k], s_cells);
-        } else {
-#pragma unroll
-            for (int k = 0; k < 32; ++k) idx[k] = quant_linear<NB>(v[k], bd);
-        }
-
         float rn = 0.f;
         uint32_t sbits = 0;
-        if (QJL) {
-            float r[32];
+        if (MODE == MODE_PAGED && fast) {
+            // decisions on y = x_rot itself (x_n = y / den is never formed); with QJL the
+            // residual r = (x_n - c) norm = (y - c den) (norm / den), its sign that of one fma
+            const float r128 = 128.f * rcp;
 #pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                r[k] = (v[k] - s_cent[idx[k]]) * norm;
-                sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
+            for (int k = 0; k < 32; ++k) idx[k] = quant_cell_y(v[k], den, r128, s_cells);
+            if (QJL) {
+                float r[32];
+#pragma unroll
+                for (int k = 0; k < 32; ++k) {
+                    r[k] = __builtin_fmaf(-s_cent[idx[k]], den, v[k]);
+                    sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
+                }
+                rn = __builtin_sqrtf(row_sumsq(r)) * (norm * rcp);
+                if (norm == 0.f) sbits = 0xffffffffu;  // r = (0 - c) 0 = +-0: sign(0) counts as +1
             }
-            rn = __builtin_sqrtf(row_sumsq(r));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 32; ++k) v[k] = tq_div_rn(v[k], den, rcp);  // x / (norm + 1e-8)
+            if (fast) {
+#pragma unroll
+                for (int k = 0; k < 32; ++k) idx[k] = quant_cell(v[k], s_cells);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 32; ++k) idx[k] = quant_linear<NB>(v[k], bd);
+            }
+            if (QJL) {
+                float r[32];
+#pragma unroll
+                for (int k = 0; k < 32; ++k) {
+                    r[k] = (v[k] - s_cent[idx[k]]) * norm;
+                    sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
+                }
+                rn = __builtin_sqrtf(row_sumsq(r));
+            }
         }
 
         if (MODE == MODE_UNPACKED) {
@@ -279,7 +334,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
             int64_t blk, r_in_blk;
             if (p.idx32) {
                 const uint32_t sl = write ? (uint32_t)slot : 0u, bs = (uint32_t)p.block_size;
-                const uint32_t b = sl / bs;
+                const uint32_t b = tq_udiv_apply(sl, p.blk_div);
                 blk = b;
                 r_in_blk = sl - b * bs;
             } else {
@@ -336,12 +391,26 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
     }
 }
 
+template <int BITS, bool QJL, int MODE, int DT>
+__global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
+    compress_rows<BITS, QJL, MODE, DT>(p, blockIdx.x, gridDim.x);
+}
+
+// K and V of one layer in one launch (same bits; V without QJL): workgroups [0, gk) take K, the
+// rest V.  One launch instead of two halves the fixed cost of a K + V cache update.
+template <int BITS, bool QJL_K, int DT>
+__global__ __launch_bounds__(256) void compress_kv_kernel(CompressParams pk, CompressParams pv, int gk) {
+    if ((int)blockIdx.x < gk) compress_rows<BITS, QJL_K, MODE_PAGED, DT>(pk, blockIdx.x, gk);
+    else compress_rows<BITS, false, MODE_PAGED, DT>(pv, blockIdx.x - gk, gridDim.x - gk);
+}
+
 template <int MODE>
 int launch_compress(const CompressParams& p, int bits, int qjl, hipStream_t stream) {
     if (p.n_rows <= 0) return TQ_OK;
-    // Workgroups loop over 64-row groups; 2048 of them (8 per CU) amortise the LDS set-up.
+    // Workgroups loop over 64-row groups.  At most kCompressGrid of them: as many as are
+    // resident at once, so the per-workgroup LDS set-up is paid once per resident slot.
     int64_t groups = (p.n_rows + kRowsPerWG - 1) / kRowsPerWG;
-    int grid = (int)(groups < 2048 ? groups : 2048);
+    int grid = (int)(groups < kCompressGrid ? groups : kCompressGrid);
 #define TQ_LAUNCH_DT(B, Q, DT) hipLaunchKernelGGL((compress_kernel<B, Q, MODE, DT>), dim3(grid), dim3(256), 0, stream, p)
 #define TQ_LAUNCH(B, Q)                                   \
     do {                                                  \
@@ -428,14 +497,16 @@ extern "C" int tq_tile_offsets(int block_size, int bits, int use_qjl, int64_t* o
     return TQ_OK;
 }
 
-extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_stride_head,
-                                 int64_t num_tokens, int num_heads, int head_dim,
-                                 const void* slot_mapping, int slot_dtype,
-                                 void* cache, int64_t cache_stride_block, int64_t cache_stride_head,
-                                 int64_t num_blocks, int block_size,
-                                 int bits, int use_qjl, int tile_layout, int rotate, float wht_scale,
-                                 const float* centroids, const float* boundaries,
-                                 tq_stream_t stream) {
+namespace {
+
+// Validates one paged compression and fills its parameters (TQ_OK, or the error to return;
+// *empty when there is nothing to write).
+int paged_params(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_stride_head, int64_t num_tokens,
+                 int num_heads, int head_dim, const void* slot_mapping, int slot_dtype, void* cache,
+                 int64_t cache_stride_block, int64_t cache_stride_head, int64_t num_blocks, int block_size, int bits,
+                 int use_qjl, int tile_layout, int rotate, float wht_scale, const float* centroids,
+                 const float* boundaries, CompressParams* out, bool* empty) {
+    *empty = false;
     if (head_dim != TQ_HEAD_DIM) return TQ_ERR_HEAD_DIM;
     if (bits < 2 || bits > 4) return TQ_ERR_BITS;
     if (block_size <= 0 || block_size % 16) return TQ_ERR_BLOCK_SIZE;
@@ -444,7 +515,10 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
     if (tile_layout != TQ_TILE_ROWS && tile_layout != TQ_TILE_KEYS && tile_layout != TQ_TILE_VALUES)
         return TQ_ERR_INVALID_ARGUMENT;
     if (tile_layout == TQ_TILE_VALUES && use_qjl) return TQ_ERR_INVALID_ARGUMENT;
-    if (num_tokens == 0 || num_blocks == 0) return TQ_OK;
+    if (num_tokens == 0 || num_blocks == 0) {
+        *empty = true;
+        return TQ_OK;
+    }
     if (!x || !slot_mapping || !cache || !centroids || !boundaries) return TQ_ERR_INVALID_ARGUMENT;
     int rc = check_x(x, x_dtype);
     if (rc) return rc;
@@ -480,5 +554,84 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
                num_tokens * x_stride_token + (int64_t)num_heads * x_stride_head < (1ll << 31))
                   ? 1
                   : 0;
+    if (p.idx32) {
+        p.tok_div = tq_make_udiv((uint32_t)num_tokens);
+        p.blk_div = tq_make_udiv((uint32_t)block_size);
+    }
+    *out = p;
+    return TQ_OK;
+}
+
+int paged_target_params(const tq_paged_target* t, int x_dtype, int64_t num_tokens, int num_heads, int head_dim,
+                        const void* slot_mapping, int slot_dtype, int64_t num_blocks, int block_size, int rotate,
+                        float wht_scale, CompressParams* out, bool* empty) {
+    if (!t) return TQ_ERR_INVALID_ARGUMENT;
+    return paged_params(t->x, x_dtype, t->x_stride_token, t->x_stride_head, num_tokens, num_heads, head_dim,
+                        slot_mapping, slot_dtype, t->cache, t->cache_stride_block, t->cache_stride_head, num_blocks,
+                        block_size, t->bits, t->use_qjl, t->tile_layout, rotate, wht_scale, t->centroids,
+                        t->boundaries, out, empty);
+}
+
+}  // namespace
+
+extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_stride_head,
+                                 int64_t num_tokens, int num_heads, int head_dim,
+                                 const void* slot_mapping, int slot_dtype,
+                                 void* cache, int64_t cache_stride_block, int64_t cache_stride_head,
+                                 int64_t num_blocks, int block_size,
+                                 int bits, int use_qjl, int tile_layout, int rotate, float wht_scale,
+                                 const float* centroids, const float* boundaries,
+                                 tq_stream_t stream) {
+    CompressParams p;
+    bool empty;
+    const int rc = paged_params(x, x_dtype, x_stride_token, x_stride_head, num_tokens, num_heads, head_dim, slot_mapping,
+                                slot_dtype, cache, cache_stride_block, cache_stride_head, num_blocks, block_size, bits,
+                                use_qjl, tile_layout, rotate, wht_scale, centroids, boundaries, &p, &empty);
+    if (rc || empty) return rc;
     return launch_compress<MODE_PAGED>(p, bits, use_qjl, (hipStream_t)stream);
+}
+
+extern "C" int tq_compress_paged_kv(const tq_paged_target* k, const tq_paged_target* v, int x_dtype,
+                                    int64_t num_tokens, int num_heads, int head_dim,
+                                    const void* slot_mapping, int slot_dtype, int64_t num_blocks, int block_size,
+                                    int rotate, float wht_scale, tq_stream_t stream) {
+    CompressParams pk, pv;
+    bool ek, ev;
+    int rc = paged_target_params(k, x_dtype, num_tokens, num_heads, head_dim, slot_mapping, slot_dtype, num_blocks,
+                                 block_size, rotate, wht_scale, &pk, &ek);
+    if (rc) return rc;
+    rc = paged_target_params(v, x_dtype, num_tokens, num_heads, head_dim, slot_mapping, slot_dtype, num_blocks,
+                             block_size, rotate, wht_scale, &pv, &ev);
+    if (rc || ek) return rc;  // both are empty together (same tokens, same blocks)
+    const hipStream_t st = (hipStream_t)stream;
+    if (k->bits != v->bits || v->use_qjl) {
+        // not one kernel: two launches
+        rc = launch_compress<MODE_PAGED>(pk, k->bits, k->use_qjl, st);
+        return rc ? rc : launch_compress<MODE_PAGED>(pv, v->bits, v->use_qjl, st);
+    }
+    // K workgroups first, then as many V workgroups: at most 1024 of each
+    const int64_t groups = (pk.n_rows + kRowsPerWG - 1) / kRowsPerWG;
+    const int gk = (int)(groups < kCompressGrid * 4 / 5 ? groups : kCompressGrid * 4 / 5);
+    const int grid = 2 * gk;
+#define TQ_KV_DT(B, Q, DT) \
+    hipLaunchKernelGGL((compress_kv_kernel<B, Q, DT>), dim3(grid), dim3(256), 0, st, pk, pv, gk)
+#define TQ_KV(B, Q)                                             \
+    do {                                                        \
+        if (x_dtype == TQ_BF16) TQ_KV_DT(B, Q, TQ_BF16);        \
+        else if (x_dtype == TQ_F16) TQ_KV_DT(B, Q, TQ_F16);     \
+        else TQ_KV_DT(B, Q, TQ_F32);                            \
+    } while (0)
+    switch (k->bits * 2 + (k->use_qjl ? 1 : 0)) {
+        case 4: TQ_KV(2, false); break;
+        case 5: TQ_KV(2, true); break;
+        case 6: TQ_KV(3, false); break;
+        case 7: TQ_KV(3, true); break;
+        case 8: TQ_KV(4, false); break;
+        case 9: TQ_KV(4, true); break;
+        default: return TQ_ERR_BITS;
+    }
+#undef TQ_KV
+#undef TQ_KV_DT
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? TQ_OK : (int)e;
 }

@@ -60,6 +60,23 @@ class TQKVView(ctypes.Structure):
     ]
 
 
+class TQPagedTarget(ctypes.Structure):
+    """tq_paged_target: one tensor of a K + V cache update."""
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_stride_token", ctypes.c_int64),
+        ("x_stride_head", ctypes.c_int64),
+        ("cache", ctypes.c_void_p),
+        ("cache_stride_block", ctypes.c_int64),
+        ("cache_stride_head", ctypes.c_int64),
+        ("bits", ctypes.c_int32),
+        ("use_qjl", ctypes.c_int32),
+        ("tile_layout", ctypes.c_int32),
+        ("centroids", ctypes.c_void_p),
+        ("boundaries", ctypes.c_void_p),
+    ]
+
+
 TILE_ROWS, TILE_KEYS, TILE_VALUES = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 64 << 20  # TQ_NOALLOC_SCRATCH_BYTES
 
@@ -82,6 +99,11 @@ SIGNATURES = {
         _i32,
         [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _i32,
          _i32, _i32, _i32, _i32, _f32, _vp, _vp, _vp],
+    ),
+    "tq_compress_paged_kv": (
+        _i32,
+        [ctypes.POINTER(TQPagedTarget), ctypes.POINTER(TQPagedTarget), _i32, _i64, _i32, _i32, _vp, _i32, _i64, _i32,
+         _i32, _f32, _vp],
     ),
     "tq_tile_bytes": (_i64, [_i32, _i32, _i32]),
     "tq_tile_offsets": (

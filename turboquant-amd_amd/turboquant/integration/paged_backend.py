@@ -33,7 +33,7 @@ from typing import Optional, Sequence
 import torch
 
 from turboquant.core import make_codebook, make_wht_matrix
-from turboquant.kernels.paged import PagedKVFormat, compress_paged, decode_paged, prefill_paged
+from turboquant.kernels.paged import PagedKVFormat, compress_paged, compress_paged_kv, decode_paged, prefill_paged
 from turboquant.kernels.rotation import wht_rows
 
 
@@ -107,6 +107,14 @@ class TurboQuantPagedState:
         else:
             compress_paged(x, slot_mapping, cache, self.k_format, self.k_centroids, self.k_boundaries,
                            rotate=not self.weights_fused)
+
+    def compress_kv_and_scatter(self, k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor,
+                                v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+        """The layer's K + V cache update in one launch: compress_and_scatter of k (K cache) and
+        of v (V cache) at the same slots."""
+        compress_paged_kv(k, v, slot_mapping, k_cache, v_cache, self.k_format, self.v_format,
+                          (self.k_centroids, self.k_boundaries), (self.v_centroids, self.v_boundaries),
+                          rotate=not self.weights_fused)
 
     def decode(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor,
                seq_lens: torch.Tensor, sm_scale: Optional[float] = None, sparse_threshold: float = 0.0,

@@ -180,6 +180,68 @@ def compress_paged(
     return cache
 
 
+def _target(x: torch.Tensor, cache: torch.Tensor, fmt: PagedKVFormat, cb, dev, keep: list):
+    cent = cb[0].to(device=dev, dtype=torch.float32).contiguous()
+    bnd = cb[1].to(device=dev, dtype=torch.float32).contiguous()
+    if cent.numel() != 2 ** fmt.bits or bnd.numel() != 2 ** fmt.bits - 1:
+        raise ValueError(f"need {2 ** fmt.bits} centroids and {2 ** fmt.bits - 1} boundaries for bits={fmt.bits}")
+    keep += [x, cent, bnd]
+    return _lib.TQPagedTarget(x.data_ptr(), x.stride(0), x.stride(1), cache.data_ptr(), cache.stride(0), cache.stride(1),
+                              fmt.bits, int(fmt.qjl), fmt.layout_code, cent.data_ptr(), bnd.data_ptr())
+
+
+def compress_paged_kv(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    k_fmt: PagedKVFormat,
+    v_fmt: PagedKVFormat,
+    k_codebook,
+    v_codebook,
+    rotate: bool = True,
+):
+    """compress_paged of k into k_cache and of v into v_cache (same tokens and slots) in one
+    launch: a layer's K + V cache update (the reference calls turbo4_fp8_compress_and_scatter
+    once per tensor, integration/vllm_backend.py:179-230).  k_codebook / v_codebook are
+    (centroids, boundaries)."""
+    dev = _lib.require_gpu("compress_paged_kv", k, v, slot_mapping, k_cache, v_cache)
+    _check_roles(k_fmt, v_fmt)
+    if k.dim() != 3 or k.shape[2] != k_fmt.head_dim or v.shape != k.shape:
+        raise ValueError(f"k and v must both be [T, H, {k_fmt.head_dim}], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if k.dtype != v.dtype:
+        raise TypeError("k and v must share a dtype")
+    if k_fmt.block_size != v_fmt.block_size:
+        raise ValueError("k and v caches must share the block size")
+    T, H, _ = k.shape
+    _check_cache(k_cache, k_fmt, "compress_paged_kv (K)")
+    _check_cache(v_cache, v_fmt, "compress_paged_kv (V)")
+    if k_cache.shape[:2] != v_cache.shape[:2] or k_cache.shape[1] != H:
+        raise ValueError("k_cache and v_cache must be [num_blocks, H, *] for the same blocks and heads")
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != T:
+        raise ValueError("slot_mapping must be [T]")
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise TypeError("slot_mapping must be int32 or int64")
+
+    def ok(x):
+        return x if (x.stride(2) == 1 and x.stride(0) % 8 == 0 and x.stride(1) % 8 == 0 and x.data_ptr() % 32 == 0) \
+            else x.contiguous()
+
+    k, v = ok(k), ok(v)
+    slot_mapping = slot_mapping.contiguous()
+    keep: list = []
+    tk = _target(k, k_cache, k_fmt, k_codebook, dev, keep)
+    tv = _target(v, v_cache, v_fmt, v_codebook, dev, keep)
+    rc = _lib.lib().tq_compress_paged_kv(
+        ctypes.byref(tk), ctypes.byref(tv), _lib.dtype_code(k), T, H, k_fmt.head_dim,
+        slot_mapping.data_ptr(), _lib.dtype_code(slot_mapping), k_cache.shape[0], k_fmt.block_size,
+        int(bool(rotate)), wht_scale(k_fmt.head_dim), _lib.stream_handle(dev),
+    )
+    _lib.check(rc, "tq_compress_paged_kv")
+    return k_cache, v_cache
+
+
 _WORKSPACES: dict = {}
 
 
