@@ -242,7 +242,9 @@ def test_decode_bad_block_entries_are_skipped(dev):
 
 
 def test_packed_attention_v7_api(dev):
-    from turboquant.kernels.packed_attention import packed_attention
+    """packed_attention against the fp64 oracle and against the product's attention_unpacked_ref
+    (kernels/packed_attention.py:273-284 of the reference) on the same unpacked data."""
+    from turboquant.kernels.packed_attention import attention_unpacked_ref, packed_attention
     from turboquant.kernels.packed_compress import permute_signs_for_chunked
     rng = np.random.default_rng(3)
     cb = _cb(2)
@@ -267,6 +269,11 @@ def test_packed_attention_v7_api(dev):
             v = odec.dequant_values({"idx": vi[h], "norm": vn[h].view(np.uint16)}, cb.double().numpy(), 2)
             want = odec.decode_dense(Q[h:h + 1].astype(np.float64), Qp[h:h + 1].astype(np.float64), k, sg, rn, v, 1.0, cs)
             np.testing.assert_allclose(got[h], want[0], rtol=RTOL, atol=ATOL)
+            # the product's unpacked formulation on the GPU (fp32 torch ops) on the same data
+            f = lambda a: torch.from_numpy(np.ascontiguousarray(a)).float().to(dev)[None]  # noqa: E731
+            ref = attention_unpacked_ref(f(Q[h]), f(Qp[h]), f(k), f(sg), f(rn), f(v), cs)
+            np.testing.assert_allclose(ref[0].cpu().numpy(), want[0], rtol=1e-4, atol=1e-5)
+            np.testing.assert_allclose(got[h], ref[0].cpu().numpy(), rtol=RTOL, atol=ATOL)
 
 
 def _skip_allowance(margins, thresh, delta=2e-3):

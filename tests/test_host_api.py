@@ -30,6 +30,59 @@ def test_make_codebook_matches_golden(bits):
     assert torch.equal(ct, torch.tensor(g["centroids"], dtype=torch.float32))
 
 
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_committed_codebook_table_is_the_solver_output(bits):
+    """The d = 128 table served without scipy holds exactly what the quadrature solver returns."""
+    pytest.importorskip("scipy")
+    from turboquant.core import codebook
+    c, b = codebook._table()[bits]
+    c2, b2 = codebook._solve(128, bits)
+    assert c == c2 and b == b2
+    from turboquant.kernels.packed_compress import _solve_kernel_recipe
+    assert list(codebook.kernel_table()[bits]) == _solve_kernel_recipe(128, bits)
+
+
+def test_make_codebook_without_scipy(monkeypatch):
+    """d = 128 codebooks come from the committed table when scipy cannot be imported; other
+    dimensions still need the solver and say so."""
+    import sys
+    from turboquant.core import codebook, make_codebook
+    monkeypatch.setitem(sys.modules, "scipy", None)
+    monkeypatch.setitem(sys.modules, "scipy.integrate", None)
+    codebook._solve.cache_clear()
+    g = json.loads((ROOT / "tests" / "golden" / "codebooks.json").read_text())["books"]
+    for bits in (1, 2, 3, 4):
+        c, b = make_codebook(128, bits)
+        assert torch.equal(c, torch.tensor(g[str(bits)]["centroids"], dtype=torch.float32))
+        assert torch.equal(b, torch.tensor(g[str(bits)]["boundaries"], dtype=torch.float32))
+    from turboquant.kernels.packed_compress import solve_codebook as kernel_codebook
+    assert kernel_codebook(128, 3).shape == (8,)
+    with pytest.raises(ImportError):
+        make_codebook(96, 3)
+    codebook._solve.cache_clear()
+
+
+def test_attention_unpacked_ref_against_oracle():
+    """The product's unpacked formulation (plain torch ops, runs on the CPU) against the fp64
+    dense oracle: Q.K_mse + Q_proj.(signs * rnorm * corr_scale), softmax, times V."""
+    import numpy as np
+    from oracle import decode as odec
+    from turboquant.kernels.packed_attention import attention_unpacked_ref
+    rng = np.random.default_rng(12)
+    BH, Sk, D = 3, 77, 128
+    cs = math.sqrt(math.pi / 2) / D
+    Q, Qp = rng.standard_normal((BH, D)) * 0.3, rng.standard_normal((BH, D)) * 0.3
+    K, V = rng.standard_normal((BH, Sk, D)), rng.standard_normal((BH, Sk, D))
+    S = np.where(rng.random((BH, Sk, D)) < 0.5, -1.0, 1.0)
+    R = rng.random((BH, Sk)) * 2.0
+    f = lambda a: torch.from_numpy(a).float()  # noqa: E731
+    got = attention_unpacked_ref(f(Q), f(Qp), f(K), f(S), f(R), f(V), cs).numpy()
+    assert got.shape == (BH, D)
+    for h in range(BH):
+        want = odec.decode_dense(Q[h:h + 1], Qp[h:h + 1], K[h], S[h], R[h], V[h], 1.0, cs)
+        np.testing.assert_allclose(got[h], want[0], rtol=1e-4, atol=1e-5)
+
+
 def test_make_codebook_dtype_and_scaling():
     from turboquant.core import make_codebook, solve_codebook
     c, b = make_codebook(128, 3, dtype=torch.float16)

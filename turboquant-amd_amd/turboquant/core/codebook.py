@@ -6,15 +6,44 @@ Lloyd-Max quantizer of that Gaussian.  The iteration is the reference's
 rounds of "centroid = conditional mean over its cell (scipy QUADPACK)" followed by
 "boundary = midpoint of neighbouring centroids".  The integrand and the operation order are
 kept identical so that the float values agree exactly with the reference on the same scipy.
+
+For d = 128 (the head dimension of every kernel here) the solved codebooks of bits 1-4 are
+committed in codebook_d128.json (written by make_codebook_table.py from the same solver) and
+served from there, so hosts without scipy get the same floats; other d are solved on demand.
+The table also holds the centroids of the kernel files' own recipe (kernels/packed_compress.py).
 """
 
 from __future__ import annotations
 
 import functools
+import json
 import math
+import os
 from typing import Optional
 
 import torch
+
+TABLE_D = 128
+TABLE_BITS = (1, 2, 3, 4)
+TABLE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "codebook_d128.json")
+
+
+@functools.lru_cache(maxsize=None)
+def _table() -> dict:
+    with open(TABLE_PATH) as f:
+        t = json.load(f)
+    if t.get("d") != TABLE_D:
+        raise ValueError(f"{TABLE_PATH}: expected d = {TABLE_D}")
+    return {int(b): (tuple(v["centroids"]), tuple(v["boundaries"])) for b, v in t["bits"].items()}
+
+
+@functools.lru_cache(maxsize=None)
+def kernel_table() -> dict:
+    """bits -> centroids of the kernel files' own codebook recipe for d = 128 (the variant that
+    turboquant.kernels.packed_compress.solve_codebook computes), from the committed table."""
+    with open(TABLE_PATH) as f:
+        t = json.load(f)
+    return {int(b): tuple(c) for b, c in t["kernel_recipe_centroids"].items()}
 
 
 @functools.lru_cache(maxsize=None)
@@ -50,7 +79,10 @@ def solve_codebook(d: int, bits: int) -> tuple[list[float], list[float]]:
     """
     if d <= 0 or bits <= 0:
         raise ValueError("d and bits must be positive")
-    c, b = _solve(int(d), int(bits))
+    if int(d) == TABLE_D and int(bits) in TABLE_BITS:
+        c, b = _table()[int(bits)]
+    else:
+        c, b = _solve(int(d), int(bits))
     return list(c), list(b)
 
 

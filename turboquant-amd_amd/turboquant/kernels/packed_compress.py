@@ -18,7 +18,16 @@ from turboquant import _lib
 def solve_codebook(d: int, bits: int) -> torch.Tensor:
     """Kernel-file Lloyd-Max variant: centroids start uniform on +-3.5 sigma (cell midpoints),
     cells extend to +-10.5 sigma, up to 200 rounds until the centroid change is < 1e-10.
-    Returns fp32 centroids [2^bits] (kernels/packed_compress.py:21-41)."""
+    Returns fp32 centroids [2^bits] (kernels/packed_compress.py:21-41).  For d = 128, bits 1-4
+    the values come from the committed table (turboquant/core/codebook_d128.json, written by the
+    same recipe), so no scipy is needed."""
+    from turboquant.core import codebook as _cb
+    if int(d) == _cb.TABLE_D and int(bits) in _cb.TABLE_BITS:
+        return torch.tensor(_cb.kernel_table()[int(bits)], dtype=torch.float32)
+    return torch.tensor(_solve_kernel_recipe(int(d), int(bits)), dtype=torch.float32)
+
+
+def _solve_kernel_recipe(d: int, bits: int) -> list:
     from scipy import integrate
 
     n_levels = 2 ** bits
@@ -44,7 +53,7 @@ def solve_codebook(d: int, bits: int) -> torch.Tensor:
         if max(abs(new_c[i] - centroids[i]) for i in range(n_levels)) < 1e-10:
             break
         centroids = new_c
-    return torch.tensor(centroids, dtype=torch.float32)
+    return centroids
 
 
 def _rows(packed: torch.Tensor, row_bytes: int, what: str) -> torch.Tensor:
