@@ -7,8 +7,10 @@ rnorm for QJL keys only).  The payload order is the layout:
   "rows"  : all idx rows (16*bits bytes each), then all sign rows (16 bytes each);
   "keys"  : per 16-row sub-tile, for row n = 0..15 and dim quarter g = 0..3, one chunk: the
             idx bytes of dims 32g..32g+31 of row n, then (QJL) their 4 sign bytes;
-  "values": per 16-row sub-tile, for row group g = 0..3 and dim group n = 0..15, one chunk:
-            the idx bytes of dims 8n..8n+7 of rows 4g, 4g+1, 4g+2, 4g+3 in turn.
+  "values": per 16-row sub-tile, for row group g = 0..3 and dim group n = 0..15, one chunk of
+            4*bits bytes: a little-endian stream of 32 bits-wide fields, field 4j + r holding
+            the index of dim 8n + j of row 4g + r (dimension-major: the four rows' fields of one
+            dim are adjacent).
 Here the sub-tiles are assembled chunk by chunk (build_subtile / split_subtile) rather than
 through byte-position formulas.
 Reference array-of-slots layout [num_blocks, bs, Hkv, slot] (kernels/sparse_v.py:293-304):
@@ -18,6 +20,8 @@ per token idx bytes, [signs], fp16 norm, [fp16 rnorm], zero padding.
 from __future__ import annotations
 
 import numpy as np
+
+from oracle import packing as _pack
 
 
 def tile_offsets(block_size: int, bits: int, qjl: bool):
@@ -42,10 +46,11 @@ def build_subtile(idx: np.ndarray, signs: np.ndarray | None, bits: int, layout: 
                     out += bytes(signs[n, 4 * g: 4 * g + 4])
     elif layout == "values":
         assert signs is None
+        f = _pack.unpack_indices(idx, bits)           # [16 rows, 128 dims]
         for g in range(4):
             for n in range(16):
-                for r in range(4):
-                    out += bytes(idx[4 * g + r, bits * n: bits * (n + 1)])
+                fields = [int(f[4 * g + r, 8 * n + j]) for j in range(8) for r in range(4)]
+                out += bytes(_pack.pack_indices(np.array([fields]), bits)[0])
     else:
         raise ValueError(layout)
     return bytes(out)
@@ -64,10 +69,14 @@ def split_subtile(buf: bytes, bits: int, qjl: bool, layout: str):
                 if qjl:
                     signs[n, 4 * g: 4 * g + 4] = take(4)
     else:
+        f = np.zeros((16, 128), np.int64)
         for g in range(4):
             for n in range(16):
-                for r in range(4):
-                    idx[4 * g + r, bits * n: bits * (n + 1)] = take(bits)
+                fields = _pack.unpack_indices(take(4 * bits)[None], bits, 32)[0]
+                for j in range(8):
+                    for r in range(4):
+                        f[4 * g + r, 8 * n + j] = fields[4 * j + r]
+        idx[:] = _pack.pack_indices(f, bits)
     return idx, signs
 
 
@@ -79,6 +88,8 @@ def _tile_rows(tile: np.ndarray, block_size: int, bits: int, qjl: bool, layout: 
         signs = tile[off_signs:off_signs + 16 * block_size].reshape(block_size, 16).copy() if qjl else None
         return idx, signs
     P = idx_row + (16 if qjl else 0)
+    if layout == "values":
+        return values_subtiles_to_rows(tile[:block_size * P].reshape(block_size // 16, 16 * P), bits), None
     idx = np.zeros((block_size, idx_row), np.uint8)
     signs = np.zeros((block_size, 16), np.uint8) if qjl else None
     for j in range(block_size // 16):
@@ -97,6 +108,10 @@ def _set_tile_rows(tile: np.ndarray, idx: np.ndarray, signs, block_size: int, bi
             tile[off_signs:off_signs + 16 * block_size] = signs.reshape(-1)
         return
     P = idx_row + (16 if qjl else 0)
+    if layout == "values":
+        # vectorised form of build_subtile (the two are checked against each other)
+        tile[:block_size * P] = rows_to_values_subtiles(idx, bits).reshape(-1)
+        return
     for j in range(block_size // 16):
         b = build_subtile(idx[16 * j:16 * j + 16], signs[16 * j:16 * j + 16] if qjl else None, bits, layout)
         tile[16 * P * j: 16 * P * (j + 1)] = np.frombuffer(b, np.uint8)
@@ -181,8 +196,11 @@ def to_slots(cache: np.ndarray, block_size: int, bits: int, qjl: bool, slot_byte
 
 def subtile_row_positions(bits: int, qjl: bool, layout: str) -> np.ndarray:
     """pos[j] = byte of the row-major 16-row payload ([16 idx rows][16 sign rows]) that byte j
-    of the lane-grouped sub-tile holds.  Derived by running build_subtile on byte ids (low and
-    high byte planes separately: build_subtile only moves bytes), not by a second formula."""
+    of the "keys" sub-tile holds.  Derived by running build_subtile on byte ids (low and high
+    byte planes separately: build_subtile only moves bytes in this layout), not by a second
+    formula.  (The "values" layout moves bits-wide fields, not bytes: values_subtiles_to_rows.)"""
+    if layout != "keys":
+        raise ValueError("byte positions exist for the keys layout only")
     idx_row = 16 * bits
     ids_idx = np.arange(16 * idx_row, dtype=np.int64).reshape(16, idx_row)
     ids_sg = (16 * idx_row + np.arange(256, dtype=np.int64)).reshape(16, 16) if qjl else None
@@ -192,6 +210,25 @@ def subtile_row_positions(bits: int, qjl: bool, layout: str) -> np.ndarray:
         s8 = ((ids_sg >> shift) & 0xFF).astype(np.uint8) if qjl else None
         planes.append(np.frombuffer(build_subtile(i8, s8, bits, layout), np.uint8).astype(np.int64))
     return planes[0] | (planes[1] << 8)
+
+
+def values_subtiles_to_rows(sub: np.ndarray, bits: int) -> np.ndarray:
+    """"values" sub-tile payloads [m, 256 * bits] -> packed index rows [16 m, 16 * bits],
+    vectorised: every chunk's 32 fields are unpacked (little-endian bit order), indexed as
+    (g, n, j, r) and transposed to (row 4g + r, dim 8n + j)."""
+    m = sub.shape[0]
+    b = np.unpackbits(np.ascontiguousarray(sub).reshape(m, 64, 4 * bits), axis=2, bitorder="little")
+    f = (b.reshape(m, 64, 32, bits).astype(np.int64) << np.arange(bits)).sum(axis=3)
+    f = f.reshape(m, 4, 16, 8, 4).transpose(0, 1, 4, 2, 3).reshape(16 * m, 128)
+    return _pack.pack_indices(f, bits)
+
+
+def rows_to_values_subtiles(idx: np.ndarray, bits: int) -> np.ndarray:
+    """Inverse of values_subtiles_to_rows: packed rows [16 m, 16 * bits] -> payloads [m, 256 * bits]."""
+    m = idx.shape[0] // 16
+    f = _pack.unpack_indices(idx, bits).reshape(m, 4, 4, 16, 8).transpose(0, 1, 3, 4, 2)  # (g, n, j, r)
+    bitv = ((f.reshape(m, 64, 32, 1) >> np.arange(bits)) & 1).astype(np.uint8).reshape(m, 64, 32 * bits)
+    return np.packbits(bitv, axis=2, bitorder="little").reshape(m, 256 * bits)
 
 
 def tiles_to_tokens(tiles: np.ndarray, block_size: int, bits: int, qjl: bool, layout: str) -> dict:
@@ -204,6 +241,9 @@ def tiles_to_tokens(tiles: np.ndarray, block_size: int, bits: int, qjl: bool, la
     if layout == "rows":
         idx = tiles[:, :block_size * idx_row].reshape(n * block_size, idx_row)
         signs = tiles[:, off_signs:off_signs + 16 * block_size].reshape(n * block_size, 16) if qjl else None
+    elif layout == "values":
+        idx = values_subtiles_to_rows(tiles[:, :block_size * P].reshape(n * (block_size // 16), 16 * P), bits)
+        signs = None
     else:
         pos = subtile_row_positions(bits, qjl, layout)
         sub = tiles[:, :block_size * P].reshape(n * (block_size // 16), 16 * P)

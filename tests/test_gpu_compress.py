@@ -433,6 +433,51 @@ def test_compress_paged_kv_matches_two_launches(dev, dtype, kb, kq, vb, klayout,
         k, v = k.flip(0).contiguous(), v.flip(0).contiguous()
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_compress_paged_values_appends(dev, bits):
+    """Values tiles interleave the fields of four consecutive rows.  Writing a block's tokens one
+    call at a time (decode appends: each call sets its own fields and keeps the neighbours'),
+    in a scrambled order, over a block that held other data, gives the bytes of one call over
+    all tokens; so does a call whose slots start mid-group (prefill after a partial block)."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
+    T, H, bs, nb = 40, 3, 16, 4
+    g = torch.Generator().manual_seed(30 + bits)
+    x = torch.randn(T, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    slots = torch.arange(5, 5 + T, dtype=torch.int64)     # starts at row 5 of block 0
+    fmt = PagedKVFormat(bits=bits, qjl=False, block_size=bs, layout="values")
+    cb = tuple(t.to(dev) for t in _codebook(bits))
+    want = allocate_cache(nb, H, fmt, device=dev)
+    compress_paged(x, slots.to(dev), want, fmt, *cb)
+    got = allocate_cache(nb, H, fmt, device=dev)
+    got.random_(0, 256, generator=torch.Generator(device=dev).manual_seed(1))
+    pre = got.clone()
+    order = torch.randperm(T, generator=g)
+    for t in order.tolist():
+        compress_paged(x[t:t + 1], slots[t:t + 1].to(dev), got, fmt, *cb)
+    torch.cuda.synchronize()
+    # rows 0-4 of block 0 were never written: their fields keep the old bits
+    pl_got = opaged.tiles_to_tokens(got.reshape(nb * H, -1).cpu().numpy(), bs, bits, False, "values")
+    pl_pre = opaged.tiles_to_tokens(pre.reshape(nb * H, -1).cpu().numpy(), bs, bits, False, "values")
+    pl_want = opaged.tiles_to_tokens(want.reshape(nb * H, -1).cpu().numpy(), bs, bits, False, "values")
+    rows = np.arange(nb * H * bs).reshape(nb, H, bs)
+    written = np.zeros((nb, bs), bool)
+    written.reshape(-1)[slots.numpy()] = True
+    for b in range(nb):
+        for h in range(H):
+            for r in range(bs):
+                i = rows[b, h, r]
+                src = pl_want if written[b, r] else pl_pre
+                assert np.array_equal(pl_got["idx"][i], src["idx"][i]), (b, h, r)
+                if written[b, r]:
+                    assert pl_got["norm"][i] == pl_want["norm"][i]
+    # the same tokens again in one call over the appended cache: bytes of the whole-batch write
+    # wherever a token was written
+    compress_paged(x, slots.to(dev), got, fmt, *cb)
+    pl_got2 = opaged.tiles_to_tokens(got.reshape(nb * H, -1).cpu().numpy(), bs, bits, False, "values")
+    sel = rows[:, :, :][written[:, None, :].repeat(H, 1)]
+    assert np.array_equal(pl_got2["idx"][sel], pl_want["idx"][sel])
+
+
 def test_compress_paged_kv_rejections(dev):
     from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged_kv
     T, H, bs, nb = 8, 2, 16, 2

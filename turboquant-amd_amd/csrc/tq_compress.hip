@@ -20,7 +20,8 @@ struct CompressParams {
     int64_t x_stride_head;   // elements
     int64_t num_tokens;
     int num_heads;
-    int64_t n_rows;          // num_tokens * num_heads
+    int64_t tok_rows;        // rows per head: num_tokens, rounded up to 4 in paged mode
+    int64_t n_rows;          // tok_rows * num_heads
     int rotate;
     float wht_scale;
     const float* centroids;
@@ -32,7 +33,7 @@ struct CompressParams {
     int64_t stride_block, stride_head, num_blocks;
     int block_size;
     int idx32;  // rows and slots below 2^31: 32-bit index arithmetic
-    tq_udiv tok_div, blk_div;  // by num_tokens and block_size (32-bit index arithmetic)
+    tq_udiv tok_div, blk_div;  // by tok_rows and block_size (32-bit index arithmetic)
     int tile_layout;  // TQ_TILE_ROWS / TQ_TILE_KEYS / TQ_TILE_VALUES
     int64_t off_signs, off_norm, off_rnorm;
     // unpacked output
@@ -203,6 +204,126 @@ __device__ __forceinline__ int quant_cell_y(float y, float den, float r128, cons
     return (int)e.y + (__builtin_fmaf(__uint_as_float(e.x), den, -y) < 0.f ? 1 : 0);
 }
 
+// ---- values tile layout ----
+// Chunk 16g + n of a 16-row sub-tile (4 * BITS bytes) holds, at field 4j + r (BITS bits each,
+// little-endian), dim 8n + j of row 4g + r: the four rows' fields of one dim are adjacent, so a
+// decode lane turns one field group into one PV operand with one table lookup.  A row's lane q
+// (dims 32q..32q+31) owns fields of chunks n = 4q + i, i = 0..3.  Its slice i holds fields 8i + j
+// at bits 4 BITS j (BITS words): room for the other three rows' fields in between.
+template <int BITS>
+struct ValueSlices {
+    uint32_t w[4][BITS];
+};
+template <int BITS>
+__device__ __forceinline__ ValueSlices<BITS> value_slices(const int (&idx)[32]) {
+    ValueSlices<BITS> s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) s.w[i][k] = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int pos = 4 * BITS * j;  // a field never straddles two words here
+            s.w[i][pos >> 5] |= (uint32_t)idx[8 * i + j] << (pos & 31);
+        }
+    }
+    return s;
+}
+// The fields of one slice (every 4th field position), as words.
+template <int BITS>
+__device__ __forceinline__ uint32_t value_field_mask(int k) {
+    if (BITS == 2) return 0x03030303u;
+    if (BITS == 4) return 0x000F000Fu;
+    return k == 0 ? 0x07007007u : (k == 1 ? 0x70070070u : 0x00700700u);  // fields at 12 j
+}
+// a << s over BITS words (s = BITS r, r = 0..3; for 2 and 4 bits no field crosses a word)
+template <int BITS>
+__device__ __forceinline__ void shl_words(const uint32_t (&a)[BITS], uint32_t s, uint32_t (&o)[BITS]) {
+#pragma unroll
+    for (int k = 0; k < BITS; ++k) {
+        if (BITS == 3 && k > 0)
+            o[k] = (uint32_t)(((((uint64_t)a[k]) << 32) | a[k - 1]) >> (32 - s));
+        else
+            o[k] = a[k] << s;
+    }
+}
+
+// Writes this lane's fields into the values layout.  Rows 4a..4a+3 of a workgroup (lanes
+// 16a'..16a'+15 of one wave) that land on slots 4k..4k+3 fill whole chunks: their slices are
+// exchanged through this wave's part of xchg and each lane stores one chunk.  Any other row
+// sets its own fields with atomic and / or on the chunk words (other rows of the chunk, written
+// by other launches or workgroups, are untouched).
+template <int BITS>
+__device__ __forceinline__ void store_values(const ValueSlices<BITS>& vs, bool write, int64_t slot, uint8_t* tile,
+                                             int64_t r_in_blk, int q, uint32_t* xchg) {
+    constexpr int VS = BITS == 3 ? 4 : BITS;  // words per slice in the exchange (b64 / b128 access)
+    const int lane = threadIdx.x & 63;
+    const int rr = (threadIdx.x >> 2) & 3;    // row of the lane within its group of 4 rows
+    const int64_t s0 = __shfl(slot, lane & ~12);
+    const bool ok = write && (s0 & 3) == 0 && slot == s0 + rr;
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
+    const bool full = ((bal >> (lane & 48)) & 0xffffull) == 0xffffull;
+    uint8_t* sub = tile + (r_in_blk & ~(int64_t)15) * (16 * BITS);
+    const int g = (int)((r_in_blk & 15) >> 2);
+    if (full) {
+        uint32_t* gx = xchg + (threadIdx.x >> 4) * (64 * VS);  // this group: [q][i][row][VS]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t* d = gx + ((q * 4 + i) * 4 + rr) * VS;
+            if (VS == 2) {
+                *reinterpret_cast<tq_u32x2*>(d) = tq_u32x2{vs.w[i][0], vs.w[i][1 % BITS]};
+            } else {
+                *reinterpret_cast<tq_u32x4*>(d) =
+                    tq_u32x4{vs.w[i][0], vs.w[i][1 % BITS], vs.w[i][2 % BITS], BITS == 4 ? vs.w[i][3 % BITS] : 0u};
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        // chunk n = 4q + rr: slice rr of the group's rows 0..3
+        uint32_t out[BITS];
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) out[k] = 0;
+        const uint32_t* src = gx + ((q * 4 + rr) * 4) * VS;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint32_t a[BITS], sh[BITS];
+            if (VS == 2) {
+                const tq_u32x2 v = *reinterpret_cast<const tq_u32x2*>(src + r * VS);
+                a[0] = v[0];
+                a[1 % BITS] = v[1];
+            } else {
+                const tq_u32x4 v = *reinterpret_cast<const tq_u32x4*>(src + r * VS);
+#pragma unroll
+                for (int k = 0; k < BITS; ++k) a[k] = v[k];
+            }
+            shl_words<BITS>(a, (uint32_t)(BITS * r), sh);
+#pragma unroll
+            for (int k = 0; k < BITS; ++k) out[k] |= sh[k];
+        }
+        uint32_t* ch = reinterpret_cast<uint32_t*>(sub + (16 * g + 4 * q + rr) * (4 * BITS));
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) ch[k] = out[k];
+    } else if (write) {
+        const uint32_t sh = (uint32_t)(BITS * (r_in_blk & 3));
+        uint32_t m0[BITS];
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) m0[k] = value_field_mask<BITS>(k);
+        uint32_t m[BITS];
+        shl_words<BITS>(m0, sh, m);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t b[BITS];
+            shl_words<BITS>(vs.w[i], sh, b);
+            uint32_t* ch = reinterpret_cast<uint32_t*>(sub + (16 * g + 4 * q + i) * (4 * BITS));
+#pragma unroll
+            for (int k = 0; k < BITS; ++k) {
+                __hip_atomic_fetch_and(ch + k, ~m[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_or(ch + k, b[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
 // The body of the compression kernels: workgroup wg of nwg takes 64-row groups wg, wg + nwg, ...
 template <int BITS, bool QJL, int MODE, int DT>
 __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, int nwg) {
@@ -211,6 +332,8 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
     __shared__ float s_cent[NC];
     __shared__ uint2 s_cells[kCells];
     __shared__ int s_bad;
+    // values layout: slices exchanged within each group of 4 rows (16 groups x 64 slices)
+    __shared__ __align__(16) uint32_t s_xchg[MODE == MODE_PAGED ? 1024 * (BITS == 3 ? 4 : BITS) : 1];
     if (threadIdx.x < NC) s_cent[threadIdx.x] = p.centroids[threadIdx.x];
     if (threadIdx.x == 0) s_bad = 0;
     // Boundaries are uniform: the loads below become scalar loads kept in SGPRs.
@@ -228,19 +351,24 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
 
     for (int64_t row0 = (int64_t)wg * kRowsPerWG; row0 < p.n_rows; row0 += (int64_t)nwg * kRowsPerWG) {
         const int64_t row = row0 + row_in_wg;
-        const bool row_ok = row < p.n_rows;
-        // Paged rows are head-major so that a workgroup's rows are consecutive tokens.
+        bool row_ok = row < p.n_rows;
+        // Paged rows are head-major so that a workgroup's rows are consecutive tokens; each
+        // head's rows are padded to a multiple of 4, so rows 4a..4a+3 (one 16-lane group of a
+        // wave) are tokens 4k..4k+3 of one head.
         int64_t tok, head;
         if (MODE == MODE_PAGED) {
             if (p.idx32) {
-                const uint32_t r = row_ok ? (uint32_t)row : 0u, nt = (uint32_t)p.num_tokens;
+                const uint32_t r = row_ok ? (uint32_t)row : 0u, nt = (uint32_t)p.tok_rows;
                 const uint32_t h = tq_udiv_apply(r, p.tok_div);
                 head = h;
                 tok = r - h * nt;
             } else {
-                head = row_ok ? row / p.num_tokens : 0;
-                tok = row_ok ? row - head * p.num_tokens : 0;
+                head = row_ok ? row / p.tok_rows : 0;
+                tok = row_ok ? row - head * p.tok_rows : 0;
             }
+            row_ok = row_ok && tok < p.num_tokens;
+            tok = row_ok ? tok : 0;
+            head = row_ok ? head : 0;
         } else {
             head = 0;
             tok = row_ok ? row : 0;
@@ -342,6 +470,13 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                 r_in_blk = write ? slot - blk * p.block_size : 0;
             }
             uint8_t* tile = p.cache + blk * p.stride_block + head * p.stride_head;
+            if (p.tile_layout == TQ_TILE_VALUES) {
+                if (BITS >= 2) store_values<BITS < 2 ? 2 : BITS>(value_slices<BITS < 2 ? 2 : BITS>(idx), write, slot, tile,
+                                                                  r_in_blk, q, s_xchg);
+                if (write && q == 0)
+                    reinterpret_cast<uint16_t*>(tile + p.off_norm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(norm);
+                continue;
+            }
             // this lane's 32 indices: 4 * BITS bytes of the row's little-endian bit stream
             uint32_t w[BITS];
 #pragma unroll
@@ -361,20 +496,6 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
 #pragma unroll
                     for (int j = 0; j < BITS; ++j) ch[j] = w[j];
                     if (QJL) ch[BITS] = sbits;
-                } else if (p.tile_layout == TQ_TILE_VALUES) {
-                    // dims 8n..8n+7 (n = 4q + i) of row 4g + r go to chunk (16g + n) at byte r * BITS
-                    uint8_t* st = tile + (r_in_blk & ~(int64_t)15) * (16 * BITS);
-                    const int t16 = (int)(r_in_blk & 15), g = t16 >> 2, r = t16 & 3;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        uint8_t* d = st + (16 * g + 4 * q + i) * (4 * BITS) + r * BITS;
-                        // bytes BITS*i .. BITS*i + BITS - 1 of the lane's stream
-#pragma unroll
-                        for (int k = 0; k < BITS; ++k) {
-                            const int byte = BITS * i + k;
-                            d[k] = (uint8_t)(w[byte >> 2] >> (8 * (byte & 3)));
-                        }
-                    }
                 } else {
                     uint32_t* irow = reinterpret_cast<uint32_t*>(tile + r_in_blk * (16 * BITS) + 4 * BITS * q);
 #pragma unroll
@@ -465,6 +586,7 @@ extern "C" int tq_polarquant_compress(const void* x, int x_dtype, int64_t x_row_
     p.x_stride_token = x_row_stride;
     p.x_stride_head = 0;
     p.num_tokens = n_rows;
+    p.tok_rows = n_rows;
     p.num_heads = 1;
     p.n_rows = n_rows;
     p.rotate = rotate ? 1 : 0;
@@ -533,7 +655,8 @@ int paged_params(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_s
     p.x_stride_head = x_stride_head;
     p.num_tokens = num_tokens;
     p.num_heads = num_heads;
-    p.n_rows = num_tokens * num_heads;
+    p.tok_rows = (num_tokens + 3) & ~(int64_t)3;
+    p.n_rows = p.tok_rows * num_heads;
     p.rotate = rotate ? 1 : 0;
     p.wht_scale = wht_scale;
     p.centroids = centroids;
@@ -555,7 +678,7 @@ int paged_params(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_s
                   ? 1
                   : 0;
     if (p.idx32) {
-        p.tok_div = tq_make_udiv((uint32_t)num_tokens);
+        p.tok_div = tq_make_udiv((uint32_t)p.tok_rows);
         p.blk_div = tq_make_udiv((uint32_t)block_size);
     }
     *out = p;

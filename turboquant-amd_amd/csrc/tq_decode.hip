@@ -130,7 +130,8 @@ struct TileRaw {
     uint32_t kw[KB];                      // dims 32g..32g+31 of token n: 32*KB bits
     uint32_t ks;                          // sign bits of the same dims
     uint32_t kn[NV ? 2 : 4], krn[NV ? 2 : 4], vn[NV ? 2 : 4];  // fp16 norms of tokens 4g..4g+3
-    uint32_t vw[4][VB == 3 ? 2 : 1];      // dims 8n..8n+7 of tokens 4g..4g+3
+    uint32_t vw[4][VB == 3 ? 2 : 1];      // dims 8n..8n+7 of tokens 4g..4g+3; values tile layout:
+                                          // vw[k][0], k < VB, the words of the lane's chunk
 };
 
 template <bool NV>
@@ -209,21 +210,35 @@ __device__ __forceinline__ void load_tile(TileRaw<KB, KQJL, VB, NV>& t, const Ti
         }
     }
     auto rv = make_rsrc(tl.base[R_VIDX], nrec(R_VIDX));
+    if (!MASKED && v_lg) {
+        // values tile layout: the lane's chunk (4 * VB bytes) in one load
+        if (VB == 2) {
+            tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, o.vidx, 0, 0);
+            t.vw[0][0] = w[0];
+            t.vw[1][0] = w[1];
+        } else if (VB == 3) {
+            typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+            u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rv, o.vidx, 0, 0);
+            t.vw[0][0] = w[0];
+            t.vw[1][0] = w[1];
+            t.vw[2][0] = w[2];
+        } else {
+            tq_u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rv, o.vidx, 0, 0);
+            t.vw[0][0] = w[0];
+            t.vw[1][0] = w[1];
+            t.vw[2][0] = w[2];
+            t.vw[3][0] = w[3];
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const uint32_t off = MASKED ? o.vidx + r * vstep : o.vidx;
         if (VB == 3) {
-            // lane-grouped: row r's 3 bytes at 3r of the chunk, read as the aligned 8-byte
-            // window at (3r & ~3) and shifted down by (3r & 3) bytes (then selected as bytes 0..2)
-            const int soff = MASKED ? 0 : sgpr(v_lg ? ((3 * r) & ~3) : r * vstep);
+            const int soff = MASKED ? 0 : sgpr(r * vstep);
             tq_u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rv, off, soff, 0);
-            if (v_lg) {
-                t.vw[r][0] = __builtin_amdgcn_alignbit(w[1], w[0], 8 * ((3 * r) & 3));
-                t.vw[r][VB == 3 ? 1 : 0] = 0;
-            } else {
-                t.vw[r][0] = w[0];
-                t.vw[r][VB == 3 ? 1 : 0] = w[1];
-            }
+            t.vw[r][0] = w[0];
+            t.vw[r][VB == 3 ? 1 : 0] = w[1];
             continue;
         }
         const int soff = MASKED ? 0 : sgpr(r * vstep);
@@ -381,6 +396,20 @@ __device__ __forceinline__ void compute_tile(const TileRaw<KB, KQJL, VB, NV>& cu
     // ---------------- PV product ----------------
     tq_u32x2 bw = {tq_pack_half2(pv[0], pv[1]), tq_pack_half2(pv[2], pv[3])};
     const tq_half4 bop = __builtin_bit_cast(tq_half4, bw);
+    if (NV && p.v_lg) {
+        // values tile layout: field group a of the chunk is dim 8n + a of tokens 4g..4g+3, two
+        // pair lookups give the A operand directly
+        uint32_t cw[VB];
+#pragma unroll
+        for (int k = 0; k < VB; ++k) cw[k] = cur.vw[k][0];
+#pragma unroll
+        for (int a = 0; a < 8; ++a) {
+            const tq_u32x2 aw = {lds_read(pair_addr<2 * VB>(cw, 4 * VB * a, vbank)),
+                                 lds_read(pair_addr<2 * VB>(cw, 4 * VB * a + 2 * VB, vbank))};
+            st.acc[a] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(tq_half4, aw), bop, st.acc[a], 0, 0, 0);
+        }
+        return;
+    }
     uint32_t w[4][1];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -551,10 +580,9 @@ void decode_kernel(DecodeParams p) {
     o.krn = (uint32_t)(4 * g * p.rrow[R_KRNORM]);
     o.vn = (uint32_t)(4 * g * p.rrow[R_VNORM]);
     if (NV && p.v_lg) {
-        // chunk (16g + n) of the 16-row sub-tile, row 4g + r at r * VB (vstep); a 3-bit field is
-        // shifted to bytes 0..2 at load time
+        // chunk (16g + n) of the 16-row sub-tile, read whole
         o.vidx = (uint32_t)((16 * g + n) * 4 * VB);
-        o.vsel = 0x0c020100u;
+        o.vsel = 0;
     } else {
         int start = VB * n;
         o.vsel = 0;

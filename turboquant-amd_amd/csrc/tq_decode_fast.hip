@@ -19,7 +19,9 @@
 //   acc^T[dim][col] += V^T[128 x 32] . P^T[32 x 16]           8 x mfma_f32_16x16x32_f16 per pair
 //       k-slots 0-3 of lane group g are tile A's tokens 4g..4g+3, slots 4-7 tile B's; column
 //       col < 8 takes tile A's p from its own lane and tile B's from lane col + 8 (DPP row
-//       rotate), so columns 0-7 accumulate both tiles and columns 8-15 are ignored.
+//       rotate), so columns 0-7 accumulate both tiles and columns 8-15 are ignored.  The values
+//       tile stores each dim's four tokens side by side, so one table lookup per tile and dim
+//       is the A operand (no lane-local transposes).
 // MFMA output layout (16x16): lane l holds rows 4(l/16)+r, column l%16 - after the QK product
 // lane (col, g) owns tokens 4g..4g+3, the B-operand layout of the PV product.
 //
@@ -111,10 +113,6 @@ constexpr int sign_replicas() {
     return (quad_table<KB>() || quad_table<VB>()) ? 16 : 32;
 }
 
-__device__ __forceinline__ uint32_t pick_halves(uint32_t hi_src, uint32_t lo_src, int s) {
-    return __builtin_amdgcn_perm(hi_src, lo_src, s ? 0x07060302u : 0x05040100u);
-}
-
 __device__ __forceinline__ float half_at(const uint32_t (&w)[2], int r) {
     const uint32_t b = (r & 1) ? (w[r >> 1] >> 16) : (w[r >> 1] & 0xffffu);
     return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
@@ -150,9 +148,10 @@ struct KRaw {
     uint32_t ksA, ksB;          // sign bits of the same dims
     uint32_t kn[2], krn[2];     // fp16 norms of tokens 4g..4g+3 of the lane's tile
 };
+template <int VB>
 struct VRaw {
-    uint32_t vwA[4], vwB[4];    // index bits of dims 8n..8n+7 of tokens 4g..4g+3 (bits 0 .. 8*VB-1;
-                                // 2-bit quad tables: odd tokens at bits 16-31)
+    uint32_t vwA[VB], vwB[VB];  // chunk 16g + n of the values tile: field 4j + r = dim 8n + j of
+                                // token 4g + r (VB bits each)
     uint32_t vn[2];             // fp16 norms of tokens 4g..4g+3 of the lane's tile
 };
 // Wave-uniform description of a pair.
@@ -233,7 +232,7 @@ __device__ __forceinline__ uint64_t row_mask(int nvA, int nvB, int r) {
 
 // One pair of tiles.
 template <int KB, bool KQJL, int VB, bool COUNT>
-__device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRaw& vr, const PairInfo& pi,
+__device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRaw<VB>& vr, const PairInfo& pi,
                                              Softmax& st, const LaneCtx& c, const FastDecodeParams& p) {
     // ---------------- scores ----------------
     const tq_floatx4 sA = qk_tile<KB>(kr.kwA, c);
@@ -330,49 +329,27 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     p23.h[1] = scale_to_half(half_at(vn, 3), pr[3]);
     const tq_u32x4 bw = {p01.u, p23.u, row_swap8(p01.u), row_swap8(p23.u)};
     const tq_half8 bop = __builtin_bit_cast(tq_half8, bw);
-    auto pv_mfma = [&](const uint32_t (&la)[4], const uint32_t (&lb)[4], int q) {
+    // acc[a] (dim 8n + a): field group a of the lane's chunk is that dim's four tokens, so the
+    // lookups are the A operand as they come: k-slots 0-3 tile A's tokens, 4-7 tile B's.
 #pragma unroll
-        for (int hs = 0; hs < 2; ++hs) {
-            const tq_u32x4 aw = {pick_halves(la[1], la[0], hs), pick_halves(la[3], la[2], hs),
-                                 pick_halves(lb[1], lb[0], hs), pick_halves(lb[3], lb[2], hs)};
-            st.acc[2 * q + hs] =
-                __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, aw), bop, st.acc[2 * q + hs], 0, 0, 0);
-        }
-    };
-    if (quad_table<VB>()) {
+    for (int a = 0; a < 8; ++a) {
+        tq_u32x4 aw;
+        if (quad_table<VB>()) {
+            // one quad per tile (2 bits: a fixed table address, which goes into the ds_read offset)
+            const uint32_t fa = entry_addr<4 * VB, VB, quad_shift<VB>()>(vr.vwA, 4 * VB * a, VB == 2 ? 0u : c.vquad);
+            const uint32_t fb = entry_addr<4 * VB, VB, quad_shift<VB>()>(vr.vwB, 4 * VB * a, VB == 2 ? 0u : c.vquad);
+            const tq_u32x2 xa = lds_read2(VB == 2 ? fa + v2_quad_base<KB>() : fa);
+            const tq_u32x2 xb = lds_read2(VB == 2 ? fb + v2_quad_base<KB>() : fb);
+            aw = tq_u32x4{xa[0], xa[1], xb[0], xb[1]};
+        } else {
+            // two pairs per tile: tokens 0, 1 and 2, 3
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {
-            // dims 8n + 4qh .. 8n + 4qh + 3 of each token: one quad -> pairs q = 2qh, 2qh + 1
-            uint32_t la[2][4], lb[2][4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
-                // 2 bits: a fixed table address, which goes into the ds_read offset
-                const int pos = 4 * VB * qh + (VB == 2 ? 16 * (r & 1) : 0);
-                const uint32_t fa = entry_addr<4 * VB, 1, quad_shift<VB>()>(wa, pos, VB == 2 ? 0u : c.vquad);
-                const uint32_t fb = entry_addr<4 * VB, 1, quad_shift<VB>()>(wb, pos, VB == 2 ? 0u : c.vquad);
-                const tq_u32x2 xa = lds_read2(VB == 2 ? fa + v2_quad_base<KB>() : fa);
-                const tq_u32x2 xb = lds_read2(VB == 2 ? fb + v2_quad_base<KB>() : fb);
-                la[0][r] = xa[0];
-                la[1][r] = xa[1];
-                lb[0][r] = xb[0];
-                lb[1][r] = xb[1];
+            for (int h = 0; h < 2; ++h) {
+                aw[h] = lds_read(entry_addr<2 * VB, VB>(vr.vwA, 4 * VB * a + 2 * VB * h, c.vbank));
+                aw[2 + h] = lds_read(entry_addr<2 * VB, VB>(vr.vwB, 4 * VB * a + 2 * VB * h, c.vbank));
             }
-            pv_mfma(la[0], lb[0], 2 * qh);
-            pv_mfma(la[1], lb[1], 2 * qh + 1);
         }
-    } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t la[4], lb[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t wa[1] = {vr.vwA[r]}, wb[1] = {vr.vwB[r]};
-                la[r] = lds_read(entry_addr<2 * VB>(wa, 2 * VB * q, c.vbank));
-                lb[r] = lds_read(entry_addr<2 * VB>(wb, 2 * VB * q, c.vbank));
-            }
-            pv_mfma(la, lb, q);
-        }
+        st.acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, aw), bop, st.acc[a], 0, 0, 0);
     }
 }
 
@@ -686,25 +663,20 @@ void decode_fast_kernel(FastDecodeParams p) {
             kr.krn[1] = bb[1];
         }
     };
-    auto load_v = [&](const PairInfo& info, VRaw& vr) {
-        // One load per tile: chunk (16g + n) of the 16-row sub-tile holds dims 8n..8n+7 of rows
-        // 4g..4g+3, VB bytes each; row r's fields go to bits 0 .. 8*VB-1 of vw[r].
-        auto load1 = [&](uint32_t (&vw)[4], __amdgpu_buffer_rsrc_t rv, uint32_t soff) {
+    auto load_v = [&](const PairInfo& info, VRaw<VB>& vr) {
+        // One load per tile: chunk (16g + n) of the 16-row sub-tile, 4 * VB bytes (dims 8n..8n+7
+        // of rows 4g..4g+3, dimension-major).
+        auto load1 = [&](uint32_t (&vw)[VB], __amdgpu_buffer_rsrc_t rv, uint32_t soff) {
             if (VB == 2) {
-                // a quad table reads the odd rows' bytes in place (bits 16-31)
                 tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, o_vch, soff, 0);
-                vw[0] = a[0]; vw[1] = quad_table<VB>() ? a[0] : a[0] >> 16;
-                vw[2] = a[1]; vw[3] = quad_table<VB>() ? a[1] : a[1] >> 16;
+                vw[0] = a[0]; vw[1 % VB] = a[1];
             } else if (VB == 3) {
                 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
                 u32x3 a = __builtin_amdgcn_raw_buffer_load_b96(rv, o_vch, soff, 0);
-                vw[0] = a[0];
-                vw[1] = __builtin_amdgcn_alignbit(a[1], a[0], 24);
-                vw[2] = __builtin_amdgcn_alignbit(a[2], a[1], 16);
-                vw[3] = a[2] >> 8;
+                vw[0] = a[0]; vw[1 % VB] = a[1]; vw[2 % VB] = a[2];
             } else {
                 tq_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rv, o_vch, soff, 0);
-                vw[0] = a[0]; vw[1] = a[1]; vw[2] = a[2]; vw[3] = a[3];
+                vw[0] = a[0]; vw[1 % VB] = a[1]; vw[2 % VB] = a[2]; vw[3 % VB] = a[3];
             }
         };
         if (BIG) {
@@ -743,7 +715,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     // compiler's outstanding-load counts exact).
     KRaw<KB, KQJL> kr[2];
     PairInfo info[2];
-    VRaw vr[2];
+    VRaw<VB> vr[2];
     fetch_k(0, kr[0], info[0]);
     load_v(info[0], vr[0]);
     for (int i = 0; i < npairs; i += 2) {

@@ -222,7 +222,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         o_sg = (uint32_t)(tk * p.ksig.stride_row) + 4u * (uint32_t)(pk >> 2);
     }
     if (p.v_lg) {
-        ov = (uint32_t)((16 * (tt >> 2) + pp) * 4 * VB + (tt & 3) * VB);  // chunk: rows 4(tt/4).., dims 8pp..
+        // chunk (tt / 4, pp), byte VB (tt & 3): dims 8pp + 2 (tt & 3) and the next, rows 4 (tt / 4)..
+        ov = (uint32_t)((16 * (tt >> 2) + pp) * 4 * VB + (tt & 3) * VB);
     } else {
         ov = (uint32_t)(tt * p.vidx.stride_row + VB * pp);
     }
@@ -292,13 +293,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
         {
             const uint32_t f = __builtin_amdgcn_alignbit(w.vw[1], w.vw[0], sh_v);
             const uint8_t* tv = tab + 1024;
+            if (p.v_lg) {
+                // values tile layout: the 8 VB bits at byte VB r of chunk (g, pp) (r = tt & 3) are
+                // dims 8pp + 2r + jj (jj = 0, 1), four tokens 4g.. each: pairs of tokens go to
+                // VhatT as half2 words
+                const int g4 = tt & ~3, d0 = 8 * pp + 2 * (tt & 3);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t e = (f >> (2 * VB * k)) & ((1u << (2 * VB)) - 1u);
-                const uint32_t h2 = *reinterpret_cast<const uint32_t*>(tv + 4 * e);
-                const int d = 8 * pp + 2 * k;
-                *reinterpret_cast<uint16_t*>(b + kOffV + d * kVRow + 2 * tt) = (uint16_t)h2;
-                *reinterpret_cast<uint16_t*>(b + kOffV + (d + 1) * kVRow + 2 * tt) = (uint16_t)(h2 >> 16);
+                for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t e = (f >> (4 * VB * jj + 2 * VB * h)) & ((1u << (2 * VB)) - 1u);
+                        *reinterpret_cast<uint32_t*>(b + kOffV + (d0 + jj) * kVRow + 2 * (g4 + 2 * h)) =
+                            *reinterpret_cast<const uint32_t*>(tv + 4 * e);
+                    }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t e = (f >> (2 * VB * k)) & ((1u << (2 * VB)) - 1u);
+                    const uint32_t h2 = *reinterpret_cast<const uint32_t*>(tv + 4 * e);
+                    const int d = 8 * pp + 2 * k;
+                    *reinterpret_cast<uint16_t*>(b + kOffV + d * kVRow + 2 * tt) = (uint16_t)h2;
+                    *reinterpret_cast<uint16_t*>(b + kOffV + (d + 1) * kVRow + 2 * tt) = (uint16_t)(h2 >> 16);
+                }
             }
         }
         if (tid < 48) {

@@ -622,8 +622,10 @@ def _tile_fields(fmt: PagedKVFormat):
 @functools.lru_cache(maxsize=None)
 def _rows_positions(fmt: PagedKVFormat) -> Optional[torch.Tensor]:
     """pos[j] = byte of fmt's tile that holds byte j of the same tile in the "rows" layout
-    (None for the rows layout itself).  Norm regions coincide."""
-    if fmt.layout == "rows":
+    (None for the rows layout itself, which needs no move, and for the values layout, whose
+    chunks interleave bits-wide fields of four rows: see _values_to_rows).  Norm regions
+    coincide."""
+    if fmt.layout != "keys":
         return None
     bs, b, q = fmt.block_size, fmt.bits, fmt.qjl
     P = fmt.payload_bytes
@@ -631,20 +633,62 @@ def _rows_positions(fmt: PagedKVFormat) -> Optional[torch.Tensor]:
     R = torch.arange(bs).view(bs, 1)
     sub, t16 = (R // 16) * 16 * P, R % 16
     k = torch.arange(16 * b).view(1, -1)                    # index byte of the token
-    if fmt.layout == "keys":
-        C = 4 * b + (4 if q else 0)
-        pos[:bs * 16 * b] = (sub + (4 * t16 + k // (4 * b)) * C + k % (4 * b)).reshape(-1)
-        if q:
-            ks = torch.arange(16).view(1, -1)               # sign byte of the token
-            pos[fmt.off_signs:fmt.off_signs + bs * 16] = (sub + (4 * t16 + ks // 4) * C + 4 * b + ks % 4).reshape(-1)
-    else:
-        g, r = t16 // 4, t16 % 4
-        pos[:bs * 16 * b] = (sub + (16 * g + k // b) * (4 * b) + r * b + k % b).reshape(-1)
+    C = 4 * b + (4 if q else 0)
+    pos[:bs * 16 * b] = (sub + (4 * t16 + k // (4 * b)) * C + k % (4 * b)).reshape(-1)
+    if q:
+        ks = torch.arange(16).view(1, -1)                   # sign byte of the token
+        pos[fmt.off_signs:fmt.off_signs + bs * 16] = (sub + (4 * t16 + ks // 4) * C + 4 * b + ks % 4).reshape(-1)
     return pos
+
+
+def _fields(b: torch.Tensor, bits: int, n: int) -> torch.Tensor:
+    """uint8 [..., n * bits / 8] little-endian bit streams -> int64 fields [..., n]."""
+    bitv = (b.to(torch.int64).unsqueeze(-1) >> torch.arange(8, device=b.device)) & 1
+    return (bitv.reshape(*b.shape[:-1], n, bits) << torch.arange(bits, device=b.device)).sum(-1)
+
+
+def _stream(f: torch.Tensor, bits: int) -> torch.Tensor:
+    """Inverse of _fields: int64 fields [..., n] -> uint8 [..., n * bits / 8]."""
+    bitv = (f.unsqueeze(-1) >> torch.arange(bits, device=f.device)) & 1
+    bitv = bitv.reshape(*f.shape[:-1], -1, 8)
+    return (bitv << torch.arange(8, device=f.device)).sum(-1).to(torch.uint8)
+
+
+_CONVERT_TILES = 2048  # tiles per batch of the field-level conversion (bounds the int64 temporaries)
+
+
+def _values_to_rows(payload: torch.Tensor, bits: int) -> torch.Tensor:
+    """values-layout payloads [m, bs * 16 * bits] -> row-major index rows, same shape.  Chunk
+    16g + n of a 16-row sub-tile holds, at field 4j + r, dim 8n + j of row 4g + r."""
+    m = payload.shape[0]
+    f = _fields(payload.reshape(m, -1, 64, 4 * bits), bits, 32)          # [m, sub, chunk, field]
+    f = f.reshape(m, -1, 4, 16, 8, 4).permute(0, 1, 2, 5, 3, 4)            # (g, r, n, j)
+    return _stream(f.reshape(m, -1, 128), bits).reshape(m, -1)
+
+
+def _rows_to_values(rows: torch.Tensor, bits: int) -> torch.Tensor:
+    """Inverse of _values_to_rows."""
+    m = rows.shape[0]
+    f = _fields(rows.reshape(m, -1, 16 * bits), bits, 128)                # [m, row, dim]
+    f = f.reshape(m, -1, 4, 4, 16, 8).permute(0, 1, 2, 4, 5, 3)            # (g, n, j, r)
+    return _stream(f.reshape(m, -1, 32), bits).reshape(m, -1)
+
+
+def _convert_values(cache: torch.Tensor, fmt: PagedKVFormat, fn) -> torch.Tensor:
+    out = cache[..., :fmt.tile_bytes].clone()
+    nb, h, _ = out.shape
+    flat = out.reshape(nb * h, -1)
+    n_idx = fmt.block_size * fmt.idx_bytes
+    for i in range(0, nb * h, _CONVERT_TILES):
+        part = flat[i:i + _CONVERT_TILES, :n_idx]
+        flat[i:i + _CONVERT_TILES, :n_idx] = fn(part, fmt.bits)
+    return out
 
 
 def to_rows_layout(cache: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
     """The same tiles in the "rows" layout (a copy)."""
+    if fmt.layout == "values":
+        return _convert_values(cache, fmt, _values_to_rows)
     pos = _rows_positions(fmt)
     if pos is None:
         return cache.clone()
@@ -653,6 +697,8 @@ def to_rows_layout(cache: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
 
 def from_rows_layout(rows: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
     """Inverse of to_rows_layout."""
+    if fmt.layout == "values":
+        return _convert_values(rows, fmt, _rows_to_values)
     pos = _rows_positions(fmt)
     if pos is None:
         return rows.clone()
