@@ -156,8 +156,10 @@ def _kernel_codebook(bits):
 
 
 @pytest.mark.parametrize("bits", [2, 1, 3, 4])
-@pytest.mark.parametrize("n", [1, 1023, 4096])
+@pytest.mark.parametrize("n", [1, 1023, 4096, 131072])
 def test_compress_k_v_against_oracle(dev, bits, n, parity_log):
+    """compress_k / compress_v against the float64 restatement; 131,072 rows make every wave
+    loop over several 32-row groups."""
     from turboquant.kernels.packed_compress import compress_k, compress_k_permuted, compress_v
     g = torch.Generator().manual_seed(3000 + bits * 7 + n)
     K = torch.randn(n, 128, generator=g) * torch.exp(torch.randn(128, generator=g) * 0.5)

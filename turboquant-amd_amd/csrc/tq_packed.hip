@@ -19,8 +19,12 @@
 // every element within 2^-21 * max column norm of a boundary: the whole wave recomputes that
 // element's dot product in fp64 from the input row and the fp32 matrix (one element at a time;
 // about 1e-5 of the elements at 2 bits), so indices equal the float64 restatement of the
-// reference except within fp32 rounding of a boundary.  The row norm is an fp64 sum.  Sign bits
-// come from the fp32 products (their margin is relative to the summed terms).
+// reference except within fp32 rounding of a boundary.  The row norm is an fp64 sum and x_n is
+// rounded once from x * (1 / (norm + 1e-8)) in fp64.  Sign bits come from the fp32 products
+// (their margin is relative to the summed terms).
+//
+// The matrices are staged transposed, hi and lo parts, with one 16-byte LDS store per 8
+// consecutive positions of a column (a thread keeps one column).
 #include <mutex>
 #include <set>
 #include <utility>
@@ -63,11 +67,6 @@ __device__ __forceinline__ uint32_t or_over_groups(uint32_t x) {
     auto b = __builtin_amdgcn_permlane16_swap(y, y, false, false);
     return b[0] | b[1];
 }
-__device__ __forceinline__ double sum_over_groups_f64(double x) {
-    x += __shfl_xor(x, 16, 64);
-    x += __shfl_xor(x, 32, 64);
-    return x;
-}
 __device__ __forceinline__ float sum_over_groups(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
@@ -97,59 +96,59 @@ void packed_compress_mfma_kernel(PackedParams p) {
     _Float16* s_m1l = s_h + kD * kStride;       // PiT^T lo
     _Float16* s_m2h = s_h + 2 * kD * kStride;   // PiST^T hi [col][32ks + p] = PiST[32ks + perm2(p)][col]
     _Float16* s_m2l = s_h + 3 * kD * kStride;
-    __shared__ float s_colss[4 * kWaves * 64];
+    __shared__ float s_colss[kWaves * 64];
     __shared__ float s_colmax;
     __shared__ float s_cent[NC];
 
     const int tid = threadIdx.x;
     // float4 of 4 consecutive columns per thread and step (kWaves * 64 * 4 is a multiple of 128:
     // each thread keeps the same 4 columns and sums their squares)
-    float css[4] = {0.f, 0.f, 0.f, 0.f};
-    {
-        constexpr int kSteps = kD * kD / 4 / (kWaves * 64);
-        float4 v[kSteps], w[kSteps];
+    // Staging: task t = (column col = t % 128, group j = t / 128 of 8 positions along d) reads
+    // 8 floats of the column (consecutive threads: consecutive columns, coalesced) and writes
+    // their fp16 hi and lo parts as two 16-byte rows of the transposed matrix.  Thread tid always
+    // has column tid % 128 and sums its squares for the column norm.
+    constexpr int kThreads = kWaves * 64;
+    constexpr int kTasks = kD * (kD / 8) / kThreads;
+    float css = 0.f;
 #pragma unroll
-        for (int k = 0; k < kSteps; ++k) {
-            v[k] = reinterpret_cast<const float4*>(p.pit)[tid + k * kWaves * 64];
-            if (PROJ) w[k] = reinterpret_cast<const float4*>(p.pist)[tid + k * kWaves * 64];
+    for (int k = 0; k < kTasks; ++k) {
+        const int t = tid + k * kThreads;
+        const int col = t & (kD - 1), j = t >> 7;
+        float v[8], w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[i] = p.pit[(8 * j + i) * kD + col];
+            // PiST: position 8j + i of the permuted K slice holds dim (8j & ~31) + perm2((8j & 31) + i)
+            if (PROJ) w[i] = p.pist[((8 * j & ~31) + perm2((8 * j & 31) + i)) * kD + col];
         }
+        tq_half8 h, l, hw, lw;
 #pragma unroll
-        for (int k = 0; k < kSteps; ++k) {
-            const int i = 4 * (tid + k * kWaves * 64);
-            const int d = i >> 7, col0 = i & 127;
-            const float vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                css[j] = __builtin_fmaf(vv[j], vv[j], css[j]);
-                const _Float16 h = (_Float16)vv[j];
-                s_m1h[(col0 + j) * kStride + d] = h;
-                s_m1l[(col0 + j) * kStride + d] = (_Float16)(vv[j] - (float)h);
-            }
+        for (int i = 0; i < 8; ++i) {
+            css = __builtin_fmaf(v[i], v[i], css);
+            h[i] = (_Float16)v[i];
+            l[i] = (_Float16)(v[i] - (float)h[i]);
             if (PROJ) {
-                // position q of the slice holding dim d: perm2(q) == d % 32
-                const int dl = d & 31;
-                const int q = dl < 16 ? 8 * (dl >> 2) + (dl & 3) : 8 * ((dl - 16) >> 2) + 4 + (dl & 3);
-                const float ww[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const _Float16 wh = (_Float16)ww[j];
-                    s_m2h[(col0 + j) * kStride + (d & ~31) + q] = wh;
-                    s_m2l[(col0 + j) * kStride + (d & ~31) + q] = (_Float16)(ww[j] - (float)wh);
-                }
+                hw[i] = (_Float16)w[i];
+                lw[i] = (_Float16)(w[i] - (float)hw[i]);
             }
+        }
+        *reinterpret_cast<tq_half8*>(s_m1h + col * kStride + 8 * j) = h;
+        *reinterpret_cast<tq_half8*>(s_m1l + col * kStride + 8 * j) = l;
+        if (PROJ) {
+            *reinterpret_cast<tq_half8*>(s_m2h + col * kStride + 8 * j) = hw;
+            *reinterpret_cast<tq_half8*>(s_m2l + col * kStride + 8 * j) = lw;
         }
     }
     if (tid < NC) s_cent[tid] = p.centroids[tid];
-    // largest column 2-norm of PiT: the near-boundary threshold scales with it.  Thread t holds
-    // partial sums of columns (4t + j) % 128; columns c's partials are at threads c/4 + 32m.
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_colss[j * kWaves * 64 + tid] = css[j];
+    // largest column 2-norm of PiT: the near-boundary threshold scales with it.  Column c's
+    // partial sums are at threads c, c + 128, ...
+    s_colss[tid] = css;
     __syncthreads();
     if (tid < 64) {
         float m = 0.f;
         for (int c = tid; c < kD; c += 64) {
             float t = 0.f;
-            for (int u = c >> 2; u < kWaves * 64; u += 32) t += s_colss[(c & 3) * kWaves * 64 + u];
+            for (int u = c; u < kThreads; u += kD) t += s_colss[u];
             m = fmaxf(m, t);
         }
 #pragma unroll
@@ -164,16 +163,18 @@ void packed_compress_mfma_kernel(PackedParams p) {
     const uint32_t near_bits = __float_as_uint(kNearRel * __builtin_sqrtf(s_colmax));
     // idx = #{b <= v} and whether some boundary lies within the threshold of v, from the signs
     // and magnitudes of v - b (integer arithmetic: no compare-and-select chains)
+    const float near_thr = __uint_as_float(near_bits);
     auto quantize = [&](float v, uint32_t& k, bool& nb) {
-        uint32_t neg = 0, mind = 0xffffffffu;
+        uint32_t neg = 0;
+        float m = __builtin_huge_valf();
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const uint32_t d = __float_as_uint(v - bd[b]);
-            neg += d >> 31;
-            mind = __builtin_elementwise_min(mind, d & 0x7fffffffu);
+            const float d = v - bd[b];
+            neg += __float_as_uint(d) >> 31;
+            m = __builtin_fminf(m, __builtin_fabsf(d));
         }
         k = NB - neg;
-        nb = mind <= near_bits;
+        nb = m <= near_thr;
     };
 
     const int lane = tid & 63;
@@ -210,7 +211,8 @@ void packed_compress_mfma_kernel(PackedParams p) {
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ss = __builtin_fma((double)xv[ks][e], (double)xv[ks][e], ss);
-            ss = sum_over_groups_f64(ss);
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
             const double nrm = __builtin_sqrt(ss);
             // the fp16 norm is rounded from this fp32 value (as the reference's .half() of an fp32
             // norm); without the barrier the compiler may round fp64 -> fp16 in one step
@@ -264,10 +266,10 @@ void packed_compress_mfma_kernel(PackedParams p) {
         // elements near a boundary.  Element e = 32 rt + 4 cb + r of a lane is
         // rot[row0 + 16 rt + n][16 cb + 4 g + r]. ----
         uint32_t kf[8 * kRT];
-        uint64_t near = 0;
+        uint32_t nearw[kRT];
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) {
-            const bool live = row0 + 16 * rt + n < p.n_rows;
+            nearw[rt] = 0;
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb) {
                 kf[8 * rt + cb] = 0;
@@ -277,10 +279,12 @@ void packed_compress_mfma_kernel(PackedParams p) {
                     bool nb;
                     quantize(acc[rt][cb][r], k, nb);
                     kf[8 * rt + cb] |= k << (BITS * r);
-                    if (nb && live) near |= 1ull << (32 * rt + 4 * cb + r);
+                    nearw[rt] |= nb ? (1u << (4 * cb + r)) : 0u;
                 }
             }
+            if (row0 + 16 * rt + n >= p.n_rows) nearw[rt] = 0;
         }
+        uint64_t near = nearw[0] | (kRT > 1 ? ((uint64_t)nearw[kRT > 1 ? 1 : 0] << 32) : 0ull);
         // Exact decisions, one near element at a time (about 1e-5 of them): the whole wave
         // computes that row's norm and dot product in fp64 (x * (1 / (norm + 1e-8)) @ PiT as the
         // reference orders it) and the owning lane rewrites the element's index field.  The
