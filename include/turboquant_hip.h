@@ -131,8 +131,11 @@ int tq_compress_packed(const void* x, int x_dtype, int64_t x_row_stride, int64_t
  *                  g (dims 32g..32g+31): the 4*bits index bytes of those dims, then their 4
  *                  sign bytes (QJL) - what one lane of the decode kernel reads for one key;
  *   TQ_TILE_VALUES chunk (16g + n) of 4*bits bytes for row group g (rows 4g..4g+3) and dim
- *                  group n (dims 8n..8n+7): the bits bytes of those 8 dims of row 4g + r at
- *                  r*bits (no QJL) - what one lane reads for the value product.
+ *                  group n (dims 8n..8n+7): a little-endian stream of 32 bits-wide fields,
+ *                  field 4j + r = dim 8n + j of row 4g + r (dimension-major; no QJL) - what
+ *                  one lane reads for the value product, the four rows of a dim side by side.
+ *                  The fields of one chunk belong to four rows: a one-row write sets its own
+ *                  fields with atomic and / or (ABI version 3; version 2 was row-major).
  * The lane-grouped layouts let a decode lane fetch its key data and its value data for a
  * 16-token tile with one load each.
  */

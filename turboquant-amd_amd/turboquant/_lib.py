@@ -18,7 +18,7 @@ import torch
 
 LIB_NAME = "libturboquant_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / "lib" / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 HEAD_DIM = 128
 
 TQ_F32, TQ_F16, TQ_BF16, TQ_I32, TQ_I64 = 0, 1, 2, 3, 4

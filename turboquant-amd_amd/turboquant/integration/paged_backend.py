@@ -271,10 +271,10 @@ class TurboQuantPagedImpl:
 
     def do_kv_cache_update(self, layer, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                            slot_mapping: torch.Tensor) -> None:
-        """Compress key / value [num_tokens, num_kv_heads, head_size] into their slots."""
+        """Compress key / value [num_tokens, num_kv_heads, head_size] into their slots (one
+        launch for both: tq_compress_paged_kv)."""
         k_cache, v_cache = self.state.split_kv_cache(kv_cache)
-        self.state.compress_and_scatter(key, k_cache, slot_mapping, is_value=False)
-        self.state.compress_and_scatter(value, v_cache, slot_mapping, is_value=True)
+        self.state.compress_kv_and_scatter(key, value, k_cache, v_cache, slot_mapping)
 
     def forward(self, layer, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                 attn_metadata: Optional[PagedDecodeMetadata], output: Optional[torch.Tensor] = None,
