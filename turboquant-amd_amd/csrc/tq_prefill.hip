@@ -5,10 +5,10 @@
 // the causal limit of a serving extend step (query i of a sequence of length L with n new
 // tokens sits at position L - n + i and sees keys 0 .. L - n + i).
 //
-// Workgroup (256 threads, 4 waves) = (sequence s, KV head kh, block of 64 rows); a row is one
+// Workgroup (256 threads, 4 waves) = (sequence s, KV head kh, block of 128 rows); a row is one
 // (new token i, query head of the GQA group) pair, rows ordered token-major, so a workgroup
-// serves 64 / G tokens with all G heads of the group and each K/V tile is dequantised once for
-// all of them.  The cache is walked in 16-token tiles (a tile never spans two blocks).  Per
+// serves 128 / G tokens with all G heads of the group and each K/V tile is dequantised once for
+// all of them.  A wave owns two 16-row MFMA tiles: every LDS fragment it reads feeds two MFMAs.  The cache is walked in 16-token tiles (a tile never spans two blocks).  Per
 // tile the 256 threads dequantise into one of two LDS buffers (8 dims of one token per thread,
 // for the keys and for the values; mappings in the kernel) while the waves compute on the other:
 //   Khat [16 tok][128] fp16 = c[idx] * cscale       row stride 272 B (16 B pad: no bank clash)
@@ -17,7 +17,7 @@
 //                                                    40 B, so the 4 dim rows a wave writes at
 //                                                    once start 16 banks apart
 //   kn1, kr2, vn [16] f32 = norm * c1, rnorm * c2, vnorm (c1, c2 below)
-// Each wave computes for its 16 rows (MFMA layout: lane l, n = l % 16, g = l / 16):
+// Each wave computes for each of its two 16-row tiles (MFMA layout: lane l, n = l % 16, g = l / 16):
 //   S^T [16 tok x 16 rows] = Khat . Q^T     4 x mfma_f32_16x16x32_f16 (B: q row n in registers)
 //   T^T = Shat . QP^T                        4 x mfma_f32_16x16x32_f16 (QJL keys)
 //   lane (n, g) holds tokens 4g + r of row n: s = kn1 * S + kr2 * T (log2 units), masked;
@@ -35,7 +35,8 @@ constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kWhtH = 0.08838834764831845f;  // 1 / sqrt(128)
 
-constexpr int kRowsPerWG = 64;
+constexpr int kRT = 2;                           // 16-row MFMA tiles per wave
+constexpr int kRowsPerWG = 64 * kRT;
 constexpr int kKRow = 272;                       // bytes per token row of Khat / Shat
 constexpr int kOffS = 16 * kKRow;                // Shat
 constexpr int kVRow = 40;                        // bytes per dim row of VhatT (16 tokens + pad)
@@ -97,7 +98,7 @@ struct Raw {
 };
 
 template <int KB, bool KQJL, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_kernel(PrefillParams p) {
     extern __shared__ __attribute__((aligned(16))) uint8_t s_lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -128,13 +129,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             tv[tid] = tq_pack_half2(p.v_cent[tid & ((1 << VB) - 1)] * p.v_cs, p.v_cent[tid >> VB] * p.v_cs);
     }
 
-    // ---- this lane's row: (token i, head gh) ----
-    const int R = rb * kRowsPerWG + wave * 16 + n;
-    const int i = R / G;
-    const int gh = R - i * G;
-    const bool rvalid = i < nq;
-    const int head = kh * G + gh;
-    const int qpos = p.causal ? L - nq + i : L - 1;  // last key position the row sees
+    // ---- this lane's rows: (token i, head gh) of MFMA tile rt, rows 32 wave + 16 rt + n ----
+    int iR[kRT], headR[kRT], qposR[kRT];
+    bool rvalid[kRT];
+#pragma unroll
+    for (int rt = 0; rt < kRT; ++rt) {
+        const int R = rb * kRowsPerWG + wave * 16 * kRT + 16 * rt + n;
+        const int i = R / G;
+        const int gh = R - i * G;
+        iR[rt] = i;
+        rvalid[rt] = i < nq;
+        headR[rt] = kh * G + gh;
+        qposR[rt] = p.causal ? L - nq + i : L - 1;  // last key position the row sees
+    }
     // last key position any row of the workgroup sees (rows are token-major)
     int imax = (rb * kRowsPerWG + kRowsPerWG - 1) / G;
     imax = imax < nq - 1 ? imax : nq - 1;
@@ -143,18 +150,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     t_end = t_end > 0 ? t_end : 0;
     const int ntiles = (t_end + 15) >> 4;
 
-    // ---- query operands (B of the score products): dims 32cc + 8g + j of row n ----
-    tq_half8 qop[4], qpop[4];
-    {
+    // ---- query operands (B of the score products): dims 32cc + 8g + j of row n of tile rt ----
+    tq_half8 qop[kRT][4], qpop[kRT][4];
+#pragma unroll
+    for (int rt = 0; rt < kRT; ++rt) {
+        const int i = iR[rt], head = headR[rt];
+        const bool rv = rvalid[rt];
         float x[32];
-        const int64_t off = (int64_t)(q0 + (rvalid ? i : 0)) * p.q_st + (int64_t)head * p.q_sh + 8 * g;
+        const int64_t off = (int64_t)(q0 + (rv ? i : 0)) * p.q_st + (int64_t)head * p.q_sh + 8 * g;
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
-            if (rvalid && p.q_vec) {
+            if (rv && p.q_vec) {
                 tq_load8(p.q, off + 32 * cc, p.q_dtype, &x[8 * cc]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[8 * cc + j] = rvalid ? tq_load1(p.q, off + 32 * cc + j, p.q_dtype) : 0.f;
+                for (int j = 0; j < 8; ++j) x[8 * cc + j] = rv ? tq_load1(p.q, off + 32 * cc + j, p.q_dtype) : 0.f;
             }
         }
         // x[8cc + j] is element 32cc + 8g + j: register bits = element bits 0-2 and 5-6
@@ -162,27 +172,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) qop[cc][j] = (_Float16)x[8 * cc + j];
+            for (int j = 0; j < 8; ++j) qop[rt][cc][j] = (_Float16)x[8 * cc + j];
         if (KQJL) {
-            const int64_t offp = (int64_t)(q0 + (rvalid ? i : 0)) * p.qp_st + (int64_t)head * p.qp_sh + 8 * g;
+            const int64_t offp = (int64_t)(q0 + (rv ? i : 0)) * p.qp_st + (int64_t)head * p.qp_sh + 8 * g;
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
-                if (rvalid && p.q_vec) {
+                if (rv && p.q_vec) {
                     tq_load8(p.qp, offp + 32 * cc, p.q_dtype, &x[8 * cc]);
                 } else {
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        x[8 * cc + j] = rvalid ? tq_load1(p.qp, offp + 32 * cc + j, p.q_dtype) : 0.f;
+                        x[8 * cc + j] = rv ? tq_load1(p.qp, offp + 32 * cc + j, p.q_dtype) : 0.f;
                 }
             }
             if (p.rot_qp) tq_wht_row_g4(x, kWhtH);
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) qpop[cc][j] = (_Float16)x[8 * cc + j];
+                for (int j = 0; j < 8; ++j) qpop[rt][cc][j] = (_Float16)x[8 * cc + j];
         } else {
 #pragma unroll
-            for (int cc = 0; cc < 4; ++cc) qpop[cc] = tq_half8{};
+            for (int cc = 0; cc < 4; ++cc) qpop[rt][cc] = tq_half8{};
         }
     }
 
@@ -337,33 +347,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     if (ntiles > 1) load_raw(1, rawB);
     __syncthreads();
 
-    float m = kNegInf, lsum = 0.f;
-    tq_floatx4 acc[8];
+    float m[kRT], lsum[kRT];
+    tq_floatx4 acc[kRT][8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < kRT; ++rt) {
+        m[rt] = kNegInf;
+        lsum[rt] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[rt][j] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+    }
 
     // One tile: ld holds tile ti's raw data (already in LDS) and receives tile ti + 2's; nx holds
-    // tile ti + 1's, dequantised into the other buffer at the end.
+    // tile ti + 1's, dequantised into the other buffer at the end.  Every LDS fragment feeds the
+    // MFMAs of both row tiles.
     auto step = [&](int ti, Raw& ld, const Raw& nx) {
         const int buf = ti & 1;
         const int nv = ld.nv;  // tile ti
         if (ti + 2 < ntiles) load_raw(ti + 2, ld);
         const uint8_t* b = s_lds + buf * kBuf;
         // scores^T: tokens 4g + r of row n
-        tq_floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+        tq_floatx4 sc[kRT], tj[kRT];
+#pragma unroll
+        for (int rt = 0; rt < kRT; ++rt) {
+            sc[rt] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+            tj[rt] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             const tq_half8 a = *reinterpret_cast<const tq_half8*>(
                 b + n * kKRow + 2 * (32 * cc + 8 * g));
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[cc], sc, 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < kRT; ++rt)
+                sc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[rt][cc], sc[rt], 0, 0, 0);
         }
-        tq_floatx4 tj = {0.f, 0.f, 0.f, 0.f};
         if (KQJL) {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
                 const tq_half8 a = *reinterpret_cast<const tq_half8*>(
                     b + kOffS + n * kKRow + 2 * (32 * cc + 8 * g));
-                tj = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qpop[cc], tj, 0, 0, 0);
+#pragma unroll
+                for (int rt = 0; rt < kRT; ++rt)
+                    tj[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qpop[rt][cc], tj[rt], 0, 0, 0);
             }
         }
         const tq_floatx4 kn1 = *reinterpret_cast<const tq_floatx4*>(b + kOffN + 16 * g);
@@ -371,38 +395,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
             *reinterpret_cast<const tq_floatx4*>(b + kOffN + 64 + 16 * g);
         const tq_floatx4 vn =
             *reinterpret_cast<const tq_floatx4*>(b + kOffN + 128 + 16 * g);
-        // tokens 4g + r below lim are usable and visible to the row (lim: one compare per token)
-        int lim = qpos - ti * 16 + 1 - 4 * g;
-        lim = lim < nv - 4 * g ? lim : nv - 4 * g;
-        float sv[4];
+        tq_half4v bop[kRT];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float v = __builtin_fmaf(kn1[r], sc[r], kr2[r] * tj[r]);
-            sv[r] = r < lim ? v : kNegInf;
+        for (int rt = 0; rt < kRT; ++rt) {
+            // tokens 4g + r below lim are usable and visible to the row (lim: one compare per token)
+            int lim = qposR[rt] - ti * 16 + 1 - 4 * g;
+            lim = lim < nv - 4 * g ? lim : nv - 4 * g;
+            float sv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float v = __builtin_fmaf(kn1[r], sc[rt][r], kr2[r] * tj[rt][r]);
+                sv[r] = r < lim ? v : kNegInf;
+            }
+            float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            mt = max_over_groups(mt);
+            const float m_new = fmaxf(m[rt], mt);
+            if (__builtin_amdgcn_ballot_w64(m_new > m[rt])) {
+                const float alpha = m_new > m[rt] ? __builtin_amdgcn_exp2f(m[rt] - m_new) : 1.f;  // 0 while m = -inf
+                lsum[rt] *= alpha;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[rt][j] *= alpha;
+            }
+            m[rt] = m_new;
+            const float nb = m_new == kNegInf ? 0.f : -m_new;
+            float pr[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(sv[r] + nb);  // 0 for masked tokens
+            lsum[rt] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bop[rt][r] = (_Float16)(pr[r] * vn[r]);
         }
-        float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-        mt = max_over_groups(mt);
-        const float m_new = fmaxf(m, mt);
-        if (__builtin_amdgcn_ballot_w64(m_new > m)) {
-            const float alpha = m_new > m ? __builtin_amdgcn_exp2f(m - m_new) : 1.f;  // 0 while m = -inf
-            lsum *= alpha;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] *= alpha;
-        }
-        m = m_new;
-        const float nb = m_new == kNegInf ? 0.f : -m_new;
-        float pr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(sv[r] + nb);  // 0 for masked tokens
-        lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-        tq_half4v bop;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) bop[r] = (_Float16)(pr[r] * vn[r]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const tq_half4v a = *reinterpret_cast<const tq_half4v*>(
                 b + kOffV + (16 * j + n) * kVRow + 8 * g);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, acc[j], 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < kRT; ++rt)
+                acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop[rt], acc[rt][j], 0, 0, 0);
         }
         if (ti + 1 < ntiles) store_tile(ti + 1, nx, buf ^ 1);
         __syncthreads();
@@ -414,21 +443,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3, 3))) voi
     }
 
     // ---- normalise, rotate, write ----
-    const float l = sum_over_groups(lsum);
-    const float inv = l > 0.f ? p.v_cinv / l : 0.f;
-    float o[32];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[4 * j + r] = acc[j][r] * inv;
-    // o[4j + r] is dim 16j + 4g + r: register bits = dim bits 0-1 and 4-6
-    if (p.rot_out) tq_wht_row_g4(o, kWhtH);
-    if (rvalid) {
-        const int64_t ob = (int64_t)(q0 + i) * p.out_st + (int64_t)head * p.out_sh + 4 * g;
+    for (int rt = 0; rt < kRT; ++rt) {
+        const float l = sum_over_groups(lsum[rt]);
+        const float inv = l > 0.f ? p.v_cinv / l : 0.f;
+        float o[32];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) tq_store1(p.out, ob + 16 * j + r, p.out_dtype, o[4 * j + r]);
+            for (int r = 0; r < 4; ++r) o[4 * j + r] = acc[rt][j][r] * inv;
+        // o[4j + r] is dim 16j + 4g + r: register bits = dim bits 0-1 and 4-6
+        if (p.rot_out) tq_wht_row_g4(o, kWhtH);
+        if (rvalid[rt]) {
+            const int64_t ob = (int64_t)(q0 + iR[rt]) * p.out_st + (int64_t)headR[rt] * p.out_sh + 4 * g;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tq_store1(p.out, ob + 16 * j + r, p.out_dtype, o[4 * j + r]);
+        }
     }
 }
 
