@@ -778,8 +778,8 @@ struct ReduceParams {
 // Split-K merge, one wave per (sequence, query head):
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:128-140)
 // The chunk maxima and denominators are read one lane per chunk and reduced across the wave;
-// the rows acc_c are summed in chunk order with lane d covering dims 2d, 2d+1, eight rows in
-// flight at a time.  Sequences of one chunk were written by the decode kernel (unless the output
+// the rows acc_c are summed in chunk order with lane d covering dims 2d, 2d+1, sixteen chunks
+// (rows, maxima, denominators) requested together.  Sequences of one chunk were written by the decode kernel (unless the output
 // is rotated: then every sequence is written here); empty ones are written as zero here.
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -803,40 +803,35 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
     if (nch == 1 && !p.rot_out) return;
     const int64_t base = sh * p.n_chunks;
-    float M = kNegInf;
-    for (int c0 = 0; c0 < nch; c0 += 64) {
-        const int c = c0 + lane;
-        M = fmaxf(M, c < nch ? p.ws_m[base + c] : kNegInf);
-    }
-    M = wave_max(M);
-    float den = 0.f, a0 = 0.f, a1 = 0.f;
-    if (M != kNegInf) {
-        for (int c0 = 0; c0 < nch; c0 += 64) {
-            const int c = c0 + lane;
-            const float w = c < nch ? __builtin_amdgcn_exp2f(p.ws_m[base + c] - M) : 0.f;
-            if (c < nch) den = __builtin_fmaf(w, p.ws_l[base + c], den);
-            const int nb = nch - c0 < 64 ? nch - c0 : 64;
-            const float2* rows = reinterpret_cast<const float2*>(p.ws_acc + (base + c0) * TQ_HEAD_DIM) + lane;
-            int k = 0;
-            for (; k + 8 <= nb; k += 8) {
-                float2 v[8];
+    // Batches of 16 chunks: the batch's rows, maxima and denominators are all requested before
+    // any of them is used (the rows do not depend on the maxima), so a batch costs one load
+    // round.  Per batch the running max M rescales what was summed so far.
+    float M = kNegInf, den = 0.f, a0 = 0.f, a1 = 0.f;
+    const float2* rows = reinterpret_cast<const float2*>(p.ws_acc + base * TQ_HEAD_DIM) + lane;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+        const int nb = nch - c0 < 16 ? nch - c0 : 16;
+        const bool mine = lane < nb;
+        const float mc = mine ? p.ws_m[base + c0 + lane] : kNegInf;
+        const float lc = mine ? p.ws_l[base + c0 + lane] : 0.f;
+        float2 v[16];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = rows[(int64_t)(k + j) * (TQ_HEAD_DIM / 2)];
+        for (int j = 0; j < 16; ++j) v[j] = j < nb ? rows[(int64_t)(c0 + j) * (TQ_HEAD_DIM / 2)] : make_float2(0.f, 0.f);
+        const float Mb = wave_max(mc);
+        const float Mn = fmaxf(M, Mb);
+        if (Mn == kNegInf) continue;  // every chunk so far empty
+        const float alpha = M == kNegInf ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+        den *= alpha;
+        a0 *= alpha;
+        a1 *= alpha;
+        M = Mn;
+        const float w = mine ? __builtin_amdgcn_exp2f(mc - M) : 0.f;
+        den += wave_sum(w * lc);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k + j));
-                    a0 = __builtin_fmaf(wj, v[j].x, a0);
-                    a1 = __builtin_fmaf(wj, v[j].y, a1);
-                }
-            }
-            for (; k < nb; ++k) {
-                const float2 v = rows[(int64_t)k * (TQ_HEAD_DIM / 2)];
-                const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), k));
-                a0 = __builtin_fmaf(wk, v.x, a0);
-                a1 = __builtin_fmaf(wk, v.y, a1);
-            }
+        for (int j = 0; j < 16; ++j) {
+            const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+            a0 = __builtin_fmaf(wj, v[j].x, a0);
+            a1 = __builtin_fmaf(wj, v[j].y, a1);
         }
-        den = wave_sum(den);
     }
     float inv = den > 0.f ? 1.0f / den : 0.f;
     if (p.rot_out) {
