@@ -228,6 +228,25 @@ typedef struct tq_kv_view {
 } tq_kv_view;
 
 /*
+ * Paged compression into caller-described row-major regions (dst->layout = TQ_TILE_ROWS): the
+ * same math and decisions as tq_compress_paged, with token t / head h written at
+ *   region R: R.ptr + block * R.stride_block + h * R.stride_head + row * R.stride_row
+ * (block = slot / block_size, row = slot % block_size): 16*bits index bytes (idx), 16 sign bytes
+ * and an fp16 residual norm (signs, rnorm: dst->qjl only), the fp16 norm (norm).  All regions
+ * share stride_block and stride_head; rnorm shares norm's stride_row; pointers and strides
+ * 2-byte aligned (4-byte aligned index / sign rows are written with 32-bit stores).  Codebook:
+ * dst->centroids and boundaries (2^bits and 2^bits - 1 fp32).  For the reference's
+ * array-of-slots cache [num_blocks, 2, block_size, Hkv, slot] (kernels/sparse_v.py:293-304;
+ * per token: index bytes, sign bytes, fp16 norm, fp16 residual norm, padding) this is the
+ * scatter of integration/vllm_backend.py:223-230 into that cache, in place.
+ */
+int tq_compress_regions(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_stride_head,
+                        int64_t num_tokens, int num_heads, int head_dim,
+                        const void* slot_mapping, int slot_dtype, const tq_kv_view* dst,
+                        const float* boundaries, int64_t num_blocks, int block_size,
+                        int rotate, float wht_scale, tq_stream_t stream);
+
+/*
  * Packed asymmetric split-K decode attention (one query token per sequence), GQA-shared KV.
  * For sequence s, query head h, KV head kh = h / (num_q_heads/num_kv_heads), token t < seq_lens[s]:
  *   score = sm_scale * ( q.(k_cb[idx_t] * norm_t) + corr_scale * rnorm_t * (qp.sign_t) )

@@ -501,6 +501,93 @@ def test_compress_paged_kv_rejections(dev):
         compress_paged_kv(k, k, slots, kc, vc, kf, vf, cb, tuple(t.to(dev) for t in _codebook(2)))
 
 
+@pytest.mark.parametrize("bits,qjl,slot_bytes", [
+    (3, False, 50),    # the reference's 3-bit slot: 48 index bytes + fp16 norm (2-byte stores)
+    (3, False, 64),    # padded slot: 4-byte aligned rows
+    (3, True, 68),     # indices, signs, norm, residual norm
+    (2, True, 54),     # signs at an offset that is only 2-byte aligned
+    (4, False, 66),
+])
+@pytest.mark.parametrize("kv_view", [False, True])
+def test_compress_paged_slots_matches_tiles(dev, bits, qjl, slot_bytes, kv_view):
+    """compress_paged_slots writes into an array-of-slots cache [NB, BS, Hkv, slot] (or the K / V
+    half of a [NB, 2, BS, Hkv, slot] cache) exactly the bytes to_reference_slots reads out of a
+    compress_paged tile cache for every written token; padding bytes, unwritten slots and the
+    other half of the cache keep what they held.  A second, shorter call follows."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged, compress_paged_slots, \
+        to_reference_slots
+    T, H, bs, nb = 203, 3, 16, 20
+    g = torch.Generator().manual_seed(40 + bits + slot_bytes)
+    x = torch.randn(T, H, 128, generator=g).to(torch.bfloat16).to(dev)
+    perm = torch.randperm(nb * bs, generator=g)[:T].to(torch.int64)
+    perm[5] = -1
+    perm[6] = nb * bs + 3
+    fmt = PagedKVFormat(bits=bits, qjl=qjl, block_size=bs, layout="keys" if qjl else "values")
+    tb = fmt.token_bytes
+    cb = tuple(t.to(dev) for t in _codebook(bits))
+    tiles = allocate_cache(nb, H, fmt, device=dev)
+    if kv_view:
+        full = torch.randint(0, 256, (nb, 2, bs, H, slot_bytes), dtype=torch.uint8, generator=g).to(dev)
+        slots = full[:, 1]
+    else:
+        full = torch.randint(0, 256, (nb, bs, H, slot_bytes), dtype=torch.uint8, generator=g).to(dev)
+        slots = full
+    pre = full.clone()
+    for n in (T, 57):
+        s = perm[:n].to(dev)
+        compress_paged(x[:n], s, tiles, fmt, *cb)
+        compress_paged_slots(x[:n], s, slots, fmt, *cb)
+        torch.cuda.synchronize()
+        want = to_reference_slots(tiles, fmt, slot_bytes).cpu()
+        got = slots.cpu()
+        written = torch.zeros(nb * bs, dtype=torch.bool)
+        ok = perm[:T]
+        written[ok[(ok >= 0) & (ok < nb * bs)]] = True
+        written = written.reshape(nb, bs)
+        assert torch.equal(got[written][..., :tb], want[written][..., :tb]), f"payload differs after {n} tokens"
+        pre_s = (pre[:, 1] if kv_view else pre).cpu()
+        assert torch.equal(got[..., tb:], pre_s[..., tb:]), "padding bytes changed"
+        assert torch.equal(got[~written], pre_s[~written]), "unwritten slots changed"
+        if kv_view:
+            assert torch.equal(full[:, 0].cpu(), pre[:, 0].cpu()), "the other half of the cache changed"
+        x = x.flip(0).contiguous()
+
+
+def test_compress_to_tq_cache_then_decode(dev):
+    """The reference's 3-bit [NB, 2, BS, Hkv, 128] slot cache filled by compress_to_tq_cache (K
+    and V, one launch each) decodes with tq_v11 to what the tile-layout decode gives for the
+    same tokens compressed into tiles (two kernels, two layouts, one answer)."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged, decode_paged
+    from turboquant.kernels.sparse_v import compress_to_tq_cache, tq_v11
+    Hkv, G, bs, S, L = 4, 6, 32, 2, 300
+    Hq = Hkv * G
+    nblk = math.ceil(L / bs)
+    nb = S * nblk + 3
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(S * L, Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(S * L, Hkv, 128, generator=g).to(torch.bfloat16).to(dev)
+    bt = torch.randperm(nb, generator=g)[: S * nblk].reshape(S, nblk).to(torch.int32)
+    tok = torch.arange(L)
+    slot = torch.cat([bt[s, tok // bs].to(torch.int64) * bs + tok % bs for s in range(S)]).to(dev)
+    cent, bnd = (t.to(dev) for t in _codebook(3))
+    cache = torch.zeros((nb, 2, bs, Hkv, 128), dtype=torch.uint8, device=dev)
+    compress_to_tq_cache(k, slot, cache, 0, cent, bnd)
+    compress_to_tq_cache(v, slot, cache, 1, cent, bnd)
+    kf = PagedKVFormat(bits=3, qjl=False, block_size=bs, layout="keys")
+    vf = PagedKVFormat(bits=3, qjl=False, block_size=bs, layout="values")
+    kc, vc = allocate_cache(nb, Hkv, kf, device=dev), allocate_cache(nb, Hkv, vf, device=dev)
+    compress_paged(k, slot, kc, kf, cent, bnd)
+    compress_paged(v, slot, vc, vf, cent, bnd)
+    q = torch.randn(S, Hq, 128, generator=g).to(torch.float16).to(dev)
+    lens = torch.full((S,), L, dtype=torch.int32, device=dev)
+    sm = 1 / math.sqrt(128)
+    out_aos = torch.empty_like(q)
+    tq_v11(out_aos, q, cache, cent, bt.to(dev), lens, sm)
+    out_tiles = decode_paged(q, kc, kf, cent, vc, vf, cent, bt.to(dev), lens, sm)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_aos.float(), out_tiles.float(), rtol=1e-2, atol=1e-3)
+
+
 @pytest.mark.parametrize("bits,qjl", [(2, False), (2, True), (3, False), (3, True), (4, False), (4, True)])
 @pytest.mark.parametrize("block_size", [16, 32])
 @pytest.mark.parametrize("layout", ["keys", "values", "rows"])

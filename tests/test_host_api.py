@@ -315,6 +315,31 @@ def test_host_side_argument_rejection():
     assert kvc(ctypes.byref(tk), ctypes.byref(tk), 24) == -8
     assert L.tq_compress_paged_kv(ctypes.byref(tk), ctypes.byref(tk), 2, 0, 8, 128, fake, 3, 10, 16, 1, 0.1,
                                   None) == 0   # no tokens: nothing to launch
+    # compress into caller-described row-major regions (array-of-slots caches): 50-byte slots,
+    # 4 heads, block 16, 3-bit MSE-only
+    rv = _lib.TQKVView()
+    rv.idx = _lib.TQRegion(0x1000, 16 * 4 * 50, 50, 0, 4 * 50)
+    rv.norm = _lib.TQRegion(0x1000 + 48, 16 * 4 * 50, 50, 0, 4 * 50)
+    rv.centroids, rv.bits, rv.qjl, rv.layout = fake, 3, 0, 0
+    reg = lambda v, n=10: L.tq_compress_regions(fake, 2, 512, 128, n, 4, 128, fake, 3,  # noqa: E731
+                                                 None if v is None else ctypes.byref(v), fake, 10, 16, 1, 0.1, None)
+    assert reg(None) == -1                    # no view
+    rv.layout = 1
+    assert reg(rv) == -1                      # only the row-major layout
+    rv.layout = 0
+    rv.norm.stride_head = 52
+    assert reg(rv) == -1                      # regions of one slot share the block and head strides
+    rv.norm.stride_head = 50
+    rv.norm.ptr = 0x1000 + 49
+    assert reg(rv) == -4                      # fp16 norms need 2-byte alignment
+    rv.norm.ptr = 0x1000 + 48
+    rv.qjl = 1
+    assert reg(rv) == -1                      # QJL needs sign and residual-norm regions
+    rv.qjl = 0
+    rv.bits = 5
+    assert reg(rv) == -3
+    rv.bits = 3
+    assert reg(rv, 0) == 0                    # no tokens: nothing to launch
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -35,7 +35,9 @@ struct CompressParams {
     int idx32;  // rows and slots below 2^31: 32-bit index arithmetic
     tq_udiv tok_div, blk_div;  // by tok_rows and block_size (32-bit index arithmetic)
     int tile_layout;  // TQ_TILE_ROWS / TQ_TILE_KEYS / TQ_TILE_VALUES
-    int64_t off_signs, off_norm, off_rnorm;
+    int64_t off_signs, off_norm, off_rnorm;  // region offsets from the tile (or idx region) base
+    int64_t rs_idx, rs_sig, rs_norm;          // row strides of the index, sign and norm regions
+    int narrow;                               // index / sign rows only 2-byte aligned: 16-bit stores
     // unpacked output
     int64_t* indices;
     float* norms;
@@ -474,7 +476,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                 if (BITS >= 2) store_values<BITS < 2 ? 2 : BITS>(value_slices<BITS < 2 ? 2 : BITS>(idx), write, slot, tile,
                                                                   r_in_blk, q, s_xchg);
                 if (write && q == 0)
-                    reinterpret_cast<uint16_t*>(tile + p.off_norm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(norm);
+                    *reinterpret_cast<uint16_t*>(tile + p.off_norm + r_in_blk * p.rs_norm) = (uint16_t)tq_f32_to_f16_bits(norm);
                 continue;
             }
             // this lane's 32 indices: 4 * BITS bytes of the row's little-endian bit stream
@@ -497,15 +499,32 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                     for (int j = 0; j < BITS; ++j) ch[j] = w[j];
                     if (QJL) ch[BITS] = sbits;
                 } else {
-                    uint32_t* irow = reinterpret_cast<uint32_t*>(tile + r_in_blk * (16 * BITS) + 4 * BITS * q);
+                    // row-major regions (this library's rows layout, or caller-described regions
+                    // such as the reference's array-of-slots cache)
+                    uint8_t* ip = tile + r_in_blk * p.rs_idx + 4 * BITS * q;
+                    uint8_t* sp = tile + p.off_signs + r_in_blk * p.rs_sig + 4 * q;
+                    if (!p.narrow) {
 #pragma unroll
-                    for (int j = 0; j < BITS; ++j) irow[j] = w[j];
-                    if (QJL) *reinterpret_cast<uint32_t*>(tile + p.off_signs + r_in_blk * 16 + 4 * q) = sbits;
+                        for (int j = 0; j < BITS; ++j) reinterpret_cast<uint32_t*>(ip)[j] = w[j];
+                        if (QJL) *reinterpret_cast<uint32_t*>(sp) = sbits;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < BITS; ++j) {
+                            reinterpret_cast<uint16_t*>(ip)[2 * j] = (uint16_t)w[j];
+                            reinterpret_cast<uint16_t*>(ip)[2 * j + 1] = (uint16_t)(w[j] >> 16);
+                        }
+                        if (QJL) {
+                            reinterpret_cast<uint16_t*>(sp)[0] = (uint16_t)sbits;
+                            reinterpret_cast<uint16_t*>(sp)[1] = (uint16_t)(sbits >> 16);
+                        }
+                    }
                 }
                 if (q == 0) {
-                    reinterpret_cast<uint16_t*>(tile + p.off_norm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(norm);
+                    *reinterpret_cast<uint16_t*>(tile + p.off_norm + r_in_blk * p.rs_norm) =
+                        (uint16_t)tq_f32_to_f16_bits(norm);
                     if (QJL)
-                        reinterpret_cast<uint16_t*>(tile + p.off_rnorm)[r_in_blk] = (uint16_t)tq_f32_to_f16_bits(rn);
+                        *reinterpret_cast<uint16_t*>(tile + p.off_rnorm + r_in_blk * p.rs_norm) =
+                            (uint16_t)tq_f32_to_f16_bits(rn);
                 }
             }
         }
@@ -627,7 +646,7 @@ int paged_params(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_s
                  int num_heads, int head_dim, const void* slot_mapping, int slot_dtype, void* cache,
                  int64_t cache_stride_block, int64_t cache_stride_head, int64_t num_blocks, int block_size, int bits,
                  int use_qjl, int tile_layout, int rotate, float wht_scale, const float* centroids,
-                 const float* boundaries, CompressParams* out, bool* empty) {
+                 const float* boundaries, CompressParams* out, bool* empty, const tq_kv_view* regions = nullptr) {
     *empty = false;
     if (head_dim != TQ_HEAD_DIM) return TQ_ERR_HEAD_DIM;
     if (bits < 2 || bits > 4) return TQ_ERR_BITS;
@@ -646,8 +665,10 @@ int paged_params(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_s
     if (rc) return rc;
     if (x_stride_token % 8 || x_stride_head % 8) return TQ_ERR_ALIGNMENT;
     const tq_tile_geom g = tq_make_tile_geom(block_size, bits, use_qjl);
-    if (!aligned(cache, 16) || cache_stride_block % 16 || cache_stride_head % 16) return TQ_ERR_ALIGNMENT;
-    if (cache_stride_head < g.bytes && num_heads > 1) return TQ_ERR_INVALID_ARGUMENT;
+    if (!regions) {
+        if (!aligned(cache, 16) || cache_stride_block % 16 || cache_stride_head % 16) return TQ_ERR_ALIGNMENT;
+        if (cache_stride_head < g.bytes && num_heads > 1) return TQ_ERR_INVALID_ARGUMENT;
+    }
     CompressParams p = {};
     p.x = x;
     p.x_dtype = x_dtype;
@@ -672,6 +693,30 @@ int paged_params(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_s
     p.off_signs = g.off_signs;
     p.off_norm = g.off_norm;
     p.off_rnorm = g.off_rnorm;
+    p.rs_idx = 16 * bits;
+    p.rs_sig = 16;
+    p.rs_norm = 2;
+    p.narrow = 0;
+    if (regions) {
+        // caller-described row-major regions sharing one (block, head) base: offsets from the
+        // index region, per-region row strides
+        const tq_region& ri = regions->idx;
+        const uint8_t* b0 = static_cast<const uint8_t*>(ri.ptr);
+        auto off = [&](const tq_region& r) { return static_cast<int64_t>(static_cast<const uint8_t*>(r.ptr) - b0); };
+        p.off_norm = off(regions->norm);
+        p.rs_idx = ri.stride_row;
+        p.rs_norm = regions->norm.stride_row;
+        if (use_qjl) {
+            p.off_signs = off(regions->signs);
+            p.off_rnorm = off(regions->rnorm);
+            p.rs_sig = regions->signs.stride_row;
+        } else {
+            p.off_signs = p.off_rnorm = 0;
+        }
+        const bool four = aligned(ri.ptr, 4) && ri.stride_block % 4 == 0 && ri.stride_head % 4 == 0 &&
+                          ri.stride_row % 4 == 0 && (!use_qjl || (p.off_signs % 4 == 0 && p.rs_sig % 4 == 0));
+        p.narrow = four ? 0 : 1;
+    }
     // rows, slots and x element offsets all below 2^31
     p.idx32 = (p.n_rows < (1ll << 31) && num_blocks * (int64_t)block_size < (1ll << 31) &&
                num_tokens * x_stride_token + (int64_t)num_heads * x_stride_head < (1ll << 31))
@@ -712,6 +757,37 @@ extern "C" int tq_compress_paged(const void* x, int x_dtype, int64_t x_stride_to
                                 use_qjl, tile_layout, rotate, wht_scale, centroids, boundaries, &p, &empty);
     if (rc || empty) return rc;
     return launch_compress<MODE_PAGED>(p, bits, use_qjl, (hipStream_t)stream);
+}
+
+extern "C" int tq_compress_regions(const void* x, int x_dtype, int64_t x_stride_token, int64_t x_stride_head,
+                                   int64_t num_tokens, int num_heads, int head_dim, const void* slot_mapping,
+                                   int slot_dtype, const tq_kv_view* dst, const float* boundaries,
+                                   int64_t num_blocks, int block_size, int rotate, float wht_scale,
+                                   tq_stream_t stream) {
+    if (!dst || dst->layout != TQ_TILE_ROWS || dst->signs_permuted) return TQ_ERR_INVALID_ARGUMENT;
+    const int qjl = dst->qjl ? 1 : 0;
+    const tq_region& ri = dst->idx;
+    auto same_base = [&](const tq_region& r) {
+        return r.stride_block == ri.stride_block && r.stride_head == ri.stride_head;
+    };
+    auto two = [](const tq_region& r) {
+        return aligned(r.ptr, 2) && r.stride_block % 2 == 0 && r.stride_head % 2 == 0 && r.stride_row % 2 == 0;
+    };
+    if (num_tokens > 0 && num_blocks > 0) {
+        if (!ri.ptr || !dst->norm.ptr || (qjl && (!dst->signs.ptr || !dst->rnorm.ptr))) return TQ_ERR_INVALID_ARGUMENT;
+        if (!same_base(dst->norm) || (qjl && (!same_base(dst->signs) || !same_base(dst->rnorm))))
+            return TQ_ERR_INVALID_ARGUMENT;
+        if (qjl && dst->rnorm.stride_row != dst->norm.stride_row) return TQ_ERR_INVALID_ARGUMENT;
+        if (!two(ri) || !two(dst->norm) || (qjl && (!two(dst->signs) || !two(dst->rnorm)))) return TQ_ERR_ALIGNMENT;
+    }
+    CompressParams p;
+    bool empty;
+    const int rc = paged_params(x, x_dtype, x_stride_token, x_stride_head, num_tokens, num_heads, head_dim, slot_mapping,
+                                slot_dtype, const_cast<void*>(ri.ptr), ri.stride_block, ri.stride_head, num_blocks,
+                                block_size, dst->bits, qjl, TQ_TILE_ROWS, rotate, wht_scale, dst->centroids, boundaries,
+                                &p, &empty, dst);
+    if (rc || empty) return rc;
+    return launch_compress<MODE_PAGED>(p, dst->bits, qjl, (hipStream_t)stream);
 }
 
 extern "C" int tq_compress_paged_kv(const tq_paged_target* k, const tq_paged_target* v, int x_dtype,

@@ -105,6 +105,11 @@ SIGNATURES = {
         [ctypes.POINTER(TQPagedTarget), ctypes.POINTER(TQPagedTarget), _i32, _i64, _i32, _i32, _vp, _i32, _i64, _i32,
          _i32, _f32, _vp],
     ),
+    "tq_compress_regions": (
+        _i32,
+        [_vp, _i32, _i64, _i64, _i64, _i32, _i32, _vp, _i32, ctypes.POINTER(TQKVView), _vp, _i64, _i32, _i32, _f32,
+         _vp],
+    ),
     "tq_tile_bytes": (_i64, [_i32, _i32, _i32]),
     "tq_tile_offsets": (
         _i32,

@@ -725,6 +725,53 @@ def to_reference_slots(cache: torch.Tensor, fmt: PagedKVFormat, slot_bytes: Opti
     return out
 
 
+def compress_paged_slots(x: torch.Tensor, slot_mapping: torch.Tensor, slots: torch.Tensor, fmt: PagedKVFormat,
+                         centroids: torch.Tensor, boundaries: torch.Tensor, rotate: bool = True) -> torch.Tensor:
+    """compress_paged straight into an array-of-slots cache view slots [num_blocks, block_size,
+    Hkv, slot_bytes] uint8 (the reference's per-token slot: index bytes, [sign bytes], fp16 norm,
+    [fp16 residual norm], padding; kernels/sparse_v.py:293-304), token t at
+    slots[slot_mapping[t] // block_size, slot_mapping[t] % block_size].  The view may be strided
+    (e.g. tq_cache[:, 0] of a [num_blocks, 2, block_size, Hkv, slot] cache); fmt gives bits and
+    QJL (its tile layout is not used).  One tq_compress_regions launch."""
+    dev = _lib.require_gpu("compress_paged_slots", x, slot_mapping, slots, centroids, boundaries)
+    if slots.dtype != torch.uint8 or slots.dim() != 4 or slots.stride(3) != 1:
+        raise ValueError("slots must be uint8 [num_blocks, block_size, Hkv, slot_bytes] with contiguous slots")
+    nb, bs, h, sb = slots.shape
+    if sb < fmt.token_bytes:
+        raise ValueError(f"slots of {sb} bytes cannot hold {fmt.token_bytes} bytes per token")
+    if x.dim() != 3 or x.shape[2] != fmt.head_dim or x.shape[1] != h:
+        raise ValueError(f"x must be [T, {h}, {fmt.head_dim}], got {tuple(x.shape)}")
+    T = x.shape[0]
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != T:
+        raise ValueError("slot_mapping must be [T]")
+    if slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise TypeError("slot_mapping must be int32 or int64")
+    cent = centroids.to(device=dev, dtype=torch.float32).contiguous()
+    bnd = boundaries.to(device=dev, dtype=torch.float32).contiguous()
+    if cent.numel() != 2 ** fmt.bits or bnd.numel() != 2 ** fmt.bits - 1:
+        raise ValueError(f"need {2 ** fmt.bits} centroids and {2 ** fmt.bits - 1} boundaries for bits={fmt.bits}")
+    if x.stride(2) != 1 or x.stride(0) % 8 or x.stride(1) % 8 or x.data_ptr() % 32:
+        x = x.contiguous()
+    slot_mapping = slot_mapping.contiguous()
+    base = slots.data_ptr()
+    s_blk, s_row, s_head = slots.stride(0), slots.stride(1), slots.stride(2)
+    view = _lib.TQKVView()
+    view.layout = _LAYOUTS["rows"]
+    pos = 0
+    for name, _, width in _tile_fields(fmt):
+        setattr(view, name, _region(base + pos, s_blk, s_head, s_row))
+        pos += width
+    view.centroids = cent.data_ptr()
+    view.bits, view.qjl, view.signs_permuted = fmt.bits, int(fmt.qjl), 0
+    rc = _lib.lib().tq_compress_regions(
+        x.data_ptr(), _lib.dtype_code(x), x.stride(0), x.stride(1), T, h, fmt.head_dim,
+        slot_mapping.data_ptr(), _lib.dtype_code(slot_mapping), ctypes.byref(view), bnd.data_ptr(), nb, bs,
+        int(bool(rotate)), wht_scale(fmt.head_dim), _lib.stream_handle(dev),
+    )
+    _lib.check(rc, "tq_compress_regions")
+    return slots
+
+
 def from_reference_slots(slots: torch.Tensor, fmt: PagedKVFormat) -> torch.Tensor:
     """Inverse of to_reference_slots: [num_blocks, block_size, Hkv, slot_bytes] -> tile layout."""
     nb, bs, h, _ = slots.shape

@@ -21,7 +21,8 @@ from __future__ import annotations
 import torch
 
 from turboquant import _lib
-from turboquant.kernels.paged import choose_tokens_per_chunk, concurrent_units, run_decode
+from turboquant.kernels.paged import (PagedKVFormat, choose_tokens_per_chunk, compress_paged_slots, concurrent_units,
+                                     run_decode)
 
 D = 128
 DQ3 = D * 3 // 8  # 48 index bytes per slot
@@ -40,6 +41,19 @@ def _aos_view(cache: torch.Tensor, kv: int, centroids: torch.Tensor) -> _lib.TQK
     view.bits, view.qjl, view.signs_permuted = 3, 0, 0
     view.centroid_scale = _lib.centroid_scale(centroids)
     return view
+
+
+def compress_to_tq_cache(x, slot_mapping, tq_cache, kv_idx: int, centroids, boundaries, rotate: bool = True):
+    """Write x [T, Hkv, 128] into the 3-bit MSE-only slots of tq_cache [num_blocks, 2 (K/V),
+    block_size, Hkv, slot_bytes] (48 index bytes + fp16 norm per slot, the layout the v11 / v12
+    decode reads, kernels/sparse_v.py:293-304) at slot_mapping, K (kv_idx 0) or V (1), in place:
+    one tq_compress_regions launch (negative slots skipped)."""
+    if tq_cache.dtype != torch.uint8 or tq_cache.dim() != 5 or tq_cache.shape[1] != 2:
+        raise ValueError("tq_cache must be uint8 [num_blocks, 2, block_size, num_kv_heads, slot_bytes]")
+    if kv_idx not in (0, 1):
+        raise ValueError("kv_idx must be 0 (K) or 1 (V)")
+    fmt = PagedKVFormat(bits=3, qjl=False, block_size=tq_cache.shape[2])
+    return compress_paged_slots(x, slot_mapping, tq_cache[:, kv_idx], fmt, centroids, boundaries, rotate=rotate)
 
 
 def tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, scale,
