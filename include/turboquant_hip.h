@@ -44,7 +44,7 @@ typedef struct ihipStream_t* tq_stream_t; /* == hipStream_t */
 #define TQ_ERR_GQA              (-6)  /* num_q_heads / num_kv_heads not an integer in [1,16] */
 #define TQ_ERR_DTYPE            (-7)
 #define TQ_ERR_BLOCK_SIZE       (-8)  /* block_size not a positive multiple of 16 */
-#define TQ_ERR_CHUNK            (-9)  /* tokens_per_chunk not a positive multiple of 16 */
+#define TQ_ERR_CHUNK            (-9)  /* tokens_per_chunk not 0 or a positive multiple of 16 */
 #define TQ_ERR_SCRATCH_LIMIT    (-10) /* tq_decode_noalloc: the call needs more than the fixed scratch */
 
 /* ---- dtype codes ------------------------------------------------------------- */
@@ -253,14 +253,22 @@ int tq_compress_regions(const void* x, int x_dtype, int64_t x_stride_token, int6
  *   out   = sum_t softmax(score)_t * v_cb[vidx_t] * vnorm_t          (fp32 accumulation)
  * with qp = q_proj (or q when q_proj == NULL). Follows attention_unpacked_ref
  * (kernels/packed_attention.py:273-284) with the correct split combine of kernels/attention.py:121-140.
- * Sparse-V (sparse_threshold > 0, kernels/sparse_v.py:108-149): within each chunk of
- * tokens_per_chunk tokens, processed in tiles of 16 tokens with a running max m, token t's V is
- * skipped when max over the GQA group of exp(score - m) <= sparse_threshold; skipped tokens
- * still count in the softmax denominator.
+ * Split-K: tokens_per_chunk > 0 (a multiple of 16) cuts every sequence into chunks of that many
+ * tokens, one work unit per (sequence, KV head, chunk).  tokens_per_chunk = 0 selects the
+ * balanced schedule on the paged fast path: the 32-token tile pairs of all (sequence, KV head)
+ * segments, sequences in order and a sequence's KV heads after each other, are dealt to the
+ * R = min(P, resident waves) waves of one launch (tq_decode_concurrent_units), wave w taking
+ * pairs [floor(w P / R), floor((w + 1) P / R)) of the P in all; its pieces are the chunks.  On
+ * the general kernel 0 picks fixed chunks that fit the same workspace.
+ * Sparse-V (sparse_threshold > 0, kernels/sparse_v.py:108-149): within each chunk, processed
+ * in tiles of 16 tokens with a running max m, token t's V is skipped when max over the GQA
+ * group of exp(score - m) <= sparse_threshold; skipped tokens still count in the softmax
+ * denominator.
  * q, q_proj: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
  * out: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
  * block_tables: int32 [num_seqs, block_table_stride]; entries outside [0, num_blocks) are skipped.
- * max_seq_len: an upper bound of seq_lens (sizes the grid); longer sequences are truncated.
+ * max_seq_len: an upper bound of seq_lens (sizes the grid); longer sequences are truncated
+ *   (the balanced schedule: to max_seq_len tokens).
  * workspace: >= tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk),
  *   256-byte aligned (split-K partial results; no initial contents needed).  Calls that overlap
  *   in time must not share a workspace.
@@ -378,7 +386,8 @@ int tq_decode_noalloc(const void* q, int q_dtype, int64_t q_stride_seq, int64_t 
 /* Work units (one per sequence, KV head and chunk of tokens_per_chunk tokens) that tq_decode
  * can run at once on the current device for this configuration: resident waves per compute
  * unit of the kernel variant tq_decode would pick, times the compute units.  Callers size
- * tokens_per_chunk from it so that the grid fills whole rounds.  No counterpart in the
+ * tokens_per_chunk from it so that the grid fills whole rounds; on the paged fast path it is
+ * also the wave count R of the balanced schedule (tokens_per_chunk = 0).  No counterpart in the
  * reference (its Triton launcher sizes the split from a fixed program target,
  * kernels/attention.py:202-211).
  * norm_row_bytes: row stride of the K / V norm streams (2 for the paged tile layout). */

@@ -7,7 +7,8 @@ reference/pytorch_reference.py:123-158), out = softmax(s) . (v_cb[vidx_t] * vnor
 
 decode_dense is the plain softmax.  decode_chunked follows the kernel's partition, which the
 Sparse-V rule depends on (kernels/sparse_v.py:108-149): tokens are cut into chunks of
-`chunk` tokens and each chunk is walked in 16-token tiles with a running max m; after a tile
+`chunk` tokens (or into given pieces: the kernel's balanced schedule) and each chunk is walked
+in 16-token tiles with a running max m; after a tile
 updates m, token t's V is dropped when max_h exp(s_h,t - m_h) <= threshold (h over the GQA
 group), while exp(s - m) still enters the denominator.  Chunks are merged with the (m, l, acc)
 rule of kernels/attention.py:121-140.  With threshold <= 0 it equals decode_dense.
@@ -64,9 +65,18 @@ def decode_dense(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale):
     return (p @ v) / p.sum(axis=1, keepdims=True)
 
 
-def decode_chunked(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, chunk: int,
+def _chunks(L: int, chunk):
+    """(c0, c1) ranges: fixed chunks of `chunk` tokens, or, for a list of (t0, t1) pieces, those
+    (the split of the kernel's balanced schedule)."""
+    if isinstance(chunk, (int, np.integer)):
+        return [(c0, min(c0 + int(chunk), L)) for c0 in range(0, L, int(chunk))]
+    return [(int(a), min(int(b), L)) for a, b in chunk if a < L]
+
+
+def decode_chunked(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, chunk,
                    threshold: float = 0.0, tile: int = 16):
-    """Chunk/tile walk of the kernel; returns (out [G,128], skipped_tokens, total_tokens)."""
+    """Chunk/tile walk of the kernel; returns (out [G,128], skipped_tokens, total_tokens).
+    chunk: tokens per chunk, or the list of (t0, t1) pieces of the sequence."""
     G = q.shape[0]
     L = k_mse.shape[0]
     if L == 0:
@@ -74,8 +84,7 @@ def decode_chunked(q, qp, k_mse, signs, rnorm, v, sm_scale, corr_scale, chunk: i
     s_all = scores(q, qp, k_mse, signs, rnorm, sm_scale, corr_scale)
     parts = []
     skipped = 0
-    for c0 in range(0, L, chunk):
-        c1 = min(c0 + chunk, L)
+    for c0, c1 in _chunks(L, chunk):
         m = np.full(G, -np.inf)
         lsum = np.zeros(G)
         acc = np.zeros((G, v.shape[1]))
@@ -106,8 +115,7 @@ def sparse_v_margins(q, qp, k_mse, signs, rnorm, sm_scale, corr_scale, chunk: in
     L = k_mse.shape[0]
     s_all = scores(q, qp, k_mse, signs, rnorm, sm_scale, corr_scale)
     out = np.empty(L)
-    for c0 in range(0, L, chunk):
-        c1 = min(c0 + chunk, L)
+    for c0, c1 in _chunks(L, chunk):
         m = np.full(q.shape[0], -np.inf)
         for t0 in range(c0, c1, tile):
             t1 = min(t0 + tile, c1)

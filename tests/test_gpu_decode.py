@@ -85,9 +85,10 @@ def oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, qp=None, chunk=None, thresh=0.
             if chunk is None:
                 out[s, hs] = odec.decode_dense(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs)
             else:
-                o, sk, tt = odec.decode_chunked(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs, chunk, thresh, tile=tile)
+                ch = chunk[(s, kh)] if isinstance(chunk, dict) else chunk   # dict: per-segment pieces
+                o, sk, tt = odec.decode_chunked(q[s, hs], qpv[s, hs], k, sg, rn, v, sm, cs, ch, thresh, tile=tile)
                 if margins is not None:
-                    margins.append(odec.sparse_v_margins(q[s, hs], qpv[s, hs], k, sg, rn, sm, cs, chunk, tile=tile))
+                    margins.append(odec.sparse_v_margins(q[s, hs], qpv[s, hs], k, sg, rn, sm, cs, ch, tile=tile))
                 out[s, hs] = o
                 skipped += sk
                 total += tt
@@ -197,6 +198,68 @@ def test_decode_sparse_v_matches_chunked_oracle(dev):
     dense, _, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=256, thresh=0.0)
     want_dense, _, _ = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, q_round=qr)
     np.testing.assert_allclose(dense, want_dense, rtol=RTOL, atol=ATOL)
+
+
+def _balanced_pieces(dev, lens, Hq, Hkv, kb, kq, vb, max_blocks, bs, share=False):
+    """The pieces tq_decode's balanced schedule cuts, from the device's resident waves."""
+    from turboquant.kernels.paged import balanced_partition, concurrent_units
+    R = max(4, concurrent_units(dev, kb, kq, vb, Hq, Hkv, 2, share))
+    return balanced_partition(lens, Hkv, R, max_blocks * bs)
+
+
+@pytest.mark.parametrize("scale", ["short", "long"])
+@pytest.mark.parametrize("kb,kq,vb,G,bs", [(3, True, 3, 6, 16), (2, True, 2, 8, 16), (4, False, 4, 4, 32),
+                                           (3, False, 2, 1, 64), (2, False, 4, 3, 16)])
+def test_decode_balanced_many_sequences(dev, kb, kq, vb, G, bs, scale):
+    """tokens_per_chunk = 0 (the balanced schedule) over 150 ragged sequences: empty ones, single
+    tokens, lengths off the 32-token pairs.  Every wave's scan of seq_lens crosses three
+    64-sequence blocks; "short" has fewer pairs than resident waves (one pair per wave, segments
+    merged from up to ~50 pieces), "long" more (pieces cross sequences and KV heads)."""
+    Hkv = 2
+    Hq = G * Hkv
+    rng = np.random.default_rng(kb * 10 + vb + G)
+    pool = [0, 1, 31, 32, 33, 95, 200, 640, 1500] if scale == "short" else [0, 1, 33, 700, 1999, 4100]
+    lens = [int(x) for x in rng.choice(pool, size=150)]
+    case = build_case(300 + kb + 7 * vb + G, len(lens), Hq, Hkv, lens, kb, kq, vb, bs)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    pieces = _balanced_pieces(dev, lens, Hq, Hkv, kb, kq, vb, case["bt"].shape[1], bs)
+    print(f"{sum(len(v) for v in pieces.values())} pieces over {len(pieces)} segments", flush=True)
+    got, _, qr = run_gpu(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk=0)
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=qr)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    assert np.all(got[np.array(lens) == 0] == 0.0)
+
+
+def test_decode_balanced_all_empty(dev):
+    """No tokens at all: no wave has work, the plan still says so, every output is zero."""
+    lens = [0, 0, 0]
+    case = build_case(9, 3, 8, 2, [1, 1, 1], 3, True, 3, 16)
+    case["seq_lens"] = np.array(lens, np.int32)
+    got, _, _ = run_gpu(dev, case, 8, 2, 3, True, 3, 16, 0.1, 0.0, chunk=0)
+    assert np.all(got == 0.0)
+
+
+@pytest.mark.parametrize("bs", [16, 32])
+def test_decode_balanced_sparse_v_pieces(dev, bs):
+    """Sparse-V under the balanced schedule: the kernel's pieces (balanced_partition with the
+    device's resident waves) are the chunks the oracle walks; outputs agree and skip counts agree
+    up to the tokens within rounding of the threshold."""
+    S, Hq, Hkv = 5, 12, 2
+    lens = [4000, 9000, 3, 2500, 6000]
+    case = build_case(61 + bs, S, Hq, Hkv, lens, 3, True, 3, bs)
+    case["q"] *= 4.0
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    pieces = _balanced_pieces(dev, lens, Hq, Hkv, 3, True, 3, case["bt"].shape[1], bs)
+    thresh = 1e-4
+    got, st, qr = run_gpu(dev, case, Hq, Hkv, 3, True, 3, bs, sm, cs, chunk=0, thresh=thresh, stats=True)
+    margins = []
+    want, sk, tot = oracle_out(case, Hq, Hkv, 3, True, 3, sm, cs, chunk=pieces, thresh=thresh, q_round=qr,
+                               tile=32 if bs >= 32 else 16, margins=margins)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    allow = _skip_allowance(margins, thresh)
+    print(f"balanced Sparse-V: skipped gpu {int(st[0])} oracle {sk} of {tot} (within rounding {allow})")
+    assert int(st[1]) == tot and sk > 0
+    assert abs(int(st[0]) - sk) <= allow
 
 
 def test_decode_workspace_reuse(dev):

@@ -84,7 +84,7 @@ def test_decode_rotated_matches_oracle(dev, kb, kq, vb, G):
     lens = [37, 1, 300, 0]
     case = build_case(500 + 7 * kb + vb + G, len(lens), Hq, Hkv, lens, kb, kq, vb, bs)
     sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
-    for chunk in (64, 512):
+    for chunk in (64, 512, 0):      # 0: the balanced schedule
         out, q = _decode(dev, case, Hq, Hkv, kb, kq, vb, bs, sm, cs, chunk, rotate=True)
         q64 = q.float().cpu().numpy().astype(np.float64)
         want_rot, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=q64 @ H64)

@@ -12,6 +12,7 @@ import math
 import pathlib
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -230,6 +231,83 @@ def test_chunk_choice_fills_whole_rounds():
     # variable lengths on the host shrink chunks towards the balanced load
     lens = [2048] * 63 + [131072]
     assert choose_tokens_per_chunk(64, 8, 131072, 3072, lens) < choose_tokens_per_chunk(64, 8, 131072, 3072)
+
+
+def test_balanced_partition_against_brute_force():
+    """balanced_partition (the host mirror of the kernel's balanced schedule) against a pair-by-
+    pair assignment: list every 32-token pair of every (sequence, KV head) segment in order,
+    give pair x to the worker w with floor(w P / R) <= x < floor((w + 1) P / R) by direct
+    search, and cut each segment where the worker changes."""
+    from turboquant.kernels.paged import balanced_partition
+    rng = np.random.default_rng(4)
+    for trial in range(60):
+        S = int(rng.integers(1, 90))
+        hkv = int(rng.choice([1, 2, 3, 8]))
+        lens = [int(x) for x in rng.choice([0, 1, 16, 31, 32, 33, 100, 700, 3000], size=S)]
+        cap = int(rng.choice([10 ** 9, 500, 64]))
+        workers = int(rng.choice([1, 7, 64, 3072]))
+        got = balanced_partition(lens, hkv, workers, cap)
+        Ls = [min(L, cap) for L in lens]
+        segs = [(s, kh) for s in range(S) for kh in range(hkv)]
+        owner = []  # (segment, pair) per global pair
+        for s, kh in segs:
+            owner += [((s, kh), j) for j in range(-(-Ls[s] // 32))]
+        P = len(owner)
+        if P == 0:
+            assert got == {}
+            continue
+        R = min(P, workers)
+        bounds = [w * P // R for w in range(R + 1)]
+        worker_of = np.searchsorted(bounds, np.arange(P), side="right") - 1
+        want = {}
+        for x, (seg, j) in enumerate(owner):
+            s = seg[0]
+            if j == 0 or worker_of[x] != worker_of[x - 1]:
+                want.setdefault(seg, []).append([32 * j, 32 * (j + 1)])
+            else:
+                want[seg][-1][1] = 32 * (j + 1)
+        want = {k: [(a, min(b, Ls[k[0]])) for a, b in v] for k, v in want.items()}
+        assert got == want, (trial, S, hkv, workers, cap)
+        # pieces tile each sequence exactly, in 32-token steps
+        for (s, kh), pcs in got.items():
+            assert pcs[0][0] == 0 and pcs[-1][1] == Ls[s]
+            assert all(b == c for (_, b), (c, _) in zip(pcs[:-1], pcs[1:]))
+            assert all(a % 32 == 0 for a, _ in pcs)
+
+
+def test_chunk_planner_picks_balanced_beyond_one_round(monkeypatch):
+    """Fixed chunks while the planner's units fit one round of resident waves, the balanced
+    schedule (0) when they need more or the lengths are unknown (config 3 / 4 / 5 shapes,
+    3072 or 4096 resident waves as on MI355X)."""
+    import random
+    from turboquant.kernels import paged
+    from turboquant.kernels.paged import PagedKVFormat, plan_tokens_per_chunk
+    kf2, vf2 = PagedKVFormat(bits=2, qjl=True), PagedKVFormat(bits=2, layout="values")
+    kf3, vf3 = PagedKVFormat(bits=3, qjl=True), PagedKVFormat(bits=3, layout="values")
+    kf4, vf4 = PagedKVFormat(bits=4), PagedKVFormat(bits=4, layout="values")
+    cpu = torch.device("cpu")
+    assert plan_tokens_per_chunk(cpu, 64, 64, 8, 131072, kf2, vf2) == 0      # lengths unknown
+    monkeypatch.setattr(paged, "concurrent_units", lambda dev, kb, *a: 3072 if kb != 4 else 4096)
+    r5 = random.Random(5)
+    lens5 = [int(round(math.exp(r5.uniform(math.log(2048), math.log(131072))))) for _ in range(64)]
+    assert plan_tokens_per_chunk(cpu, 64, 64, 8, max(lens5), kf2, vf2, seq_lens_host=lens5) == 0
+    r3 = random.Random(3)
+    lens3 = [r3.randint(1024, 8192) for _ in range(32)]
+    assert plan_tokens_per_chunk(cpu, 32, 32, 8, max(lens3), kf4, vf4, seq_lens_host=lens3) > 0
+    assert plan_tokens_per_chunk(cpu, 64, 48, 8, 32768, kf3, vf3, seq_lens_host=[32768] * 64) == 5472
+
+
+def test_balanced_workspace_and_chunk_rejection():
+    from turboquant import _lib
+    L = _lib.lib()
+    # tokens_per_chunk 0: plan (int64 per sequence + 1) + partial rows for 128 x 256 CUs plus
+    # one per (sequence, query head), each 128 fp32 + m + l
+    S, Hq = 64, 64
+    rows = 128 * 256 + S * Hq
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert L.tq_decode_workspace_bytes(S, Hq, 131072, 0) == up(8 * (S + 1)) + up(rows * 512) + 2 * up(rows * 4)
+    assert L.tq_decode_workspace_bytes(S, Hq, 131072, -16) == 0
+    assert L.tq_decode_workspace_bytes(S, Hq, 131072, 0) < 64 * 1024 * 1024  # fits the no-alloc scratch
 
 
 # ---------------------------------------------------------------- C ABI

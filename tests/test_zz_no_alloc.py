@@ -68,10 +68,13 @@ def _reference(c, chunk, thresh, stats):
     from turboquant.kernels.paged import decode_paged
     return decode_paged(c["q"], c["k_cache"], c["kf"], c["kc"], c["v_cache"], c["vf"], c["vc"], c["bt"], c["lens"],
                         sparse_threshold=thresh, max_seq_len=int(c["lens"].max()), tokens_per_chunk=chunk,
-                        workspace=torch.empty(1 << 24, dtype=torch.uint8, device=c["q"].device), skip_stats=stats)
+                        workspace=torch.empty(_lib.lib().tq_decode_workspace_bytes(
+                            len(c["lens"]), c["q"].shape[1], int(c["lens"].max()), chunk),
+                            dtype=torch.uint8, device=c["q"].device), skip_stats=stats)
 
 
-@pytest.mark.parametrize("rounds", [[([3000, 17, 1200, 0, 2047, 512, 95, 4096], 256, 1e-4), ([700, 33, 160], 64, 0.0)]])
+@pytest.mark.parametrize("rounds", [[([3000, 17, 1200, 0, 2047, 512, 95, 4096], 256, 1e-4), ([700, 33, 160], 64, 0.0)],
+                                    [([3000, 17, 1200, 0, 2047, 512, 95, 4096], 0, 1e-4), ([700, 33, 160], 0, 0.0)]])
 def test_noalloc_matches_workspace_entry(dev, rounds):
     for i, (lens, chunk, thresh) in enumerate(rounds):
         c = _case(dev, 90 + i, lens)

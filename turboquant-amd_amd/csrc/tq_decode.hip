@@ -30,6 +30,7 @@
 
 #include <cmath>
 #include <cstdlib>
+#include <mutex>
 
 namespace {
 
@@ -773,6 +774,9 @@ struct ReduceParams {
     int64_t out_ss, out_sh;
     int rot_out;  // write out x H
     float wht_h;
+    // balanced schedule: partial rows [slot][group][128] located through the decode kernel's plan
+    int balanced, n_workers, hkv, group, len_cap;
+    const int64_t* plan;
 };
 
 // Split-K merge, one wave per (sequence, query head):
@@ -797,12 +801,34 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     const int64_t s = sh / p.hq;
     const int h = (int)(sh - s * p.hq);
     const int lane = threadIdx.x;
-    int L = p.seq_lens[s];
-    L = L < p.cap ? L : p.cap;
-    int nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
-    nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
-    if (nch == 1 && !p.rot_out) return;
-    const int64_t base = sh * p.n_chunks;
+    int nch;
+    int64_t base, stride;  // partial row of the first piece, rows between pieces
+    if (!p.balanced) {
+        int L = p.seq_lens[s];
+        L = L < p.cap ? L : p.cap;
+        nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
+        nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
+        if (nch == 1 && !p.rot_out) return;
+        base = sh * p.n_chunks;
+        stride = 1;
+    } else {
+        // the workers w0..w1 that hold segment (s, kh): partial slots w0 + g .. w1 + g
+        const int kh = h / p.group;
+        const int np = tq_bal_pairs(p.seq_lens[s], p.len_cap);
+        nch = 0;
+        base = 0;
+        stride = p.group;
+        if (np > 0) {
+            const int64_t P = p.plan[0] * p.hkv;
+            const int64_t R = P < p.n_workers ? P : (int64_t)p.n_workers;
+            const int64_t x0 = p.plan[1 + s] * p.hkv + (int64_t)kh * np;
+            const int64_t w0 = tq_bal_worker(x0, P, R);
+            const int64_t w1 = tq_bal_worker(x0 + np - 1, P, R);
+            if (w0 == w1 && !p.rot_out) return;  // written by the decode kernel
+            nch = (int)(w1 - w0 + 1);
+            base = (w0 + s * p.hkv + kh) * p.group + (h - kh * p.group);
+        }
+    }
     // Batches of 16 chunks: the batch's rows, maxima and denominators are all requested before
     // any of them is used (the rows do not depend on the maxima), so a batch costs one load
     // round.  Per batch the running max M rescales what was summed so far.
@@ -811,11 +837,12 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     for (int c0 = 0; c0 < nch; c0 += 16) {
         const int nb = nch - c0 < 16 ? nch - c0 : 16;
         const bool mine = lane < nb;
-        const float mc = mine ? p.ws_m[base + c0 + lane] : kNegInf;
-        const float lc = mine ? p.ws_l[base + c0 + lane] : 0.f;
+        const float mc = mine ? p.ws_m[base + (int64_t)(c0 + lane) * stride] : kNegInf;
+        const float lc = mine ? p.ws_l[base + (int64_t)(c0 + lane) * stride] : 0.f;
         float2 v[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = j < nb ? rows[(int64_t)(c0 + j) * (TQ_HEAD_DIM / 2)] : make_float2(0.f, 0.f);
+        for (int j = 0; j < 16; ++j)
+            v[j] = j < nb ? rows[(int64_t)(c0 + j) * stride * (TQ_HEAD_DIM / 2)] : make_float2(0.f, 0.f);
         const float Mb = wave_max(mc);
         const float Mn = fmaxf(M, Mb);
         if (Mn == kNegInf) continue;  // every chunk so far empty
@@ -892,8 +919,16 @@ bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
 
 int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num_q_heads, int n_chunks, int chunk,
                   int cap, const int32_t* seq_lens, void* out, int out_dtype, int64_t out_ss, int64_t out_sh,
-                  int rot_out, hipStream_t st) {
-    ReduceParams rp;
+                  int rot_out, hipStream_t st, const FastDecodeParams* bal = nullptr) {
+    ReduceParams rp = {};
+    if (bal) {
+        rp.balanced = 1;
+        rp.n_workers = bal->n_workers;
+        rp.hkv = bal->hkv;
+        rp.group = bal->group;
+        rp.len_cap = bal->len_cap;
+        rp.plan = bal->plan;
+    }
     rp.rot_out = rot_out;
     rp.wht_h = kWhtH;
     rp.ws_acc = ws_acc;
@@ -950,8 +985,63 @@ bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block
 
 }  // namespace
 
+// Balanced schedule: partial rows for up to 16 resident waves per CU of the largest gfx950
+// (256 CUs) at 8 query heads per group, plus one per (sequence, query head).
+constexpr int kTqMaxCus = 256;
+size_t bal_rows(int num_seqs, int num_q_heads) {
+    return (size_t)kTqBalRowsPerCu * kTqMaxCus + (size_t)num_seqs * num_q_heads;
+}
+size_t bal_plan_bytes(int num_seqs) { return align_up((size_t)(num_seqs + 1) * sizeof(int64_t), 256); }
+
+// Fixed chunks for the general kernel under tokens_per_chunk = 0: as many per sequence as the
+// balanced workspace holds (at most one more than its extra rows per (sequence, query head)).
+int general_chunk(int num_seqs, int num_q_heads, int max_seq_len, bool pair) {
+    const int64_t tiles = max_seq_len > 0 ? (max_seq_len + 15) / 16 : 1;
+    int64_t n = 1 + (int64_t)kTqBalRowsPerCu * kTqMaxCus / ((int64_t)num_seqs * num_q_heads);
+    n = n < tiles ? n : tiles;
+    int64_t c = 16 * ((tiles + n - 1) / n);
+    if (pair && c % 32) c += 16;
+    return (int)c;
+}
+
+// Resident waves of the fast kernel on the current device (one launch's workers), cached per
+// (device, kernel, LDS bytes).
+int resident_waves(const void* kern, size_t lds, int* waves) {
+    struct Entry {
+        int dev;
+        const void* kern;
+        size_t lds;
+        int waves;
+    };
+    static Entry cache[64];
+    static int n_cache = 0;
+    static std::mutex mu;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_cache; ++i)
+        if (cache[i].dev == dev && cache[i].kern == kern && cache[i].lds == lds) {
+            *waves = cache[i].waves;
+            return TQ_OK;
+        }
+    int blocks = 0, cus = 0;
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return (int)e;
+    *waves = blocks * 4 * cus;
+    if (*waves < 4) *waves = 4;
+    if (n_cache < 64) cache[n_cache++] = Entry{dev, kern, lds, *waves};
+    return TQ_OK;
+}
+
 extern "C" size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len, int tokens_per_chunk) {
-    if (num_seqs <= 0 || num_q_heads <= 0 || tokens_per_chunk <= 0) return 0;
+    if (num_seqs <= 0 || num_q_heads <= 0 || tokens_per_chunk < 0) return 0;
+    if (tokens_per_chunk == 0) {
+        const size_t rows = bal_rows(num_seqs, num_q_heads);
+        return bal_plan_bytes(num_seqs) + align_up(rows * TQ_HEAD_DIM * sizeof(float), 256) +
+               2 * align_up(rows * sizeof(float), 256);
+    }
     const size_t slots = (size_t)num_seqs * num_q_heads * n_chunks_for(max_seq_len, tokens_per_chunk);
     // acc, m, l per (sequence, query head, chunk)
     return align_up(slots * TQ_HEAD_DIM * sizeof(float), 256) + 2 * align_up(slots * sizeof(float), 256);
@@ -1007,7 +1097,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     if (k->bits < 2 || k->bits > 4 || v->bits < 2 || v->bits > 4) return TQ_ERR_BITS;
     if (v->qjl) return TQ_ERR_INVALID_ARGUMENT;
     if (block_size <= 0 || block_size % 16) return TQ_ERR_BLOCK_SIZE;
-    if (tokens_per_chunk <= 0 || tokens_per_chunk % 16) return TQ_ERR_CHUNK;
+    if (tokens_per_chunk < 0 || tokens_per_chunk % 16) return TQ_ERR_CHUNK;  // 0: balanced
     if (q_dtype != TQ_F32 && q_dtype != TQ_F16 && q_dtype != TQ_BF16) return TQ_ERR_DTYPE;
     if (out_dtype != TQ_F32 && out_dtype != TQ_F16 && out_dtype != TQ_BF16) return TQ_ERR_DTYPE;
     if (max_blocks_per_seq < 0 || num_blocks < 0) return TQ_ERR_INVALID_ARGUMENT;
@@ -1054,18 +1144,24 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     // so chunks start on such a block (tokens_per_chunk rounded up to a multiple of 32; the
     // workspace this needs is never larger).
     const bool sparse_pair = sparse_threshold > 0.f && block_size >= 32 && block_tables;
-    if (sparse_pair && tokens_per_chunk % 32) tokens_per_chunk += 16;
-    const int n_chunks = n_chunks_for(max_seq_len, tokens_per_chunk);
     const size_t need = tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return TQ_ERR_WORKSPACE;
+    bool big = false;
+    const bool fast = fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &big);
+    // tokens_per_chunk = 0: the balanced schedule on the fast kernel; fixed chunks that fit the
+    // same workspace on the general one
+    const bool balanced = tokens_per_chunk == 0 && fast;
+    if (tokens_per_chunk == 0 && !fast)
+        tokens_per_chunk = general_chunk(num_seqs, num_q_heads, max_seq_len, sparse_pair);
+    if (!balanced && sparse_pair && tokens_per_chunk % 32) tokens_per_chunk += 16;
+    const int n_chunks = balanced ? 1 : n_chunks_for(max_seq_len, tokens_per_chunk);
 
     const size_t slots = (size_t)num_seqs * num_q_heads * n_chunks;
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const float k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
     const float v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
     const bool share = k->centroids == v->centroids && k->bits == v->bits && k_cscale == v_cscale;
-    bool big = false;
-    if (fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &big)) {
+    if (fast) {
         FastDecodeParams f = {};
         f.big = big ? 1 : 0;
         f.q = q;
@@ -1115,10 +1211,33 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.qp_mul = corr_scale * k_cscale;
         f.chunk = tokens_per_chunk;
         f.n_chunks = n_chunks;
-        f.ws_acc = reinterpret_cast<float*>(ws);
-        f.ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));
-        f.ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(f.ws_m) + align_up(slots * sizeof(float), 256));
         f.skip_stats = skip_stats;
+        int64_t grid;
+        if (balanced) {
+            const size_t rows = bal_rows(num_seqs, num_q_heads);
+            int waves = 0;
+            // the plain instance, as tq_decode_concurrent_units counts it (the statistics and
+            // 64-bit instances share its register budget and LDS)
+            const int orc = resident_waves(tq_decode_fast_kernel_ptr(k->bits, k->qjl != 0, v->bits), lds_total, &waves);
+            if (orc) return orc;
+            // partial slots stay below workers + num_seqs * num_kv_heads
+            const int64_t wmax = (int64_t)(rows / group) - (int64_t)num_seqs * num_kv_heads;
+            f.balanced = 1;
+            f.n_workers = (int)(waves < wmax ? waves : wmax);
+            const int cap = max_blocks_per_seq * block_size;
+            f.len_cap = max_seq_len > 0 && max_seq_len < cap ? max_seq_len : cap;
+            f.plan = reinterpret_cast<int64_t*>(ws);
+            uint8_t* wsr = ws + bal_plan_bytes(num_seqs);
+            f.ws_acc = reinterpret_cast<float*>(wsr);
+            f.ws_m = reinterpret_cast<float*>(wsr + align_up(rows * TQ_HEAD_DIM * sizeof(float), 256));
+            f.ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(f.ws_m) + align_up(rows * sizeof(float), 256));
+            grid = (f.n_workers + 3) / 4;
+        } else {
+            f.ws_acc = reinterpret_cast<float*>(ws);
+            f.ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));
+            f.ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(f.ws_m) + align_up(slots * sizeof(float), 256));
+            grid = ((int64_t)num_seqs * num_kv_heads * n_chunks + 3) / 4;
+        }
         f.out = out;
         f.out_dtype = out_dtype;
         f.out_ss = out_stride_seq;
@@ -1127,14 +1246,12 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.rot_qp = rotate && !q_proj;
         f.rot_out = rotate;
         f.wht_h = kWhtH;
-        const int64_t units = (int64_t)num_seqs * num_kv_heads * n_chunks;
-        const int64_t grid = (units + 3) / 4;
         if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
         int frc = tq_decode_fast_launch(f, k->bits, k->qjl != 0, v->bits, grid, lds_total, (hipStream_t)stream);
         if (frc) return frc;
         return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
                              max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq,
-                             out_stride_head, rotate, (hipStream_t)stream);
+                             out_stride_head, rotate, (hipStream_t)stream, balanced ? &f : nullptr);
     }
     float* ws_acc = reinterpret_cast<float*>(ws);
     float* ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));

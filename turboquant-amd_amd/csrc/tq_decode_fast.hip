@@ -124,6 +124,17 @@ __device__ __forceinline__ uint32_t row_swap8(uint32_t x) {
 }
 __device__ __forceinline__ float row_swap8f(float x) { return __uint_as_float(row_swap8(__float_as_uint(x))); }
 
+// inclusive prefix sum over the 64 lanes (once per wave and 64 sequences: cross-lane moves)
+__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_up((int)v, d, 64);
+        if (lane >= d) v += t;
+    }
+    return v;
+}
+
 __device__ __forceinline__ float max_over_groups(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
@@ -373,6 +384,73 @@ void decode_fast_kernel(FastDecodeParams p) {
     // before reading a tile, so this is part of each unit's start-up.
     constexpr int SREP = sign_replicas<KB, VB>();
     const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t wv = (int64_t)blockIdx.x * 4 + wave;  // this wave's unit (chunks) or worker (balanced)
+    const int cap = p.max_blocks * p.block_size;
+
+    // ---- this wave's work, settled before the tables are built: idle workgroups skip them ----
+    // Balanced schedule: the pair range [bal_pos, bal_end) of worker wv and the sequence bal_s
+    // (bal_np pairs per KV head, bal_q pairs per KV head before it) that holds its first pair.
+    int64_t bal_pos = 0, bal_end = 0, bal_q = 0;
+    int bal_s = 0, bal_np = 0;
+    if (p.balanced) {
+        int64_t tot = 0;
+        for (int b = 0; b < p.num_seqs; b += 64) {
+            const int sl = b + lane;
+            const uint32_t np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
+            tot += (int64_t)__builtin_amdgcn_readlane(wave_incl_scan_u32(np), 63);
+        }
+        const int64_t P = tot * p.hkv;
+        const int64_t R = P < p.n_workers ? P : (int64_t)p.n_workers;
+        const bool planner = wv == 0;  // writes the plan the merge reads
+        if (wv < R) {
+            bal_pos = tq_bal_begin(wv, P, R);
+            bal_end = tq_bal_begin(wv + 1, P, R);
+        }
+        if (planner || wv < R) {
+            int64_t carry = 0;
+            bool found = wv >= R;
+            for (int b = 0; b < p.num_seqs; b += 64) {
+                const int sl = b + lane;
+                const uint32_t np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
+                const uint32_t incl = wave_incl_scan_u32(np);
+                if (planner && sl < p.num_seqs) p.plan[1 + sl] = carry + (int64_t)(incl - np);
+                if (!found) {
+                    const uint64_t m =
+                        __builtin_amdgcn_ballot_w64(sl < p.num_seqs && (carry + (int64_t)incl) * p.hkv > bal_pos);
+                    if (m) {
+                        const int l = __builtin_ctzll(m);
+                        bal_s = b + l;
+                        bal_np = (int)__builtin_amdgcn_readlane(np, l);
+                        bal_q = carry + (int64_t)__builtin_amdgcn_readlane(incl, l) - bal_np;
+                        found = true;
+                    }
+                }
+                carry += (int64_t)__builtin_amdgcn_readlane(incl, 63);
+                if (found && !planner) break;
+            }
+            if (planner && lane == 0) p.plan[0] = tot;
+        }
+        if ((int64_t)blockIdx.x * 4 >= R) return;  // the whole workgroup idle
+    } else {
+        // fixed chunks: units in (sequence, chunk, KV head) order; a workgroup whose four units
+        // all start past their sequence's end is idle
+        bool any = false;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t unit = (int64_t)blockIdx.x * 4 + u;
+            const int64_t sc_ = unit / p.hkv;
+            const int ci = (int)(sc_ % p.n_chunks);
+            const int64_t su = sc_ / p.n_chunks;
+            if (su < p.num_seqs) {
+                int Lu = p.seq_lens[su];
+                Lu = Lu < cap ? Lu : cap;
+                any = any || ci * p.chunk < Lu;
+            }
+        }
+        if (!any) return;
+    }
     if (KQJL) {
         // entry e (one per thread): 8 sign bits -> 8 fp4 values +1 (0x2) / -1 (0xA)
         uint32_t w = 0;
@@ -421,7 +499,6 @@ void decode_fast_kernel(FastDecodeParams p) {
     if (vown) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>(), 1);
     __syncthreads();
 
-    const int lane = threadIdx.x & 63;
     const int g = lane >> 4;
     const int n = lane & 15;
     const int hcol = n & 7;
@@ -439,21 +516,67 @@ void decode_fast_kernel(FastDecodeParams p) {
         asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
     c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // Units in (sequence, chunk, KV head) order: the four waves of a workgroup get the same
-    // chunk of one sequence (equal work).
-    const int64_t unit = (int64_t)blockIdx.x * 4 + wave;
-    const int kh = (int)(unit % p.hkv);
-    const int64_t sc_ = unit / p.hkv;
-    const int ci = (int)(sc_ % p.n_chunks);
-    const int64_t s = sc_ / p.n_chunks;
-    if (s >= p.num_seqs) return;
-    int L = p.seq_lens[s];
-    const int cap = p.max_blocks * p.block_size;
-    L = L < cap ? L : cap;
-    const int t_begin = ci * p.chunk;
-    if (t_begin >= L) return;
-    const int t_end = (t_begin + p.chunk < L) ? t_begin + p.chunk : L;
+    // ---- loop-invariant lane offsets inside a tile ----
+    // lane-grouped tiles: the lane's key chunk (row n, dims 32g..) and value chunk (rows
+    // 4g..4g+3, dims 8n..8n+7) inside a 16-row sub-tile
+    const uint32_t o_kch = (uint32_t)((4 * n + g) * (4 * KB + (KQJL ? 4 : 0)));
+    const uint32_t o_vch = (uint32_t)((16 * g + n) * 4 * VB);
+    const uint32_t o_norm = (uint32_t)(8 * g);  // tokens 4g..4g+3, 2 bytes each
+    const uint64_t hi8 = 0xff00ff00ff00ff00ull;
+
+    // Balanced schedule: the KV head and the pair offset of bal_pos inside its segment.
+    int kh_b = 0;
+    int64_t pp = 0;
+    if (p.balanced && bal_pos < bal_end) {
+        const int64_t off = bal_pos - bal_q * p.hkv;
+        kh_b = (int)(off / bal_np);
+        pp = off - (int64_t)kh_b * bal_np;
+    }
+    unsigned long long cnt_tot = 0, cnt_kept = 0;
+
+    // ---- pieces: one (sequence, KV head, token range) per pass ----
+    // Fixed chunks: the wave's one unit (units in (sequence, chunk, KV head) order, so the four
+    // waves of a workgroup get the same chunk of one sequence).  Balanced: the segments the
+    // worker's pair range crosses.
+    for (;;) {
+    int64_t s;
+    int kh, L, t_begin, t_end;
+    bool direct;           // the piece is the whole sequence: write the output here
+    int64_t prow_base;     // partial row of the group's first head
+    int64_t prow_step;     // rows between the group's heads
+    int64_t take = 0;      // balanced: pairs of this piece
+    if (!p.balanced) {
+        kh = (int)(wv % p.hkv);
+        const int64_t sc_ = wv / p.hkv;
+        const int ci = (int)(sc_ % p.n_chunks);
+        s = sc_ / p.n_chunks;
+        if (s >= p.num_seqs) break;
+        L = p.seq_lens[s];
+        L = L < cap ? L : cap;
+        t_begin = ci * p.chunk;
+        if (t_begin >= L) break;
+        t_end = (t_begin + p.chunk < L) ? t_begin + p.chunk : L;
+        int nch = (L + p.chunk - 1) / p.chunk;
+        nch = nch < p.n_chunks ? nch : p.n_chunks;
+        // (a rotated output is written by decode_reduce_kernel, which takes single chunks too)
+        direct = nch == 1 && !p.rot_out;
+        prow_base = (s * p.hq + (int64_t)kh * p.group) * p.n_chunks + ci;
+        prow_step = p.n_chunks;
+    } else {
+        if (bal_pos >= bal_end) break;
+        s = bal_s;
+        kh = kh_b;
+        L = p.seq_lens[s];
+        L = L < p.len_cap ? L : p.len_cap;
+        take = (int64_t)bal_np - pp;
+        take = take < bal_end - bal_pos ? take : bal_end - bal_pos;
+        t_begin = (int)(32 * pp);
+        t_end = (int)(32 * (pp + take));
+        t_end = t_end < L ? t_end : L;
+        direct = pp == 0 && take == bal_np && !p.rot_out;
+        prow_base = (wv + s * p.hkv + kh) * p.group;
+        prow_step = 1;
+    }
 
     // ---- query operands ----
     const int head = kh * p.group + hcol;
@@ -533,19 +656,12 @@ void decode_fast_kernel(FastDecodeParams p) {
         c.sc_hi = c.sc_lo = 127;
     }
 
-    // ---- loop-invariant lane offsets inside a tile ----
-    // lane-grouped tiles: the lane's key chunk (row n, dims 32g..) and value chunk (rows
-    // 4g..4g+3, dims 8n..8n+7) inside a 16-row sub-tile
-    const uint32_t o_kch = (uint32_t)((4 * n + g) * (4 * KB + (KQJL ? 4 : 0)));
-    const uint32_t o_vch = (uint32_t)((16 * g + n) * 4 * VB);
-    const uint32_t o_norm = (uint32_t)(8 * g);  // tokens 4g..4g+3, 2 bytes each
     // One descriptor per head (tiles at 32-bit scalar offsets from it), or, for a cache spanning
     // 2 GiB or more (BIG), one per tile from a 64-bit base.
     const uint8_t* kunit = p.kbase + (int64_t)kh * p.k_sh;
     const uint8_t* vunit = p.vbase + (int64_t)kh * p.v_sh;
     const auto rk = rsrc(kunit);
     const auto rv = rsrc(vunit);
-    const uint64_t hi8 = 0xff00ff00ff00ff00ull;
 
     // ---- tile walk ----
     const int nblk_seq = (L + p.block_size - 1) / p.block_size;  // >= 1
@@ -731,17 +847,14 @@ void decode_fast_kernel(FastDecodeParams p) {
     // ---- combine the lane groups and the two tile halves ----
     float lsum = sum_over_groups(st.lsum);
     lsum += row_swap8f(lsum);
-    if (COUNT && lane == 0) {
-        atomicAdd(p.skip_stats, (unsigned long long)(st.n_tot - st.n_kept));
-        atomicAdd(p.skip_stats + 1, (unsigned long long)st.n_tot);
+    if (COUNT) {
+        cnt_tot += (unsigned long long)st.n_tot;
+        cnt_kept += (unsigned long long)st.n_kept;
     }
     const bool writer = c.lo8 && hvalid;
     // acc[nn][r] is dim 8 * (4g + r) + nn of head col; v_cinv undoes the V table scale.
     const float vs = p.v_cinv;
-    int nch = (L + p.chunk - 1) / p.chunk;
-    nch = nch < p.n_chunks ? nch : p.n_chunks;
-    // (a rotated output is written by decode_reduce_kernel, which takes single chunks too)
-    if (nch == 1 && !p.rot_out) {
+    if (direct) {
         if (writer) {
             const float inv = lsum > 0.f ? vs / lsum : 0.f;
             const int64_t ob = s * p.out_ss + (int64_t)head * p.out_sh + 32 * g;
@@ -750,10 +863,8 @@ void decode_fast_kernel(FastDecodeParams p) {
 #pragma unroll
                 for (int nn = 0; nn < 8; ++nn) tq_store1(p.out, ob + 8 * r + nn, p.out_dtype, st.acc[nn][r] * inv);
         }
-        return;
-    }
-    if (writer) {
-        const int64_t slot = ((s * p.hq + head) * (int64_t)p.n_chunks + ci);
+    } else if (writer) {
+        const int64_t slot = prow_base + (int64_t)hcol * prow_step;
         if (g == 0) {
             p.ws_m[slot] = st.m == kNegInf ? kNegInf : st.m * p.c_exp;  // log2 units for the merge
             p.ws_l[slot] = lsum;
@@ -764,6 +875,30 @@ void decode_fast_kernel(FastDecodeParams p) {
             dst[2 * r] = make_float4(st.acc[0][r] * vs, st.acc[1][r] * vs, st.acc[2][r] * vs, st.acc[3][r] * vs);
             dst[2 * r + 1] = make_float4(st.acc[4][r] * vs, st.acc[5][r] * vs, st.acc[6][r] * vs, st.acc[7][r] * vs);
         }
+    }
+    if (!p.balanced) break;
+    // next piece: the rest of the segment, the next KV head, or the next non-empty sequence
+    bal_pos += take;
+    pp += take;
+    if (pp == bal_np) {
+        pp = 0;
+        if (++kh_b == p.hkv) {
+            kh_b = 0;
+            while (bal_pos < bal_end) {
+                bal_q += bal_np;
+                if (++bal_s >= p.num_seqs) {
+                    bal_pos = bal_end;  // unreachable with the lengths the range was cut from
+                    break;
+                }
+                bal_np = tq_bal_pairs(p.seq_lens[bal_s], p.len_cap);
+                if (bal_np > 0) break;
+            }
+        }
+    }
+    }  // pieces
+    if (COUNT && lane == 0 && cnt_tot) {
+        atomicAdd(p.skip_stats, cnt_tot - cnt_kept);
+        atomicAdd(p.skip_stats + 1, cnt_tot);
     }
 }
 

@@ -8,6 +8,27 @@
 
 #include "turboquant_hip.h"
 
+// ---- balanced split-K schedule (tokens_per_chunk = 0) ----
+// The work is the stream of 32-token tile pairs of every (sequence, KV head) segment, sequences
+// in order and the KV heads of a sequence after each other: segment (s, kh) holds
+// np(s) = ceil(min(seq_len[s], len_cap) / 32) pairs and starts at pair hkv * Q(s) + kh * np(s),
+// Q(s) being the sum of np over the sequences before s.  With P pairs in all and R workers
+// (waves; R <= P, so none is empty) worker w takes pairs [floor(w P / R), floor((w + 1) P / R)),
+// which may cross segments.  The partial result of worker w for segment g = s * hkv + kh sits
+// in partial slot w + g: along the workers the touched segments never decrease, so w + g never
+// repeats, and slots stay below R + num_seqs * hkv.
+__host__ __device__ inline int64_t tq_bal_begin(int64_t w, int64_t P, int64_t R) { return w * P / R; }
+// the worker holding pair x (0 <= x < P): the largest w with floor(w P / R) <= x
+__host__ __device__ inline int64_t tq_bal_worker(int64_t x, int64_t P, int64_t R) { return ((x + 1) * R - 1) / P; }
+__host__ __device__ inline int tq_bal_pairs(int len, int len_cap) {
+    len = len < len_cap ? len : len_cap;
+    return len > 0 ? (len + 31) >> 5 : 0;
+}
+// Workspace of the balanced schedule: the plan (int64: total pairs per KV head, then Q(s) for
+// every sequence, written by the decode kernel for the merge), then acc / m / l rows for
+// kTqBalRowsPerCu * CUs + num_seqs * num_q_heads (sequence, query head) partials.
+constexpr int kTqBalRowsPerCu = 128;  // 16 resident waves per CU x 8 query heads per group
+
 struct FastDecodeParams {
     const void* q;
     int64_t q_ss, q_sh;
@@ -43,7 +64,11 @@ struct FastDecodeParams {
     int sparse_pair; // Sparse-V running max per 32-token pair (block_size >= 32) instead of per tile
     float qp_mul;    // corr_scale * k_cscale
     int chunk, n_chunks;
-    float* ws_acc;   // [num_seqs][hq][n_chunks][128]
+    int balanced;     // balanced schedule (chunk and n_chunks unused)
+    int n_workers;    // balanced: resident waves of the launch (R before the min with P)
+    int len_cap;      // balanced: tokens of a sequence processed at most
+    int64_t* plan;    // balanced: [1 + num_seqs] int64 written by worker 0
+    float* ws_acc;   // chunks: [num_seqs][hq][n_chunks][128]; balanced: [slot][group][128]
     float* ws_m;     // [num_seqs][hq][n_chunks], log2 units
     float* ws_l;
     unsigned long long* skip_stats;

@@ -321,17 +321,28 @@ def plan_tokens_per_chunk(device: torch.device, num_seqs: int, num_q_heads: int,
                           share_codebook: bool = False, seq_lens_host=None, norm_row_bytes: int = 2) -> int:
     """tokens_per_chunk for tq_decode on this device and configuration.
 
-    Per-unit cost beyond its tiles: about fourteen tiles of set-up (the workgroup's LDS tables,
-    the query operands, the first loads; calibrated on MI355X with configs 3-5), plus writing
-    and re-reading its partial results (group heads x 128 fp32, twice) expressed in tiles of
-    K+V data.
+    With the sequence lengths known (seq_lens_host), fixed chunks from a round model whose
+    per-unit cost beyond its tiles is about fourteen tiles of set-up (the workgroup's LDS
+    tables, the query operands, the first loads; calibrated on MI355X with configs 3-5), plus
+    writing and re-reading its partial results (group heads x 128 fp32, twice) expressed in
+    tiles of K+V data, as long as its units fit in one round of resident waves: each wave then
+    runs one unit inside one sequence.  When they would need more rounds, or the lengths are
+    unknown, 0: the balanced schedule, every resident wave taking an equal share of all the
+    tile pairs (balanced_partition).  Measured on MI355X: config 5 (log-uniform 2K..128K,
+    several rounds) 387-390 us balanced vs 415-433 us in fixed chunks; config 3 (one round)
+    49.3 vs 52.3 us and config 4 (equal lengths, one round) 405-408 vs 412 us the other way.
     """
+    if seq_lens_host is None:
+        return 0
     group = num_q_heads // max(1, num_kv_heads)
     tile_bytes = 16 * (k_fmt.token_bytes + v_fmt.token_bytes)
     overhead = 14.0 + group * 1024.0 / tile_bytes
-    units = concurrent_units(device, k_fmt.bits, k_fmt.qjl, v_fmt.bits, num_q_heads, num_kv_heads,
+    slots = concurrent_units(device, k_fmt.bits, k_fmt.qjl, v_fmt.bits, num_q_heads, num_kv_heads,
                              norm_row_bytes, share_codebook)
-    return choose_tokens_per_chunk(num_seqs, num_kv_heads, max_seq_len, units, seq_lens_host, overhead)
+    chunk = choose_tokens_per_chunk(num_seqs, num_kv_heads, max_seq_len, slots, seq_lens_host, overhead)
+    msl = max(1, max_seq_len)
+    units = num_kv_heads * sum(-(-min(max(int(x), 0), msl) // chunk) for x in seq_lens_host)
+    return chunk if units <= slots else 0
 
 
 def concurrent_units(device: torch.device, k_bits: int, k_qjl: bool, v_bits: int, num_q_heads: int,
@@ -340,6 +351,43 @@ def concurrent_units(device: torch.device, k_bits: int, k_qjl: bool, v_bits: int
     idx = device.index if device.index is not None else torch.cuda.current_device()
     return _concurrent_units(idx, k_bits, bool(k_qjl), v_bits, num_q_heads, num_kv_heads, norm_row_bytes,
                              bool(share_codebook))
+
+
+def balanced_partition(seq_lens_host, num_kv_heads: int, workers: int, len_cap: int) -> dict:
+    """The split-K pieces of tq_decode's balanced schedule (tokens_per_chunk = 0): for every
+    (sequence, KV head) with tokens, the list of token ranges [t0, t1) that separate waves
+    process (each with its own running max; the merge combines them).
+
+    The work is the stream of 32-token tile pairs of the (sequence, KV head) segments, sequences
+    in order and a sequence's KV heads after each other (ceil(min(len, len_cap) / 32) pairs per
+    segment); with P pairs in all and R = min(P, workers) waves, wave w takes pairs
+    [floor(w P / R), floor((w + 1) P / R)).  workers is concurrent_units(...) of the
+    configuration and len_cap = min(max_seq_len, max_blocks_per_seq * block_size)."""
+    lens = [max(0, min(int(x), int(len_cap))) for x in seq_lens_host]
+    pairs = [(L + 31) // 32 for L in lens]
+    P = num_kv_heads * sum(pairs)
+    out = {}
+    if P == 0:
+        return out
+    R = min(P, int(workers))
+    pos = 0
+    for s, (L, n) in enumerate(zip(lens, pairs)):
+        for kh in range(num_kv_heads):
+            if n == 0:
+                continue
+            a, b = pos, pos + n
+            # worker boundaries strictly inside the segment
+            w = (a * R) // P + 1                      # first boundary index past a (floor(wP/R) > a)
+            while (w * P) // R <= a:
+                w += 1
+            cuts = [a]
+            while w < R and (w * P) // R < b:
+                cuts.append((w * P) // R)
+                w += 1
+            cuts.append(b)
+            out[(s, kh)] = [(32 * (c0 - a), min(L, 32 * (c1 - a))) for c0, c1 in zip(cuts[:-1], cuts[1:])]
+            pos = b
+    return out
 
 
 def _region(ptr: int, stride_block: int, stride_head: int, stride_row: int, stride_seq: int = 0) -> _lib.TQRegion:
@@ -502,7 +550,8 @@ def decode_paged(
         raise ValueError("centroid counts must match the formats' bit widths")
     # One tensor for both codebooks lets the kernel keep a single LDS pair table.
     share = kc.data_ptr() == vc.data_ptr()
-    chunk = tokens_per_chunk or plan_tokens_per_chunk(dev, S, Hq, Hkv, msl, k_fmt, v_fmt, share, seq_lens_host)
+    chunk = (plan_tokens_per_chunk(dev, S, Hq, Hkv, msl, k_fmt, v_fmt, share, seq_lens_host)
+             if tokens_per_chunk is None else int(tokens_per_chunk))
     kv = paged_view(k_cache, k_fmt, kc)
     vv = paged_view(v_cache, v_fmt, vc)
     return run_decode(
