@@ -1150,7 +1150,11 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     const bool fast = fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &big);
     // tokens_per_chunk = 0: the balanced schedule on the fast kernel; fixed chunks that fit the
     // same workspace on the general one
-    const bool balanced = tokens_per_chunk == 0 && fast;
+    // (the kernel keeps pair positions in 32 bits: at most num_seqs * num_kv_heads * ceil(len / 32))
+    const int bal_cap = max_blocks_per_seq * block_size;
+    const int bal_len = max_seq_len > 0 && max_seq_len < bal_cap ? max_seq_len : bal_cap;
+    const bool balanced = tokens_per_chunk == 0 && fast &&
+                          (int64_t)num_seqs * num_kv_heads * ((bal_len + 31) / 32) < (1ll << 31);
     if (tokens_per_chunk == 0 && !fast)
         tokens_per_chunk = general_chunk(num_seqs, num_q_heads, max_seq_len, sparse_pair);
     if (!balanced && sparse_pair && tokens_per_chunk % 32) tokens_per_chunk += 16;
@@ -1224,8 +1228,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
             const int64_t wmax = (int64_t)(rows / group) - (int64_t)num_seqs * num_kv_heads;
             f.balanced = 1;
             f.n_workers = (int)(waves < wmax ? waves : wmax);
-            const int cap = max_blocks_per_seq * block_size;
-            f.len_cap = max_seq_len > 0 && max_seq_len < cap ? max_seq_len : cap;
+            f.len_cap = bal_len;
             f.plan = reinterpret_cast<int64_t*>(ws);
             uint8_t* wsr = ws + bal_plan_bytes(num_seqs);
             f.ws_acc = reinterpret_cast<float*>(wsr);
@@ -1246,7 +1249,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.rot_qp = rotate && !q_proj;
         f.rot_out = rotate;
         f.wht_h = kWhtH;
-        if (grid > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
+        if (grid > (1 << 29)) return TQ_ERR_INVALID_ARGUMENT;  // unit indices stay below 2^31
         int frc = tq_decode_fast_launch(f, k->bits, k->qjl != 0, v->bits, grid, lds_total, (hipStream_t)stream);
         if (frc) return frc;
         return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,

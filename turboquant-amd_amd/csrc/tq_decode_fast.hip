@@ -386,17 +386,20 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t wv = (int64_t)blockIdx.x * 4 + wave;  // this wave's unit (chunks) or worker (balanced)
+    const int wv = (int)blockIdx.x * 4 + wave;  // this wave's unit (chunks) or worker (balanced)
     const int cap = p.max_blocks * p.block_size;
 
     // ---- this wave's work, settled before the tables are built: idle workgroups skip them ----
     // Balanced schedule: the pair range [bal_pos, bal_end) of worker wv and the sequence bal_s
     // (bal_np pairs per KV head, bal_q pairs per KV head before it) that holds its first pair.
-    int64_t bal_pos = 0, bal_end = 0, bal_q = 0;
+    int bal_pos = 0, bal_end = 0, bal_q = 0;  // below 2^31 pairs (checked on the host)
     int bal_s = 0, bal_np = 0;
     if (p.balanced) {
-        int64_t tot = 0;
-        for (int b = 0; b < p.num_seqs; b += 64) {
+        // the first 64 sequences' pairs and prefix sums are kept for the second pass
+        const uint32_t np0 = lane < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[lane], p.len_cap) : 0u;
+        const uint32_t incl0 = wave_incl_scan_u32(np0);
+        int64_t tot = (int64_t)__builtin_amdgcn_readlane(incl0, 63);
+        for (int b = 64; b < p.num_seqs; b += 64) {
             const int sl = b + lane;
             const uint32_t np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
             tot += (int64_t)__builtin_amdgcn_readlane(wave_incl_scan_u32(np), 63);
@@ -405,16 +408,19 @@ void decode_fast_kernel(FastDecodeParams p) {
         const int64_t R = P < p.n_workers ? P : (int64_t)p.n_workers;
         const bool planner = wv == 0;  // writes the plan the merge reads
         if (wv < R) {
-            bal_pos = tq_bal_begin(wv, P, R);
-            bal_end = tq_bal_begin(wv + 1, P, R);
+            bal_pos = (int)tq_bal_begin(wv, P, R);
+            bal_end = (int)tq_bal_begin(wv + 1, P, R);
         }
         if (planner || wv < R) {
             int64_t carry = 0;
             bool found = wv >= R;
             for (int b = 0; b < p.num_seqs; b += 64) {
                 const int sl = b + lane;
-                const uint32_t np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
-                const uint32_t incl = wave_incl_scan_u32(np);
+                uint32_t np = np0, incl = incl0;
+                if (b > 0) {
+                    np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
+                    incl = wave_incl_scan_u32(np);
+                }
                 if (planner && sl < p.num_seqs) p.plan[1 + sl] = carry + (int64_t)(incl - np);
                 if (!found) {
                     const uint64_t m =
@@ -423,7 +429,7 @@ void decode_fast_kernel(FastDecodeParams p) {
                         const int l = __builtin_ctzll(m);
                         bal_s = b + l;
                         bal_np = (int)__builtin_amdgcn_readlane(np, l);
-                        bal_q = carry + (int64_t)__builtin_amdgcn_readlane(incl, l) - bal_np;
+                        bal_q = (int)(carry + (int64_t)__builtin_amdgcn_readlane(incl, l)) - bal_np;
                         found = true;
                     }
                 }
@@ -451,6 +457,8 @@ void decode_fast_kernel(FastDecodeParams p) {
         }
         if (!any) return;
     }
+    // ---- LDS tables (one share per thread of the workgroup) ----
+    {
     if (KQJL) {
         // entry e (one per thread): 8 sign bits -> 8 fp4 values +1 (0x2) / -1 (0xA)
         uint32_t w = 0;
@@ -498,6 +506,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>(), 0);
     if (vown) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>(), 1);
     __syncthreads();
+    }
 
     const int g = lane >> 4;
     const int n = lane & 15;
@@ -526,11 +535,11 @@ void decode_fast_kernel(FastDecodeParams p) {
 
     // Balanced schedule: the KV head and the pair offset of bal_pos inside its segment.
     int kh_b = 0;
-    int64_t pp = 0;
+    int pp = 0;
     if (p.balanced && bal_pos < bal_end) {
-        const int64_t off = bal_pos - bal_q * p.hkv;
-        kh_b = (int)(off / bal_np);
-        pp = off - (int64_t)kh_b * bal_np;
+        const int off = bal_pos - bal_q * p.hkv;
+        kh_b = off / bal_np;
+        pp = off - kh_b * bal_np;
     }
     unsigned long long cnt_tot = 0, cnt_kept = 0;
 
@@ -539,16 +548,16 @@ void decode_fast_kernel(FastDecodeParams p) {
     // waves of a workgroup get the same chunk of one sequence).  Balanced: the segments the
     // worker's pair range crosses.
     for (;;) {
-    int64_t s;
+    int s;
     int kh, L, t_begin, t_end;
     bool direct;           // the piece is the whole sequence: write the output here
-    int64_t prow_base;     // partial row of the group's first head
-    int64_t prow_step;     // rows between the group's heads
-    int64_t take = 0;      // balanced: pairs of this piece
+    int prow_base;         // partial row of the group's first head
+    int prow_step;         // rows between the group's heads
+    int take = 0;          // balanced: pairs of this piece
     if (!p.balanced) {
-        kh = (int)(wv % p.hkv);
-        const int64_t sc_ = wv / p.hkv;
-        const int ci = (int)(sc_ % p.n_chunks);
+        kh = wv % p.hkv;
+        const int sc_ = wv / p.hkv;
+        const int ci = sc_ % p.n_chunks;
         s = sc_ / p.n_chunks;
         if (s >= p.num_seqs) break;
         L = p.seq_lens[s];
@@ -560,7 +569,7 @@ void decode_fast_kernel(FastDecodeParams p) {
         nch = nch < p.n_chunks ? nch : p.n_chunks;
         // (a rotated output is written by decode_reduce_kernel, which takes single chunks too)
         direct = nch == 1 && !p.rot_out;
-        prow_base = (s * p.hq + (int64_t)kh * p.group) * p.n_chunks + ci;
+        prow_base = (s * p.hq + kh * p.group) * p.n_chunks + ci;
         prow_step = p.n_chunks;
     } else {
         if (bal_pos >= bal_end) break;
@@ -568,92 +577,14 @@ void decode_fast_kernel(FastDecodeParams p) {
         kh = kh_b;
         L = p.seq_lens[s];
         L = L < p.len_cap ? L : p.len_cap;
-        take = (int64_t)bal_np - pp;
+        take = bal_np - pp;
         take = take < bal_end - bal_pos ? take : bal_end - bal_pos;
-        t_begin = (int)(32 * pp);
-        t_end = (int)(32 * (pp + take));
+        t_begin = 32 * pp;
+        t_end = 32 * (pp + take);
         t_end = t_end < L ? t_end : L;
         direct = pp == 0 && take == bal_np && !p.rot_out;
         prow_base = (wv + s * p.hkv + kh) * p.group;
         prow_step = 1;
-    }
-
-    // ---- query operands ----
-    const int head = kh * p.group + hcol;
-    const bool hvalid = hcol < p.group;
-    c.hmask = __builtin_amdgcn_ballot_w64(hvalid);
-    {
-        float qv[32];
-        const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
-        if (hvalid && p.q_vec) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) tq_load8(p.q, qoff + 8 * i, p.q_dtype, &qv[8 * i]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 32; ++i) qv[i] = hvalid ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
-        }
-        if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);  // q x H: elements 32g + i
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) c.qop[cc][j] = (_Float16)qv[8 * cc + j];
-    }
-    if (KQJL) {
-        // fp8 operand element m (byte m of 32) of lane group g is dim (m < 16 ? 0 : 64) + 16 g + (m & 15)
-        // (the pairing of an fp4 A operand with an fp8 B operand in the 16x16x128 MFMA).
-        float x[32];
-        const int64_t off = s * p.qp_ss + (int64_t)head * p.qp_sh + 16 * g;
-        if (hvalid && p.q_vec) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                tq_load8(p.qp, off + 8 * i, p.q_dtype, &x[8 * i]);
-                tq_load8(p.qp, off + 64 + 8 * i, p.q_dtype, &x[16 + 8 * i]);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                x[i] = hvalid ? tq_load1(p.qp, off + i, p.q_dtype) : 0.f;
-                x[16 + i] = hvalid ? tq_load1(p.qp, off + 64 + i, p.q_dtype) : 0.f;
-            }
-        }
-        // q x H: x[i] is element 16g + (i & 15) + 64 (i >> 4), so register bits 0-3 and 4 are
-        // element bits 0-3 and 6, lane bits 4-5 element bits 4-5
-        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);
-        // One E8M0 scale per column (query head): a lane's 32 fp8 elements straddle two of the
-        // instruction's 32-wide scale blocks (dims 16g.. and 64 + 16g..), so the scale is uniform
-        // over the column's four lane groups; a head whose q_proj is orders of magnitude below
-        // its group's largest still gets its own exponent and keeps its precision.
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            x[i] *= p.qp_mul;
-            amax = fmaxf(amax, fabsf(x[i]));
-        }
-        amax = max_over_groups(amax);  // lanes col, col ^ 16, col ^ 32, col ^ 48
-        // 2^b brings the head's largest magnitude into [128, 256): inside the fp8 e4m3 normal range
-        int b = 0;
-        if (amax > 0.f && amax < __builtin_huge_valf()) b = 7 - ilogbf(amax);
-        b = b < -100 ? -100 : (b > 100 ? 100 : b);
-        c.sc_hi = 127 - b;
-        c.sc_lo = 127 - b - 4;
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            float xs[4], rs[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) xs[k] = ldexpf(x[4 * d + k], b);
-            int wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[0], xs[1], 0, false);
-            wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[2], xs[3], wh, true);
-            rs[0] = (xs[0] - __builtin_amdgcn_cvt_f32_fp8(wh, 0)) * 16.f;
-            rs[1] = (xs[1] - __builtin_amdgcn_cvt_f32_fp8(wh, 1)) * 16.f;
-            rs[2] = (xs[2] - __builtin_amdgcn_cvt_f32_fp8(wh, 2)) * 16.f;
-            rs[3] = (xs[3] - __builtin_amdgcn_cvt_f32_fp8(wh, 3)) * 16.f;
-            int wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[0], rs[1], 0, false);
-            wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[2], rs[3], wl, true);
-            c.qph[d] = wh;
-            c.qpl[d] = wl;
-        }
-    } else {
-        c.sc_hi = c.sc_lo = 127;
     }
 
     // One descriptor per head (tiles at 32-bit scalar offsets from it), or, for a cache spanning
@@ -816,6 +747,96 @@ void decode_fast_kernel(FastDecodeParams p) {
         vr.vn[1] = a[1];
     };
 
+    // ---- query operands: loads (converted once the first pair's loads are issued, so the
+    // block-table, query and first K/V round trips overlap) ----
+    const int head = kh * p.group + hcol;
+    const bool hvalid = hcol < p.group;
+    c.hmask = __builtin_amdgcn_ballot_w64(hvalid);
+    float qv[32];
+    {
+        const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
+        if (hvalid && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tq_load8(p.q, qoff + 8 * i, p.q_dtype, &qv[8 * i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) qv[i] = hvalid ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
+        }
+    }
+    // fp8 operand element m (byte m of 32) of lane group g is dim (m < 16 ? 0 : 64) + 16 g + (m & 15)
+    // (the pairing of an fp4 A operand with an fp8 B operand in the 16x16x128 MFMA).
+    float x[32];
+    if constexpr (KQJL) {
+        const int64_t off = s * p.qp_ss + (int64_t)head * p.qp_sh + 16 * g;
+        if (hvalid && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                tq_load8(p.qp, off + 8 * i, p.q_dtype, &x[8 * i]);
+                tq_load8(p.qp, off + 64 + 8 * i, p.q_dtype, &x[16 + 8 * i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                x[i] = hvalid ? tq_load1(p.qp, off + i, p.q_dtype) : 0.f;
+                x[16 + i] = hvalid ? tq_load1(p.qp, off + 64 + i, p.q_dtype) : 0.f;
+            }
+        }
+    }
+    // All data of a pair is loaded one pair ahead (two register sets).  Pairs past the end read
+    // block data that is never used (every fetch issues the same loads, which keeps the
+    // compiler's outstanding-load counts exact).
+    KRaw<KB, KQJL> kr[2];
+    PairInfo info[2];
+    VRaw<VB> vr[2];
+    fetch_k(0, kr[0], info[0]);
+    load_v(info[0], vr[0]);
+    // ---- query operands: conversion ----
+    if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);  // q x H: elements 32g + i
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c.qop[cc][j] = (_Float16)qv[8 * cc + j];
+    if constexpr (KQJL) {
+        // q x H: x[i] is element 16g + (i & 15) + 64 (i >> 4), so register bits 0-3 and 4 are
+        // element bits 0-3 and 6, lane bits 4-5 element bits 4-5
+        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);
+        // One E8M0 scale per column (query head): a lane's 32 fp8 elements straddle two of the
+        // instruction's 32-wide scale blocks (dims 16g.. and 64 + 16g..), so the scale is uniform
+        // over the column's four lane groups; a head whose q_proj is orders of magnitude below
+        // its group's largest still gets its own exponent and keeps its precision.
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            x[i] *= p.qp_mul;
+            amax = fmaxf(amax, fabsf(x[i]));
+        }
+        amax = max_over_groups(amax);  // lanes col, col ^ 16, col ^ 32, col ^ 48
+        // 2^b brings the head's largest magnitude into [128, 256): inside the fp8 e4m3 normal range
+        int b = 0;
+        if (amax > 0.f && amax < __builtin_huge_valf()) b = 7 - ilogbf(amax);
+        b = b < -100 ? -100 : (b > 100 ? 100 : b);
+        c.sc_hi = 127 - b;
+        c.sc_lo = 127 - b - 4;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            float xs[4], rs[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xs[k] = ldexpf(x[4 * d + k], b);
+            int wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[0], xs[1], 0, false);
+            wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[2], xs[3], wh, true);
+            rs[0] = (xs[0] - __builtin_amdgcn_cvt_f32_fp8(wh, 0)) * 16.f;
+            rs[1] = (xs[1] - __builtin_amdgcn_cvt_f32_fp8(wh, 1)) * 16.f;
+            rs[2] = (xs[2] - __builtin_amdgcn_cvt_f32_fp8(wh, 2)) * 16.f;
+            rs[3] = (xs[3] - __builtin_amdgcn_cvt_f32_fp8(wh, 3)) * 16.f;
+            int wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[0], rs[1], 0, false);
+            wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[2], rs[3], wl, true);
+            c.qph[d] = wh;
+            c.qpl[d] = wl;
+        }
+    } else {
+        c.sc_hi = c.sc_lo = 127;
+    }
+
     Softmax st;
     st.m = kNegInf;
     st.lsum = 0.f;
@@ -826,14 +847,6 @@ void decode_fast_kernel(FastDecodeParams p) {
 
     const int ntiles = (t_end - t_begin + 15) >> 4;
     const int npairs = (ntiles + 1) >> 1;
-    // All data of a pair is loaded one pair ahead (two register sets).  Pairs past the end read
-    // block data that is never used (every fetch issues the same loads, which keeps the
-    // compiler's outstanding-load counts exact).
-    KRaw<KB, KQJL> kr[2];
-    PairInfo info[2];
-    VRaw<VB> vr[2];
-    fetch_k(0, kr[0], info[0]);
-    load_v(info[0], vr[0]);
     for (int i = 0; i < npairs; i += 2) {
         fetch_k(i + 1, kr[1], info[1]);
         load_v(info[1], vr[1]);
