@@ -2,8 +2,10 @@
 //
 // One 128-dim row per 4 lanes (32 dims each), so a wave64 works on 16 rows and a 256-thread
 // workgroup on 64 rows.  The Walsh-Hadamard rotation is 5 in-register butterfly stages (dim
-// bits 0-4) plus 2 cross-lane stages (DPP, no LDS); indices come from a 257-cell LDS table of
-// the boundaries (one compare per value); each lane stores its 4 * bits packed bytes at once.
+// bits 0-4; for 16-bit inputs the first one is a v_dot2 that also converts to fp32) plus 2
+// cross-lane stages (DPP, no LDS); indices come from an LDS cell table of the boundaries (129
+// cells in the paged kernels, 257 for polarquant_compress; one compare per value); each lane
+// stores its 4 * bits packed bytes at once.
 // Row math follows turboquant/core/quantizer.py:141-174:
 //   x_rot = x @ H; norm = |x_rot|; x_n = x_rot / (norm + 1e-8); idx = #{b < x_n};
 //   r = (x_n - c[idx]) * norm; rnorm = |r|; sign = r >= 0.
@@ -141,6 +143,99 @@ __device__ __forceinline__ void wht_row(float (&v)[32], int q, float h) {
     for (int k = 0; k < 32; ++k) v[k] *= hs;
 }
 
+// A lane's 32 input elements of a row as raw words: 4 x 16 bytes for 16-bit types, 8 x 16 for fp32.
+template <int DT>
+struct RawRow {
+    tq_u32x4 w[DT == TQ_F32 ? 8 : 4];
+};
+template <int DT>
+__device__ __forceinline__ void load_raw(const void* base, int64_t off, RawRow<DT>& r) {
+    constexpr int N = DT == TQ_F32 ? 8 : 4;
+    const tq_u32x4* p = DT == TQ_F32 ? reinterpret_cast<const tq_u32x4*>(static_cast<const float*>(base) + off)
+                                     : reinterpret_cast<const tq_u32x4*>(static_cast<const uint16_t*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < N; ++i) r.w[i] = p[i];
+}
+template <int DT>
+__device__ __forceinline__ void raw_to_float(const RawRow<DT>& r, float (&v)[32]) {
+#pragma unroll
+    for (int i = 0; i < (DT == TQ_F32 ? 8 : 4); ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t w = r.w[i][k];
+            if (DT == TQ_F32) {
+                v[4 * i + k] = __uint_as_float(w);
+            } else if (DT == TQ_BF16) {
+                v[8 * i + 2 * k] = tq_bf16_to_f32(w & 0xffffu);
+                v[8 * i + 2 * k + 1] = tq_bf16_to_f32(w >> 16);
+            } else {
+                v[8 * i + 2 * k] = tq_f16_to_f32(w & 0xffffu);
+                v[8 * i + 2 * k + 1] = tq_f16_to_f32(w >> 16);
+            }
+        }
+}
+
+// The paged kernels' rotation without its scale: v <- x H (H the +-1 Sylvester matrix), so that
+// y = h v.  The lane's inputs enter multiplied by sigma = (-1)^(q bit 0 + q bit 1); the cross-lane
+// stages then compute own - partner in the lower lane and own + partner in the upper, and each
+// leaves the right sign (a lower lane's partner arrives negated relative to it, stage by stage),
+// so no final negation or scale pass is needed.  16-bit inputs: the first stage (dims bit 0, the
+// two halves of a loaded dword) is one v_dot2_f32 per output with weights sigma (1, 1) and
+// sigma (1, -1), which also does the conversion to fp32.
+template <int DT>
+__device__ __forceinline__ void rotate_unscaled(const RawRow<DT>& r, int q, float (&v)[32]) {
+    const bool neg = ((q ^ (q >> 1)) & 1) != 0;
+    if (DT == TQ_F32) {
+        raw_to_float<DT>(r, v);
+        const float sg = neg ? -1.f : 1.f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) v[k] *= sg;
+#pragma unroll
+        for (int k = 0; k < 32; k += 2) {
+            const float u = v[k], w = v[k + 1];
+            v[k] = u + w;
+            v[k + 1] = u - w;
+        }
+    } else {
+        // weights (lo, hi) as 16-bit pairs: +1 = 0x3F80 (bf16) / 0x3C00 (f16), sign bit 0x8000
+        const uint32_t one = DT == TQ_BF16 ? 0x3F803F80u : 0x3C003C00u;
+        const uint32_t wp = neg ? (one | 0x80008000u) : one;   // sigma ( 1,  1)
+        const uint32_t wm = wp ^ 0x80000000u;                  // sigma ( 1, -1)
+        // The eight products of one 16-byte word group sit in one asm block that ends in wait
+        // states: a dot2 result read by the next VALU instruction or the one after it was read
+        // stale (measured: a compiler-scheduled read one instruction later gave wrong rotations).
+#define TQ_DOT2_8(OP)                                                                                      \
+    asm(OP " %0, %8, %12, 0\n\t" OP " %1, %8, %13, 0\n\t" OP " %2, %9, %12, 0\n\t" OP " %3, %9, %13, 0\n\t" \
+        OP " %4, %10, %12, 0\n\t" OP " %5, %10, %13, 0\n\t" OP " %6, %11, %12, 0\n\t" OP " %7, %11, %13, 0\n\t" \
+        "s_nop 3"                                                                                          \
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7]) \
+        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(wp), "v"(wm))
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const tq_u32x4 w = r.w[i];
+            float o[8];
+            if (DT == TQ_BF16) TQ_DOT2_8("v_dot2_f32_bf16");
+            else TQ_DOT2_8("v_dot2_f32_f16");
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[8 * i + k] = o[k];
+        }
+#undef TQ_DOT2_8
+    }
+#pragma unroll
+    for (int b = 2; b < 32; b <<= 1) {
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            if (!(k & b)) {
+                const float u = v[k], w = v[k | b];
+                v[k] = u + w;
+                v[k | b] = u - w;
+            }
+        }
+    }
+    fmac_dpp32<kDppXor1>(v, (q & 1) ? 1.f : -1.f);
+    fmac_dpp32<kDppXor2>(v, (q & 2) ? 1.f : -1.f);
+}
+
 // Left searchsorted over NB sorted boundaries (count of boundaries < x) for |x| <= 1 through a
 // table of 256 cells of width 1/128 over [-1, 1] (plus one cell for x = 1): cell k holds
 // c0 = #{b < edge_k - eps} and the one boundary inside [edge_k - eps, edge_k+1 + eps] (or +inf),
@@ -176,20 +271,24 @@ __device__ __forceinline__ int quant_linear(float x, const float (&bd)[NB]) {
     return x != x ? NB : cnt;
 }
 
-// Paged mode: round-to-nearest cells and decisions on y itself.  Cell k (0..256) covers
-// 128 x + 128 in [k - 1/2, k + 1/2] and holds c0 = #{b < lo_k - eps} and the one boundary inside
-// [lo_k - eps, hi_k + eps] (or +inf); the cell of x = y / den is the low mantissa bits of
-// fl(y (128 / den) + 128 + 1.5 * 2^23) (one fma; a tie lands in either neighbour, both cover it,
-// and the approximate 128 / den moves x by far less than eps).  The decision b < y / den is the
-// sign of b den - y, one fma of the exact product (den > 0): exact for this y, with no rounded
-// quotient in between.
-constexpr float kCellMagic = 12583040.f;          // 1.5 * 2^23 + 128
+// Paged mode: round-to-nearest cells and decisions on z itself.  Cell k (0..128) covers
+// 64 x + 64 in [k - 1/2, k + 1/2] and holds c0 = #{b < lo_k - eps} and the one boundary inside
+// [lo_k - eps, hi_k + eps] (or +inf); the cell of x = z / den is the low mantissa bits of
+// fl(z (64 / den) + 64 + 1.5 * 2^23) (one fma; a tie lands in either neighbour, both cover it,
+// and the approximate 64 / den moves x by far less than eps).  The decision b < z / den is the
+// sign of b den - z, one fma of the exact product (den > 0): exact for this z, with no rounded
+// quotient in between.  Cells of width 1/64 (the d = 128 codebooks keep at least 0.023 between
+// boundaries): the cells a row's values fall in (x ~ N(0, 1/128)) then lie within one period of
+// the LDS banks, which the 1/128 table's lookups did not (measured: 2.5 % faster on config 2).
+constexpr int kCellsRn = 129;
+constexpr float kCellsRnScale = 64.f;
+constexpr float kCellMagic = 12583040.f - 64.f;   // 1.5 * 2^23 + 64
 constexpr uint32_t kCellMagicBase = 0x4B400000u;  // bits of 1.5 * 2^23
 template <int NB>
 __device__ __forceinline__ void build_cells_rn(const float (&bd)[NB], const float* boundaries, uint2* tab, int* bad) {
     constexpr float eps = 1e-5f;
-    for (int k = threadIdx.x; k < kCells; k += blockDim.x) {
-        const float lo = ((float)k - 128.5f) * (1.f / 128.f) - eps, hi = ((float)k - 127.5f) * (1.f / 128.f) + eps;
+    for (int k = threadIdx.x; k < kCellsRn; k += blockDim.x) {
+        const float lo = ((float)k - 64.5f) * (1.f / 64.f) - eps, hi = ((float)k - 63.5f) * (1.f / 64.f) + eps;
         int c0 = 0, c1 = 0;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
@@ -201,9 +300,9 @@ __device__ __forceinline__ void build_cells_rn(const float (&bd)[NB], const floa
         tab[k] = make_uint2(__float_as_uint(b), (uint32_t)c0);
     }
 }
-__device__ __forceinline__ int quant_cell_y(float y, float den, float r128, const uint2* tab) {
-    const uint2 e = tab[__float_as_uint(__builtin_fmaf(y, r128, kCellMagic)) - kCellMagicBase];
-    return (int)e.y + (__builtin_fmaf(__uint_as_float(e.x), den, -y) < 0.f ? 1 : 0);
+__device__ __forceinline__ int quant_cell_y(float z, float den, float rscale, const uint2* tab) {
+    const uint2 e = tab[__float_as_uint(__builtin_fmaf(z, rscale, kCellMagic)) - kCellMagicBase];
+    return (int)e.y + (__builtin_fmaf(__uint_as_float(e.x), den, -z) < 0.f ? 1 : 0);
 }
 
 // ---- values tile layout ----
@@ -347,6 +446,8 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
     else build_cells<NB>(bd, p.boundaries, s_cells, &s_bad);
     __syncthreads();
     const bool cells = s_bad == 0;
+    // 1e-8 in the units of the unscaled rotation (paged mode)
+    const float den_eps = (MODE == MODE_PAGED && p.rotate) ? 1e-8f / p.wht_scale : 1e-8f;
 
     const int q = threadIdx.x & 3;              // dims 32q..32q+31
     const int row_in_wg = threadIdx.x >> 2;     // 0..63
@@ -376,34 +477,56 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
             tok = row_ok ? row : 0;
         }
 
+        // Rows that are not written (padding, past the end) read token 0 of head 0, a row of the
+        // same launch, and their results are dropped: no separate zero fill.
+        int64_t off;
+        if (p.idx32) off = (uint32_t)tok * (uint32_t)p.x_stride_token + (uint32_t)head * (uint32_t)p.x_stride_head + 32u * q;
+        else off = tok * p.x_stride_token + head * p.x_stride_head + 32 * q;
+        RawRow<DT> raw;
+        load_raw<DT>(p.x, off, raw);
         float v[32];
-        if (row_ok) {
-            int64_t off;
-            if (p.idx32) off = (uint32_t)tok * (uint32_t)p.x_stride_token + (uint32_t)head * (uint32_t)p.x_stride_head + 32u * q;
-            else off = tok * p.x_stride_token + head * p.x_stride_head + 32 * q;
+        float norm, den, rcp;
+        bool fast;
+        if (MODE == MODE_PAGED) {
+            // v = z, y = scale z (the rotation's scale h, or 1 without rotation)
+            if (p.rotate) rotate_unscaled<DT>(raw, q, v);
+            else raw_to_float<DT>(raw, v);
+            const float scale = p.rotate ? p.wht_scale : 1.f;
+            const float nz = __builtin_sqrtf(row_sumsq(v));
+            fast = cells && !__builtin_amdgcn_ballot_w64(!(nz < __builtin_huge_valf()));
+            if (fast) {
+                // x_n = y / (|y| + 1e-8) = z / (|z| + 1e-8 / scale): decisions on z and this
+                // denominator; 128 / den only places the lookup cell, an approximate reciprocal
+                // does (it moves x by far less than the cells' eps)
+                norm = nz * scale;
+                den = nz + den_eps;
+                rcp = __builtin_amdgcn_rcpf(den);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) tq_load8(p.x, off + 8 * i, DT, &v[8 * i]);
+                for (int k = 0; k < 32; ++k) v[k] *= scale;
+                norm = __builtin_sqrtf(row_sumsq(v));
+                den = norm + 1e-8f;
+                rcp = 1.0f / den;
+            }
         } else {
-#pragma unroll
-            for (int k = 0; k < 32; ++k) v[k] = 0.f;
+            raw_to_float<DT>(raw, v);
+            if (p.rotate) wht_row(v, q, p.wht_scale);
+            norm = __builtin_sqrtf(row_sumsq(v));
+            den = norm + 1e-8f;
+            rcp = 1.0f / den;
+            // |x| <= 1 unless the norm is not finite (then x may be NaN: searchsorted puts it last)
+            fast = cells && !__builtin_amdgcn_ballot_w64(!(norm < __builtin_huge_valf()));
         }
-        if (p.rotate) wht_row(v, q, p.wht_scale);
-
-        const float norm = __builtin_sqrtf(row_sumsq(v));
-        const float den = norm + 1e-8f;
-        const float rcp = 1.0f / den;
-        // |x| <= 1 unless the norm is not finite (then x may be NaN: searchsorted puts it last)
-        const bool fast = cells && !__builtin_amdgcn_ballot_w64(!(norm < __builtin_huge_valf()));
 
         int idx[32];
         float rn = 0.f;
         uint32_t sbits = 0;
         if (MODE == MODE_PAGED && fast) {
-            // decisions on y = x_rot itself (x_n = y / den is never formed); with QJL the
-            // residual r = (x_n - c) norm = (y - c den) (norm / den), its sign that of one fma
-            const float r128 = 128.f * rcp;
+            // decisions on z itself (x_n = z / den is never formed); with QJL the residual
+            // r = (x_n - c) norm = (z - c den) (norm / den), its sign that of one fma
+            const float rscale = kCellsRnScale * rcp;
 #pragma unroll
-            for (int k = 0; k < 32; ++k) idx[k] = quant_cell_y(v[k], den, r128, s_cells);
+            for (int k = 0; k < 32; ++k) idx[k] = quant_cell_y(v[k], den, rscale, s_cells);
             if (QJL) {
                 float r[32];
 #pragma unroll
@@ -411,7 +534,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                     r[k] = __builtin_fmaf(-s_cent[idx[k]], den, v[k]);
                     sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
                 }
-                rn = __builtin_sqrtf(row_sumsq(r)) * (norm * rcp);
+                rn = __builtin_sqrtf(row_sumsq(r)) * (norm / den);
                 if (norm == 0.f) sbits = 0xffffffffu;  // r = (0 - c) 0 = +-0: sign(0) counts as +1
             }
         } else {
