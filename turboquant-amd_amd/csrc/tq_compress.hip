@@ -305,6 +305,41 @@ __device__ __forceinline__ int quant_cell_y(float z, float den, float rscale, co
     return (int)e.y + (__builtin_fmaf(__uint_as_float(e.x), den, -z) < 0.f ? 1 : 0);
 }
 
+// The lane's 32 indices as 4 * BITS bytes of the little-endian BITS-bit stream.  2 and 4 bits
+// (fields never straddle a word): a tree of v_lshl_or_b32, one per field after the first of
+// each word (the compiler's form took a shift per field and an or3 per two).
+__device__ __forceinline__ uint32_t lshl_or(uint32_t a, int sh, uint32_t b) {
+    uint32_t r;
+    asm("v_lshl_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "i"(sh), "v"(b));
+    return r;
+}
+template <int BITS>
+__device__ __forceinline__ void pack_stream(const int (&idx)[32], uint32_t (&w)[BITS]) {
+    if constexpr (BITS == 4 || BITS == 2) {
+        constexpr int F = 32 / BITS;  // fields per word
+#pragma unroll
+        for (int j = 0; j < BITS; ++j) {
+            uint32_t t[F];
+#pragma unroll
+            for (int k = 0; k < F; ++k) t[k] = (uint32_t)idx[F * j + k];
+#pragma unroll
+            for (int span = 1, sh = BITS; span < F; span *= 2, sh *= 2)
+#pragma unroll
+                for (int k = 0; k < F; k += 2 * span) t[k] = lshl_or(t[k + span], sh, t[k]);
+            w[j] = t[0];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < BITS; ++j) w[j] = 0;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            const int pos = BITS * k, wi = pos >> 5, sh = pos & 31;
+            w[wi] |= (uint32_t)idx[k] << sh;
+            if (sh + BITS > 32) w[wi + 1] |= (uint32_t)idx[k] >> (32 - sh);
+        }
+    }
+}
+
 // ---- values tile layout ----
 // Chunk 16g + n of a 16-row sub-tile (4 * BITS bytes) holds, at field 4j + r (BITS bits each,
 // little-endian), dim 8n + j of row 4g + r: the four rows' fields of one dim are adjacent, so a
@@ -604,14 +639,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
             }
             // this lane's 32 indices: 4 * BITS bytes of the row's little-endian bit stream
             uint32_t w[BITS];
-#pragma unroll
-            for (int j = 0; j < BITS; ++j) w[j] = 0;
-#pragma unroll
-            for (int k = 0; k < 32; ++k) {
-                const int pos = BITS * k, wi = pos >> 5, sh = pos & 31;
-                w[wi] |= (uint32_t)idx[k] << sh;
-                if (sh + BITS > 32) w[wi + 1] |= (uint32_t)idx[k] >> (32 - sh);
-            }
+            pack_stream<BITS>(idx, w);
             if (write) {
                 if (p.tile_layout == TQ_TILE_KEYS) {
                     // chunk (4n + q) of the row's 16-row sub-tile: index bytes, then sign bytes
