@@ -577,7 +577,8 @@ def main():
                                                     "note": "MI355X Triton, shape unstated (README.md:102-103)"}}
     if mfma is not None:
         details["mfma_busy_fraction_headline"] = mfma
-    for name, prof in (("config5", "decode_fast_kernel_config5_pmc.md"), ("prefill", "prefill_kernel_4x4096_pmc.md")):
+    for name, prof in (("config3", "decode_fast_kernel_config3_pmc.md"), ("config5", "decode_fast_kernel_config5_pmc.md"),
+                       ("prefill", "prefill_kernel_4x4096_pmc.md")):
         v = profile_value(prof, "mfma_busy_fraction")
         if v is not None:
             details.setdefault("mfma_busy_fraction_by_kernel", {})[name] = v
