@@ -390,6 +390,17 @@ def published_shapes(dev, steps, warmup):
     return out
 
 
+# batch and sequence length of each workload as the bench line's config states them (the
+# longest context where the lengths vary)
+WORKLOAD_SHAPE = {
+    "config4": {"global_batch": 64, "seq_len": 32768},
+    "config3": {"global_batch": 32, "seq_len": 8192},
+    "config5": {"global_batch": 64, "seq_len": 131072},
+    "config2": {"global_batch": 16384, "seq_len": 1},
+    "prefill": {"global_batch": 4, "seq_len": 4096},
+}
+
+
 def profile_value(name, key):
     """A `key: value` line of a committed rocprof summary under profiles/ (None if absent)."""
     path = ROOT / "profiles" / name
@@ -598,7 +609,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": head["workload"], "global_batch": 64, "seq_len": 32768, "parallelism": "none"},
+        "config": {"workload": head["workload"], **WORKLOAD_SHAPE.get(head["workload"].split(":")[0], {}),
+                   "parallelism": "none"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(head.get("hbm_gbs", head.get("compress_gbs", 0.0)), 2),
