@@ -52,10 +52,19 @@ struct CompressParams {
 // a wave works on 16 rows and a 256-thread workgroup on 64.  Five Hadamard stages (dims bits
 // 0-4) run in registers, two (dims bits 5, 6 = lane bits 0, 1) through DPP quad_perm.
 constexpr int kRowsPerWG = 64;
-// Grid cap of the grid-stride compress launches: 256 CUs x 5 resident 256-thread workgroups
-// (89 VGPRs allow 5 waves per SIMD).  Measured on config-2 shapes (131,072 rows): 1280 beats
-// 2048 (one group per workgroup) and 512 / 768; the fused K + V launch is best near 2 x 1024.
-constexpr int kCompressGrid = 1280;
+// Grid of the grid-stride compress launches: one round of the workgroups the device holds at
+// once (CUs x resident 256-thread workgroups of the kernel instance, from the occupancy query),
+// so every workgroup builds its LDS table once and no second, partial round is left over.
+// Measured on config 2 (fused K + V, 4 resident workgroups per CU): 512 per tensor (one round)
+// 23.8 us, 1024 (two rounds) 23.9-24.1 us, 768 24.6 us, 1536 25.1 us, 2048 25.8 us.
+template <typename K>
+int resident_grid(K kernel) {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, 256, 0) != hipSuccess || per <= 0 || cus <= 0)
+        return 1024;
+    return per * cus;
+}
 constexpr int kDppXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
 template <int CTRL>
@@ -698,11 +707,14 @@ __global__ __launch_bounds__(256) void compress_kv_kernel(CompressParams pk, Com
 template <int MODE>
 int launch_compress(const CompressParams& p, int bits, int qjl, hipStream_t stream) {
     if (p.n_rows <= 0) return TQ_OK;
-    // Workgroups loop over 64-row groups.  At most kCompressGrid of them: as many as are
-    // resident at once, so the per-workgroup LDS set-up is paid once per resident slot.
-    int64_t groups = (p.n_rows + kRowsPerWG - 1) / kRowsPerWG;
-    int grid = (int)(groups < kCompressGrid ? groups : kCompressGrid);
-#define TQ_LAUNCH_DT(B, Q, DT) hipLaunchKernelGGL((compress_kernel<B, Q, MODE, DT>), dim3(grid), dim3(256), 0, stream, p)
+    // Workgroups loop over 64-row groups; at most as many workgroups as are resident at once.
+    const int64_t groups = (p.n_rows + kRowsPerWG - 1) / kRowsPerWG;
+#define TQ_LAUNCH_DT(B, Q, DT)                                                                       \
+    do {                                                                                             \
+        static const int res = resident_grid(compress_kernel<B, Q, MODE, DT>);                       \
+        const int grid = (int)(groups < res ? groups : res);                                         \
+        hipLaunchKernelGGL((compress_kernel<B, Q, MODE, DT>), dim3(grid), dim3(256), 0, stream, p);  \
+    } while (0)
 #define TQ_LAUNCH(B, Q)                                   \
     do {                                                  \
         if (p.x_dtype == TQ_BF16) TQ_LAUNCH_DT(B, Q, TQ_BF16); \
@@ -959,12 +971,14 @@ extern "C" int tq_compress_paged_kv(const tq_paged_target* k, const tq_paged_tar
         rc = launch_compress<MODE_PAGED>(pk, k->bits, k->use_qjl, st);
         return rc ? rc : launch_compress<MODE_PAGED>(pv, v->bits, v->use_qjl, st);
     }
-    // K workgroups first, then as many V workgroups: at most 1024 of each
+    // K workgroups first, then as many V workgroups: half the resident workgroups each
     const int64_t groups = (pk.n_rows + kRowsPerWG - 1) / kRowsPerWG;
-    const int gk = (int)(groups < kCompressGrid * 4 / 5 ? groups : kCompressGrid * 4 / 5);
-    const int grid = 2 * gk;
-#define TQ_KV_DT(B, Q, DT) \
-    hipLaunchKernelGGL((compress_kv_kernel<B, Q, DT>), dim3(grid), dim3(256), 0, st, pk, pv, gk)
+#define TQ_KV_DT(B, Q, DT)                                                                          \
+    do {                                                                                            \
+        static const int res = resident_grid(compress_kv_kernel<B, Q, DT>) / 2;                     \
+        const int gk = (int)(groups < res ? groups : (res > 0 ? res : 1));                          \
+        hipLaunchKernelGGL((compress_kv_kernel<B, Q, DT>), dim3(2 * gk), dim3(256), 0, st, pk, pv, gk); \
+    } while (0)
 #define TQ_KV(B, Q)                                             \
     do {                                                        \
         if (x_dtype == TQ_BF16) TQ_KV_DT(B, Q, TQ_BF16);        \
