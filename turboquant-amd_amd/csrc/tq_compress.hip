@@ -528,6 +528,15 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
         else off = tok * p.x_stride_token + head * p.x_stride_head + 32 * q;
         RawRow<DT> raw;
         load_raw<DT>(p.x, off, raw);
+        // the slot goes out with the row (token 0's for rows that are not written, whose result
+        // is dropped): its round trip overlaps the row's instead of following the quantisation
+        uint32_t slo = 0, shi = 0;
+        if (MODE == MODE_PAGED) {
+            const uint32_t* sp = reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.slot_mapping) +
+                                                                   tok * (p.slot_i64 ? 8 : 4));
+            slo = sp[0];
+            shi = sp[p.slot_i64 ? 1 : 0];
+        }
         float v[32];
         float norm, den, rcp;
         bool fast;
@@ -622,11 +631,8 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                 }
             }
         } else {
-            int64_t slot = -1;
-            if (row_ok) {
-                slot = p.slot_i64 ? static_cast<const int64_t*>(p.slot_mapping)[tok]
-                                  : (int64_t) static_cast<const int32_t*>(p.slot_mapping)[tok];
-            }
+            const int64_t slot =
+                !row_ok ? -1 : (p.slot_i64 ? (int64_t)(((uint64_t)shi << 32) | slo) : (int64_t)(int32_t)slo);
             const bool write = row_ok && slot >= 0 && slot < p.num_blocks * p.block_size;
             int64_t blk, r_in_blk;
             if (p.idx32) {
