@@ -362,9 +362,12 @@ size_t tq_decode_workspace_bytes(int num_seqs, int num_q_heads, int max_seq_len,
  * results go to a fixed array of TQ_NOALLOC_SCRATCH_BYTES inside this library (one copy per
  * GPU, held from the library's load on that GPU until the process ends; its device address is
  * looked up once per device on the first call there).  Same arguments (minus the workspace),
- * checks, kernels and results as tq_decode.  Returns TQ_ERR_SCRATCH_LIMIT, before any launch,
- * when tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk) exceeds
- * TQ_NOALLOC_SCRATCH_BYTES (choose a larger tokens_per_chunk).  Calls that overlap in time on
+ * checks, kernels and results as tq_decode.  Before any HIP call it returns TQ_ERR_CHUNK for a
+ * tokens_per_chunk that is negative or not a multiple of 16, then TQ_ERR_SCRATCH_LIMIT when
+ * tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk) exceeds
+ * TQ_NOALLOC_SCRATCH_BYTES, for fixed chunks (choose a larger tokens_per_chunk) and for the
+ * balanced schedule (tokens_per_chunk = 0: about 17 MB plus 520 bytes per (sequence, query
+ * head), so beyond about 96k such pairs; choose fixed chunks).  Calls that overlap in time on
  * one GPU share its array and race; nothing is carried between calls.
  * No counterpart in the reference: for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid allocation).

@@ -502,9 +502,9 @@ def test_decode_qjl_small_heads_beside_large(dev, kb, vb, layouts):
     softmax spread of ~1 log unit: precision its QJL operand would lose to a block scale shared
     with the head 1e4 larger (its elements would fall to the bottom of fp8's range) shows in its
     output.  That head is checked against the fp64 oracle at the contract tolerance; the larger
-    ones only share the group: their logits span 4 to 1e4 log units, where the fast kernel's
-    fp8 hi + lo operand (2^-8 relative on the QJL term, a small correction of realistic scores)
-    and the oracle's own ties decide the one-hot softmax."""
+    ones only share the group: their logits span 4 to 1e4 log units, where the last bits of any
+    operand and the oracle's own ties decide the one-hot softmax (every head at realistic logits:
+    test_decode_qjl_operand_every_head)."""
     from turboquant.kernels.paged import PagedKVFormat, decode_paged
     S, Hkv, G, bs = 2, 2, 8, 16
     Hq = Hkv * G
@@ -540,6 +540,42 @@ def test_decode_qjl_small_heads_beside_large(dev, kb, vb, layouts):
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got[:, small], want[:, small], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("kb,vb", [(3, 3), (2, 2), (4, 4)])
+@pytest.mark.parametrize("layouts", [("keys", "values"), ("rows", "rows")])
+def test_decode_qjl_operand_every_head(dev, kb, vb, layouts):
+    """Explicit q_proj whose magnitudes span 1e-2 .. 1e2 across the heads of one GQA group and
+    1 .. 64 across the four 32-dim blocks of each head (the blocks of the fast kernel's per-lane
+    fp6 scales), the cache's own key and residual norms, N(0,1) queries: logits stay in a
+    realistic range, and every head is checked against the fp64 oracle at the contract
+    tolerance (the QJL term of the larger heads moves their logits by several log units)."""
+    from turboquant.kernels.paged import PagedKVFormat, decode_paged
+    S, Hkv, G, bs = 3, 2, 8, 16
+    Hq = Hkv * G
+    lens = [300, 77, 1000]
+    case = build_case(640 + kb, S, Hq, Hkv, lens, kb, True, vb, bs, layouts=layouts)
+    rng = np.random.default_rng(641 + kb)
+    head_scale = 10.0 ** np.linspace(-2.0, 2.0, G)[np.arange(Hq) % G]
+    block_scale = np.repeat(4.0 ** rng.permutation(4), 32) / 8.0  # dims 32b..32b+31 share one scale
+    qp = (rng.standard_normal((S, Hq, 128)) * head_scale[None, :, None] * block_scale[None, None, :]).astype(np.float32)
+    kf = PagedKVFormat(bits=kb, qjl=True, block_size=bs, layout=layouts[0])
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=layouts[1])
+    q_t = torch.from_numpy(case["q"]).to(torch.bfloat16).to(dev)
+    qp_t = torch.from_numpy(qp).to(torch.bfloat16).to(dev)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    for chunk in (64, 0):
+        out = decode_paged(q_t, torch.from_numpy(case["k_cache"]).to(dev), kf, _cb(kb).to(dev),
+                           torch.from_numpy(case["v_cache"]).to(dev), vf, _cb(vb).to(dev),
+                           torch.from_numpy(case["bt"]).to(dev), torch.from_numpy(case["seq_lens"]).to(dev),
+                           sm_scale=sm, corr_scale=cs, q_proj=qp_t, tokens_per_chunk=chunk)
+        torch.cuda.synchronize()
+        want, _, _ = oracle_out(case, Hq, Hkv, kb, True, vb, sm, cs,
+                                qp=qp_t.float().cpu().numpy().astype(np.float64),
+                                q_round=q_t.float().cpu().numpy().astype(np.float64))
+        got = out.float().cpu().numpy()
+        assert np.isfinite(got).all()
+        np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.parametrize("kb,kq,vb", [(3, True, 3), (4, False, 4), (2, True, 2)])

@@ -420,6 +420,32 @@ def test_host_side_argument_rejection():
     assert reg(rv, 0) == 0                    # no tokens: nothing to launch
 
 
+def test_noalloc_refusals_before_any_hip_call():
+    """tq_decode_noalloc checks the chunk, then the fixed scratch size, for fixed chunks and for
+    the balanced schedule (tokens_per_chunk = 0), before touching any pointer or HIP call."""
+    from turboquant import _lib
+    L = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced
+    kv = _lib.TQKVView()
+    kv.bits = 3
+
+    def call(S, Hq, msl, chunk):
+        return L.tq_decode_noalloc(fake, 2, Hq * 128, 128, None, 0, 0, S, Hq, 8, 128, ctypes.byref(kv),
+                                   ctypes.byref(kv), 16, 10, fake, 1, 1, fake, msl, 0.1, 0.0, 0.0, chunk,
+                                   fake, 2, Hq * 128, 128, None, None)
+
+    limit = _lib.NOALLOC_SCRATCH_BYTES
+    # balanced schedule: 17 MB + 520 B per (sequence, query head) passes the limit near 9.6e4 rows
+    assert L.tq_decode_workspace_bytes(2048, 48, 1 << 17, 0) > limit
+    assert call(2048, 48, 1 << 17, 0) == -10
+    assert "tokens_per_chunk" in _lib.status_string(-10)
+    # fixed chunks beyond the scratch
+    assert call(2, 48, 1 << 20, 16) == -10
+    # an invalid chunk is reported as such, whatever the size
+    assert call(2048, 48, 1 << 17, 8) == -9
+    assert call(2, 48, 100, -16) == -9
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     from turboquant import _lib
     monkeypatch.setattr(_lib, "_lib", None)

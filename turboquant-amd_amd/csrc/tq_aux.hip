@@ -106,10 +106,11 @@ extern "C" const char* tq_status_string(int status) {
         case TQ_ERR_GQA: return "num_q_heads must be a multiple of num_kv_heads with group size <= 16";
         case TQ_ERR_DTYPE: return "unsupported dtype";
         case TQ_ERR_BLOCK_SIZE: return "block_size must be a positive multiple of 16";
-        case TQ_ERR_CHUNK: return "tokens_per_chunk must be a positive multiple of 16";
+        case TQ_ERR_CHUNK: return "tokens_per_chunk must be 0 (balanced schedule) or a positive multiple of 16";
         case TQ_ERR_SCRATCH_LIMIT:
             return "the call needs more split-K scratch than tq_decode_noalloc's fixed array "
-                   "(TQ_NOALLOC_SCRATCH_BYTES): use a larger tokens_per_chunk";
+                   "(TQ_NOALLOC_SCRATCH_BYTES): use a larger tokens_per_chunk, or fixed chunks instead of the "
+                   "balanced schedule (tokens_per_chunk 0) for very large batches";
         default: break;
     }
     if (status > 0) return hipGetErrorString((hipError_t)status);

@@ -951,10 +951,11 @@ int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num
 
 // The fast kernel reads this library's tile layout: per cache one block stride and one head
 // stride for all regions, rows of 16*bits index bytes, 16 sign bytes and 2-byte norms, the
-// other regions after the index region of the same tile.  *big: some tile lies 2 GiB or more
-// from its head's base (64-bit per-tile addressing).
+// other regions after the index region of the same tile.  *addr: TQ_ADDR_BIG when some tile
+// lies 2 GiB or more from its head's base (64-bit per-tile addressing), else TQ_ADDR_STREAM when
+// the two caches together are larger than the last-level cache, else TQ_ADDR_CACHED.
 bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block_size, int64_t num_blocks,
-                  const int32_t* block_tables, bool* big) {
+                  const int32_t* block_tables, int* addr) {
     // num_blocks >= 1: unreadable table entries are redirected to block 0 and masked
     if (!block_tables || num_blocks < 1 || group > 8 || k->signs_permuted) return false;
     if (block_size & (block_size - 1)) return false;  // 16 << tile_shift
@@ -979,7 +980,8 @@ bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block
     auto stride_ok = [&](const tq_region& r) { return r.stride_block > 0 && r.stride_block < (1ll << 30); };
     if (!stride_ok(k->idx) || !stride_ok(v->idx)) return false;
     auto small = [&](const tq_region& r) { return num_blocks * r.stride_block < (1ll << 31) - (1ll << 16); };
-    *big = !(small(k->idx) && small(v->idx));
+    const int64_t extent = num_blocks * (k->idx.stride_block + v->idx.stride_block);
+    *addr = !(small(k->idx) && small(v->idx)) ? TQ_ADDR_BIG : extent > kTqStreamBytes ? TQ_ADDR_STREAM : TQ_ADDR_CACHED;
     return true;
 }
 
@@ -1146,8 +1148,8 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     const bool sparse_pair = sparse_threshold > 0.f && block_size >= 32 && block_tables;
     const size_t need = tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return TQ_ERR_WORKSPACE;
-    bool big = false;
-    const bool fast = fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &big);
+    int addr = TQ_ADDR_CACHED;
+    const bool fast = fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &addr);
     // tokens_per_chunk = 0: the balanced schedule on the fast kernel; fixed chunks that fit the
     // same workspace on the general one
     // (the kernel keeps pair positions in 32 bits: at most num_seqs * num_kv_heads * ceil(len / 32))
@@ -1167,7 +1169,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     const bool share = k->centroids == v->centroids && k->bits == v->bits && k_cscale == v_cscale;
     if (fast) {
         FastDecodeParams f = {};
-        f.big = big ? 1 : 0;
+        f.addr = addr;
         f.q = q;
         f.q_ss = q_stride_seq;
         f.q_sh = q_stride_head;

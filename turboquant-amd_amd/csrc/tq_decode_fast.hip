@@ -9,10 +9,12 @@
 //   S_X^T[token][col] = K_X[16 x 128] . Q^T[128 x 16]         4 x mfma_f32_16x16x32_f16 per tile
 //       K_X: a pair of packed indices -> half2 of centroids through an LDS table;
 //       column col of Q holds query head col & 7, so both halves of the output hold all heads.
-//   QJL_X^T = (+-1)[16 x 128] . QP^T                           2 x mfma_scale_f32_16x16x128_f8f6f4
+//   QJL_X^T = (+-1)[16 x 128] . QP^T                           3 x mfma_scale_f32_16x16x128_f8f6f4
 //       sign bits -> fp4 +-1 through a byte-indexed LDS table (one dword per 8 signs); q_proj
-//       in fp8 as hi + lo parts with E8M0 block scales (relative error <= 2^-8 on a term that
-//       is a small correction of the score).
+//       as three fp6 (e2m3) parts with per-lane E8M0 block scales: the error of each element is
+//       at most 2^-14 of the largest magnitude of its 32-element block (fp16 q_proj, the
+//       reference's operand, carries 2^-11 of each element).  fp4 x fp6 runs at the fp4 rate:
+//       three of these cost less matrix time than two fp4 x fp8 products.
 //   Lanes with col < 8 keep tile A's scores and lanes with col >= 8 tile B's, so after the
 //   merge one wave holds 32 tokens x 8 heads of scores (4 per lane): the online softmax, the
 //   Sparse-V test and the conversions run once per pair.
@@ -183,8 +185,8 @@ struct Softmax {
 // Per-lane constants of the compute step.
 struct LaneCtx {
     tq_half8 qop[4];            // q (fp16), MFMA chunk cc: dims 32g + 8cc + j
-    tq_i32x8 qph, qpl;          // q_proj * corr * cscale * 2^b in fp8: hi, (x - hi) * 16
-    int sc_hi, sc_lo;           // E8M0 scales undoing 2^b and 2^(b+4)
+    tq_i32x8 qp6[3];            // q_proj * corr * cscale * 2^b as three fp6 parts (6 dwords each)
+    int qsc;                    // E8M0 scales of the parts in bytes 0-2: 2^-b, 2^-(b+5), 2^-(b+10)
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
     uint32_t vquad;                // 3-bit V quad table base (a 3-bit K quad table is at address 0)
     uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
@@ -226,8 +228,10 @@ __device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, const LaneCtx& c) {
 #pragma unroll
     for (int b = 4; b < 8; ++b) a[b] = 0;  // fp4 operand: only the first four dwords are read
     tq_floatx4 t = {0.f, 0.f, 0.f, 0.f};
-    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qph, t, 4, 0, 0, 127, 0, c.sc_hi);
-    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qpl, t, 4, 0, 0, 127, 0, c.sc_lo);
+    // A: fp4 (format 4), B: fp6 e2m3 (format 2); the B scale is byte 0, 1, 2 of qsc
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[0], t, 4, 2, 0, 127, 0, c.qsc);
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[1], t, 4, 2, 0, 127, 1, c.qsc);
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[2], t, 4, 2, 0, 127, 2, c.qsc);
     return t;
 }
 
@@ -342,8 +346,7 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     const tq_half8 bop = __builtin_bit_cast(tq_half8, bw);
     // acc[a] (dim 8n + a): field group a of the lane's chunk is that dim's four tokens, so the
     // lookups are the A operand as they come: k-slots 0-3 tile A's tokens, 4-7 tile B's.
-#pragma unroll
-    for (int a = 0; a < 8; ++a) {
+    auto vlook = [&](int a) -> tq_u32x4 {
         tq_u32x4 aw;
         if (quad_table<VB>()) {
             // one quad per tile (2 bits: a fixed table address, which goes into the ds_read offset)
@@ -360,8 +363,28 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
                 aw[2 + h] = lds_read(entry_addr<2 * VB, VB>(vr.vwB, 4 * VB * a + 2 * VB * h, c.vbank));
             }
         }
-        st.acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, aw), bop, st.acc[a], 0, 0, 0);
+        return aw;
+    };
+    // Software pipeline: the lookups of dim group a + 2 are issued before the product of group
+    // a, so a wave has two groups of LDS reads in flight behind each MFMA (the schedule below
+    // pins that order; left to itself the scheduler waited for every pair of reads).
+    tq_u32x4 w0 = vlook(0), w1 = vlook(1);
+#pragma unroll
+    for (int a = 0; a < 8; ++a) {
+        tq_u32x4 w2 = w1;
+        if (a + 2 < 8) w2 = vlook(a + 2);
+        st.acc[a] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, w0), bop, st.acc[a], 0, 0, 0);
+        w0 = w1;
+        w1 = w2;
     }
+    constexpr int kReads = quad_table<VB>() ? 2 : 4;  // LDS reads per dim group
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kReads, 0);  // DS reads: groups 0 and 1
+#pragma unroll
+    for (int a = 0; a < 6; ++a) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA of group a
+        __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);  // DS reads of group a + 2
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
 // Waves per SIMD (register budget 512 / waves): QJL keys need the fp8 q_proj operands.
@@ -372,11 +395,19 @@ constexpr int fast_waves() {
 
 // COUNT: Sparse-V skip statistics requested (a separate instance keeps the counting off the
 // common path).
-// BIG: a cache spanning 2 GiB or more (tiles addressed from 64-bit per-tile bases).
-template <int KB, bool KQJL, int VB, bool COUNT, bool BIG>
+// ADDR: how K / V tiles are addressed and cached.
+//   TQ_ADDR_CACHED: 32-bit offsets from one descriptor per head; loads allocate in the caches
+//       (K + V fit the 256 MB last-level cache, so repeated decodes of them can hit there);
+//   TQ_ADDR_STREAM: the same addressing with non-temporal (streaming) loads, for caches larger
+//       than the last-level cache, where every byte is read once per decode;
+//   TQ_ADDR_BIG: a cache spanning 2 GiB or more: tiles addressed from 64-bit per-tile bases,
+//       streaming loads.
+template <int KB, bool KQJL, int VB, bool COUNT, int ADDR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
                                                                      fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
+    constexpr bool BIG = ADDR == TQ_ADDR_BIG;
+    constexpr int AUX = ADDR == TQ_ADDR_CACHED ? 0 : 2;  // buffer-load cache policy: 2 = non-temporal
     extern __shared__ uint32_t s_lds[];
     // Tables: fp4 sign table (QJL), K table, V table, at the byte offsets chosen by the host
     // (multiples of each table's size).  A replicated table's entry is computed once and its
@@ -662,16 +693,16 @@ void decode_fast_kernel(FastDecodeParams p) {
             constexpr int C = 4 * KB + (KQJL ? 4 : 0);
             uint32_t d[5];
             if (C == 8) {
-                tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, o_kch, soff, 0);
+                tq_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rk, o_kch, soff, AUX);
                 d[0] = v[0]; d[1] = v[1];
             } else if (C == 12) {
                 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-                u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rk, o_kch, soff, 0);
+                u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(rk, o_kch, soff, AUX);
                 d[0] = v[0]; d[1] = v[1]; d[2] = v[2];
             } else {
-                tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, o_kch, soff, 0);
+                tq_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rk, o_kch, soff, AUX);
                 d[0] = v[0]; d[1] = v[1]; d[2] = v[2]; d[3] = v[3];
-                if (C == 20) d[4] = __builtin_amdgcn_raw_buffer_load_b32(rk, o_kch + 16u, soff, 0);
+                if (C == 20) d[4] = __builtin_amdgcn_raw_buffer_load_b32(rk, o_kch + 16u, soff, AUX);
             }
 #pragma unroll
             for (int j = 0; j < KB; ++j) kw[j] = d[j];
@@ -686,11 +717,11 @@ void decode_fast_kernel(FastDecodeParams p) {
             // lanes with col < 8 read tile A's norms, the others tile B's
             tq_u32x2 a, bb = {0u, 0u};
             if (c.lo8) {
-                a = __builtin_amdgcn_raw_buffer_load_b64(rkA, o_norm, 2u * r0[0] + p.d_kn, 0);
-                if (KQJL) bb = __builtin_amdgcn_raw_buffer_load_b64(rkA, o_norm, 2u * r0[0] + p.d_krn, 0);
+                a = __builtin_amdgcn_raw_buffer_load_b64(rkA, o_norm, 2u * r0[0] + p.d_kn, AUX);
+                if (KQJL) bb = __builtin_amdgcn_raw_buffer_load_b64(rkA, o_norm, 2u * r0[0] + p.d_krn, AUX);
             } else {
-                a = __builtin_amdgcn_raw_buffer_load_b64(rkB, o_norm, 2u * r0[1] + p.d_kn, 0);
-                if (KQJL) bb = __builtin_amdgcn_raw_buffer_load_b64(rkB, o_norm, 2u * r0[1] + p.d_krn, 0);
+                a = __builtin_amdgcn_raw_buffer_load_b64(rkB, o_norm, 2u * r0[1] + p.d_kn, AUX);
+                if (KQJL) bb = __builtin_amdgcn_raw_buffer_load_b64(rkB, o_norm, 2u * r0[1] + p.d_krn, AUX);
             }
             kr.kn[0] = a[0];
             kr.kn[1] = a[1];
@@ -701,11 +732,11 @@ void decode_fast_kernel(FastDecodeParams p) {
         load_k(kr.kwA, kr.ksA, rk, kb[0] + r0[0] * P);
         load_k(kr.kwB, kr.ksB, rk, kb[1] + r0[1] * P);
         const NormAddr na = norm_addr(kb[0] + 2u * r0[0], kb[1] + 2u * r0[1]);
-        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_kn, 0);
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_kn, AUX);
         kr.kn[0] = a[0];
         kr.kn[1] = a[1];
         if (KQJL) {
-            tq_u32x2 bb = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_krn, 0);
+            tq_u32x2 bb = __builtin_amdgcn_raw_buffer_load_b64(rk, na.vo, na.so + p.d_krn, AUX);
             kr.krn[0] = bb[0];
             kr.krn[1] = bb[1];
         }
@@ -715,14 +746,14 @@ void decode_fast_kernel(FastDecodeParams p) {
         // of rows 4g..4g+3, dimension-major).
         auto load1 = [&](uint32_t (&vw)[VB], __amdgpu_buffer_rsrc_t rv, uint32_t soff) {
             if (VB == 2) {
-                tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, o_vch, soff, 0);
+                tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, o_vch, soff, AUX);
                 vw[0] = a[0]; vw[1 % VB] = a[1];
             } else if (VB == 3) {
                 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-                u32x3 a = __builtin_amdgcn_raw_buffer_load_b96(rv, o_vch, soff, 0);
+                u32x3 a = __builtin_amdgcn_raw_buffer_load_b96(rv, o_vch, soff, AUX);
                 vw[0] = a[0]; vw[1 % VB] = a[1]; vw[2 % VB] = a[2];
             } else {
-                tq_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rv, o_vch, soff, 0);
+                tq_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rv, o_vch, soff, AUX);
                 vw[0] = a[0]; vw[1 % VB] = a[1]; vw[2 % VB] = a[2]; vw[3 % VB] = a[3];
             }
         };
@@ -732,8 +763,8 @@ void decode_fast_kernel(FastDecodeParams p) {
             load1(vr.vwA, rvA, info.r0A * (uint32_t)(16 * VB));
             load1(vr.vwB, rvB, info.r0B * (uint32_t)(16 * VB));
             tq_u32x2 a;
-            if (c.lo8) a = __builtin_amdgcn_raw_buffer_load_b64(rvA, o_norm, 2u * info.r0A + p.d_vn, 0);
-            else a = __builtin_amdgcn_raw_buffer_load_b64(rvB, o_norm, 2u * info.r0B + p.d_vn, 0);
+            if (c.lo8) a = __builtin_amdgcn_raw_buffer_load_b64(rvA, o_norm, 2u * info.r0A + p.d_vn, AUX);
+            else a = __builtin_amdgcn_raw_buffer_load_b64(rvB, o_norm, 2u * info.r0B + p.d_vn, AUX);
             vr.vn[0] = a[0];
             vr.vn[1] = a[1];
             return;
@@ -742,7 +773,7 @@ void decode_fast_kernel(FastDecodeParams p) {
         load1(vr.vwB, rv, info.vbB + info.r0B * (uint32_t)(16 * VB));
         // norm of row j of a tile at row0 of its block: d_vn + 2 (row0 + j)
         const NormAddr na = norm_addr(info.vbA + 2u * info.r0A, info.vbB + 2u * info.r0B);
-        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, na.vo, na.so + p.d_vn, 0);
+        tq_u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rv, na.vo, na.so + p.d_vn, AUX);
         vr.vn[0] = a[0];
         vr.vn[1] = a[1];
     };
@@ -763,23 +794,17 @@ void decode_fast_kernel(FastDecodeParams p) {
             for (int i = 0; i < 32; ++i) qv[i] = hvalid ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
         }
     }
-    // fp8 operand element m (byte m of 32) of lane group g is dim (m < 16 ? 0 : 64) + 16 g + (m & 15)
-    // (the pairing of an fp4 A operand with an fp8 B operand in the 16x16x128 MFMA).
+    // fp6 operand element m of lane group g is dim 32 g + m (the pairing of an fp4 A operand
+    // with an fp6 B operand in the 16x16x128 MFMA, measured), the dims of the lane's key chunk.
     float x[32];
     if constexpr (KQJL) {
-        const int64_t off = s * p.qp_ss + (int64_t)head * p.qp_sh + 16 * g;
+        const int64_t off = s * p.qp_ss + (int64_t)head * p.qp_sh + 32 * g;
         if (hvalid && p.q_vec) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                tq_load8(p.qp, off + 8 * i, p.q_dtype, &x[8 * i]);
-                tq_load8(p.qp, off + 64 + 8 * i, p.q_dtype, &x[16 + 8 * i]);
-            }
+            for (int i = 0; i < 4; ++i) tq_load8(p.qp, off + 8 * i, p.q_dtype, &x[8 * i]);
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                x[i] = hvalid ? tq_load1(p.qp, off + i, p.q_dtype) : 0.f;
-                x[16 + i] = hvalid ? tq_load1(p.qp, off + 64 + i, p.q_dtype) : 0.f;
-            }
+            for (int i = 0; i < 32; ++i) x[i] = hvalid ? tq_load1(p.qp, off + i, p.q_dtype) : 0.f;
         }
     }
     // All data of a pair is loaded one pair ahead (two register sets).  Pairs past the end read
@@ -797,44 +822,51 @@ void decode_fast_kernel(FastDecodeParams p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) c.qop[cc][j] = (_Float16)qv[8 * cc + j];
     if constexpr (KQJL) {
-        // q x H: x[i] is element 16g + (i & 15) + 64 (i >> 4), so register bits 0-3 and 4 are
-        // element bits 0-3 and 6, lane bits 4-5 element bits 4-5
-        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);
-        // One E8M0 scale per column (query head): a lane's 32 fp8 elements straddle two of the
-        // instruction's 32-wide scale blocks (dims 16g.. and 64 + 16g..), so the scale is uniform
-        // over the column's four lane groups; a head whose q_proj is orders of magnitude below
-        // its group's largest still gets its own exponent and keeps its precision.
+        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);  // q_proj x H: elements 32g + i
+        // One E8M0 scale per lane: its 32 elements are one 32-wide scale block of the instruction.
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             x[i] *= p.qp_mul;
             amax = fmaxf(amax, fabsf(x[i]));
         }
-        amax = max_over_groups(amax);  // lanes col, col ^ 16, col ^ 32, col ^ 48
-        // 2^b brings the head's largest magnitude into [128, 256): inside the fp8 e4m3 normal range
+        // 2^b brings the block's largest magnitude into [2, 4) (e2m3 holds magnitudes up to 7.5)
         int b = 0;
-        if (amax > 0.f && amax < __builtin_huge_valf()) b = 7 - ilogbf(amax);
-        b = b < -100 ? -100 : (b > 100 ? 100 : b);
-        c.sc_hi = 127 - b;
-        c.sc_lo = 127 - b - 4;
+        if (amax > 0.f && amax < __builtin_huge_valf()) b = 1 - ilogbf(amax);
+        b = b < -117 ? -117 : (b > 117 ? 117 : b);
+        c.qsc = (127 - b) | ((122 - b) << 8) | ((117 - b) << 16);
+        // x 2^b = hi + mid / 32 + lo / 1024 + e: each part rounded to nearest even (the
+        // conversion divides by its scale argument), the residuals before it exact in fp32; the
+        // last part is at most 4 in magnitude, so |e| <= 2^-3 / 1024 = 2^-13 next to a block
+        // maximum of at least 2.
+        typedef float f32x16 __attribute__((ext_vector_type(16)));
+        typedef int i32x6 __attribute__((ext_vector_type(6)));
+        float r[32];
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            float xs[4], rs[4];
+        for (int i = 0; i < 32; ++i) r[i] = ldexpf(x[i], b);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) xs[k] = ldexpf(x[4 * d + k], b);
-            int wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[0], xs[1], 0, false);
-            wh = __builtin_amdgcn_cvt_pk_fp8_f32(xs[2], xs[3], wh, true);
-            rs[0] = (xs[0] - __builtin_amdgcn_cvt_f32_fp8(wh, 0)) * 16.f;
-            rs[1] = (xs[1] - __builtin_amdgcn_cvt_f32_fp8(wh, 1)) * 16.f;
-            rs[2] = (xs[2] - __builtin_amdgcn_cvt_f32_fp8(wh, 2)) * 16.f;
-            rs[3] = (xs[3] - __builtin_amdgcn_cvt_f32_fp8(wh, 3)) * 16.f;
-            int wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[0], rs[1], 0, false);
-            wl = __builtin_amdgcn_cvt_pk_fp8_f32(rs[2], rs[3], wl, true);
-            c.qph[d] = wh;
-            c.qpl[d] = wl;
+        for (int part = 0; part < 3; ++part) {
+            // packed element 2i comes from the first vector's element i, 2i + 1 from the second's
+            f32x16 ev, od;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                ev[i] = r[2 * i];
+                od[i] = r[2 * i + 1];
+            }
+            const float sc = part == 0 ? 1.0f : 0.03125f;  // code = RNE(value / sc)
+            const i32x6 code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, sc);
+#pragma unroll
+            for (int j = 0; j < 6; ++j) c.qp6[part][j] = code[j];
+            c.qp6[part][6] = 0;
+            c.qp6[part][7] = 0;
+            if (part < 2) {
+                const auto dq = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, 1.0f);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) r[i] = part == 0 ? r[i] - dq[i] : __builtin_fmaf(r[i], 32.f, -dq[i]);
+            }
         }
     } else {
-        c.sc_hi = c.sc_lo = 127;
+        c.qsc = 127;
     }
 
     Softmax st;
@@ -917,17 +949,21 @@ void decode_fast_kernel(FastDecodeParams p) {
 
 }  // namespace
 
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count, bool big) {
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count, int addr) {
+#define TQ_FP_A(KB, KQ, VB, A)                                                                         \
+    if (addr == A)                                                                                     \
+        return count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, A>                            \
+                     : (const void*)decode_fast_kernel<KB, KQ, VB, false, A>;
 #define TQ_FP(KB, KQ, VB)                                                                              \
-    if (kb == KB && kq == KQ && vb == VB)                                                              \
-        return big ? (count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, true>                  \
-                            : (const void*)decode_fast_kernel<KB, KQ, VB, false, true>)                \
-                   : (count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, false>                 \
-                            : (const void*)decode_fast_kernel<KB, KQ, VB, false, false>);
+    if (kb == KB && kq == KQ && vb == VB) {                                                            \
+        TQ_FP_A(KB, KQ, VB, TQ_ADDR_CACHED) TQ_FP_A(KB, KQ, VB, TQ_ADDR_STREAM) TQ_FP_A(KB, KQ, VB, TQ_ADDR_BIG) \
+        return nullptr;                                                                                \
+    }
 #define TQ_FP_V(KB, KQ) TQ_FP(KB, KQ, 2) TQ_FP(KB, KQ, 3) TQ_FP(KB, KQ, 4)
     TQ_FP_V(2, false) TQ_FP_V(2, true) TQ_FP_V(3, false) TQ_FP_V(3, true) TQ_FP_V(4, false) TQ_FP_V(4, true)
 #undef TQ_FP_V
 #undef TQ_FP
+#undef TQ_FP_A
     return nullptr;
 }
 
@@ -990,7 +1026,7 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream) {
-    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats, prm.big != 0);
+    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats, prm.addr);
     if (!kern) return TQ_ERR_BITS;
     FastDecodeParams p = prm;
     void* args[] = {&p};

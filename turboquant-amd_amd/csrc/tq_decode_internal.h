@@ -77,11 +77,21 @@ struct FastDecodeParams {
     int64_t out_ss, out_sh;
     int rot_q, rot_qp, rot_out;  // rotate q / q_proj by H on load, the output by H on the write
     float wht_h;                 // 1 / sqrt(128)
-    int big;                     // a cache spans 2 GiB or more: 64-bit per-tile addressing
+    int addr;                    // TQ_ADDR_*: tile addressing and cache policy of the K / V loads
 };
 
-// decode_fast_kernel<kb, kq, vb, count, big> (nullptr: unsupported bit widths).
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false, bool big = false);
+// Tile addressing and cache policy of decode_fast_kernel's K / V loads.
+enum {
+    TQ_ADDR_CACHED = 0,  // 32-bit offsets per head; loads allocate in the caches
+    TQ_ADDR_STREAM = 1,  // 32-bit offsets per head; non-temporal loads
+    TQ_ADDR_BIG = 2,     // 64-bit per-tile bases (a cache spanning 2 GiB or more); non-temporal loads
+};
+// K + V caches larger than this (the MI355X last-level "Infinity" cache, 256 MB) are read with
+// non-temporal loads: every byte is read once per decode and nothing would be kept anyway.
+constexpr int64_t kTqStreamBytes = 256ll << 20;
+
+// decode_fast_kernel<kb, kq, vb, count, addr> (nullptr: unsupported bit widths).
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false, int addr = TQ_ADDR_CACHED);
 
 // LDS byte offsets of the fp4 sign table, the K and the V tables, a 512-byte scratch, and the
 // total.

@@ -55,8 +55,12 @@ extern "C" int tq_decode_noalloc(const void* q, int q_dtype, int64_t q_stride_se
                                  void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
                                  unsigned long long* skip_stats,
                                  tq_stream_t stream) {
-    // Size checks first: a request beyond the fixed array is refused before any HIP call.
-    if (num_seqs > 0 && num_q_heads > 0 && tokens_per_chunk > 0 &&
+    // Checks first, before any HIP call: an invalid chunk, then a request beyond the fixed
+    // array, for fixed chunks and for the balanced schedule (tokens_per_chunk = 0, whose
+    // workspace grows with num_seqs * num_q_heads; tq_decode_impl runs a general-kernel fallback
+    // of that schedule inside the same workspace size).
+    if (tokens_per_chunk < 0 || tokens_per_chunk % 16) return TQ_ERR_CHUNK;
+    if (num_seqs > 0 && num_q_heads > 0 &&
         tq_decode_workspace_bytes(num_seqs, num_q_heads, max_seq_len, tokens_per_chunk) > (size_t)TQ_NOALLOC_SCRATCH_BYTES)
         return TQ_ERR_SCRATCH_LIMIT;
     void* ws = nullptr;
