@@ -329,7 +329,123 @@ def compress_case(dev, steps, warmup):
     alg = 2 * (T * H * D * 2 + T * H * w["fmt"].token_bytes) + T * 4
     return {"workload": "config2: turbo4 paged compress K+V, 16384 tok x 8 heads bf16, bs 16",
             "us_per_layer": ms * 1e3, "mean_us": t["mean_ms"] * 1e3, "algorithmic_bytes": alg,
-            "compress_gbs": alg / (ms * 1e-3) / 1e9, "frac_of_8tbs": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            "compress_gbs": alg / (ms * 1e-3) / 1e9, "frac_of_8tbs": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}, w
+
+
+def config1_case(dev, steps, warmup):
+    """Benchmark config 1 on the GPU: polarquant_compress of K [1024, 128] fp32 N(0,1) from seed 0,
+    turbo3 + QJL, the 128 x 128 normalized WHT, d = 128 Lloyd-Max codebook (the reference's
+    CPU-runnable case; int64 indices, fp32 norms, signs, k_mse as the reference returns them)."""
+    import torch
+    from turboquant.core import PolarQuantConfig, make_codebook, make_wht_matrix, polarquant_compress
+    torch.manual_seed(0)
+    K = torch.randn(1024, 128)
+    cent, bnd = make_codebook(D, 3)
+    H = make_wht_matrix(D)
+    cfg = PolarQuantConfig(head_dim=D, bits=3, use_qjl=True)
+    Kd, cd, bd, Hd = K.to(dev), cent.to(dev), bnd.to(dev), H.to(dev)
+    t = timed(lambda: polarquant_compress(Kd, cd, bd, cfg, Hd), steps, warmup, settle_s=0.05)
+    out = polarquant_compress(Kd, cd, bd, cfg, Hd)
+    torch.cuda.synchronize()
+    us = t["median_ms"] * 1e3
+    return {"workload": "config1: polarquant_compress K [1024,128] fp32 N(0,1) seed 0, turbo3 + QJL, WHT",
+            "us": us, "us_per_layer": us}, (K, cent, bnd, H, out)
+
+
+def parity_leg(c1, w2):
+    """Compress parity measured in this run, outside every timed region, with the CPU oracle as
+    the checker: config 1's GPU output (polarquant_compress) and config 2's paged caches as the
+    timed steps left them, every index against the oracle's fp32 restatement of the reference
+    and its float64 shadow (oracle.compress.classify_strict: mismatches counted by their distance
+    from the boundary between the two indices, in fp32 ulps; a mismatch beyond 1 ulp passes only
+    where the GPU agrees with float64), sign bits likewise around the centroid."""
+    import numpy as np
+    import torch
+    from oracle import compress as ocomp
+    from oracle import packing as opack
+    from oracle import paged as opaged
+    from turboquant.core import make_wht_matrix
+    res = {}
+    K, cent, bnd, H, out = c1
+    ref = ocomp.polarquant_compress(K, cent, bnd, 8, True, H)
+    ref64 = ocomp.polarquant_compress_fp64(K, cent, bnd, True, True)
+    st = ocomp.classify_strict(out["indices"].cpu().numpy(), ref["indices"].numpy(), ref["x_normalized"].numpy(),
+                               bnd.numpy(), ref64["indices"].numpy())
+    sg = (out["signs"].cpu() > 0).numpy()
+    sr = (ref["signs"] > 0).numpy()
+    s64 = (ref64["signs"] > 0).numpy()
+    same = out["indices"].cpu().numpy() == ref["indices"].numpy()
+    st["sign_mismatches"] = int((sg != sr).sum())
+    st["sign_mismatches_fp64_differs"] = int(((sg != sr) & same & (sg != s64)).sum())
+    st["norm_max_rel_err"] = float(((out["norms"].cpu() - ref["norms"]).abs() / ref["norms"].clamp_min(1e-30)).max())
+    res["config1"] = st
+    T, Hh, bs = COMPRESS_T, COMPRESS_H, COMPRESS_BS
+    slots = w2["slots"].long().cpu().numpy()
+    blk, row = slots // bs, slots % bs
+    H128 = make_wht_matrix(D)
+    c4, b4 = w2["c"].cpu(), w2["b"].cpu()
+    for which, x, cache, fmt in (("K", w2["k"], w2["kc"], w2["fmt"]), ("V", w2["v"], w2["vc"], w2["vfmt"])):
+        got = np.zeros((T, Hh, D), np.int64)
+        for h in range(Hh):
+            tok = opaged.tiles_to_tokens(cache[:, h].cpu().numpy(), bs, 4, False, fmt.layout)
+            got[:, h] = opack.unpack_indices(tok["idx"][blk * bs + row], 4)
+        xf = x.float().cpu().reshape(T * Hh, D)
+        ref = ocomp.polarquant_compress(xf, c4, b4, 16, False, H128)
+        ref64 = ocomp.polarquant_compress_fp64(xf, c4, b4, False, True)
+        res[f"config2 {which}"] = ocomp.classify_strict(got.reshape(T * Hh, D), ref["indices"].numpy(),
+                                                        ref["x_normalized"].numpy(), b4.numpy(), ref64["indices"].numpy())
+    tot = {}
+    for v in res.values():
+        for k, n in v.items():
+            if isinstance(n, int):
+                tot[k] = tot.get(k, 0) + n
+    res["all"] = tot
+    res["source"] = "measured in this run (bench.py parity leg, oracle/ as the checker)"
+    return res
+
+
+def cpu_baseline_compress(c1, w2, seconds=6.0):
+    """The reference's CPU polarquant_compress (oracle/compress.py, its torch fp32 formulation)
+    timed on the host cores: config 1 whole (repeated), config 2 on a sample of 2048 tokens x 8
+    heads of K and V, scaled by rows to the full 16384 tokens."""
+    import torch
+    from oracle import compress as ocomp
+    from turboquant.core import make_wht_matrix
+    K, cent, bnd, H, _ = c1
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        ocomp.polarquant_compress(K, cent, bnd, 8, True, H)
+        n += 1
+    c1_us = (time.perf_counter() - t0) / n * 1e6
+    H128 = make_wht_matrix(D)
+    c4, b4 = w2["c"].cpu(), w2["b"].cpu()
+    rows = 2048 * COMPRESS_H
+    xs = [w2[k][:2048].float().cpu().reshape(rows, D) for k in ("k", "v")]
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for x in xs:
+            ocomp.polarquant_compress(x, c4, b4, 16, False, H128)
+        n += 1
+    c2_us = (time.perf_counter() - t0) / n * 1e6 * (COMPRESS_T / 2048)
+    return {"config1": {"value": round(c1_us, 1), "unit": "us", "cores": torch.get_num_threads(), "kind": "port",
+                        "sample": "the whole config-1 call, repeated"},
+            "config2": {"value": round(c2_us, 1), "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
+                        "sample": "K and V of 2048 of 16384 tokens x 8 heads, scaled by rows (the paged scatter "
+                                  "is not included)"}}
+
+
+def stream_reference(dev):
+    """Untimed for the headline: this box's HBM streaming rates in the same process, so that a
+    decode time can be read against the box it ran on (read: torch.amax over 2 GiB of int64;
+    copy: 1 GiB read + 1 GiB written)."""
+    import torch
+    x = torch.ones(1 << 28, dtype=torch.int64, device=dev)
+    y = torch.empty(1 << 27, dtype=torch.int64, device=dev)
+    r = timed(lambda: torch.amax(x), 20, 3, settle_s=0.05)["median_ms"]
+    c = timed(lambda: y.copy_(x[: 1 << 27]), 20, 3, settle_s=0.05)["median_ms"]
+    del x, y
+    torch.cuda.empty_cache()
+    return {"read_2gib_gbs": round((2 << 30) / (r * 1e-3) / 1e9, 1), "copy_1gib_gbs": round((2 << 30) / (c * 1e-3) / 1e9, 1)}
 
 
 def published_shapes(dev, steps, warmup):
@@ -418,16 +534,6 @@ def profiled_traffic():
         if v is not None else (None, None)
 
 
-def parity_counts():
-    """Compress index mismatches of configs 1 and 2 against the oracle, by distance from the
-    nearest codebook boundary, as the GPU parity tests last recorded them."""
-    path = ROOT / "profiles" / "compress_parity_config1_config2.md"
-    if not path.exists():
-        return None
-    m = re.search(r"```json\n(.*?)\n```", path.read_text(), re.S)
-    return json.loads(m.group(1)) if m else None
-
-
 def cpu_info():
     model = None
     try:
@@ -509,9 +615,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the host legs: CPU baselines and the oracle parity check")
     ap.add_argument("--no-published", action="store_true", help="skip the reference-published shapes")
-    ap.add_argument("--only", choices=["config2", "config3", "config4", "config5", "prefill", "published"],
+    ap.add_argument("--only", choices=["config1", "config2", "config3", "config4", "config5", "prefill", "published"],
                     default=None)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 256 MiB device-to-device copy (reference for rocprof byte counters)")
@@ -549,6 +656,9 @@ def main():
         head, state4 = decode_case("config4", dev, steps, warmup, time_rotated=True)
         print(f"# config4 {head['us_per_layer']:.1f} us/layer (mean {head['mean_us']:.1f}), {head['hbm_gbs']:.0f} GB/s",
               file=sys.stderr, flush=True)
+        if args.only is None:
+            extra["stream_reference"] = stream_reference(dev)
+            print(f"# stream reference {extra['stream_reference']}", file=sys.stderr, flush=True)
         if not args.no_cpu_baseline:
             cpu = cpu_baseline_decode(state4)
             print(f"# cpu baseline {cpu['value']:.0f} us/layer ({cpu['cores']} threads)", file=sys.stderr, flush=True)
@@ -564,10 +674,24 @@ def main():
         rp = prefill_case(dev, min(steps, 20), min(warmup, 5))
         extra["prefill"] = rp
         print(f"# prefill {rp['us_per_layer']:.1f} us/layer, {rp['tflops']:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    w2 = c1 = None
     if want("config2"):
-        r2 = compress_case(dev, steps, warmup)
+        r2, w2 = compress_case(dev, steps, warmup)
         extra["config2"] = r2
         print(f"# config2 {r2['us_per_layer']:.1f} us, {r2['compress_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    if want("config2") or args.only == "config1":
+        r1, c1 = config1_case(dev, steps, warmup)
+        extra["config1"] = r1
+        print(f"# config1 {r1['us']:.1f} us", file=sys.stderr, flush=True)
+    if c1 is not None and w2 is not None and not args.no_cpu_baseline:
+        extra["parity"] = parity_leg(c1, w2)
+        print(f"# parity leg: {extra['parity']['all']}", file=sys.stderr, flush=True)
+        extra["cpu_baselines_compress"] = cpu_baseline_compress(c1, w2)
+        print(f"# cpu baselines (compress): config1 {extra['cpu_baselines_compress']['config1']['value']:.0f} us, "
+              f"config2 {extra['cpu_baselines_compress']['config2']['value']:.0f} us", file=sys.stderr, flush=True)
+    if w2 is not None:
+        del w2
+        torch.cuda.empty_cache()
     if (args.only == "published") or (args.only is None and not args.no_published):
         extra["reference_published_shapes"] = published_shapes(dev, steps, warmup)
         print("# published shapes done", file=sys.stderr, flush=True)
@@ -593,9 +717,11 @@ def main():
         v = profile_value(prof, "mfma_busy_fraction")
         if v is not None:
             details.setdefault("mfma_busy_fraction_by_kernel", {})[name] = v
-    par = parity_counts()
-    if par is not None:
-        details["parity"] = par
+    details["operand_precision"] = {
+        "qk": "q and dequantized K in fp16 (centroid tables scaled into [1, 2) x c), fp32 accumulation",
+        "qjl": "fp4 +-1 signs x q_proj*corr as three fp6 e2m3 parts with per-32-element E8M0 scales "
+               "(each element within 2^-14 of its block's largest magnitude; fp16 carries 2^-11 of each)",
+        "pv": "dequantized V and p * norm in fp16, fp32 accumulation; softmax in fp32"}
     line = {
         "metric": METRIC,
         "value": round(us, 3),

@@ -102,15 +102,16 @@ int tq_polarquant_compress_matrix(const void* x, int x_dtype, int64_t x_row_stri
  *   K (pist != NULL): resid = (rot - centroids[idx]) * norm; rnorm = |resid|;
  *                     proj = resid @ pist; sign bit = proj >= 0.
  * pit, pist: f32 [128][128] row-major.  The products run on the matrix cores with each operand
- * split into fp16 hi + lo (error ~1e-8 on a unit-norm rotation); every index within 2^-21 x the
- * largest column norm of pit of a boundary is decided from the row's fp64 norm and dot product,
- * so the indices equal those of an exact (fp64) computation except within fp32 rounding of a
- * boundary.  The reference's fp16 dot products are not reproduced.  Outputs (contiguous rows):
+ * split into fp16 hi + lo (error <= 1.77e-6 x column norm + 3.4e-7, derived in tq_packed.hip);
+ * every index within 2^-19 x the largest column norm of pit + 2^-21 of a boundary is decided
+ * from the row's fp64 norm and dot product, so the indices equal those of an exact (fp64)
+ * computation except within fp32 rounding of a boundary.  The reference's fp16 dot products are not reproduced.  Outputs (contiguous rows):
  * idx_out u8 [n_rows][16*bits] little-endian bit stream (2 bits: byte j = sum_c idx[4j+c] << 2c),
  * signs_out u8 [n_rows][16] (bit b of byte j = dim 8j+b), rnorm_out / norm_out fp16 [n_rows]
  * (uint16 storage).  signs_out and rnorm_out are read only with pist.  bits: 1..4 (the
- * reference: 2).  pit / pist 16-byte aligned.  Needs 148 KB (K) / 74 KB (V) of LDS per
- * workgroup; TQ_ERR_WORKSPACE if the device has less.
+ * reference: 2).  pit / pist 16-byte aligned.  Needs 139,264 B (K) / 69,632 B (V) of dynamic
+ * LDS per workgroup plus the kernel's static arrays (about 2 KB); TQ_ERR_WORKSPACE if the device
+ * has less.
  */
 int tq_compress_packed(const void* x, int x_dtype, int64_t x_row_stride, int64_t n_rows, int head_dim,
                        const float* pit, const float* pist, const float* centroids, const float* boundaries,

@@ -107,6 +107,25 @@ def test_wht_matrix(d):
     assert wht_scale(d) == float(H.abs().max())
 
 
+def test_wht_detection_cache_follows_the_tensor():
+    """wht_magnitude caches its answer per tensor object and version: an in-place edit, a new
+    tensor (even at a reused address) or a copy is looked at again."""
+    from turboquant.core.rotation import make_wht_matrix, wht_magnitude
+    H = make_wht_matrix(128)
+    h = wht_magnitude(H)
+    assert h is not None and wht_magnitude(H) == h
+    H[3, 5] = -H[3, 5]
+    assert wht_magnitude(H) is None
+    H[3, 5] = -H[3, 5]
+    assert wht_magnitude(H) == h
+    del H
+    for _ in range(4):
+        G = torch.randn(128, 128)
+        assert wht_magnitude(G) is None
+        del G
+    assert wht_magnitude(make_wht_matrix(128).clone()) == h
+
+
 def test_wht_roundtrip_and_norms():
     from turboquant.core import make_wht_matrix
     H = make_wht_matrix(128)
@@ -135,6 +154,62 @@ def test_weight_fusion_equivalence():
     sd = {"l0.qkv_proj.weight": W.clone(), "l0.o_proj.weight": Wo.clone(), "other": torch.ones(1)}
     out = apply_weight_fusion(sd, nh, nkv, D)
     torch.testing.assert_close(out["l0.qkv_proj.weight"], fused)
+
+
+def _emulate_packed_rot(x, m, worst):
+    """rot = x @ m as tq_packed.hip computes it: both operands split into fp16 hi + lo, then for
+    each 32-dim K slice three products (hi.hi, hi.lo, lo.hi) of exact fp16 products added to an
+    fp32 accumulator, one rounding per product step.  worst: every rounding pushed a full fp32
+    ulp away from the exact running sum (the per-step error the bound in tq_packed.hip allows)."""
+    f16 = lambda a: a.astype(np.float16).astype(np.float64)  # noqa: E731
+    xh = f16(x)
+    xl = f16(x - xh)
+    mh = f16(m)
+    ml = f16(m - mh)
+    acc = np.zeros((x.shape[0], m.shape[1]), np.float32)
+    exact = np.zeros_like(acc, dtype=np.float64)
+    for ks in range(4):
+        sl = slice(32 * ks, 32 * ks + 32)
+        for a, b in ((xh, mh), (xh, ml), (xl, mh)):
+            exact = exact + a[:, sl] @ b[sl, :]
+            nxt = acc.astype(np.float64) + a[:, sl] @ b[sl, :]
+            r = nxt.astype(np.float32)
+            if worst:
+                r = np.nextafter(r, np.where(r.astype(np.float64) >= exact, np.float32(np.inf), np.float32(-np.inf)))
+            acc = r
+    return acc.astype(np.float64)
+
+
+def test_packed_compress_error_bound_holds_under_emulation():
+    """The near-boundary band of tq_compress_packed (2^-19 x the largest column norm + 2^-21,
+    derived in csrc/tq_packed.hip) against an emulation of its arithmetic on adversarial rows:
+    Gaussian rows, rows with one large and 127 sub-2^-13 elements (fp16 subnormal splits), rows
+    whose partial sums are large and cancel across the K slices, and a matrix with tiny entries.
+    The worst-case rounding variant pushes every accumulation step a full ulp the wrong way."""
+    rng = np.random.default_rng(21)
+    q, _ = np.linalg.qr(rng.standard_normal((128, 128)))
+    tiny = q.copy()
+    tiny[rng.random(q.shape) < 0.3] *= 1e-5
+    rows = [rng.standard_normal((256, 128))]
+    spiky = np.full((64, 128), 3e-5) * rng.choice([-1.0, 1.0], (64, 128))
+    spiky[np.arange(64), rng.integers(0, 128, 64)] = 1.0
+    rows.append(spiky)
+    cancel = np.zeros((64, 128))
+    for i in range(64):
+        j = rng.integers(0, 128)
+        cancel[i, :64] = np.sign(q[:64, j])
+        cancel[i, 64:] = -np.sign(q[64:, j]) * (np.abs(q[:64, j]).sum() / np.abs(q[64:, j]).sum())
+    rows.append(cancel)
+    x = np.concatenate(rows)
+    x = x / np.linalg.norm(x, axis=1, keepdims=True)
+    for m in (q, tiny):
+        band = 2.0 ** -19 * np.sqrt((m * m).sum(axis=0)).max() + 2.0 ** -21
+        exact = x @ m
+        for worst in (False, True):
+            err = np.abs(_emulate_packed_rot(x, m, worst) - exact).max()
+            assert err < band, (err, band, worst)
+        # and the band is not vacuous: the worst case uses a visible part of it
+        assert np.abs(_emulate_packed_rot(x, m, True) - exact).max() > band / 64
 
 
 def test_polarquant_config_properties():

@@ -39,8 +39,8 @@
 // read once per pair (lanes of tile A and tile B differ in their vector offset).  A larger cache
 // (the BIG instances, picked on the host) gets one descriptor per tile from a 64-bit base and
 // reads each tile's norms with the lanes of that tile.
-// Block-table entries of the next pair come through the scalar cache (a vector load would cost
-// the texture data path a whole wave of lanes for 8 bytes).  Loads run one pair ahead.
+// Block-table entries arrive four tiles at a time in lanes 0-3 of one vector load, a loop
+// iteration ahead, and are read with v_readlane.  Tile loads run one pair ahead.
 //
 // Sparse-V (kernels/sparse_v.py:108-149): for tile X, m_X = running max through tile X; token t
 // is dropped from PV when no head of the group has exp2(c (s - m_X)) > threshold, tested as
@@ -120,6 +120,13 @@ __device__ __forceinline__ float half_at(const uint32_t (&w)[2], int r) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
 }
 
+// Each quad of lanes (4 consecutive bits) of m set when any of its bits is (s_wqm_b64).
+__device__ __forceinline__ uint64_t quad_any(uint64_t m) {
+    uint64_t q;
+    asm("s_wqm_b64 %0, %1" : "=s"(q) : "s"(m) : "scc");
+    return q;
+}
+
 // Value of lane l ^ 8 within its row of 16 lanes (DPP row_ror:8).
 __device__ __forceinline__ uint32_t row_swap8(uint32_t x) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xf, 0xf, false);
@@ -189,7 +196,6 @@ struct LaneCtx {
     int qsc;                    // E8M0 scales of the parts in bytes 0-2: 2^-b, 2^-(b+5), 2^-(b+10)
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
     uint32_t vquad;                // 3-bit V quad table base (a 3-bit K quad table is at address 0)
-    uint32_t shl8;              // 56 - 8 * (lane / 8): moves the lane's ballot byte to bits 56..63
     uint64_t hmask;             // lanes of real heads
     bool lo8;                   // column < 8: tile A
 };
@@ -257,36 +263,34 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
         tA = qjl_tile<sign_replicas<KB, VB>()>(kr.ksA, c);
         tB = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, c);
     }
-    uint64_t rm[4];
     // Rows past the end may hold any bits in a paged block: masked out of the scores, and their
-    // value norms zeroed (bit-wise, before any arithmetic).
+    // value norms zeroed (bit-wise, before any arithmetic), in partial pairs only.
     uint32_t vn[2] = {vr.vn[0], vr.vn[1]};
-    if (pi.nvA == 16 && pi.nvB == 16) {
+    float sc[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rm[r] = ~0ull;
-    } else {
+    for (int r = 0; r < 4; ++r) {
+        // Scalar copies: shuffling ext_vector elements in place has miscompiled before.
+        const float s1 = c.lo8 ? sA[r] : sB[r];
+        if (KQJL) {
+            const float s2 = c.lo8 ? tA[r] : tB[r];
+            sc[r] = __builtin_fmaf(half_at(kr.kn, r), s1, __builtin_fmaf(half_at(kr.krn, r), s2, 0.0f));
+        } else {
+            sc[r] = half_at(kr.kn, r) * s1;
+        }
+    }
+    if (pi.nvA != 16 || pi.nvB != 16) {
+        uint64_t rm[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rm[r] = row_mask(pi.nvA, pi.nvB, r);
+        for (int r = 0; r < 4; ++r) {
+            rm[r] = row_mask(pi.nvA, pi.nvB, r);
+            sc[r] = __builtin_amdgcn_inverse_ballot_w64(rm[r]) ? sc[r] : kNegInf;
+        }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const uint32_t lo = __builtin_amdgcn_inverse_ballot_w64(rm[2 * k]) ? 0x0000ffffu : 0u;
             const uint32_t hi = __builtin_amdgcn_inverse_ballot_w64(rm[2 * k + 1]) ? 0xffff0000u : 0u;
             vn[k] &= lo | hi;
         }
-    }
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        // Scalar copies: shuffling ext_vector elements in place has miscompiled before.
-        const float s1 = c.lo8 ? sA[r] : sB[r];
-        float v;
-        if (KQJL) {
-            const float s2 = c.lo8 ? tA[r] : tB[r];
-            v = __builtin_fmaf(half_at(kr.kn, r), s1, __builtin_fmaf(half_at(kr.krn, r), s2, 0.0f));
-        } else {
-            v = half_at(kr.kn, r) * s1;
-        }
-        sc[r] = __builtin_amdgcn_inverse_ballot_w64(rm[r]) ? v : kNegInf;
     }
 
     // ---------------- online softmax ----------------
@@ -321,10 +325,13 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
         for (int r = 0; r < 4; ++r) {
             const uint64_t bal = __builtin_amdgcn_ballot_w64(sc[r] > thr) & c.hmask;
             any |= bal;
-            // some head of this lane's 8-lane group (its tile's token 4g + r) passes
-            const bool keep = (uint32_t)((bal << c.shl8) >> 32) >= (1u << 24);
-            pr[r] = keep ? pr[r] : 0.f;
-            if (COUNT) kept += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(keep) & 0x0101010101010101ull);
+            // lanes of the 8-lane groups (one token of one tile, the group's heads) with a passing
+            // head, on the scalar unit: each quad of lanes OR-spread (s_wqm), then each pair of quads
+            const uint64_t q = quad_any(bal);
+            const uint64_t lo = (q | (q >> 4)) & 0x0f0f0f0f0f0f0f0full;
+            const uint64_t keepm = lo | (lo << 4);
+            pr[r] = __builtin_amdgcn_inverse_ballot_w64(keepm) ? pr[r] : 0.f;
+            if (COUNT) kept += (uint32_t)__builtin_popcountll(keepm & 0x0101010101010101ull);
         }
         if (COUNT) {
             st.n_tot += (uint32_t)(pi.nvA + pi.nvB);
@@ -554,7 +561,6 @@ void decode_fast_kernel(FastDecodeParams p) {
     c.vquad = lds0 + p.lds_v;
     if (VB == 3 && !(quad_table<KB>() && KB == 3 && p.lds_v == 0))
         asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
-    c.shl8 = 56u - 8u * (uint32_t)(lane >> 3);
 
     // ---- loop-invariant lane offsets inside a tile ----
     // lane-grouped tiles: the lane's key chunk (row n, dims 32g..) and value chunk (rows
@@ -630,21 +636,16 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int32_t* bt_row = p.bt + s * p.bt_stride;
     const int tile0 = t_begin >> 4;                               // absolute tile index of the chunk start
     const int tmask = (1 << p.tile_shift) - 1;
-    // Block numbers of the two tiles of a pair (clamped into the sequence's blocks) through the
-    // scalar cache, one pair ahead: each vector load costs the texture data path a full wave of
-    // lanes, so the eight bytes are not fetched by 64 lanes.
-    typedef __attribute__((address_space(4))) const int32_t bt_s;
-    const bt_s* bts = (const bt_s*)(uintptr_t)bt_row;
-    auto bt_pair = [&](int pi, int (&b)[2]) {
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            int lb = (tile0 + 2 * pi + x) >> p.tile_shift;
-            lb = lb < nblk_seq ? lb : nblk_seq - 1;
-            b[x] = bts[lb];
-        }
+    // Block numbers (clamped into the sequence's blocks) of tiles t .. t + 3 of the chunk in
+    // lanes 0-3 of one vector load, issued a loop iteration (two pairs) ahead of their use and
+    // read with v_readlane.  (Scalar loads of them would share the LDS reads' counter, so the
+    // pipelined lookups would wait for them.)
+    auto bt_quad = [&](int t) -> int {
+        int lb = (tile0 + t + (lane & 3)) >> p.tile_shift;
+        lb = lb < nblk_seq ? lb : nblk_seq - 1;
+        return bt_row[lb];
     };
-    int bt_next[2];
-    bt_pair(0, bt_next);
+    const uint32_t nblocks32 = p.num_blocks < 0x7fffffff ? (uint32_t)p.num_blocks : 0x7fffffffu;
 
     // Norm rows of tiles A (lanes col < 8) and B (col >= 8) in one load: the scalar offset
     // addresses the nearer tile, lanes of the farther one add the distance.
@@ -658,10 +659,9 @@ void decode_fast_kernel(FastDecodeParams p) {
         return NormAddr{o_norm + (__builtin_amdgcn_inverse_ballot_w64(up) ? d : 0u), lo};
     };
 
-    // K part of pair pi (and the block numbers of pair pi + 1); fills the V offsets of pi.
-    auto fetch_k = [&](int pi, KRaw<KB, KQJL>& kr, PairInfo& info) {
-        int blk[2] = {bt_next[0], bt_next[1]};
-        bt_pair(pi + 1, bt_next);
+    // K part of pair pi, whose tiles' block numbers are b0, b1; fills the V offsets of pi.
+    auto fetch_k = [&](int pi, int b0, int b1, KRaw<KB, KQJL>& kr, PairInfo& info) {
+        int blk[2] = {b0, b1};
         uint32_t kb[2], r0[2];
         int nv[2];
 #pragma unroll
@@ -669,9 +669,10 @@ void decode_fast_kernel(FastDecodeParams p) {
             const int i = 2 * pi + x;
             const int t0 = t_begin + 16 * i;
             int nvr = t_end - t0;
-            nvr = nvr < 0 ? 0 : (nvr > 16 ? 16 : nvr);
+            nvr &= ~(nvr >> 31);  // max(., 0)
+            nvr = nvr < 16 ? nvr : 16;
             int bk = blk[x];
-            if (bk < 0 || (int64_t)bk >= p.num_blocks) {  // unreadable entry: read block 0, mask it
+            if ((uint32_t)bk >= nblocks32) {  // unreadable entry (negative or past the cache): read block 0, mask it
                 bk = 0;
                 nvr = 0;
             }
@@ -813,7 +814,11 @@ void decode_fast_kernel(FastDecodeParams p) {
     KRaw<KB, KQJL> kr[2];
     PairInfo info[2];
     VRaw<VB> vr[2];
-    fetch_k(0, kr[0], info[0]);
+    const int bt0 = bt_quad(0);  // tiles 0-3: pair 0
+    // tiles 2-5: pairs 1 and 2, the first loop iteration (issued before pair 0's loads, as in
+    // the loop, where it precedes two pairs' loads)
+    int btw = bt_quad(2);
+    fetch_k(0, __builtin_amdgcn_readlane(bt0, 0), __builtin_amdgcn_readlane(bt0, 1), kr[0], info[0]);
     load_v(info[0], vr[0]);
     // ---- query operands: conversion ----
     if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);  // q x H: elements 32g + i
@@ -880,11 +885,13 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int ntiles = (t_end - t_begin + 15) >> 4;
     const int npairs = (ntiles + 1) >> 1;
     for (int i = 0; i < npairs; i += 2) {
-        fetch_k(i + 1, kr[1], info[1]);
+        const int btc = btw;
+        btw = bt_quad(2 * i + 6);  // the next iteration's pairs i + 3, i + 4
+        fetch_k(i + 1, __builtin_amdgcn_readlane(btc, 0), __builtin_amdgcn_readlane(btc, 1), kr[1], info[1]);
         load_v(info[1], vr[1]);
         compute_pair<KB, KQJL, VB, COUNT>(kr[0], vr[0], info[0], st, c, p);
         if (i + 1 >= npairs) break;
-        fetch_k(i + 2, kr[0], info[0]);
+        fetch_k(i + 2, __builtin_amdgcn_readlane(btc, 2), __builtin_amdgcn_readlane(btc, 3), kr[0], info[0]);
         load_v(info[0], vr[0]);
         compute_pair<KB, KQJL, VB, COUNT>(kr[1], vr[1], info[1], st, c, p);
     }

@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import functools
 import math
+import weakref
 
 import torch
 
@@ -46,21 +47,33 @@ def _sylvester_signs(d: int) -> torch.Tensor:
     return 1 - 2 * parity  # (-1)^popcount(i & j)
 
 
+# id(tensor) -> (weak reference, version counter, answer): a hit needs the same live tensor
+# object at the same version, so a new tensor at a reused address is never mistaken for it.
+_wht_cache: dict = {}
+
+
 def wht_magnitude(rotation_matrix: torch.Tensor) -> float | None:
     """h if rotation_matrix == (-1)^popcount(i&j) * h exactly for one float h, else None.
 
     make_wht_matrix on different devices can round h differently; the kernels take the
-    caller's own h, so any such matrix is accepted."""
+    caller's own h, so any such matrix is accepted.  The answer is cached per tensor object and
+    version (in-place writes bump it), so a device-resident matrix passed on every call is read
+    back to the host once, not per call."""
     if rotation_matrix.dim() != 2 or rotation_matrix.shape[0] != rotation_matrix.shape[1]:
         return None
     d = rotation_matrix.shape[0]
     if d == 0 or d & (d - 1):
         return None
+    hit = _wht_cache.get(id(rotation_matrix))
+    if hit is not None and hit[0]() is rotation_matrix and hit[1] == rotation_matrix._version:
+        return hit[2]
     m = rotation_matrix.detach().float().cpu()
     h = m[0, 0]
-    if not bool(h > 0):
-        return None
-    return float(h) if bool(torch.equal(m, _sylvester_signs(d).float() * h)) else None
+    res = float(h) if bool(h > 0) and bool(torch.equal(m, _sylvester_signs(d).float() * h)) else None
+    if len(_wht_cache) > 256:
+        _wht_cache.clear()
+    _wht_cache[id(rotation_matrix)] = (weakref.ref(rotation_matrix), rotation_matrix._version, res)
+    return res
 
 
 def is_wht_matrix(rotation_matrix: torch.Tensor) -> bool:
