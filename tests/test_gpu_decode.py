@@ -402,6 +402,64 @@ def test_sparse_v_reference_slot_layout(dev):
     assert abs(gsk - skipped) <= allow
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_sparse_v_default_is_the_reference_single_pass(dev, bs):
+    """tq_v12_sparse_v without tokens_per_chunk walks each (sequence, KV head) in one pass, as
+    the reference's grid does: against decode_chunked(chunk = whole sequence, tile = the KV
+    block), outputs at the contract tolerance and skip counts equal up to the tokens within
+    rounding of the threshold; and it differs from a split-K chunking of the same data in which
+    tokens it skips."""
+    from turboquant.kernels.sparse_v import tq_v12_sparse_v
+    rng = np.random.default_rng(80 + bs)
+    Hkv, G, S = 2, 6, 3
+    Hq = Hkv * G
+    lens = [1500, 700, 2100]
+    maxb = max(math.ceil(L / bs) for L in lens)
+    nb = S * maxb + 2
+    cache = rng.integers(0, 256, (nb, 2, bs, Hkv, 128), dtype=np.uint8)
+    norms = (rng.uniform(5, 15, (nb, 2, bs, Hkv))).astype(np.float16)
+    cache[..., 48:50] = norms.view(np.uint8).reshape(nb, 2, bs, Hkv, 2)
+    bt = rng.permutation(nb)[: S * maxb].reshape(S, maxb).astype(np.int32)
+    q = (rng.standard_normal((S, Hq, 128)) * 6).astype(np.float16)
+    cent = _cb(3)
+    t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    sm, thresh = 1 / math.sqrt(128), 1e-4
+    out = torch.empty((S, Hq, 128), dtype=torch.float16, device=dev)
+    st = torch.zeros(2, dtype=torch.int64, device=dev)
+    tq_v12_sparse_v(out, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm, thresh, skip_stats=st)
+    out_split = torch.empty_like(out)
+    st_split = torch.zeros(2, dtype=torch.int64, device=dev)
+    tq_v12_sparse_v(out_split, t(q), t(cache), cent.to(dev), t(bt), t(np.array(lens, np.int32)), sm, thresh,
+                    tokens_per_chunk=256, skip_stats=st_split)
+    torch.cuda.synchronize()
+    skipped = total = 0
+    margins = []
+    for s, L in enumerate(lens):
+        for kh in range(Hkv):
+            blks = bt[s, np.arange(L) // bs]
+            rows = np.arange(L) % bs
+            ksl = cache[blks, 0, rows, kh]
+            vsl = cache[blks, 1, rows, kh]
+            kp = {"idx": ksl[:, :48], "norm": ksl[:, 48:50].copy().view(np.uint16).reshape(-1)}
+            vp = {"idx": vsl[:, :48], "norm": vsl[:, 48:50].copy().view(np.uint16).reshape(-1)}
+            k, _, _ = odec.dequant_keys(kp, cent.double().numpy(), 3, False)
+            v = odec.dequant_values(vp, cent.double().numpy(), 3)
+            hs = slice(kh * G, (kh + 1) * G)
+            qs = q[s, hs].astype(np.float64)
+            want, sk, tot = odec.decode_chunked(qs, None, k, None, None, v, sm, 0.0, L, thresh, tile=bs)
+            margins.append(odec.sparse_v_margins(qs, None, k, None, None, sm, 0.0, L, tile=bs))
+            np.testing.assert_allclose(out[s, hs].float().cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+            skipped += sk
+            total += tot
+    gsk, gtot = st.tolist()
+    allow = _skip_allowance(margins, thresh)
+    print(f"single pass: skipped gpu {gsk} oracle {skipped} of {total} (within rounding {allow}); "
+          f"split-K 256 skipped {st_split.tolist()[0]}")
+    assert gtot == total and skipped > 0
+    assert abs(gsk - skipped) <= allow
+    assert st_split.tolist()[0] != gsk
+
+
 @pytest.mark.parametrize("layouts", [("keys", "values"), ("rows", "rows")])
 @pytest.mark.parametrize("chunk", [256, 240])
 def test_decode_sparse_v_block32(dev, layouts, chunk):

@@ -13,7 +13,13 @@ KV_BLK_SZ = block_size loop does, for block sizes 16 and 32; every 32 tokens for
 blocks), token t's V is skipped when max over the GQA group of exp(score - m) <= threshold;
 skipped tokens still count in the softmax denominator.  The work unit here is a chunk of
 tokens_per_chunk tokens (rounded up to a multiple of 32 for block sizes of 32 or more); with
-tokens_per_chunk >= the sequence length it is the reference's single pass.
+tokens_per_chunk >= the sequence length it is the reference's single pass, one work unit per
+(sequence, KV head) as the reference's grid (num_seqs, num_kv_heads) runs it
+(kernels/sparse_v.py:316,341).  That is tq_v12_sparse_v's default, so the drop-in skips the
+same tokens as the reference; a split-K chunk (faster for few long sequences, with the running
+max restarting per chunk) is an opt-in through tokens_per_chunk.  tq_v11 (no skipping) keeps
+the split-K planner by default: without the skip rule the chunking changes only the fp32
+summation order, not the result.
 """
 
 from __future__ import annotations
@@ -80,6 +86,10 @@ def tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, sc
     max_blocks = block_tables.shape[1]
     cap = max_blocks * bs
     msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+    if tokens_per_chunk is None and threshold > 0:
+        # the reference's single pass: one unit per (sequence, KV head), whole sequence
+        step = 32 if bs >= 32 else 16
+        tokens_per_chunk = max(step, -(-msl // step) * step)
     chunk = tokens_per_chunk or choose_tokens_per_chunk(
         S, hkv, msl, concurrent_units(dev, 3, False, 3, Hq, hkv, tq_cache.stride(2), True))
     kv = _aos_view(tq_cache, 0, cb)
@@ -96,7 +106,11 @@ def tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, sc
 
 def tq_v12_sparse_v(out, q, tq_cache, centroids, block_tables, seq_lens, scale,
                     threshold: float = SPARSE_V_THRESHOLD, **kw):
-    """Sparse-V decode (the role of _tq_v12_sparse_v_kernel, kernels/sparse_v.py:25-159)."""
+    """Sparse-V decode (the role of _tq_v12_sparse_v_kernel, kernels/sparse_v.py:25-159).
+
+    By default one pass over each (sequence, KV head), the reference's grid and skip
+    semantics; tokens_per_chunk=N opts into split-K chunks of N tokens (the running max the
+    skip test uses then restarts per chunk)."""
     return tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, scale, threshold, **kw)
 
 
