@@ -157,8 +157,17 @@ __device__ __forceinline__ float sum_over_groups(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-// fp16 of vn * p, rounded to nearest (v_fma_mix*_f16).
-__device__ __forceinline__ _Float16 scale_to_half(float vn, float pr) { return (_Float16)__builtin_fmaf(vn, pr, 0.0f); }
+// half2 of (vn.lo * p0, vn.hi * p1) for a word vn of two fp16 norms, each product rounded once
+// to nearest: v_fma_mixlo_f16 writes the low half, v_fma_mixhi_f16 the high half keeping the low
+// (two instructions; the compiler forms each half alone and then shifts and ors them).
+__device__ __forceinline__ uint32_t scale_to_half2(uint32_t vn, float p0, float p1) {
+    uint32_t u;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, %3, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(u)
+        : "v"(vn), "v"(p0), "v"(p1));
+    return u;
+}
 
 // Raw data of one pair of tiles.  K part: loaded one pair ahead; V part: loaded at the start
 // of its own pair (it is first needed after the QK products and the softmax).
@@ -183,8 +192,10 @@ struct PairInfo {
 };
 
 struct Softmax {
-    float m;        // running max per head (raw score units), equal in lanes col and col ^ 8
-    float lsum;     // this lane's tokens, relative to m
+    float m;        // Sparse-V: running max per head (raw score units), equal in lanes col and col ^ 8
+    float mref;     // exponent base of lsum and acc: p = exp2(c s + nb), nb = -c mref - 1
+    float nb;
+    float lsum;     // this lane's tokens
     tq_floatx4 acc[8];
     uint32_t n_tot, n_kept;  // wave-uniform
 };
@@ -197,6 +208,7 @@ struct LaneCtx {
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
     uint32_t vquad;                // 3-bit V quad table base (a 3-bit K quad table is at address 0)
     uint64_t hmask;             // lanes of real heads
+    float gap;                  // 1 / c_exp: one log2 unit of p in raw score units
     bool lo8;                   // column < 8: tile A
 };
 
@@ -252,7 +264,7 @@ __device__ __forceinline__ uint64_t row_mask(int nvA, int nvB, int r) {
 }
 
 // One pair of tiles.
-template <int KB, bool KQJL, int VB, bool COUNT>
+template <int KB, bool KQJL, int VB, int SPV>
 __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRaw<VB>& vr, const PairInfo& pi,
                                              Softmax& st, const LaneCtx& c, const FastDecodeParams& p) {
     // ---------------- scores ----------------
@@ -294,29 +306,39 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     }
 
     // ---------------- online softmax ----------------
+    // The exponent base mref moves only when some head's max passes it by more than one log2
+    // unit (gap = 1 / c), and p is taken at half scale, exp2(c (s - mref) - 1) <= 1: p * norm
+    // stays within fp16 as with the exact running max, while most pairs skip the rescale of
+    // acc and lsum.  The Sparse-V test keeps the exact running max (st.m).
     float mt = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
     mt = max_over_groups(mt);                 // this tile's max for the lane's head
     const float other = row_swap8f(mt);       // the other tile's max for the same head
-    const float m_old = st.m;
-    const float m_new = fmaxf(fmaxf(m_old, mt), other);
+    const float m_pair = fmaxf(mt, other);
     const float cexp = p.c_exp;
-    if (__builtin_amdgcn_ballot_w64(m_new > m_old) & c.hmask) {
-        const float alpha = __builtin_amdgcn_exp2f(cexp * (m_old - m_new));  // 0 while m_old = -inf
+    float m_old = 0.f, m_new = 0.f;
+    if (SPV) {
+        m_old = st.m;
+        m_new = fmaxf(m_old, m_pair);
+        st.m = m_new;
+    }
+    if (__builtin_amdgcn_ballot_w64(m_pair > st.mref + c.gap) & c.hmask) {
+        const float mb = fmaxf(st.mref, m_pair);
+        const float alpha = __builtin_amdgcn_exp2f(cexp * (st.mref - mb));  // 0 while mref = -inf
         st.lsum *= alpha;
 #pragma unroll
         for (int i = 0; i < 8; ++i) st.acc[i] *= alpha;
+        st.mref = mb;
+        st.nb = __builtin_fmaf(-cexp, mb, -1.0f);
     }
-    st.m = m_new;
-    const float nb = m_new == kNegInf ? 0.f : -cexp * m_new;
     float pr[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], cexp, nb));  // 0 for masked rows
+    for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], cexp, st.nb));  // 0 for masked rows
     st.lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 
     // ---------------- Sparse-V ----------------
     // The skip test uses the running max through the token's KV block: through its own tile for
     // 16-token blocks, through the pair (a 32-token block) otherwise.
-    if (p.sparse) {
+    if (SPV) {
         const float m_skip = (c.lo8 && !p.sparse_pair) ? fmaxf(m_old, mt) : m_new;
         const float thr = m_skip + p.thr_log;
         uint32_t kept = 0;
@@ -331,9 +353,9 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
             const uint64_t lo = (q | (q >> 4)) & 0x0f0f0f0f0f0f0f0full;
             const uint64_t keepm = lo | (lo << 4);
             pr[r] = __builtin_amdgcn_inverse_ballot_w64(keepm) ? pr[r] : 0.f;
-            if (COUNT) kept += (uint32_t)__builtin_popcountll(keepm & 0x0101010101010101ull);
+            if (SPV == 2) kept += (uint32_t)__builtin_popcountll(keepm & 0x0101010101010101ull);
         }
-        if (COUNT) {
+        if (SPV == 2) {
             st.n_tot += (uint32_t)(pi.nvA + pi.nvB);
             st.n_kept += kept;
         }
@@ -341,15 +363,9 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     }
 
     // ---------------- PV ----------------
-    union {
-        _Float16 h[2];
-        uint32_t u;
-    } p01, p23;
-    p01.h[0] = scale_to_half(half_at(vn, 0), pr[0]);
-    p01.h[1] = scale_to_half(half_at(vn, 1), pr[1]);
-    p23.h[0] = scale_to_half(half_at(vn, 2), pr[2]);
-    p23.h[1] = scale_to_half(half_at(vn, 3), pr[3]);
-    const tq_u32x4 bw = {p01.u, p23.u, row_swap8(p01.u), row_swap8(p23.u)};
+    const uint32_t p01 = scale_to_half2(vn[0], pr[0], pr[1]);
+    const uint32_t p23 = scale_to_half2(vn[1], pr[2], pr[3]);
+    const tq_u32x4 bw = {p01, p23, row_swap8(p01), row_swap8(p23)};
     const tq_half8 bop = __builtin_bit_cast(tq_half8, bw);
     // acc[a] (dim 8n + a): field group a of the lane's chunk is that dim's four tokens, so the
     // lookups are the A operand as they come: k-slots 0-3 tile A's tokens, 4-7 tile B's.
@@ -400,8 +416,8 @@ constexpr int fast_waves() {
     return KQJL ? 3 : 4;
 }
 
-// COUNT: Sparse-V skip statistics requested (a separate instance keeps the counting off the
-// common path).
+// SPV: Sparse-V off (0), on (1), on with skip statistics (2); separate instances keep the test
+// and the counting off the paths that do not use them.
 // ADDR: how K / V tiles are addressed and cached.
 //   TQ_ADDR_CACHED: 32-bit offsets from one descriptor per head; loads allocate in the caches
 //       (K + V fit the 256 MB last-level cache, so repeated decodes of them can hit there);
@@ -409,7 +425,7 @@ constexpr int fast_waves() {
 //       than the last-level cache, where every byte is read once per decode;
 //   TQ_ADDR_BIG: a cache spanning 2 GiB or more: tiles addressed from 64-bit per-tile bases,
 //       streaming loads.
-template <int KB, bool KQJL, int VB, bool COUNT, int ADDR>
+template <int KB, bool KQJL, int VB, int SPV, int ADDR>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
                                                                      fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
@@ -784,6 +800,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int head = kh * p.group + hcol;
     const bool hvalid = hcol < p.group;
     c.hmask = __builtin_amdgcn_ballot_w64(hvalid);
+    c.gap = 1.0f / p.c_exp;
     float qv[32];
     {
         const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
@@ -876,6 +893,8 @@ void decode_fast_kernel(FastDecodeParams p) {
 
     Softmax st;
     st.m = kNegInf;
+    st.mref = kNegInf;
+    st.nb = 0.f;
     st.lsum = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) st.acc[i] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
@@ -889,17 +908,17 @@ void decode_fast_kernel(FastDecodeParams p) {
         btw = bt_quad(2 * i + 6);  // the next iteration's pairs i + 3, i + 4
         fetch_k(i + 1, __builtin_amdgcn_readlane(btc, 0), __builtin_amdgcn_readlane(btc, 1), kr[1], info[1]);
         load_v(info[1], vr[1]);
-        compute_pair<KB, KQJL, VB, COUNT>(kr[0], vr[0], info[0], st, c, p);
+        compute_pair<KB, KQJL, VB, SPV>(kr[0], vr[0], info[0], st, c, p);
         if (i + 1 >= npairs) break;
         fetch_k(i + 2, __builtin_amdgcn_readlane(btc, 2), __builtin_amdgcn_readlane(btc, 3), kr[0], info[0]);
         load_v(info[0], vr[0]);
-        compute_pair<KB, KQJL, VB, COUNT>(kr[1], vr[1], info[1], st, c, p);
+        compute_pair<KB, KQJL, VB, SPV>(kr[1], vr[1], info[1], st, c, p);
     }
 
     // ---- combine the lane groups and the two tile halves ----
     float lsum = sum_over_groups(st.lsum);
     lsum += row_swap8f(lsum);
-    if (COUNT) {
+    if (SPV == 2) {
         cnt_tot += (unsigned long long)st.n_tot;
         cnt_kept += (unsigned long long)st.n_kept;
     }
@@ -918,7 +937,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     } else if (writer) {
         const int64_t slot = prow_base + (int64_t)hcol * prow_step;
         if (g == 0) {
-            p.ws_m[slot] = st.m == kNegInf ? kNegInf : st.m * p.c_exp;  // log2 units for the merge
+            p.ws_m[slot] = st.mref == kNegInf ? kNegInf : st.mref * p.c_exp;  // log2 units for the merge
             p.ws_l[slot] = lsum;
         }
         float4* dst = reinterpret_cast<float4*>(p.ws_acc + slot * TQ_HEAD_DIM + 32 * g);
@@ -948,7 +967,7 @@ void decode_fast_kernel(FastDecodeParams p) {
         }
     }
     }  // pieces
-    if (COUNT && lane == 0 && cnt_tot) {
+    if (SPV == 2 && lane == 0 && cnt_tot) {
         atomicAdd(p.skip_stats, cnt_tot - cnt_kept);
         atomicAdd(p.skip_stats + 1, cnt_tot);
     }
@@ -956,11 +975,12 @@ void decode_fast_kernel(FastDecodeParams p) {
 
 }  // namespace
 
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count, int addr) {
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, int spv, int addr) {
 #define TQ_FP_A(KB, KQ, VB, A)                                                                         \
     if (addr == A)                                                                                     \
-        return count ? (const void*)decode_fast_kernel<KB, KQ, VB, true, A>                            \
-                     : (const void*)decode_fast_kernel<KB, KQ, VB, false, A>;
+        return spv == 2 ? (const void*)decode_fast_kernel<KB, KQ, VB, 2, A>                            \
+               : spv == 1 ? (const void*)decode_fast_kernel<KB, KQ, VB, 1, A>                          \
+                          : (const void*)decode_fast_kernel<KB, KQ, VB, 0, A>;
 #define TQ_FP(KB, KQ, VB)                                                                              \
     if (kb == KB && kq == KQ && vb == VB) {                                                            \
         TQ_FP_A(KB, KQ, VB, TQ_ADDR_CACHED) TQ_FP_A(KB, KQ, VB, TQ_ADDR_STREAM) TQ_FP_A(KB, KQ, VB, TQ_ADDR_BIG) \
@@ -1033,7 +1053,7 @@ void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* ld
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream) {
-    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, prm.sparse && prm.skip_stats, prm.addr);
+    const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, !prm.sparse ? 0 : prm.skip_stats ? 2 : 1, prm.addr);
     if (!kern) return TQ_ERR_BITS;
     FastDecodeParams p = prm;
     void* args[] = {&p};

@@ -90,8 +90,9 @@ enum {
 // non-temporal loads: every byte is read once per decode and nothing would be kept anyway.
 constexpr int64_t kTqStreamBytes = 256ll << 20;
 
-// decode_fast_kernel<kb, kq, vb, count, addr> (nullptr: unsupported bit widths).
-const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, bool count = false, int addr = TQ_ADDR_CACHED);
+// decode_fast_kernel<kb, kq, vb, spv, addr> (nullptr: unsupported bit widths); spv: Sparse-V off
+// (0), on (1), on with skip statistics (2).
+const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, int spv = 0, int addr = TQ_ADDR_CACHED);
 
 // LDS byte offsets of the fp4 sign table, the K and the V tables, a 512-byte scratch, and the
 // total.

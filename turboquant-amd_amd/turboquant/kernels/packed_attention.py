@@ -130,3 +130,79 @@ def attention_unpacked_ref(Q, Q_proj, K_mse_rot, signs_float, k_r_norm, V_mse_ro
     score_qjl = torch.bmm(Q_proj.unsqueeze(1), K_qjl.transpose(1, 2).contiguous()).squeeze(1)
     attn = F.softmax(score_mse + score_qjl, dim=-1)
     return torch.bmm(attn.unsqueeze(1), V_mse_rot).squeeze(1)
+
+
+def _random_case(BH: int, Sk: int, D: int, dev, gen):
+    u8 = lambda *s: torch.randint(0, 256, s, dtype=torch.uint8, device=dev, generator=gen)  # noqa: E731
+    f16 = lambda *s: torch.rand(s, device=dev, generator=gen).half()  # noqa: E731
+    return dict(k_idx_packed=u8(BH, Sk, D // 4), k_signs_packed=u8(BH, Sk, D // 8),
+                k_r_norm=f16(BH, Sk) * 0.1, k_norm=f16(BH, Sk) + 0.5, v_idx_packed=u8(BH, Sk, D // 4),
+                v_norm=f16(BH, Sk) + 0.5,
+                Q=(torch.randn(BH, D, device=dev, generator=gen) * 0.1).half(),
+                Q_proj=(torch.randn(BH, D, device=dev, generator=gen) * 0.1).half())
+
+
+def _unpacked(case: dict, centroids, D: int):
+    BH, Sk, _ = case["k_idx_packed"].shape
+    k_idx = unpack_2bit(case["k_idx_packed"].reshape(-1, D // 4), D).reshape(BH, Sk, D).long()
+    k_sg = unpack_1bit(case["k_signs_packed"].reshape(-1, D // 8), D).reshape(BH, Sk, D)
+    v_idx = unpack_2bit(case["v_idx_packed"].reshape(-1, D // 4), D).reshape(BH, Sk, D).long()
+    return (centroids[k_idx] * case["k_norm"].float().unsqueeze(-1), k_sg.float() * 2 - 1,
+            case["k_r_norm"].float(), centroids[v_idx] * case["v_norm"].float().unsqueeze(-1))
+
+
+def run(bh_list=(8, 32, 64), sk_check=(256, 4096, 16384, 32768), sk_bench=(256, 1024, 4096, 16384, 32768),
+        warmup: int = 20, iters: int = 200, seed: int = 42, verbose: bool = True) -> dict:
+    """Self-test and benchmark of packed_attention on cuda:0 (the role of the reference
+    module's run(), kernels/packed_attention.py:347-460).
+
+    Random packed K (2-bit + permuted QJL signs) and V with fp16 norms, the 2-bit kernel
+    codebook, corr_scale = sqrt(pi/2)/sqrt(D).  Correctness: packed_attention against
+    attention_unpacked_ref on the unpacked tensors (cosine and max abs difference).  Benchmark:
+    mean device time of packed_attention and of attention_unpacked_ref per call.  Returns the
+    figures printed."""
+    from turboquant.kernels._selfcheck import time_ms
+    from turboquant.kernels.packed_compress import permute_signs_for_chunked, solve_codebook
+    dev = torch.device("cuda")
+    D = 128
+    centroids = solve_codebook(D, 2).to(dev)
+    corr_scale = math.sqrt(math.pi / 2) / math.sqrt(D)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    say = print if verbose else (lambda *a, **k: None)
+    say(f"Packed attention on {torch.cuda.get_device_name(0)}: D={D}, 2-bit K + QJL, 2-bit V")
+    res = {"correctness": [], "benchmark": []}
+
+    def call(c, perm):
+        return packed_attention(c["Q"], c["Q_proj"], c["k_idx_packed"], perm, c["k_r_norm"], c["k_norm"],
+                                c["v_idx_packed"], c["v_norm"], centroids, corr_scale)
+
+    for BH in bh_list:
+        for Sk in sk_check:
+            c = _random_case(BH, Sk, D, dev, gen)
+            kmse, sg, rn, vmse = _unpacked(c, centroids, D)
+            ref = attention_unpacked_ref(c["Q"].float(), c["Q_proj"].float(), kmse, sg, rn, vmse, corr_scale)
+            out = call(c, permute_signs_for_chunked(c["k_signs_packed"], D)).float()
+            cos = F.cosine_similarity(ref.reshape(1, -1), out.reshape(1, -1)).item()
+            err = (out - ref).abs().max().item()
+            ok = cos > 0.99
+            res["correctness"].append({"BH": BH, "Sk": Sk, "cos": cos, "max_abs_err": err, "pass": ok})
+            say(f"  BH={BH:>3} Sk={Sk:>5}: cos={cos:.6f} max|diff|={err:.2e} {'PASS' if ok else 'FAIL'}")
+            del c, kmse, sg, rn, vmse
+    say(f"{'BH':>4} {'Sk':>6} {'packed ms':>10} {'torch ms':>10} {'speedup':>8}")
+    for BH in bh_list:
+        for Sk in sk_bench:
+            c = _random_case(BH, Sk, D, dev, gen)
+            perm = permute_signs_for_chunked(c["k_signs_packed"], D)
+            p_ms = time_ms(lambda: call(c, perm), warmup, iters)
+            kmse, sg, rn, vmse = _unpacked(c, centroids, D)
+            q, qp = c["Q"].float(), c["Q_proj"].float()
+            r_ms = time_ms(lambda: attention_unpacked_ref(q, qp, kmse, sg, rn, vmse, corr_scale), warmup, iters)
+            res["benchmark"].append({"BH": BH, "Sk": Sk, "packed_ms": p_ms, "torch_ms": r_ms})
+            say(f"{BH:>4} {Sk:>6} {p_ms:>10.4f} {r_ms:>10.4f} {r_ms / p_ms:>7.2f}x")
+            del c, kmse, sg, rn, vmse
+    return res
+
+
+if __name__ == "__main__":
+    run()

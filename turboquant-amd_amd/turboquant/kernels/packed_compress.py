@@ -160,3 +160,63 @@ def compress_v(V: torch.Tensor, PiT: torch.Tensor, centroids: torch.Tensor, boun
     the residual.  Returns (v_idx uint8 [N, D*b/8], v_norm fp16 [N])."""
     idx, _, _, norm = _packed_compress(V, PiT, None, centroids, boundaries, "compress_v")
     return idx, norm
+
+
+def run(sizes=(2048, 32768, 131072, 524288), n_test: int = 131072, warmup: int = 25, iters: int = 300,
+        seed: int = 42, verbose: bool = True) -> dict:
+    """Self-test and benchmark of compress_k / compress_v on cuda:0 (the role of the reference
+    module's run(), kernels/packed_compress.py:243-330).
+
+    Correctness: n_test Gaussian rows through compress_k and compress_v with a seeded random
+    rotation pair and the 2-bit kernel codebook; the unpacked indices are compared with the same
+    formula in torch fp32 (norm, x / (norm + 1e-8) @ PiT, count of boundaries <= rot).  Then the
+    packed footprint and the mean device time per call at each N in sizes.  Returns the
+    figures printed."""
+    from turboquant.kernels._selfcheck import random_rotations, time_ms
+    dev = torch.device("cuda")
+    D = _lib.HEAD_DIM
+    PiT, PiST = random_rotations(D, seed, dev)
+    centroids = solve_codebook(D, 2).to(dev)
+    boundaries = ((centroids[:-1] + centroids[1:]) / 2.0).contiguous()
+    say = print if verbose else (lambda *a, **k: None)
+    say(f"Packed TurboQuant compress on {torch.cuda.get_device_name(0)}: D={D}, 2-bit indices + 1-bit QJL signs")
+    res = {"correctness": {}, "benchmark": []}
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 1)
+    K = torch.randn(n_test, D, device=dev, generator=gen)
+    V = torch.randn(n_test, D, device=dev, generator=gen)
+    k_idx, k_signs, k_rnorm, k_norm = compress_k(K, PiT, PiST, centroids, boundaries)
+    v_idx, v_norm = compress_v(V, PiT, centroids, boundaries)
+    for name, x, idx in (("K", K, k_idx), ("V", V, v_idx)):
+        got = unpack_2bit(idx, D).long()
+        norm = torch.linalg.vector_norm(x, dim=-1, keepdim=True)
+        rot = (x / (norm + 1e-8)) @ PiT
+        want = (rot.unsqueeze(-1) >= boundaries).sum(-1)
+        match = (got == want).float().mean().item()
+        recon_cos = torch.nn.functional.cosine_similarity(
+            (centroids[got] * norm).reshape(1, -1), (centroids[want] * norm).reshape(1, -1)).item()
+        ok = int(got.min()) >= 0 and int(got.max()) <= 3 and match > 0.99
+        res["correctness"][name] = {"idx_match": match, "recon_cos": recon_cos, "pass": ok}
+        say(f"  {name}: idx range [{int(got.min())}, {int(got.max())}], idx_match vs torch fp32 {match:.6f}, "
+            f"recon cos {recon_cos:.8f} {'PASS' if ok else 'FAIL'}")
+    sg = unpack_1bit(k_signs, D)
+    say(f"  K signs range [{int(sg.min())}, {int(sg.max())}] (expected [0, 1])")
+
+    fp16_bytes = D * 2 * 2
+    packed = D // 4 + D // 8 + 2 + 2 + D // 4 + 2
+    say(f"  memory per token-head: {fp16_bytes} B fp16 K+V -> {packed} B packed ({fp16_bytes / packed:.1f}x)")
+    say(f"{'N':>8} {'K ms':>10} {'V ms':>10} {'K+V ms':>10}")
+    for n in sizes:
+        Kb = torch.randn(n, D, device=dev, generator=gen)
+        Vb = torch.randn(n, D, device=dev, generator=gen)
+        k_ms = time_ms(lambda: compress_k(Kb, PiT, PiST, centroids, boundaries), warmup, iters)
+        v_ms = time_ms(lambda: compress_v(Vb, PiT, centroids, boundaries), warmup, iters)
+        res["benchmark"].append({"N": n, "k_ms": k_ms, "v_ms": v_ms})
+        say(f"{n:>8} {k_ms:>10.4f} {v_ms:>10.4f} {k_ms + v_ms:>10.4f}")
+        del Kb, Vb
+    return res
+
+
+if __name__ == "__main__":
+    run()

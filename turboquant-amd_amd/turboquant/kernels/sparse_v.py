@@ -117,3 +117,52 @@ def tq_v12_sparse_v(out, q, tq_cache, centroids, block_tables, seq_lens, scale,
 def tq_v11(out, q, tq_cache, centroids, block_tables, seq_lens, scale, **kw):
     """Dense decode without skipping (the role of _tq_v11_single_kernel, kernels/sparse_v.py:163-261)."""
     return tq_paged_decode_3bit(out, q, tq_cache, centroids, block_tables, seq_lens, scale, 0.0, **kw)
+
+
+def benchmark(cases=((1, 1024), (1, 4096), (1, 16384), (1, 32768), (8, 4096), (32, 4096), (64, 4096), (192, 4096)),
+              iters: int = 20, warmup: int = 3, seed: int = 42, verbose: bool = True) -> list:
+    """tq_v11 (no skipping) against tq_v12_sparse_v on cuda:0 (the role of the reference
+    module's benchmark(), kernels/sparse_v.py:264-380): 4 KV heads, GQA 6, block 32, 128-byte
+    slots of random index bytes with fp16 norms of 0.5, the fixed 8-level codebook of that
+    benchmark.  Per (batch, sequence length): mean device ms of v11, of v12 (the reference's
+    single pass) and of v12 with split-K chunks, and the cosine between the v11 and v12 outputs.
+    Returns the rows printed."""
+    import math
+
+    from turboquant.kernels._selfcheck import time_ms
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    hkv, gqa, bs, slot = 4, 6, 32, 128
+    hq = hkv * gqa
+    scale = 1.0 / math.sqrt(D)
+    centroids = torch.tensor([-1.5, -0.8, -0.3, -0.05, 0.05, 0.3, 0.8, 1.5], dtype=torch.float32, device=dev)
+    half = torch.tensor([0.5], dtype=torch.float16).view(torch.uint8)
+    say = print if verbose else (lambda *a, **k: None)
+    say(f"{'config':>16} | {'v11 ms':>9} | {'v12 ms':>9} | {'v12 split-K ms':>14} | {'speedup':>7} | {'cos':>7}")
+    rows = []
+    for ns, slen in cases:
+        nblk = -(-slen // bs)
+        total = ns * nblk + 16
+        q = torch.randn(ns, hq, D, device=dev, generator=gen).half()
+        cache = torch.randint(0, 256, (total, 2, bs, hkv, slot), dtype=torch.uint8, device=dev, generator=gen)
+        cache[..., DQ3] = int(half[0])
+        cache[..., DQ3 + 1] = int(half[1])
+        bt = (torch.arange(nblk, dtype=torch.int32, device=dev).unsqueeze(0)
+              + torch.arange(ns, dtype=torch.int32, device=dev).unsqueeze(1) * nblk).contiguous()
+        lens = torch.full((ns,), slen, dtype=torch.int32, device=dev)
+        o11, o12, o12s = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+        t11 = time_ms(lambda: tq_v11(o11, q, cache, centroids, bt, lens, scale), warmup, iters)
+        t12 = time_ms(lambda: tq_v12_sparse_v(o12, q, cache, centroids, bt, lens, scale), warmup, iters)
+        split = choose_tokens_per_chunk(ns, hkv, slen, concurrent_units(dev, 3, False, 3, hq, hkv, cache.stride(2), True))
+        t12s = time_ms(lambda: tq_v12_sparse_v(o12s, q, cache, centroids, bt, lens, scale,
+                                               tokens_per_chunk=split), warmup, iters)
+        cos = torch.nn.functional.cosine_similarity(o11.flatten().float(), o12.flatten().float(), dim=0).item()
+        rows.append({"batch": ns, "seq_len": slen, "v11_ms": t11, "v12_ms": t12, "v12_split_ms": t12s, "cos": cos})
+        say(f"  B={ns:>3d},S={slen:>5d} | {t11:>9.3f} | {t12:>9.3f} | {t12s:>14.3f} | {t11 / t12:>6.2f}x | {cos:>7.4f}")
+        del cache
+    return rows
+
+
+if __name__ == "__main__":
+    benchmark()
