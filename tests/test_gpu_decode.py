@@ -339,6 +339,73 @@ def test_packed_attention_v7_api(dev):
             np.testing.assert_allclose(got[h], ref[0].cpu().numpy(), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("perm", [True, False])
+@pytest.mark.parametrize("S,Sk,hkv,G,chunk", [(8, 256, 1, 1, 0), (3, 4096, 2, 6, 0), (2, 16, 1, 1, 0),
+                                              (5, 1024, 1, 3, 512), (4, 2048, 2, 8, 96)])
+def test_decode_row_major_arrays(dev, perm, S, Sk, hkv, G, chunk):
+    """The row-major per-sequence arrays of the v7 layout (2-bit keys with QJL, 2-bit values, no
+    block tables; Sk a multiple of 16) through tq_decode's contiguous kernel, against the fp64
+    oracle: sign rows in natural or stride-4 permuted order, GQA groups 1-8, several KV heads,
+    sequence lengths ending inside a tile, a sequence of length 0, fixed and library-chosen
+    chunks."""
+    from turboquant import _lib
+    from turboquant.kernels.paged import run_decode
+    rng = np.random.default_rng(1000 + Sk + 7 * G + perm)
+    cb = _cb(2)
+    cs = math.sqrt(math.pi / 2) / math.sqrt(128)
+    Hq = hkv * G
+    ki = rng.integers(0, 256, (S, hkv, Sk, 32), dtype=np.uint8)
+    ks = rng.integers(0, 256, (S, hkv, Sk, 16), dtype=np.uint8)
+    vi = rng.integers(0, 256, (S, hkv, Sk, 32), dtype=np.uint8)
+    kr = (rng.random((S, hkv, Sk)) * 0.1).astype(np.float16)
+    kn = (rng.random((S, hkv, Sk)) + 0.5).astype(np.float16)
+    vn = (rng.random((S, hkv, Sk)) + 0.5).astype(np.float16)
+    q = (rng.standard_normal((S, Hq, 128)) * 0.3).astype(np.float16)
+    qp = (rng.standard_normal((S, Hq, 128)) * 0.3).astype(np.float16)
+    lens = np.array([Sk, max(Sk - 5, 1), 0, 17, Sk - 16, 3, Sk, Sk // 2 + 1][:S], dtype=np.int32)
+    ks_dev = opack.permute_signs(ks.reshape(-1, 16)).reshape(ks.shape) if perm else ks
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    arrs = {"ki": t(ki), "ks": t(ks_dev), "kr": t(kr), "kn": t(kn), "vi": t(vi), "vn": t(vn)}
+
+    def region(x, row):
+        return _lib.TQRegion(x.data_ptr(), 16 * row, Sk * row, hkv * Sk * row, row)
+
+    kv = _lib.TQKVView()
+    kv.idx, kv.signs, kv.norm, kv.rnorm = region(arrs["ki"], 32), region(arrs["ks"], 16), region(arrs["kn"], 2), \
+        region(arrs["kr"], 2)
+    cbd = cb.to(dev)
+    kv.centroids = cbd.data_ptr()
+    kv.bits, kv.qjl, kv.signs_permuted = 2, 1, 1 if perm else 0
+    kv.centroid_scale = _lib.centroid_scale(cbd)
+    vv = _lib.TQKVView()
+    vv.idx, vv.norm = region(arrs["vi"], 32), region(arrs["vn"], 2)
+    vv.centroids = cbd.data_ptr()
+    vv.bits, vv.qjl, vv.signs_permuted = 2, 0, 0
+    vv.centroid_scale = kv.centroid_scale
+    out = torch.full((S, Hq, 128), float("nan"), dtype=torch.float16, device=dev)
+    sm = 1 / math.sqrt(128)
+    run_decode(t(q), kv, vv, num_kv_heads=hkv, block_size=16, num_blocks=Sk // 16, block_tables=None,
+               max_blocks_per_seq=Sk // 16, seq_lens=t(lens), max_seq_len=Sk, sm_scale=sm, corr_scale=cs,
+               q_proj=t(qp), sparse_threshold=0.0, tokens_per_chunk=chunk, out=out, workspace=None,
+               skip_stats=None, keep_alive=(cbd, arrs))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    for s in range(S):
+        L = int(lens[s])
+        for kh in range(hkv):
+            hs = slice(kh * G, (kh + 1) * G)
+            if L == 0:
+                assert np.all(got[s, hs] == 0), "an empty sequence decodes to zeros"
+                continue
+            k, sg, rn = odec.dequant_keys({"idx": ki[s, kh, :L], "norm": kn[s, kh, :L].view(np.uint16),
+                                           "signs": ks[s, kh, :L], "rnorm": kr[s, kh, :L].view(np.uint16)},
+                                          cb.double().numpy(), 2, True)
+            v = odec.dequant_values({"idx": vi[s, kh, :L], "norm": vn[s, kh, :L].view(np.uint16)},
+                                    cb.double().numpy(), 2)
+            want = odec.decode_dense(q[s, hs].astype(np.float64), qp[s, hs].astype(np.float64), k, sg, rn, v, sm, cs)
+            np.testing.assert_allclose(got[s, hs], want, rtol=RTOL, atol=ATOL, err_msg=f"seq {s} head {kh}")
+
+
 def _skip_allowance(margins, thresh, delta=2e-3):
     """Tokens whose keep margin lies within delta (natural-log units, well above the kernels'
     score rounding) of log(threshold): either decision is within rounding."""

@@ -985,6 +985,25 @@ bool fast_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, int block
     return true;
 }
 
+// decode_contig_kernel reads the reference's row-major per-sequence arrays: no block tables, 2-bit
+// keys with QJL and 2-bit values, rows following each other (16-row block strides) of 32 index
+// bytes, 16 sign bytes and 2-byte norms, aligned for its 8-byte loads, whole 16-row tiles up to
+// max_seq_len (the rows each sequence holds), GQA groups of at most 8, no Sparse-V, no rotation.
+bool contig_path_ok(const tq_kv_view* k, const tq_kv_view* v, int group, const int32_t* block_tables,
+                    int block_size, int max_seq_len, int max_blocks_per_seq, float sparse_threshold, int rotate) {
+    if (block_tables || block_size != 16 || group > 8 || sparse_threshold > 0.f || rotate) return false;
+    if (k->bits != 2 || !k->qjl || v->bits != 2) return false;
+    if (k->layout != TQ_TILE_ROWS || v->layout != TQ_TILE_ROWS) return false;
+    if (max_seq_len <= 0 || max_seq_len % 16 || max_seq_len > 16 * (int64_t)max_blocks_per_seq) return false;
+    auto rows = [&](const tq_region& r, int64_t row, uint64_t align) {
+        return r.ptr && r.stride_row == row && r.stride_block == 16 * row && (uintptr_t)r.ptr % align == 0 &&
+               (uint64_t)r.stride_seq % align == 0 && (uint64_t)r.stride_head % align == 0 &&
+               (int64_t)max_seq_len * row < (1ll << 31);  // 32-bit row offsets
+    };
+    return rows(k->idx, 32, 8) && rows(k->signs, 16, 4) && rows(k->norm, 2, 8) && rows(k->rnorm, 2, 8) &&
+           rows(v->idx, 32, 8) && rows(v->norm, 2, 8);
+}
+
 }  // namespace
 
 // Balanced schedule: partial rows for up to 16 resident waves per CU of the largest gfx950
@@ -1150,6 +1169,28 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256)) return TQ_ERR_WORKSPACE;
     int addr = TQ_ADDR_CACHED;
     const bool fast = fast_path_ok(k, v, group, block_size, num_blocks, block_tables, &addr);
+    const float k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
+    const float v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
+    const bool share = k->centroids == v->centroids && k->bits == v->bits && k_cscale == v_cscale;
+    const bool contig = !fast && contig_path_ok(k, v, group, block_tables, block_size, max_seq_len, max_blocks_per_seq,
+                                                sparse_threshold, rotate);
+    if (contig && tokens_per_chunk == 0) {
+        // one round of the resident waves, at least 8 tiles per unit (a unit's start-up is worth
+        // several tiles), and no more units than the workspace of tokens_per_chunk = 0 holds
+        uint32_t a, b, c, d;
+        size_t lds_c = 0;
+        tq_decode_fast_lds_layout(2, true, 2, share, &a, &b, &c, &d, &lds_c);
+        int waves = 0;
+        const int orc = resident_waves(tq_decode_fast_kernel_ptr(2, true, 2, 0, TQ_ADDR_CONTIG), lds_c, &waves);
+        if (orc) return orc;
+        const int64_t tiles = (int64_t)num_seqs * num_kv_heads * (max_seq_len / 16);
+        int64_t per = (tiles + waves - 1) / (waves > 0 ? waves : 1);
+        per = per < 8 ? 8 : per;
+        int64_t chunk = 16 * per;
+        const int64_t fit = general_chunk(num_seqs, num_q_heads, max_seq_len, false);
+        chunk = chunk > fit ? chunk : fit;
+        tokens_per_chunk = (int)(chunk < max_seq_len ? chunk : max_seq_len);
+    }
     // tokens_per_chunk = 0: the balanced schedule on the fast kernel; fixed chunks that fit the
     // same workspace on the general one
     // (the kernel keeps pair positions in 32 bits: at most num_seqs * num_kv_heads * ceil(len / 32))
@@ -1164,12 +1205,18 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
 
     const size_t slots = (size_t)num_seqs * num_q_heads * n_chunks;
     uint8_t* ws = static_cast<uint8_t*>(workspace);
-    const float k_cscale = k->centroid_scale > 0.f ? k->centroid_scale : 1.f;
-    const float v_cscale = v->centroid_scale > 0.f ? v->centroid_scale : 1.f;
-    const bool share = k->centroids == v->centroids && k->bits == v->bits && k_cscale == v_cscale;
-    if (fast) {
+    if (fast || contig) {
         FastDecodeParams f = {};
-        f.addr = addr;
+        f.addr = contig ? TQ_ADDR_CONTIG : addr;
+        if (contig) {
+            const tq_region* cr[6] = {&k->idx, &k->signs, &k->norm, &k->rnorm, &v->idx, &v->norm};
+            for (int a = 0; a < 6; ++a) {
+                f.contig[a].ptr = static_cast<const uint8_t*>(cr[a]->ptr);
+                f.contig[a].stride_seq = cr[a]->stride_seq;
+                f.contig[a].stride_head = cr[a]->stride_head;
+            }
+            f.contig_perm = k->signs_permuted ? 1 : 0;
+        }
         f.q = q;
         f.q_ss = q_stride_seq;
         f.q_sh = q_stride_head;
@@ -1208,7 +1255,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.num_blocks = num_blocks;
         f.bt = block_tables;
         f.bt_stride = block_table_stride;
-        f.max_blocks = max_blocks_per_seq;
+        f.max_blocks = contig ? max_seq_len / 16 : max_blocks_per_seq;  // contiguous: whole tiles up to max_seq_len
         f.seq_lens = seq_lens;
         f.c_exp = sm_scale * kLog2e / k_cscale;
         f.sparse = sparse_threshold > 0.f ? 1 : 0;

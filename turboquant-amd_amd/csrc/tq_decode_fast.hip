@@ -416,6 +416,138 @@ constexpr int fast_waves() {
     return KQJL ? 3 : 4;
 }
 
+// LDS tables (one share per thread of the workgroup): the fp4 sign table (QJL), the K and the V
+// tables at the byte offsets chosen by the host (multiples of each table's size).  A replicated
+// table's entry is computed once and its replicas (consecutive) written with 16-byte stores:
+// every workgroup builds its tables before reading a tile, so this is part of each unit's
+// start-up.  Ends with a workgroup barrier.
+template <int KB, bool KQJL, int VB>
+__device__ __forceinline__ void build_tables(const FastDecodeParams& p, uint32_t* s_lds, int tid) {
+    constexpr int SREP = sign_replicas<KB, VB>();
+    if (KQJL) {
+        // entry e (one per thread): 8 sign bits -> 8 fp4 values +1 (0x2) / -1 (0xA)
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w |= ((((uint32_t)tid >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);
+        tq_u32x4* t = reinterpret_cast<tq_u32x4*>(s_lds + p.lds_sign / 4) + tid * (SREP / 4);
+#pragma unroll
+        for (int r = 0; r < SREP / 4; ++r) t[r] = tq_u32x4{w, w, w, w};
+    }
+    // pair table: entry e -> half2(c[e & (2^b - 1)], c[e >> b]), 32 replicas;
+    // quad table: entry e -> 4 x fp16 c[(e >> bj) & (2^b - 1)], j = 0..3 (2 bits: 16 replicas)
+    // 3-bit quads are assembled from the 64 pairs of 3-bit fields, staged in a 512-byte scratch
+    // area after the tables (a static __shared__ array would move the K quad table off address 0)
+    uint32_t* s_pair3 = s_lds + p.lds_scratch / 4;
+    auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad, int which) {
+        uint32_t* t = s_lds + off / 4;
+        const int mask = (1 << bits) - 1;
+        if (quad && bits == 3) {
+            const uint32_t* pr = s_pair3 + 64 * which;
+            for (int e = tid; e < 4096; e += 256)
+                reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{pr[e & 63], pr[e >> 6]};
+        } else if (quad) {
+            // 256 entries of 8 bytes, one per thread
+            const int e = tid;
+            const uint32_t lo = tq_pack_half2(cent[e & 3] * cs, cent[(e >> 2) & 3] * cs);
+            const uint32_t hi = tq_pack_half2(cent[(e >> 4) & 3] * cs, cent[(e >> 6) & 3] * cs);
+            reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{lo, hi};
+        } else {
+            // 2^(2 bits) entries (16, 64 or 256), 32 replicas x 4 bytes
+            const int ent = 1 << (2 * bits);
+            for (int e = tid; e < ent; e += 256) {
+                const uint32_t w = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
+                tq_u32x4* d = reinterpret_cast<tq_u32x4*>(t) + e * 8;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) d[r] = tq_u32x4{w, w, w, w};
+            }
+        }
+    };
+    const bool vown = p.lds_v != p.lds_k;
+    if (quad_table<KB>() && KB == 3 && tid < 64)
+        s_pair3[tid] = tq_pack_half2(p.k_cent[tid & 7] * p.k_cscale, p.k_cent[tid >> 3] * p.k_cscale);
+    if (quad_table<VB>() && VB == 3 && vown && tid >= 64 && tid < 128)
+        s_pair3[tid] = tq_pack_half2(p.v_cent[tid & 7] * p.v_cscale, p.v_cent[(tid - 64) >> 3] * p.v_cscale);
+    if ((quad_table<KB>() && KB == 3) || (quad_table<VB>() && VB == 3)) __syncthreads();
+    fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>(), 0);
+    if (vown) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>(), 1);
+    __syncthreads();
+}
+
+// The lane's table addresses (base + replica offset) and its tile half (column < 8: tile A).
+template <int KB, int VB>
+__device__ __forceinline__ void init_lane_tables(LaneCtx& c, const FastDecodeParams& p, uint32_t* s_lds, int lane) {
+    c.lo8 = (lane & 15) < 8;
+    const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
+    c.kbank = lds0 + p.lds_k + bank4;
+    c.vbank = lds0 + p.lds_v + bank4;
+    c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
+    // 3-bit V quad table: address 0 when it is the K quad table, else its base from a VGPR (a
+    // VALU op takes one scalar operand, and the field mask is one)
+    c.vquad = lds0 + p.lds_v;
+    if (VB == 3 && !(quad_table<KB>() && KB == 3 && p.lds_v == 0))
+        asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
+}
+
+// Query operands from the lane's 32 loaded elements of q (qv) and of q_proj (x): q as fp16
+// (rotated by H first when asked), q_proj * corr * cscale as three fp6 e2m3 parts with E8M0
+// scales (QJL keys).
+template <bool KQJL>
+__device__ __forceinline__ void make_q_operands(LaneCtx& c, const FastDecodeParams& p, float (&qv)[32], float (&x)[32]) {
+    if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);  // q x H: elements 32g + i
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c.qop[cc][j] = (_Float16)qv[8 * cc + j];
+    if constexpr (KQJL) {
+        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);  // q_proj x H: elements 32g + i
+        // One E8M0 scale per lane: its 32 elements are one 32-wide scale block of the instruction.
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            x[i] *= p.qp_mul;
+            amax = fmaxf(amax, fabsf(x[i]));
+        }
+        // 2^b brings the block's largest magnitude into [2, 4) (e2m3 holds magnitudes up to 7.5)
+        int b = 0;
+        if (amax > 0.f && amax < __builtin_huge_valf()) b = 1 - ilogbf(amax);
+        b = b < -117 ? -117 : (b > 117 ? 117 : b);
+        c.qsc = (127 - b) | ((122 - b) << 8) | ((117 - b) << 16);
+        // x 2^b = hi + mid / 32 + lo / 1024 + e: each part rounded to nearest even (the
+        // conversion divides by its scale argument), the residuals before it exact in fp32; the
+        // last part is at most 4 in magnitude, so |e| <= 2^-3 / 1024 = 2^-13 next to a block
+        // maximum of at least 2.
+        typedef float f32x16 __attribute__((ext_vector_type(16)));
+        typedef int i32x6 __attribute__((ext_vector_type(6)));
+        float r[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) r[i] = ldexpf(x[i], b);
+#pragma unroll
+        for (int part = 0; part < 3; ++part) {
+            // packed element 2i comes from the first vector's element i, 2i + 1 from the second's
+            f32x16 ev, od;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                ev[i] = r[2 * i];
+                od[i] = r[2 * i + 1];
+            }
+            const float sc = part == 0 ? 1.0f : 0.03125f;  // code = RNE(value / sc)
+            const i32x6 code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, sc);
+#pragma unroll
+            for (int j = 0; j < 6; ++j) c.qp6[part][j] = code[j];
+            c.qp6[part][6] = 0;
+            c.qp6[part][7] = 0;
+            if (part < 2) {
+                const auto dq = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, 1.0f);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) r[i] = part == 0 ? r[i] - dq[i] : __builtin_fmaf(r[i], 32.f, -dq[i]);
+            }
+        }
+    } else {
+        c.qsc = 127;
+    }
+}
+
 // SPV: Sparse-V off (0), on (1), on with skip statistics (2); separate instances keep the test
 // and the counting off the paths that do not use them.
 // ADDR: how K / V tiles are addressed and cached.
@@ -432,11 +564,6 @@ void decode_fast_kernel(FastDecodeParams p) {
     constexpr bool BIG = ADDR == TQ_ADDR_BIG;
     constexpr int AUX = ADDR == TQ_ADDR_CACHED ? 0 : 2;  // buffer-load cache policy: 2 = non-temporal
     extern __shared__ uint32_t s_lds[];
-    // Tables: fp4 sign table (QJL), K table, V table, at the byte offsets chosen by the host
-    // (multiples of each table's size).  A replicated table's entry is computed once and its
-    // replicas (consecutive) written with 16-byte stores: every workgroup builds its tables
-    // before reading a tile, so this is part of each unit's start-up.
-    constexpr int SREP = sign_replicas<KB, VB>();
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -511,72 +638,13 @@ void decode_fast_kernel(FastDecodeParams p) {
         }
         if (!any) return;
     }
-    // ---- LDS tables (one share per thread of the workgroup) ----
-    {
-    if (KQJL) {
-        // entry e (one per thread): 8 sign bits -> 8 fp4 values +1 (0x2) / -1 (0xA)
-        uint32_t w = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w |= ((((uint32_t)tid >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);
-        tq_u32x4* t = reinterpret_cast<tq_u32x4*>(s_lds + p.lds_sign / 4) + tid * (SREP / 4);
-#pragma unroll
-        for (int r = 0; r < SREP / 4; ++r) t[r] = tq_u32x4{w, w, w, w};
-    }
-    // pair table: entry e -> half2(c[e & (2^b - 1)], c[e >> b]), 32 replicas;
-    // quad table: entry e -> 4 x fp16 c[(e >> bj) & (2^b - 1)], j = 0..3 (2 bits: 16 replicas)
-    // 3-bit quads are assembled from the 64 pairs of 3-bit fields, staged in a 512-byte scratch
-    // area after the tables (a static __shared__ array would move the K quad table off address 0)
-    uint32_t* s_pair3 = s_lds + p.lds_scratch / 4;
-    auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad, int which) {
-        uint32_t* t = s_lds + off / 4;
-        const int mask = (1 << bits) - 1;
-        if (quad && bits == 3) {
-            const uint32_t* pr = s_pair3 + 64 * which;
-            for (int e = tid; e < 4096; e += 256)
-                reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{pr[e & 63], pr[e >> 6]};
-        } else if (quad) {
-            // 256 entries of 8 bytes, one per thread
-            const int e = tid;
-            const uint32_t lo = tq_pack_half2(cent[e & 3] * cs, cent[(e >> 2) & 3] * cs);
-            const uint32_t hi = tq_pack_half2(cent[(e >> 4) & 3] * cs, cent[(e >> 6) & 3] * cs);
-            reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{lo, hi};
-        } else {
-            // 2^(2 bits) entries (16, 64 or 256), 32 replicas x 4 bytes
-            const int ent = 1 << (2 * bits);
-            for (int e = tid; e < ent; e += 256) {
-                const uint32_t w = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
-                tq_u32x4* d = reinterpret_cast<tq_u32x4*>(t) + e * 8;
-#pragma unroll
-                for (int r = 0; r < 8; ++r) d[r] = tq_u32x4{w, w, w, w};
-            }
-        }
-    };
-    const bool vown = p.lds_v != p.lds_k;
-    if (quad_table<KB>() && KB == 3 && tid < 64)
-        s_pair3[tid] = tq_pack_half2(p.k_cent[tid & 7] * p.k_cscale, p.k_cent[tid >> 3] * p.k_cscale);
-    if (quad_table<VB>() && VB == 3 && vown && tid >= 64 && tid < 128)
-        s_pair3[tid] = tq_pack_half2(p.v_cent[tid & 7] * p.v_cscale, p.v_cent[(tid - 64) >> 3] * p.v_cscale);
-    if ((quad_table<KB>() && KB == 3) || (quad_table<VB>() && VB == 3)) __syncthreads();
-    fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>(), 0);
-    if (vown) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>(), 1);
-    __syncthreads();
-    }
+    build_tables<KB, KQJL, VB>(p, s_lds, tid);
 
     const int g = lane >> 4;
     const int n = lane & 15;
     const int hcol = n & 7;
     LaneCtx c;
-    c.lo8 = n < 8;
-    const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
-    c.kbank = lds0 + p.lds_k + bank4;
-    c.vbank = lds0 + p.lds_v + bank4;
-    c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
-    // 3-bit V quad table: address 0 when it is the K quad table, else its base from a VGPR (a
-    // VALU op takes one scalar operand, and the field mask is one)
-    c.vquad = lds0 + p.lds_v;
-    if (VB == 3 && !(quad_table<KB>() && KB == 3 && p.lds_v == 0))
-        asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
+    init_lane_tables<KB, VB>(c, p, s_lds, lane);
 
     // ---- loop-invariant lane offsets inside a tile ----
     // lane-grouped tiles: the lane's key chunk (row n, dims 32g..) and value chunk (rows
@@ -838,58 +906,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     fetch_k(0, __builtin_amdgcn_readlane(bt0, 0), __builtin_amdgcn_readlane(bt0, 1), kr[0], info[0]);
     load_v(info[0], vr[0]);
     // ---- query operands: conversion ----
-    if (p.rot_q) tq_wht_row_g4(qv, p.wht_h);  // q x H: elements 32g + i
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) c.qop[cc][j] = (_Float16)qv[8 * cc + j];
-    if constexpr (KQJL) {
-        if (p.rot_qp) tq_wht_row_g4(x, p.wht_h);  // q_proj x H: elements 32g + i
-        // One E8M0 scale per lane: its 32 elements are one 32-wide scale block of the instruction.
-        float amax = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-            x[i] *= p.qp_mul;
-            amax = fmaxf(amax, fabsf(x[i]));
-        }
-        // 2^b brings the block's largest magnitude into [2, 4) (e2m3 holds magnitudes up to 7.5)
-        int b = 0;
-        if (amax > 0.f && amax < __builtin_huge_valf()) b = 1 - ilogbf(amax);
-        b = b < -117 ? -117 : (b > 117 ? 117 : b);
-        c.qsc = (127 - b) | ((122 - b) << 8) | ((117 - b) << 16);
-        // x 2^b = hi + mid / 32 + lo / 1024 + e: each part rounded to nearest even (the
-        // conversion divides by its scale argument), the residuals before it exact in fp32; the
-        // last part is at most 4 in magnitude, so |e| <= 2^-3 / 1024 = 2^-13 next to a block
-        // maximum of at least 2.
-        typedef float f32x16 __attribute__((ext_vector_type(16)));
-        typedef int i32x6 __attribute__((ext_vector_type(6)));
-        float r[32];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) r[i] = ldexpf(x[i], b);
-#pragma unroll
-        for (int part = 0; part < 3; ++part) {
-            // packed element 2i comes from the first vector's element i, 2i + 1 from the second's
-            f32x16 ev, od;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                ev[i] = r[2 * i];
-                od[i] = r[2 * i + 1];
-            }
-            const float sc = part == 0 ? 1.0f : 0.03125f;  // code = RNE(value / sc)
-            const i32x6 code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, sc);
-#pragma unroll
-            for (int j = 0; j < 6; ++j) c.qp6[part][j] = code[j];
-            c.qp6[part][6] = 0;
-            c.qp6[part][7] = 0;
-            if (part < 2) {
-                const auto dq = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, 1.0f);
-#pragma unroll
-                for (int i = 0; i < 32; ++i) r[i] = part == 0 ? r[i] - dq[i] : __builtin_fmaf(r[i], 32.f, -dq[i]);
-            }
-        }
-    } else {
-        c.qsc = 127;
-    }
+    make_q_operands<KQJL>(c, p, qv, x);
 
     Softmax st;
     st.m = kNegInf;
@@ -973,9 +990,244 @@ void decode_fast_kernel(FastDecodeParams p) {
     }
 }
 
+// ---- row-major per-sequence arrays (the layout of the reference's packed_attention) ----
+
+// Byte a of a value chunk built by rows_to_dim_major2 holds dim 8n + kContigDim[a].
+constexpr int kContigDim[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+
+// The lane's 2-bit value chunk (dims 8n..8n+7 of rows 4g..4g+3) from the four 16-bit row slices
+// h[r] (dim j at bits 2j): each byte of the result holds the four rows of one dim (row r at
+// bits 2r), the form the 2-bit V quad table reads; dims in the order kContigDim.  18 bit
+// operations per tile instead of a layout change in memory.
+__device__ __forceinline__ void rows_to_dim_major2(const uint32_t (&h)[4], uint32_t (&w)[2]) {
+    const uint32_t A = h[0] | (h[2] << 16);  // rows 0 | 2
+    const uint32_t B = h[1] | (h[3] << 16);  // rows 1 | 3
+    // nibble k of x: dim 2(k & 3) of rows (0, 1) for k < 4, rows (2, 3) for k >= 4; y: dim 2(k & 3) + 1
+    const uint32_t x = (A & 0x33333333u) | ((B << 2) & 0xccccccccu);
+    const uint32_t y = ((A >> 2) & 0x33333333u) | (B & 0xccccccccu);
+    // nibbles k and k + 4 side by side: bytes 0, 1 of px = dims 0, 4 (of x's parity), of qx = 2, 6
+    const uint32_t px = (x & 0x0f0f0f0fu) | ((x >> 12) & 0xf0f0f0f0u);
+    const uint32_t qx = ((x >> 4) & 0x0f0f0f0fu) | ((x >> 16) & 0xf0f0f0f0u);
+    const uint32_t py = (y & 0x0f0f0f0fu) | ((y >> 12) & 0xf0f0f0f0u);
+    const uint32_t qy = ((y >> 4) & 0x0f0f0f0fu) | ((y >> 16) & 0xf0f0f0f0u);
+    w[0] = (px & 0xffffu) | (qx << 16);  // dims 0, 4, 2, 6
+    w[1] = (py & 0xffffu) | (qy << 16);  // dims 1, 5, 3, 7
+}
+
+// Decode over the row-major per-sequence arrays of the reference's packed_attention
+// (kernels/packed_attention.py:75-196, arrays as in :290-344): K indices (16 * KB bytes per
+// row), K sign rows (16 bytes, natural or stride-4 permuted bit order), fp16 K norms and
+// residual norms, V indices (16 * VB bytes), fp16 V norms, without block tables.  2-bit K with
+// QJL, 2-bit V, fixed chunks, no Sparse-V and no rotation (tq_decode sends other requests to
+// decode_kernel).  One wave per (sequence, KV head, chunk), pairs of 16-token tiles through
+// compute_pair as in decode_fast_kernel; only the loads differ: lane (n, g) reads bytes
+// 4KB*g.. of key row n (the dims 32g..32g+31 the keys tile layout gives it) and bytes 4g..4g+3
+// of sign row n, whose 32 signs are dims 32g + m (natural) or 4m + g (permuted: q_proj is taken
+// in that order); its value chunk comes from four 16-bit slices of rows 4g..4g+3
+// (rows_to_dim_major2).  Rows past a sequence's last tile are never read (the arrays hold
+// max_blocks * 16 rows per sequence; tiles past the end re-read the last one, masked).
+template <int KB, bool KQJL, int VB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
+                                                                     fast_waves<KB, KQJL, VB>())))
+void decode_contig_kernel(FastDecodeParams p) {
+    static_assert(KB == 2 && KQJL && VB == 2, "row-major decode: 2-bit keys with QJL, 2-bit values");
+    extern __shared__ uint32_t s_lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wv = (int)blockIdx.x * 4 + wave;  // this wave's unit
+    const int cap = p.max_blocks * 16;          // rows per sequence in the arrays
+    {
+        // units in (sequence, chunk, KV head) order; a workgroup whose four units all start past
+        // their sequence's end is idle
+        bool any = false;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t unit = (int64_t)blockIdx.x * 4 + u;
+            const int64_t sc_ = unit / p.hkv;
+            const int ci = (int)(sc_ % p.n_chunks);
+            const int64_t su = sc_ / p.n_chunks;
+            if (su < p.num_seqs) {
+                int Lu = p.seq_lens[su];
+                Lu = Lu < cap ? Lu : cap;
+                any = any || ci * p.chunk < Lu;
+            }
+        }
+        if (!any) return;
+    }
+    build_tables<KB, KQJL, VB>(p, s_lds, tid);
+    const int g = lane >> 4;
+    const int n = lane & 15;
+    const int hcol = n & 7;
+    LaneCtx c;
+    init_lane_tables<KB, VB>(c, p, s_lds, lane);
+
+    const int kh = wv % p.hkv;
+    const int sc_ = wv / p.hkv;
+    const int ci = sc_ % p.n_chunks;
+    const int s = sc_ / p.n_chunks;
+    if (s >= p.num_seqs) return;
+    int L = p.seq_lens[s];
+    L = L < cap ? L : cap;
+    const int t_begin = ci * p.chunk;
+    if (t_begin >= L) return;
+    const int t_end = t_begin + p.chunk < L ? t_begin + p.chunk : L;
+    int nch = (L + p.chunk - 1) / p.chunk;
+    nch = nch < p.n_chunks ? nch : p.n_chunks;
+    const bool direct = nch == 1;
+    const int prow_base = (s * p.hq + kh * p.group) * p.n_chunks + ci;
+
+    const uint8_t* base[6];
+#pragma unroll
+    for (int a = 0; a < 6; ++a)
+        base[a] = p.contig[a].ptr + (int64_t)s * p.contig[a].stride_seq + (int64_t)kh * p.contig[a].stride_head;
+    const int ntl = (L + 15) >> 4;  // tiles holding the sequence's rows (>= 1)
+    const int tile0 = t_begin >> 4;
+    constexpr uint32_t KROW = 16 * KB, VROW = 16 * VB;
+    const uint32_t o_ki = (uint32_t)(n * KROW + 4 * KB * g);    // key row n, dims 32g..
+    const uint32_t o_ks = (uint32_t)(n * 16 + 4 * g);           // sign row n, bytes 4g..
+    const uint32_t o_v = (uint32_t)(4 * g * VROW + VB * n);     // value row 4g, dims 8n..
+    const uint32_t o_n = (uint32_t)(8 * g);                     // norms of rows 4g..4g+3
+
+    struct VRows {
+        uint32_t hA[4], hB[4];  // 16-bit slices of rows 4g..4g+3, tiles A and B
+        uint32_t vn[2];
+    };
+    auto ld2 = [](const uint8_t* b, uint32_t off) { return *reinterpret_cast<const tq_u32x2*>(b + off); };
+    auto ld1 = [](const uint8_t* b, uint32_t off) { return *reinterpret_cast<const uint32_t*>(b + off); };
+    auto ldh = [](const uint8_t* b, uint32_t off) { return (uint32_t)*reinterpret_cast<const uint16_t*>(b + off); };
+    auto fetch = [&](int pi, KRaw<KB, KQJL>& kr, VRows& vw, PairInfo& info) {
+        int nv[2];
+        uint32_t ti[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int i = 2 * pi + x;
+            int nvr = t_end - (t_begin + 16 * i);
+            nvr &= ~(nvr >> 31);  // max(., 0)
+            nv[x] = nvr < 16 ? nvr : 16;
+            const int t = tile0 + i;
+            ti[x] = (uint32_t)(t < ntl ? t : ntl - 1);  // past the end: the last tile again (masked)
+        }
+        info.nvA = nv[0];
+        info.nvB = nv[1];
+        const tq_u32x2 a = ld2(base[0], ti[0] * (16 * KROW) + o_ki);
+        const tq_u32x2 b = ld2(base[0], ti[1] * (16 * KROW) + o_ki);
+        kr.kwA[0] = a[0];
+        kr.kwA[1] = a[1];
+        kr.kwB[0] = b[0];
+        kr.kwB[1] = b[1];
+        kr.ksA = ld1(base[1], ti[0] * 256u + o_ks);
+        kr.ksB = ld1(base[1], ti[1] * 256u + o_ks);
+        // lanes with col < 8 read tile A's norms, the others tile B's
+        const uint32_t no = (c.lo8 ? ti[0] : ti[1]) * 32u + o_n;
+        const tq_u32x2 kn = ld2(base[2], no), krn = ld2(base[3], no), vn = ld2(base[5], no);
+        kr.kn[0] = kn[0];
+        kr.kn[1] = kn[1];
+        kr.krn[0] = krn[0];
+        kr.krn[1] = krn[1];
+        vw.vn[0] = vn[0];
+        vw.vn[1] = vn[1];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            vw.hA[r] = ldh(base[4], ti[0] * (16 * VROW) + o_v + r * VROW);
+            vw.hB[r] = ldh(base[4], ti[1] * (16 * VROW) + o_v + r * VROW);
+        }
+    };
+
+    // ---- query operands ----
+    const int head = kh * p.group + hcol;
+    const bool hvalid = hcol < p.group;
+    c.hmask = __builtin_amdgcn_ballot_w64(hvalid);
+    c.gap = 1.0f / p.c_exp;
+    float qv[32], x[32];
+    {
+        const int64_t qoff = s * p.q_ss + (int64_t)head * p.q_sh + 32 * g;
+        if (hvalid && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tq_load8(p.q, qoff + 8 * i, p.q_dtype, &qv[8 * i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; ++i) qv[i] = hvalid ? tq_load1(p.q, qoff + i, p.q_dtype) : 0.f;
+        }
+        // element m of lane group g pairs with sign bit 32g + m of the row: dim 32g + m, or 4m + g
+        // in the permuted order
+        const int64_t poff = s * p.qp_ss + (int64_t)head * p.qp_sh;
+        if (p.contig_perm) {
+#pragma unroll
+            for (int m = 0; m < 32; ++m) x[m] = hvalid ? tq_load1(p.qp, poff + 4 * m + g, p.q_dtype) : 0.f;
+        } else if (hvalid && p.q_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tq_load8(p.qp, poff + 32 * g + 8 * i, p.q_dtype, &x[8 * i]);
+        } else {
+#pragma unroll
+            for (int m = 0; m < 32; ++m) x[m] = hvalid ? tq_load1(p.qp, poff + 32 * g + m, p.q_dtype) : 0.f;
+        }
+    }
+    KRaw<KB, KQJL> kr[2];
+    VRows vw[2];
+    PairInfo info[2];
+    fetch(0, kr[0], vw[0], info[0]);
+    make_q_operands<KQJL>(c, p, qv, x);
+
+    Softmax st;
+    st.m = kNegInf;
+    st.mref = kNegInf;
+    st.nb = 0.f;
+    st.lsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) st.acc[i] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+    st.n_tot = 0;
+    st.n_kept = 0;
+    auto compute = [&](const KRaw<KB, KQJL>& k, const VRows& v, const PairInfo& pi) {
+        VRaw<VB> vr;
+        rows_to_dim_major2(v.hA, vr.vwA);
+        rows_to_dim_major2(v.hB, vr.vwB);
+        vr.vn[0] = v.vn[0];
+        vr.vn[1] = v.vn[1];
+        compute_pair<KB, KQJL, VB, 0>(k, vr, pi, st, c, p);
+    };
+    const int ntiles = (t_end - t_begin + 15) >> 4;
+    const int npairs = (ntiles + 1) >> 1;
+    for (int i = 0; i < npairs; i += 2) {
+        fetch(i + 1, kr[1], vw[1], info[1]);
+        compute(kr[0], vw[0], info[0]);
+        if (i + 1 >= npairs) break;
+        fetch(i + 2, kr[0], vw[0], info[0]);
+        compute(kr[1], vw[1], info[1]);
+    }
+
+    // ---- combine the lane groups and the two tile halves; acc[a][r] is dim 8(4g + r) + kContigDim[a] ----
+    float lsum = sum_over_groups(st.lsum);
+    lsum += row_swap8f(lsum);
+    if (!(c.lo8 && hvalid)) return;
+    const float vs = p.v_cinv;
+    if (direct) {
+        const float inv = lsum > 0.f ? vs / lsum : 0.f;
+        const int64_t ob = s * p.out_ss + (int64_t)head * p.out_sh + 32 * g;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int a = 0; a < 8; ++a) tq_store1(p.out, ob + 8 * r + kContigDim[a], p.out_dtype, st.acc[a][r] * inv);
+    } else {
+        const int64_t slot = prow_base + (int64_t)hcol * p.n_chunks;
+        if (g == 0) {
+            p.ws_m[slot] = st.mref == kNegInf ? kNegInf : st.mref * p.c_exp;  // log2 units for the merge
+            p.ws_l[slot] = lsum;
+        }
+        float4* dst = reinterpret_cast<float4*>(p.ws_acc + slot * TQ_HEAD_DIM + 32 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            dst[2 * r] = make_float4(st.acc[0][r] * vs, st.acc[4][r] * vs, st.acc[2][r] * vs, st.acc[6][r] * vs);
+            dst[2 * r + 1] = make_float4(st.acc[1][r] * vs, st.acc[5][r] * vs, st.acc[3][r] * vs, st.acc[7][r] * vs);
+        }
+    }
+}
+
 }  // namespace
 
 const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, int spv, int addr) {
+    if (addr == TQ_ADDR_CONTIG)
+        return (kb == 2 && kq && vb == 2 && spv == 0) ? (const void*)decode_contig_kernel<2, true, 2> : nullptr;
 #define TQ_FP_A(KB, KQ, VB, A)                                                                         \
     if (addr == A)                                                                                     \
         return spv == 2 ? (const void*)decode_fast_kernel<KB, KQ, VB, 2, A>                            \

@@ -78,6 +78,14 @@ struct FastDecodeParams {
     int rot_q, rot_qp, rot_out;  // rotate q / q_proj by H on load, the output by H on the write
     float wht_h;                 // 1 / sqrt(128)
     int addr;                    // TQ_ADDR_*: tile addressing and cache policy of the K / V loads
+    // TQ_ADDR_CONTIG (decode_contig_kernel): row-major per-sequence arrays, in this order K
+    // indices, K sign rows, K norms, K residual norms, V indices, V norms; rows of sequence s,
+    // KV head kh at ptr + s * stride_seq + kh * stride_head
+    struct {
+        const uint8_t* ptr;
+        int64_t stride_seq, stride_head;
+    } contig[6];
+    int contig_perm;             // sign rows in the stride-4 permuted order
 };
 
 // Tile addressing and cache policy of decode_fast_kernel's K / V loads.
@@ -85,6 +93,7 @@ enum {
     TQ_ADDR_CACHED = 0,  // 32-bit offsets per head; loads allocate in the caches
     TQ_ADDR_STREAM = 1,  // 32-bit offsets per head; non-temporal loads
     TQ_ADDR_BIG = 2,     // 64-bit per-tile bases (a cache spanning 2 GiB or more); non-temporal loads
+    TQ_ADDR_CONTIG = 3,  // row-major per-sequence arrays without block tables (decode_contig_kernel)
 };
 // K + V caches larger than this (the MI355X last-level "Infinity" cache, 256 MB) are read with
 // non-temporal loads: every byte is read once per decode and nothing would be kept anyway.

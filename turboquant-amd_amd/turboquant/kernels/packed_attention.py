@@ -2,9 +2,11 @@
 
 packed_attention keeps the signature of kernels/packed_attention.py:290-344 and reads the
 same arrays: 2-bit K/V indices [BH, Sk, 32], stride-4 permuted QJL sign rows [BH, Sk, 16],
-fp16 norms / residual norms [BH, Sk].  It runs the paged decode kernel (tq_decode) with a
-"contiguous" view: each of the BH query heads is a sequence with its own KV (no GQA), blocks
-of 16 tokens addressed by stride instead of a block table.
+fp16 norms / residual norms [BH, Sk].  It calls tq_decode with a "contiguous" view: each of
+the BH query heads is a sequence with its own KV (no GQA), 16-token tiles addressed by stride
+instead of a block table.  For Sk a multiple of 16 the library runs its row-major kernel
+(decode_contig_kernel: the fast kernel's pair loop with loads for these arrays); other Sk go
+through the general decode kernel.
 
 Differences from the reference, by design:
   - the split combine is the correct (m, l, acc) merge (kernels/attention.py:121-140), not
@@ -110,7 +112,9 @@ def packed_attention(Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
 
     seq_lens = torch.full((BH,), Sk, dtype=torch.int32, device=dev)
     out = torch.empty((BH, 1, D), dtype=torch.float16, device=dev)
-    chunk = _chunk_for(BH, Sk, num_splits)
+    # num_splits given: that many chunks; otherwise the library's choice (for Sk a multiple of 16,
+    # the row-major kernel with one round of the resident waves)
+    chunk = _chunk_for(BH, Sk, num_splits) if num_splits else 0
     nblk = math.ceil(Sk / BLOCK)
     run_decode(q, kv, vv, num_kv_heads=1, block_size=BLOCK, num_blocks=nblk, block_tables=None,
                max_blocks_per_seq=nblk, seq_lens=seq_lens, max_seq_len=Sk, sm_scale=1.0,
