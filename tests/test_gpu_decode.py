@@ -341,13 +341,13 @@ def test_packed_attention_v7_api(dev):
 
 @pytest.mark.parametrize("perm", [True, False])
 @pytest.mark.parametrize("S,Sk,hkv,G,chunk", [(8, 256, 1, 1, 0), (3, 4096, 2, 6, 0), (2, 16, 1, 1, 0),
-                                              (5, 1024, 1, 3, 512), (4, 2048, 2, 8, 96)])
+                                              (5, 1024, 1, 3, 512), (4, 2048, 2, 8, 96), (3, 1024, 1, 2, 16)])
 def test_decode_row_major_arrays(dev, perm, S, Sk, hkv, G, chunk):
     """The row-major per-sequence arrays of the v7 layout (2-bit keys with QJL, 2-bit values, no
     block tables; Sk a multiple of 16) through tq_decode's contiguous kernel, against the fp64
     oracle: sign rows in natural or stride-4 permuted order, GQA groups 1-8, several KV heads,
     sequence lengths ending inside a tile, a sequence of length 0, fixed and library-chosen
-    chunks."""
+    chunks (up to 64 per sequence: the merge's four-wave form)."""
     from turboquant import _lib
     from turboquant.kernels.paged import run_decode
     rng = np.random.default_rng(1000 + Sk + 7 * G + perm)

@@ -779,12 +779,15 @@ struct ReduceParams {
     const int64_t* plan;
 };
 
-// Split-K merge, one wave per (sequence, query head):
+// Split-K merge, W waves per (sequence, query head):
 //   out = sum_c 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c      (kernels/attention.py:128-140)
 // The chunk maxima and denominators are read one lane per chunk and reduced across the wave;
 // the rows acc_c are summed in chunk order with lane d covering dims 2d, 2d+1, sixteen chunks
-// (rows, maxima, denominators) requested together.  Sequences of one chunk were written by the decode kernel (unless the output
-// is rotated: then every sequence is written here); empty ones are written as zero here.
+// (rows, maxima, denominators) requested together.  With W > 1 (many chunks per sequence) wave w
+// takes batches w, w + W, ... and wave 0 combines the W partial merges through LDS, so the
+// batches' load rounds overlap.  Sequences of one chunk were written by the decode kernel
+// (unless the output is rotated: then every sequence is written here); empty ones are written
+// as zero here.
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
@@ -796,11 +799,13 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
-__global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
+template <int W>
+__global__ __launch_bounds__(64 * W) void decode_reduce_kernel(ReduceParams p) {
     const int64_t sh = blockIdx.x;
     const int64_t s = sh / p.hq;
     const int h = (int)(sh - s * p.hq);
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = W == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     int nch;
     int64_t base, stride;  // partial row of the first piece, rows between pieces
     if (!p.balanced) {
@@ -834,7 +839,7 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
     // round.  Per batch the running max M rescales what was summed so far.
     float M = kNegInf, den = 0.f, a0 = 0.f, a1 = 0.f;
     const float2* rows = reinterpret_cast<const float2*>(p.ws_acc + base * TQ_HEAD_DIM) + lane;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
+    for (int c0 = 16 * wave; c0 < nch; c0 += 16 * W) {
         const int nb = nch - c0 < 16 ? nch - c0 : 16;
         const bool mine = lane < nb;
         const float mc = mine ? p.ws_m[base + (int64_t)(c0 + lane) * stride] : kNegInf;
@@ -858,6 +863,32 @@ __global__ __launch_bounds__(64) void decode_reduce_kernel(ReduceParams p) {
             const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
             a0 = __builtin_fmaf(wj, v[j].x, a0);
             a1 = __builtin_fmaf(wj, v[j].y, a1);
+        }
+    }
+    if (W > 1) {
+        __shared__ float s_m[W], s_den[W];
+        __shared__ float2 s_acc[W][64];
+        if (lane == 0) {
+            s_m[wave] = M;
+            s_den[wave] = den;
+        }
+        s_acc[wave][lane] = make_float2(a0, a1);
+        __syncthreads();
+        if (wave != 0) return;
+        float Mt = kNegInf;
+#pragma unroll
+        for (int w = 0; w < W; ++w) Mt = fmaxf(Mt, s_m[w]);
+        den = 0.f;
+        a0 = 0.f;
+        a1 = 0.f;
+        if (Mt != kNegInf) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float f = s_m[w] == kNegInf ? 0.f : __builtin_amdgcn_exp2f(s_m[w] - Mt);
+                den = __builtin_fmaf(f, s_den[w], den);
+                a0 = __builtin_fmaf(f, s_acc[w][lane].x, a0);
+                a1 = __builtin_fmaf(f, s_acc[w][lane].y, a1);
+            }
         }
     }
     float inv = den > 0.f ? 1.0f / den : 0.f;
@@ -944,7 +975,11 @@ int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num
     rp.out_dtype = out_dtype;
     rp.out_ss = out_ss;
     rp.out_sh = out_sh;
-    hipLaunchKernelGGL(decode_reduce_kernel, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(64), 0, st, rp);
+    // four waves per (sequence, query head) when a sequence can span more than 32 chunks
+    if (!bal && n_chunks > 32)
+        hipLaunchKernelGGL(decode_reduce_kernel<4>, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(256), 0, st, rp);
+    else
+        hipLaunchKernelGGL(decode_reduce_kernel<1>, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(64), 0, st, rp);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TQ_OK : (int)e;
 }
