@@ -48,6 +48,21 @@ def _get_config(BH: int, Sk: int):
     return BLOCK, max(1, math.ceil(Sk / chunk)), 4, 1
 
 
+# Read-only [BH] int32 tensors of Sk, one per (device, BH, Sk): a per-call fill would cost a kernel
+# launch and several microseconds of host time on every call.
+_SEQ_LENS: dict = {}
+
+
+def _seq_lens(dev: torch.device, BH: int, Sk: int) -> torch.Tensor:
+    key = (dev.index, BH, Sk)
+    t = _SEQ_LENS.get(key)
+    if t is None:
+        if len(_SEQ_LENS) > 64:
+            _SEQ_LENS.clear()
+        t = _SEQ_LENS[key] = torch.full((BH,), Sk, dtype=torch.int32, device=dev)
+    return t
+
+
 def _contig_region(t: torch.Tensor, row_bytes: int, Sk: int) -> _lib.TQRegion:
     return _lib.TQRegion(t.data_ptr(), BLOCK * row_bytes, 0, Sk * row_bytes, row_bytes)
 
@@ -110,7 +125,7 @@ def packed_attention(Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
     vv.bits, vv.qjl, vv.signs_permuted = 2, 0, 0
     vv.centroid_scale = kv.centroid_scale
 
-    seq_lens = torch.full((BH,), Sk, dtype=torch.int32, device=dev)
+    seq_lens = _seq_lens(dev, BH, Sk)
     out = torch.empty((BH, 1, D), dtype=torch.float16, device=dev)
     # num_splits given: that many chunks; otherwise the library's choice (for Sk a multiple of 16,
     # the row-major kernel with one round of the resident waves)
