@@ -204,7 +204,9 @@ struct Softmax {
 struct LaneCtx {
     tq_half8 qop[4];            // q (fp16), MFMA chunk cc: dims 32g + 8cc + j
     tq_i32x8 qp6[3];            // q_proj * corr * cscale * 2^b as three fp6 parts (6 dwords each)
-    int qsc;                    // E8M0 scales of the parts in bytes 0-2: 2^-b, 2^-(b+5), 2^-(b+10)
+    // E8M0 scales of the parts in bytes 0-2 (2^-b, 2^-(b+5), 2^-(b+10)) for tile A's products in
+    // qscA and tile B's in qscB, with byte value 0 (2^-127) in the other tile's columns (lanes)
+    int qscA, qscB;
     uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
     uint32_t vquad;                // 3-bit V quad table base (a 3-bit K quad table is at address 0)
     uint64_t hmask;             // lanes of real heads
@@ -236,8 +238,11 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
     return s;
 }
 
+// QJL products of one tile accumulated onto t with B scales sc (a tile's own columns carry the
+// real scales; the other tile's columns 2^-127, so that two tiles chained on one accumulator
+// leave each column holding its own tile's term, plus at most 128 * 7.5 * 2^-127 < 6e-36).
 template <int SREP>
-__device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, const LaneCtx& c) {
+__device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, tq_floatx4 t, int sc, const LaneCtx& c) {
     constexpr int P = SREP == 32 ? 7 : 6;  // entry stride: SREP replicas x 4 bytes
     const uint32_t w[1] = {ks};
     tq_i32x8 a;
@@ -245,11 +250,10 @@ __device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, const LaneCtx& c) {
     for (int b = 0; b < 4; ++b) a[b] = (int)lds_read(entry_addr<8, 1, P>(w, 8 * b, c.sbank));
 #pragma unroll
     for (int b = 4; b < 8; ++b) a[b] = 0;  // fp4 operand: only the first four dwords are read
-    tq_floatx4 t = {0.f, 0.f, 0.f, 0.f};
-    // A: fp4 (format 4), B: fp6 e2m3 (format 2); the B scale is byte 0, 1, 2 of qsc
-    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[0], t, 4, 2, 0, 127, 0, c.qsc);
-    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[1], t, 4, 2, 0, 127, 1, c.qsc);
-    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[2], t, 4, 2, 0, 127, 2, c.qsc);
+    // A: fp4 (format 4), B: fp6 e2m3 (format 2); the B scale is byte 0, 1, 2 of sc
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[0], t, 4, 2, 0, 127, 0, sc);
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[1], t, 4, 2, 0, 127, 1, sc);
+    t = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, c.qp6[2], t, 4, 2, 0, 127, 2, sc);
     return t;
 }
 
@@ -270,10 +274,12 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     // ---------------- scores ----------------
     const tq_floatx4 sA = qk_tile<KB>(kr.kwA, c);
     const tq_floatx4 sB = qk_tile<KB>(kr.kwB, c);
-    tq_floatx4 tA = {0.f, 0.f, 0.f, 0.f}, tB = {0.f, 0.f, 0.f, 0.f};
+    // QJL: tile B's products accumulate onto tile A's; columns < 8 end with tile A's term and
+    // columns >= 8 with tile B's (the scales zero the other tile's columns), so no selects
+    tq_floatx4 t = {0.f, 0.f, 0.f, 0.f};
     if (KQJL) {
-        tA = qjl_tile<sign_replicas<KB, VB>()>(kr.ksA, c);
-        tB = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, c);
+        t = qjl_tile<sign_replicas<KB, VB>()>(kr.ksA, t, c.qscA, c);
+        t = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, t, c.qscB, c);
     }
     // Rows past the end may hold any bits in a paged block: masked out of the scores, and their
     // value norms zeroed (bit-wise, before any arithmetic), in partial pairs only.
@@ -284,7 +290,7 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
         // Scalar copies: shuffling ext_vector elements in place has miscompiled before.
         const float s1 = c.lo8 ? sA[r] : sB[r];
         if (KQJL) {
-            const float s2 = c.lo8 ? tA[r] : tB[r];
+            const float s2 = t[r];
             sc[r] = __builtin_fmaf(half_at(kr.kn, r), s1, __builtin_fmaf(half_at(kr.krn, r), s2, 0.0f));
         } else {
             sc[r] = half_at(kr.kn, r) * s1;
@@ -512,7 +518,9 @@ __device__ __forceinline__ void make_q_operands(LaneCtx& c, const FastDecodePara
         int b = 0;
         if (amax > 0.f && amax < __builtin_huge_valf()) b = 1 - ilogbf(amax);
         b = b < -117 ? -117 : (b > 117 ? 117 : b);
-        c.qsc = (127 - b) | ((122 - b) << 8) | ((117 - b) << 16);
+        const int qsc = (127 - b) | ((122 - b) << 8) | ((117 - b) << 16);
+        c.qscA = c.lo8 ? qsc : 0;
+        c.qscB = c.lo8 ? 0 : qsc;
         // x 2^b = hi + mid / 32 + lo / 1024 + e: each part rounded to nearest even (the
         // conversion divides by its scale argument), the residuals before it exact in fp32; the
         // last part is at most 4 in magnitude, so |e| <= 2^-3 / 1024 = 2^-13 next to a block
@@ -544,7 +552,7 @@ __device__ __forceinline__ void make_q_operands(LaneCtx& c, const FastDecodePara
             }
         }
     } else {
-        c.qsc = 127;
+        c.qscA = c.qscB = 127;
     }
 }
 
