@@ -1062,7 +1062,7 @@ int general_chunk(int num_seqs, int num_q_heads, int max_seq_len, bool pair) {
 
 // Resident waves of the fast kernel on the current device (one launch's workers), cached per
 // (device, kernel, LDS bytes).
-int resident_waves(const void* kern, size_t lds, int* waves) {
+int resident_waves(const void* kern, int wg_waves, size_t lds, int* waves) {
     struct Entry {
         int dev;
         const void* kern;
@@ -1081,12 +1081,14 @@ int resident_waves(const void* kern, size_t lds, int* waves) {
             *waves = cache[i].waves;
             return TQ_OK;
         }
+    const int arc = tq_decode_fast_lds_attr(kern);
+    if (arc) return arc;
     int blocks = 0, cus = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 64 * wg_waves, lds);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return (int)e;
-    *waves = blocks * 4 * cus;
-    if (*waves < 4) *waves = 4;
+    *waves = blocks * wg_waves * cus;
+    if (*waves < wg_waves) *waves = wg_waves;
     if (n_cache < 64) cache[n_cache++] = Entry{dev, kern, lds, *waves};
     return TQ_OK;
 }
@@ -1115,10 +1117,11 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     const int share = (share_codebook && k_bits == v_bits) ? 1 : 0;
     size_t lds = lds_bytes(k_bits, v_bits, share);
     if (norm_row_bytes == 2 && group <= 8) {
-        // the paged fast path (library tile layout)
-        kern = tq_decode_fast_kernel_ptr(k_bits, k_qjl != 0, v_bits);
-        uint32_t a, b, c, d;
-        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &a, &b, &c, &d, &lds);
+        // the paged fast path (library tile layout): workgroups of tq_decode_fast_wg_waves waves
+        FastLdsLayout lay;
+        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &lay);
+        return resident_waves(tq_decode_fast_kernel_ptr(k_bits, k_qjl != 0, v_bits),
+                              tq_decode_fast_wg_waves(k_bits, k_qjl != 0, v_bits, lay.total), lay.total, units);
     }
     int blocks = 0, dev = 0, cus = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, 256, lds);
@@ -1212,11 +1215,11 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     if (contig && tokens_per_chunk == 0) {
         // one round of the resident waves, at least 8 tiles per unit (a unit's start-up is worth
         // several tiles), and no more units than the workspace of tokens_per_chunk = 0 holds
-        uint32_t a, b, c, d;
-        size_t lds_c = 0;
-        tq_decode_fast_lds_layout(2, true, 2, share, &a, &b, &c, &d, &lds_c);
+        FastLdsLayout lay;
+        tq_decode_fast_lds_layout(2, true, 2, share, &lay);
         int waves = 0;
-        const int orc = resident_waves(tq_decode_fast_kernel_ptr(2, true, 2, 0, TQ_ADDR_CONTIG), lds_c, &waves);
+        const int orc = resident_waves(tq_decode_fast_kernel_ptr(2, true, 2, 0, TQ_ADDR_CONTIG),
+                                       tq_decode_fast_wg_waves(2, true, 2, lay.total), lay.total, &waves);
         if (orc) return orc;
         const int64_t tiles = (int64_t)num_seqs * num_kv_heads * (max_seq_len / 16);
         int64_t per = (tiles + waves - 1) / (waves > 0 ? waves : 1);
@@ -1280,9 +1283,17 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.k_cscale = k_cscale;
         f.v_cscale = v_cscale;
         f.v_cinv = 1.f / v_cscale;
-        size_t lds_total = 0;
-        tq_decode_fast_lds_layout(k->bits, k->qjl != 0, v->bits, share, &f.lds_sign, &f.lds_k, &f.lds_v, &f.lds_scratch,
-                                  &lds_total);
+        FastLdsLayout lay;
+        tq_decode_fast_lds_layout(k->bits, k->qjl != 0, v->bits, share, &lay);
+        const size_t lds_total = lay.total;
+        f.lds_sign = lay.sign;
+        f.lds_k = lay.k;
+        f.lds_v = lay.v;
+        f.lds_scratch = lay.scratch;
+        f.rep_s = lay.rep_s;
+        f.rep_k = lay.rep_k;
+        f.rep_v = lay.rep_v;
+        const int wpg = tq_decode_fast_wg_waves(k->bits, k->qjl != 0, v->bits, lds_total);
         f.block_size = block_size;
         int tsh = 0;
         while ((16 << tsh) < block_size) ++tsh;
@@ -1306,7 +1317,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
             int waves = 0;
             // the plain instance, as tq_decode_concurrent_units counts it (the statistics and
             // 64-bit instances share its register budget and LDS)
-            const int orc = resident_waves(tq_decode_fast_kernel_ptr(k->bits, k->qjl != 0, v->bits), lds_total, &waves);
+            const int orc = resident_waves(tq_decode_fast_kernel_ptr(k->bits, k->qjl != 0, v->bits), wpg, lds_total, &waves);
             if (orc) return orc;
             // partial slots stay below workers + num_seqs * num_kv_heads
             const int64_t wmax = (int64_t)(rows / group) - (int64_t)num_seqs * num_kv_heads;
@@ -1318,12 +1329,12 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
             f.ws_acc = reinterpret_cast<float*>(wsr);
             f.ws_m = reinterpret_cast<float*>(wsr + align_up(rows * TQ_HEAD_DIM * sizeof(float), 256));
             f.ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(f.ws_m) + align_up(rows * sizeof(float), 256));
-            grid = (f.n_workers + 3) / 4;
+            grid = (f.n_workers + wpg - 1) / wpg;
         } else {
             f.ws_acc = reinterpret_cast<float*>(ws);
             f.ws_m = reinterpret_cast<float*>(ws + align_up(slots * TQ_HEAD_DIM * sizeof(float), 256));
             f.ws_l = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(f.ws_m) + align_up(slots * sizeof(float), 256));
-            grid = ((int64_t)num_seqs * num_kv_heads * n_chunks + 3) / 4;
+            grid = ((int64_t)num_seqs * num_kv_heads * n_chunks + wpg - 1) / wpg;
         }
         f.out = out;
         f.out_dtype = out_dtype;
@@ -1333,7 +1344,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.rot_qp = rotate && !q_proj;
         f.rot_out = rotate;
         f.wht_h = kWhtH;
-        if (grid > (1 << 29)) return TQ_ERR_INVALID_ARGUMENT;  // unit indices stay below 2^31
+        if (grid * wpg > 0x7fffffffll) return TQ_ERR_INVALID_ARGUMENT;  // unit indices stay below 2^31
         int frc = tq_decode_fast_launch(f, k->bits, k->qjl != 0, v->bits, grid, lds_total, (hipStream_t)stream);
         if (frc) return frc;
         return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,

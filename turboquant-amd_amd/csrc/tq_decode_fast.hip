@@ -45,6 +45,11 @@
 // Sparse-V (kernels/sparse_v.py:108-149): for tile X, m_X = running max through tile X; token t
 // is dropped from PV when no head of the group has exp2(c (s - m_X)) > threshold, tested as
 // s > m_X + log2(threshold)/c with a ballot; dropped tokens stay in the denominator.
+#include <mutex>
+#include <set>
+#include <type_traits>
+#include <utility>
+
 #include "tq_common.h"
 #include "tq_decode_internal.h"
 
@@ -61,27 +66,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint8_t* base) {
 
 __device__ __forceinline__ uint32_t lds_read(uint32_t addr) { return *(lds_u32*)(uintptr_t)addr; }
 
-// LDS address of the table entry held in bits [pos, pos + W) of the word array w: the field is
-// moved to bit P, the log2 of the entry stride (one shift or funnel shift), and merged with the
-// table base plus the lane's replica offset (one and-or).  Tables sit at LDS offsets that are
-// multiples of their size.
-template <int W, int N, int P = 7>
-__device__ __forceinline__ uint32_t entry_addr(const uint32_t (&w)[N], int pos, uint32_t bank_addr) {
+// LDS address of the 3-bit quad table entry held in bits [pos, pos + 12) of the word array w:
+// the field is moved to bit 3 (entries of 8 bytes; one shift or funnel shift) and masked, and the
+// table base merged in (folded away for the K table at address 0).
+template <int N>
+__device__ __forceinline__ uint32_t quad3_addr(const uint32_t (&w)[N], int pos, uint32_t base) {
     const int wi = pos >> 5, sh = pos & 31;
     uint32_t f;
-    if (W == 8 && P == 3 && sh == 0) {
-        // byte 0 times 8 in one SDWA shift (the compiler turns the mask-and-shift into two ops;
-        // bytes 1-3 it selects by itself)
-        asm("v_lshlrev_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
-            : "=v"(f)
-            : "v"(3u), "v"(w[wi]));
-        return f | bank_addr;
-    }
-    if (sh + W <= 32 || wi + 1 >= N)
-        f = sh >= P ? (w[wi] >> (sh - P)) : (w[wi] << (P - sh));
+    if (sh + 12 <= 32 || wi + 1 >= N)
+        f = sh >= 3 ? (w[wi] >> (sh - 3)) : (w[wi] << (3 - sh));
     else
-        f = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - P);
-    return (f & (((1u << W) - 1u) << P)) | bank_addr;
+        f = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh - 3);
+    return (f & 0x7ff8u) | base;
 }
 
 __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
@@ -89,30 +85,34 @@ __device__ __forceinline__ tq_u32x2 lds_read2(uint32_t addr) {
     return *(lds_u32x2*)(uintptr_t)addr;
 }
 
-// 2- and 3-bit indices are looked up four at a time (a 4B-bit field -> 4 fp16 centroids, one
-// 8-byte entry) instead of in pairs.  3 bits: 4096 entries (32 KB); 2 bits: 256 entries (2 KB);
-// neither replicated.  A K quad table sits at LDS address 0 and a 2-bit V quad table at
-// v2_quad_base<KB>(), so that a 2-bit lookup address is the index byte times 8 (one SDWA shift)
-// plus a constant that goes into the ds_read offset.
+// Index fields are looked up in LDS tables: 2- and 3-bit fields four at a time (a 4B-bit field
+// -> 4 fp16 centroids, an 8-byte entry), 4-bit fields in pairs (a byte -> half2, 4 bytes), and
+// sign bytes -> 8 fp4 values +-1 (4 bytes).
+// Row tables (2-bit quads, 4-bit pairs, the sign table) are indexed by one byte of a word:
+// entry e, replica r at base + 256 e + es r (es: entry bytes), base = 64 KB x region + column
+// (0, or 128 when two tables share the rows of a region).  A lookup address is one byte permute
+// of the word and the lane's word lw = base + es (lane & (replicas - 1)): byte 0 column and
+// replica, byte 1 the field, byte 2 the region.  Each lane reads its own replica: a full row
+// (256 bytes) holds 32 quad or 64 pair / sign replicas, one per bank (pair) of the LDS.
+// 3-bit quad tables: 4096 entries of 8 bytes at 32 KB-aligned offsets (a K table at 0), not
+// replicated (quad3_addr).
 template <int B>
 constexpr bool quad_table() {
     return B == 3 || B == 2;
 }
-// Bit position of the field in a quad table address (log2 of the entry stride).
+// Entry bytes of a row table.
 template <int B>
-constexpr int quad_shift() {
-    return 3;
+constexpr uint32_t row_entry_bytes() {
+    return B == 2 ? 8u : 4u;
 }
-// LDS address of a 2-bit V quad table: after the K table at 0 (2-bit quads: 2 KB; 3-bit quads
-// and 4-bit pair tables: 32 KB).
-template <int KB>
-constexpr uint32_t v2_quad_base() {
-    return KB == 2 ? 2048u : 32768u;
+__device__ __forceinline__ uint32_t row_addr(uint32_t w, int k, uint32_t lw) {
+    // bytes: lw.0 (column + replica), w.k (the field), lw.2 (region), 0
+    return __builtin_amdgcn_perm(lw, w, 0x0c060004u | ((uint32_t)k << 8));
 }
-// Replicas of the fp4 sign table (fewer when a quad table takes the LDS).
-template <int KB, int VB>
-constexpr int sign_replicas() {
-    return (quad_table<KB>() || quad_table<VB>()) ? 16 : 32;
+// The row-table address of the byte at bit pos (a multiple of 8) of the word array w.
+template <int N>
+__device__ __forceinline__ uint32_t row_addr_at(const uint32_t (&w)[N], int pos, uint32_t lw) {
+    return row_addr(w[pos >> 5], (pos & 31) >> 3, lw);
 }
 
 __device__ __forceinline__ float half_at(const uint32_t (&w)[2], int r) {
@@ -207,8 +207,8 @@ struct LaneCtx {
     // E8M0 scales of the parts in bytes 0-2 (2^-b, 2^-(b+5), 2^-(b+10)) for tile A's products in
     // qscA and tile B's in qscB, with byte value 0 (2^-127) in the other tile's columns (lanes)
     int qscA, qscB;
-    uint32_t kbank, vbank, sbank;  // table base + replica offset of this lane
-    uint32_t vquad;                // 3-bit V quad table base (a 3-bit K quad table is at address 0)
+    uint32_t klw, vlw, slw;     // lane words of the K, V and sign row tables (row_addr)
+    uint32_t vquad;             // 3-bit V quad table base (a 3-bit K quad table is at address 0)
     uint64_t hmask;             // lanes of real heads
     float gap;                  // 1 / c_exp: one log2 unit of p in raw score units
     bool lo8;                   // column < 8: tile A
@@ -221,17 +221,17 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
     for (int cc = 0; cc < 4; ++cc) {
         tq_u32x4 a;
         if (quad_table<KB>()) {
-            // dims 8cc..8cc+7 of the lane's 32: two quads; the K quad table sits at LDS address 0,
-            // so the address is the field times 8
-            const tq_u32x2 lo = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc), 0u));
-            const tq_u32x2 hi = lds_read2(entry_addr<4 * KB, KB, quad_shift<KB>()>(kw, 4 * KB * (2 * cc + 1), 0u));
+            // dims 8cc..8cc+7 of the lane's 32: two quads (a 3-bit K quad table sits at LDS
+            // address 0, so its address is the field times 8)
+            const tq_u32x2 lo = lds_read2(KB == 3 ? quad3_addr(kw, 24 * cc, 0u) : row_addr_at(kw, 16 * cc, c.klw));
+            const tq_u32x2 hi = lds_read2(KB == 3 ? quad3_addr(kw, 24 * cc + 12, 0u) : row_addr_at(kw, 16 * cc + 8, c.klw));
             a[0] = lo[0];
             a[1] = lo[1];
             a[2] = hi[0];
             a[3] = hi[1];
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) a[j] = lds_read(entry_addr<2 * KB>(kw, 2 * KB * (4 * cc + j), c.kbank));
+            for (int j = 0; j < 4; ++j) a[j] = lds_read(row_addr(kw[cc], j, c.klw));
         }
         s = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), c.qop[cc], s, 0, 0, 0);
     }
@@ -241,13 +241,10 @@ __device__ __forceinline__ tq_floatx4 qk_tile(const uint32_t (&kw)[KB], const La
 // QJL products of one tile accumulated onto t with B scales sc (a tile's own columns carry the
 // real scales; the other tile's columns 2^-127, so that two tiles chained on one accumulator
 // leave each column holding its own tile's term, plus at most 128 * 7.5 * 2^-127 < 6e-36).
-template <int SREP>
 __device__ __forceinline__ tq_floatx4 qjl_tile(uint32_t ks, tq_floatx4 t, int sc, const LaneCtx& c) {
-    constexpr int P = SREP == 32 ? 7 : 6;  // entry stride: SREP replicas x 4 bytes
-    const uint32_t w[1] = {ks};
     tq_i32x8 a;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) a[b] = (int)lds_read(entry_addr<8, 1, P>(w, 8 * b, c.sbank));
+    for (int b = 0; b < 4; ++b) a[b] = (int)lds_read(row_addr(ks, b, c.slw));
 #pragma unroll
     for (int b = 4; b < 8; ++b) a[b] = 0;  // fp4 operand: only the first four dwords are read
     // A: fp4 (format 4), B: fp6 e2m3 (format 2); the B scale is byte 0, 1, 2 of sc
@@ -278,8 +275,8 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     // columns >= 8 with tile B's (the scales zero the other tile's columns), so no selects
     tq_floatx4 t = {0.f, 0.f, 0.f, 0.f};
     if (KQJL) {
-        t = qjl_tile<sign_replicas<KB, VB>()>(kr.ksA, t, c.qscA, c);
-        t = qjl_tile<sign_replicas<KB, VB>()>(kr.ksB, t, c.qscB, c);
+        t = qjl_tile(kr.ksA, t, c.qscA, c);
+        t = qjl_tile(kr.ksB, t, c.qscB, c);
     }
     // Rows past the end may hold any bits in a paged block: masked out of the scores, and their
     // value norms zeroed (bit-wise, before any arithmetic), in partial pairs only.
@@ -378,18 +375,18 @@ __device__ __forceinline__ void compute_pair(const KRaw<KB, KQJL>& kr, const VRa
     auto vlook = [&](int a) -> tq_u32x4 {
         tq_u32x4 aw;
         if (quad_table<VB>()) {
-            // one quad per tile (2 bits: a fixed table address, which goes into the ds_read offset)
-            const uint32_t fa = entry_addr<4 * VB, VB, quad_shift<VB>()>(vr.vwA, 4 * VB * a, VB == 2 ? 0u : c.vquad);
-            const uint32_t fb = entry_addr<4 * VB, VB, quad_shift<VB>()>(vr.vwB, 4 * VB * a, VB == 2 ? 0u : c.vquad);
-            const tq_u32x2 xa = lds_read2(VB == 2 ? fa + v2_quad_base<KB>() : fa);
-            const tq_u32x2 xb = lds_read2(VB == 2 ? fb + v2_quad_base<KB>() : fb);
+            // one quad per tile
+            const uint32_t fa = VB == 3 ? quad3_addr(vr.vwA, 12 * a, c.vquad) : row_addr_at(vr.vwA, 8 * a, c.vlw);
+            const uint32_t fb = VB == 3 ? quad3_addr(vr.vwB, 12 * a, c.vquad) : row_addr_at(vr.vwB, 8 * a, c.vlw);
+            const tq_u32x2 xa = lds_read2(fa);
+            const tq_u32x2 xb = lds_read2(fb);
             aw = tq_u32x4{xa[0], xa[1], xb[0], xb[1]};
         } else {
             // two pairs per tile: tokens 0, 1 and 2, 3
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                aw[h] = lds_read(entry_addr<2 * VB, VB>(vr.vwA, 4 * VB * a + 2 * VB * h, c.vbank));
-                aw[2 + h] = lds_read(entry_addr<2 * VB, VB>(vr.vwB, 4 * VB * a + 2 * VB * h, c.vbank));
+                aw[h] = lds_read(row_addr_at(vr.vwA, 16 * a + 8 * h, c.vlw));
+                aw[2 + h] = lds_read(row_addr_at(vr.vwB, 16 * a + 8 * h, c.vlw));
             }
         }
         return aw;
@@ -421,78 +418,121 @@ template <int KB, bool KQJL, int VB>
 constexpr int fast_waves() {
     return KQJL ? 3 : 4;
 }
+// Most waves per workgroup (the launch bound): a compute unit's resident waves in one workgroup.
+// The host launches fewer per workgroup when the tables leave room for several workgroups per
+// compute unit (tq_decode_fast_wg_waves).
+template <int KB, bool KQJL, int VB>
+constexpr int fast_wg_waves() {
+    return 4 * fast_waves<KB, KQJL, VB>();
+}
 
-// LDS tables (one share per thread of the workgroup): the fp4 sign table (QJL), the K and the V
-// tables at the byte offsets chosen by the host (multiples of each table's size).  A replicated
-// table's entry is computed once and its replicas (consecutive) written with 16-byte stores:
-// every workgroup builds its tables before reading a tile, so this is part of each unit's
-// start-up.  Ends with a workgroup barrier.
+// Fixed chunks: work unit u is (sequence s, chunk ci, KV head kh), sequence-major (u = (s *
+// n_chunks + ci) * hkv + kh): consecutive workgroups, which the dispatcher deals round-robin to
+// the XCDs, take neighbouring chunks of one sequence, so every XCD gets a share of each
+// sequence.  Returns whether the unit holds tokens.
+__device__ __forceinline__ bool chunk_unit(int u, const FastDecodeParams& p, int cap, int& s, int& ci, int& kh,
+                                           int& L) {
+    kh = u % p.hkv;
+    const int t = u / p.hkv;
+    ci = t % p.n_chunks;
+    s = t / p.n_chunks;
+    if (s >= p.num_seqs) return false;
+    L = p.seq_lens[s];
+    L = L < cap ? L : cap;
+    return ci * p.chunk < L;
+}
+// Whether any unit of this workgroup's waves holds tokens (else the workgroup returns before
+// building its tables): lane w of each wave tests wave w's unit, all lengths in one load round.
+// Unit indices stay below 2^31 (checked on the host).
+__device__ __forceinline__ bool chunk_group_busy(const FastDecodeParams& p, int cap, int wpg) {
+    const int lane = (int)(threadIdx.x & 63);
+    bool busy = false;
+    if (lane < wpg) {
+        int s, ci, kh, L;
+        busy = chunk_unit((int)blockIdx.x * wpg + lane, p, cap, s, ci, kh, L);
+    }
+    return __builtin_amdgcn_ballot_w64(busy) != 0;
+}
+
+// LDS tables, built by the whole workgroup before any tile is read (part of each wave's
+// start-up): the fp4 sign table (QJL) and the K and V tables at the offsets and with the
+// replica counts chosen by the host (tq_decode_fast_lds_layout).  The scaled fp16 centroids are
+// first staged in the 512-byte scratch area (K in dwords 0-63, V in 64-127: 3-bit: the 64 pairs
+// of fields as half2; 2-bit: the 16 pairs; 4-bit: the 16 values), then every entry is read from
+// there.  Row tables are written with 16-byte stores, consecutive threads along a row (a wave
+// writes 1 KB of consecutive bytes).  Ends with a workgroup barrier.
 template <int KB, bool KQJL, int VB>
 __device__ __forceinline__ void build_tables(const FastDecodeParams& p, uint32_t* s_lds, int tid) {
-    constexpr int SREP = sign_replicas<KB, VB>();
-    if (KQJL) {
-        // entry e (one per thread): 8 sign bits -> 8 fp4 values +1 (0x2) / -1 (0xA)
-        uint32_t w = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) w |= ((((uint32_t)tid >> j) & 1u) ? 0x2u : 0xAu) << (4 * j);
-        tq_u32x4* t = reinterpret_cast<tq_u32x4*>(s_lds + p.lds_sign / 4) + tid * (SREP / 4);
-#pragma unroll
-        for (int r = 0; r < SREP / 4; ++r) t[r] = tq_u32x4{w, w, w, w};
-    }
-    // pair table: entry e -> half2(c[e & (2^b - 1)], c[e >> b]), 32 replicas;
-    // quad table: entry e -> 4 x fp16 c[(e >> bj) & (2^b - 1)], j = 0..3 (2 bits: 16 replicas)
-    // 3-bit quads are assembled from the 64 pairs of 3-bit fields, staged in a 512-byte scratch
-    // area after the tables (a static __shared__ array would move the K quad table off address 0)
-    uint32_t* s_pair3 = s_lds + p.lds_scratch / 4;
-    auto fill = [&](uint32_t off, const float* cent, float cs, int bits, bool quad, int which) {
-        uint32_t* t = s_lds + off / 4;
-        const int mask = (1 << bits) - 1;
-        if (quad && bits == 3) {
-            const uint32_t* pr = s_pair3 + 64 * which;
-            for (int e = tid; e < 4096; e += 256)
-                reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{pr[e & 63], pr[e >> 6]};
-        } else if (quad) {
-            // 256 entries of 8 bytes, one per thread
-            const int e = tid;
-            const uint32_t lo = tq_pack_half2(cent[e & 3] * cs, cent[(e >> 2) & 3] * cs);
-            const uint32_t hi = tq_pack_half2(cent[(e >> 4) & 3] * cs, cent[(e >> 6) & 3] * cs);
-            reinterpret_cast<tq_u32x2*>(t)[e] = tq_u32x2{lo, hi};
-        } else {
-            // 2^(2 bits) entries (16, 64 or 256), 32 replicas x 4 bytes
-            const int ent = 1 << (2 * bits);
-            for (int e = tid; e < ent; e += 256) {
-                const uint32_t w = tq_pack_half2(cent[e & mask] * cs, cent[e >> bits] * cs);
-                tq_u32x4* d = reinterpret_cast<tq_u32x4*>(t) + e * 8;
-#pragma unroll
-                for (int r = 0; r < 8; ++r) d[r] = tq_u32x4{w, w, w, w};
-            }
+    const int NT = (int)__builtin_amdgcn_workgroup_size_x();
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(s_lds);
+    uint32_t* st = s_lds + p.lds_scratch / 4;
+    const bool vown = p.lds_v != p.lds_k;
+    auto stage = [&](auto bits_c, const float* cent, float cs, int t) {
+        constexpr int bits = decltype(bits_c)::value;
+        const int x = t & 63;  // entry of this table's staging area
+        if (bits == 3) st[t] = tq_pack_half2(cent[x & 7] * cs, cent[x >> 3] * cs);
+        if (bits == 2 && x < 16) st[t] = tq_pack_half2(cent[x & 3] * cs, cent[x >> 2] * cs);
+        if (bits == 4 && x < 16) st[t] = tq_pack_half2(cent[x] * cs, 0.f);
+    };
+    if (tid < 64) stage(std::integral_constant<int, KB>{}, p.k_cent, p.k_cscale, tid);
+    if (vown && tid >= 64 && tid < 128) stage(std::integral_constant<int, VB>{}, p.v_cent, p.v_cscale, tid);
+    // row table at base with es-byte entries, rep + 1 replicas; value(e): 16 bytes of entry e
+    auto fill_row = [&](uint32_t base, uint32_t es, uint32_t rep, auto value) {
+        const int S = (int)(es * (rep + 1) / 16);  // 16-byte stores per row: 8 or 16
+        const int sh = S == 16 ? 4 : 3;
+        for (int i = tid; i < 256 * S; i += NT) {
+            const int e = i >> sh;
+            *reinterpret_cast<tq_u32x4*>(lds8 + base + 256 * e + 16 * (i & (S - 1))) = value(e);
         }
     };
-    const bool vown = p.lds_v != p.lds_k;
-    if (quad_table<KB>() && KB == 3 && tid < 64)
-        s_pair3[tid] = tq_pack_half2(p.k_cent[tid & 7] * p.k_cscale, p.k_cent[tid >> 3] * p.k_cscale);
-    if (quad_table<VB>() && VB == 3 && vown && tid >= 64 && tid < 128)
-        s_pair3[tid] = tq_pack_half2(p.v_cent[tid & 7] * p.v_cscale, p.v_cent[(tid - 64) >> 3] * p.v_cscale);
-    if ((quad_table<KB>() && KB == 3) || (quad_table<VB>() && VB == 3)) __syncthreads();
-    fill(p.lds_k, p.k_cent, p.k_cscale, KB, quad_table<KB>(), 0);
-    if (vown) fill(p.lds_v, p.v_cent, p.v_cscale, VB, quad_table<VB>(), 1);
+    if (KQJL) {
+        // sign byte e -> 8 fp4 values: bit j set +1 (0x2), clear -1 (0xA), in nibble j
+        fill_row(p.lds_sign, 4u, p.rep_s, [&](int e) {
+            uint32_t x = (uint32_t)e;  // bit j -> bit 4j
+            x = (x | (x << 12)) & 0x000f000fu;
+            x = (x | (x << 6)) & 0x03030303u;
+            x = (x | (x << 3)) & 0x11111111u;
+            const uint32_t w = 0xaaaaaaaau ^ (x << 3);
+            return tq_u32x4{w, w, w, w};
+        });
+    }
+    __syncthreads();
+    auto fill_codes = [&](auto bits_c, uint32_t base, uint32_t rep, const uint32_t* sv) {
+        constexpr int bits = decltype(bits_c)::value;
+        if constexpr (bits == 2) {
+            // 4 x fp16 c[(e >> 2j) & 3], j = 0..3
+            fill_row(base, 8u, rep, [&](int e) {
+                const uint32_t lo = sv[e & 15], hi = sv[e >> 4];
+                return tq_u32x4{lo, hi, lo, hi};
+            });
+        } else if constexpr (bits == 4) {
+            // half2(c[e & 15], c[e >> 4])
+            fill_row(base, 4u, rep, [&](int e) {
+                const uint32_t w = (sv[e & 15] & 0xffffu) | (sv[e >> 4] << 16);
+                return tq_u32x4{w, w, w, w};
+            });
+        } else {
+            // 4096 entries of 8 bytes: 4 x fp16 c[(e >> 3j) & 7], from the pairs of fields
+            tq_u32x2* t = reinterpret_cast<tq_u32x2*>(lds8 + base);
+            for (int e = tid; e < 4096; e += NT) t[e] = tq_u32x2{sv[e & 63], sv[e >> 6]};
+        }
+    };
+    fill_codes(std::integral_constant<int, KB>{}, p.lds_k, p.rep_k, st);
+    if (vown) fill_codes(std::integral_constant<int, VB>{}, p.lds_v, p.rep_v, st + 64);
     __syncthreads();
 }
 
-// The lane's table addresses (base + replica offset) and its tile half (column < 8: tile A).
+// The lane's row-table words and 3-bit V table base, and its tile half (column < 8: tile A).
 template <int KB, int VB>
-__device__ __forceinline__ void init_lane_tables(LaneCtx& c, const FastDecodeParams& p, uint32_t* s_lds, int lane) {
+__device__ __forceinline__ void init_lane_tables(LaneCtx& c, const FastDecodeParams& p, int lane) {
     c.lo8 = (lane & 15) < 8;
-    const uint32_t bank4 = 4u * (uint32_t)(lane & 31);
-    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u32*)s_lds;
-    c.kbank = lds0 + p.lds_k + bank4;
-    c.vbank = lds0 + p.lds_v + bank4;
-    c.sbank = lds0 + p.lds_sign + 4u * (uint32_t)(lane & (sign_replicas<KB, VB>() - 1));
+    c.klw = p.lds_k + row_entry_bytes<KB>() * ((uint32_t)lane & p.rep_k);
+    c.vlw = p.lds_v + row_entry_bytes<VB>() * ((uint32_t)lane & p.rep_v);
+    c.slw = p.lds_sign + 4u * ((uint32_t)lane & p.rep_s);
     // 3-bit V quad table: address 0 when it is the K quad table, else its base from a VGPR (a
     // VALU op takes one scalar operand, and the field mask is one)
-    c.vquad = lds0 + p.lds_v;
-    if (VB == 3 && !(quad_table<KB>() && KB == 3 && p.lds_v == 0))
-        asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
+    c.vquad = p.lds_v;
+    if (VB == 3 && !(KB == 3 && p.lds_v == 0)) asm volatile("v_mov_b32 %0, %1" : "=v"(c.vquad) : "s"(c.vquad));
 }
 
 // Query operands from the lane's 32 loaded elements of q (qv) and of q_proj (x): q as fp16
@@ -566,8 +606,8 @@ __device__ __forceinline__ void make_q_operands(LaneCtx& c, const FastDecodePara
 //   TQ_ADDR_BIG: a cache spanning 2 GiB or more: tiles addressed from 64-bit per-tile bases,
 //       streaming loads.
 template <int KB, bool KQJL, int VB, int SPV, int ADDR>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
-                                                                     fast_waves<KB, KQJL, VB>())))
+__global__ __launch_bounds__((64 * fast_wg_waves<KB, KQJL, VB>()))
+__attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(), fast_waves<KB, KQJL, VB>())))
 void decode_fast_kernel(FastDecodeParams p) {
     constexpr bool BIG = ADDR == TQ_ADDR_BIG;
     constexpr int AUX = ADDR == TQ_ADDR_CACHED ? 0 : 2;  // buffer-load cache policy: 2 = non-temporal
@@ -575,7 +615,8 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wv = (int)blockIdx.x * 4 + wave;  // this wave's unit (chunks) or worker (balanced)
+    const int wpg = (int)(__builtin_amdgcn_workgroup_size_x() >> 6);  // waves per workgroup
+    const int wv = (int)blockIdx.x * wpg + wave;  // this wave's unit (chunks) or worker (balanced)
     const int cap = p.max_blocks * p.block_size;
 
     // ---- this wave's work, settled before the tables are built: idle workgroups skip them ----
@@ -627,24 +668,9 @@ void decode_fast_kernel(FastDecodeParams p) {
             }
             if (planner && lane == 0) p.plan[0] = tot;
         }
-        if ((int64_t)blockIdx.x * 4 >= R) return;  // the whole workgroup idle
-    } else {
-        // fixed chunks: units in (sequence, chunk, KV head) order; a workgroup whose four units
-        // all start past their sequence's end is idle
-        bool any = false;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t unit = (int64_t)blockIdx.x * 4 + u;
-            const int64_t sc_ = unit / p.hkv;
-            const int ci = (int)(sc_ % p.n_chunks);
-            const int64_t su = sc_ / p.n_chunks;
-            if (su < p.num_seqs) {
-                int Lu = p.seq_lens[su];
-                Lu = Lu < cap ? Lu : cap;
-                any = any || ci * p.chunk < Lu;
-            }
-        }
-        if (!any) return;
+        if ((int64_t)blockIdx.x * wpg >= R) return;  // the whole workgroup idle
+    } else if (!chunk_group_busy(p, cap, wpg)) {
+        return;
     }
     build_tables<KB, KQJL, VB>(p, s_lds, tid);
 
@@ -652,7 +678,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     const int n = lane & 15;
     const int hcol = n & 7;
     LaneCtx c;
-    init_lane_tables<KB, VB>(c, p, s_lds, lane);
+    init_lane_tables<KB, VB>(c, p, lane);
 
     // ---- loop-invariant lane offsets inside a tile ----
     // lane-grouped tiles: the lane's key chunk (row n, dims 32g..) and value chunk (rows
@@ -673,9 +699,8 @@ void decode_fast_kernel(FastDecodeParams p) {
     unsigned long long cnt_tot = 0, cnt_kept = 0;
 
     // ---- pieces: one (sequence, KV head, token range) per pass ----
-    // Fixed chunks: the wave's one unit (units in (sequence, chunk, KV head) order, so the four
-    // waves of a workgroup get the same chunk of one sequence).  Balanced: the segments the
-    // worker's pair range crosses.
+    // Fixed chunks: the wave's one unit (chunk_unit).  Balanced: the segments the worker's pair
+    // range crosses.
     for (;;) {
     int s;
     int kh, L, t_begin, t_end;
@@ -684,15 +709,9 @@ void decode_fast_kernel(FastDecodeParams p) {
     int prow_step;         // rows between the group's heads
     int take = 0;          // balanced: pairs of this piece
     if (!p.balanced) {
-        kh = wv % p.hkv;
-        const int sc_ = wv / p.hkv;
-        const int ci = sc_ % p.n_chunks;
-        s = sc_ / p.n_chunks;
-        if (s >= p.num_seqs) break;
-        L = p.seq_lens[s];
-        L = L < cap ? L : cap;
+        int ci;
+        if (!chunk_unit(wv, p, cap, s, ci, kh, L)) break;
         t_begin = ci * p.chunk;
-        if (t_begin >= L) break;
         t_end = (t_begin + p.chunk < L) ? t_begin + p.chunk : L;
         int nch = (L + p.chunk - 1) / p.chunk;
         nch = nch < p.n_chunks ? nch : p.n_chunks;
@@ -1035,50 +1054,28 @@ __device__ __forceinline__ void rows_to_dim_major2(const uint32_t (&h)[4], uint3
 // (rows_to_dim_major2).  Rows past a sequence's last tile are never read (the arrays hold
 // max_blocks * 16 rows per sequence; tiles past the end re-read the last one, masked).
 template <int KB, bool KQJL, int VB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(),
-                                                                     fast_waves<KB, KQJL, VB>())))
+__global__ __launch_bounds__((64 * fast_wg_waves<KB, KQJL, VB>()))
+__attribute__((amdgpu_waves_per_eu(fast_waves<KB, KQJL, VB>(), fast_waves<KB, KQJL, VB>())))
 void decode_contig_kernel(FastDecodeParams p) {
     static_assert(KB == 2 && KQJL && VB == 2, "row-major decode: 2-bit keys with QJL, 2-bit values");
     extern __shared__ uint32_t s_lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wv = (int)blockIdx.x * 4 + wave;  // this wave's unit
+    const int wpg = (int)(__builtin_amdgcn_workgroup_size_x() >> 6);  // waves per workgroup
+    const int wv = (int)blockIdx.x * wpg + wave;  // this wave's unit
     const int cap = p.max_blocks * 16;          // rows per sequence in the arrays
-    {
-        // units in (sequence, chunk, KV head) order; a workgroup whose four units all start past
-        // their sequence's end is idle
-        bool any = false;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t unit = (int64_t)blockIdx.x * 4 + u;
-            const int64_t sc_ = unit / p.hkv;
-            const int ci = (int)(sc_ % p.n_chunks);
-            const int64_t su = sc_ / p.n_chunks;
-            if (su < p.num_seqs) {
-                int Lu = p.seq_lens[su];
-                Lu = Lu < cap ? Lu : cap;
-                any = any || ci * p.chunk < Lu;
-            }
-        }
-        if (!any) return;
-    }
+    if (!chunk_group_busy(p, cap, wpg)) return;
     build_tables<KB, KQJL, VB>(p, s_lds, tid);
     const int g = lane >> 4;
     const int n = lane & 15;
     const int hcol = n & 7;
     LaneCtx c;
-    init_lane_tables<KB, VB>(c, p, s_lds, lane);
+    init_lane_tables<KB, VB>(c, p, lane);
 
-    const int kh = wv % p.hkv;
-    const int sc_ = wv / p.hkv;
-    const int ci = sc_ % p.n_chunks;
-    const int s = sc_ / p.n_chunks;
-    if (s >= p.num_seqs) return;
-    int L = p.seq_lens[s];
-    L = L < cap ? L : cap;
+    int s, ci, kh, L;
+    if (!chunk_unit(wv, p, cap, s, ci, kh, L)) return;
     const int t_begin = ci * p.chunk;
-    if (t_begin >= L) return;
     const int t_end = t_begin + p.chunk < L ? t_begin + p.chunk : L;
     int nch = (L + p.chunk - 1) / p.chunk;
     nch = nch < p.n_chunks ? nch : p.n_chunks;
@@ -1254,70 +1251,87 @@ const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, int spv, int addr
     return nullptr;
 }
 
-void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
-                               uint32_t* lds_v, uint32_t* lds_scratch, size_t* total) {
-    // Each table at a multiple of its size (pair tables are addressed by OR).  Fixed addresses
-    // first: a K quad table at 0 (and any K table when a 2-bit V quad table follows it), a 2-bit
-    // V quad table right after the K table (its own copy even when K and V share a codebook);
-    // then the others, largest first, at the lowest free multiple of their size.
-    const bool kquad = kb == 3 || kb == 2, vquad = vb == 3 || vb == 2;
-    const bool v2 = vquad && vb == 2;
-    const size_t ks = kquad ? (kb == 3 ? (size_t)4096 * 8 : (size_t)256 * 8) : ((size_t)1 << (2 * kb)) * 128;
-    const size_t vs = vquad ? (vb == 3 ? (size_t)4096 * 8 : (size_t)256 * 8) : ((size_t)1 << (2 * vb)) * 128;
-    const size_t ss = kq ? (size_t)256 * 4 * ((kquad || vquad) ? 16 : 32) : 0;
-    struct Used {
-        size_t off, size;
-    } used[4];
-    int nu = 0;
-    size_t end = 0;
-    auto take = [&](uint32_t* o, size_t off, size_t size) {
-        *o = (uint32_t)off;
-        used[nu++] = {off, size};
-        end = off + size > end ? off + size : end;
-    };
-    auto place = [&](uint32_t* o, size_t size) {
-        for (size_t off = 0;; off += size) {
-            bool ok = true;
-            for (int i = 0; i < nu; ++i)
-                if (off < used[i].off + used[i].size && used[i].off < off + size) ok = false;
-            if (ok) {
-                take(o, off, size);
-                return;
-            }
-        }
-    };
-    const bool kfixed = kquad || v2;
-    if (kfixed) take(lds_k, 0, ks);
-    if (v2) take(lds_v, kb == 2 ? 2048 : 32768, vs);  // v2_quad_base<KB>() in the kernel
-    struct T {
-        size_t size;
+void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, FastLdsLayout* l) {
+    *l = FastLdsLayout{};
+    // 3-bit quad tables in [0, 64 KB): K at 0, then V's own
+    uint32_t end3 = 0;
+    if (kb == 3) end3 = 32768;
+    if (vb == 3 && !share) {
+        l->v = end3;
+        end3 += 32768;
+    }
+    // row tables in 64 KB regions after them: a full row each when there are enough regions
+    // (2 without 3-bit tables, 1 with: 128 KB in all), else the first two share a region's
+    // rows in 128-byte halves
+    struct Row {
         uint32_t* off;
-    } t[3];
+        uint32_t* rep;
+        uint32_t es;
+    } rt[3];
     int n = 0;
-    if (ss) t[n++] = {ss, lds_sign};
-    else *lds_sign = 0;
-    if (!kfixed) t[n++] = {ks, lds_k};
-    if (!v2 && !share) t[n++] = {vs, lds_v};
-    for (int i = 0; i < n; ++i)
-        for (int j = i + 1; j < n; ++j)
-            if (t[j].size > t[i].size) {
-                T x = t[i];
-                t[i] = t[j];
-                t[j] = x;
-            }
-    for (int i = 0; i < n; ++i) place(t[i].off, t[i].size);
-    if (share && !v2) *lds_v = *lds_k;
-    *lds_scratch = (uint32_t)end;  // 512 bytes: pairs of 3-bit fields while the quad tables are built
-    *total = end + 512;
+    if (kb != 3) rt[n++] = {&l->k, &l->rep_k, kb == 2 ? 8u : 4u};
+    if (vb != 3 && !share) rt[n++] = {&l->v, &l->rep_v, vb == 2 ? 8u : 4u};
+    if (kq) rt[n++] = {&l->sign, &l->rep_s, 4u};
+    const int regions = end3 ? 1 : 2;
+    const int halves = n > regions ? 2 : 0;
+    uint32_t reg = end3 ? 65536u : 0u;
+    for (int i = 0; i < n; ++i) {
+        if (i < halves) {
+            *rt[i].off = reg + 128u * (uint32_t)(i & 1);
+            *rt[i].rep = 128u / rt[i].es - 1u;
+            if (i & 1) reg += 65536u;
+        } else {
+            *rt[i].off = reg;
+            *rt[i].rep = 256u / rt[i].es - 1u;
+            reg += 65536u;
+        }
+    }
+    if (share) {
+        l->v = l->k;
+        l->rep_v = l->rep_k;
+    }
+    // 512 bytes of scratch (pairs of 3-bit fields while a quad table is built): the hole
+    // between one 3-bit table and the row regions, else at the end
+    const uint32_t end = n ? reg : end3;
+    l->scratch = (end3 == 32768 && n) ? 32768u : end;
+    l->total = (size_t)(end > l->scratch + 512 ? end : l->scratch + 512);
+}
+
+int tq_decode_fast_lds_attr(const void* kern) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    static std::mutex mu;
+    static std::set<std::pair<const void*, int>> done;
+    std::lock_guard<std::mutex> lk(mu);
+    if (done.count({kern, dev})) return TQ_OK;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kTqFastLdsMax);
+    if (e != hipSuccess) return (int)e;
+    done.insert({kern, dev});
+    return TQ_OK;
+}
+
+int tq_decode_fast_wg_waves(int kb, bool kq, int vb, size_t lds_bytes) {
+    (void)kb;
+    (void)vb;
+    const int cu_waves = kq ? fast_wg_waves<2, true, 2>() : fast_wg_waves<2, false, 2>();
+    // workgroups whose tables fit a compute unit's LDS together, a divisor of its waves
+    int wgs = lds_bytes ? (int)(kTqLdsPerCu / lds_bytes) : 4;
+    wgs = wgs < 1 ? 1 : wgs > 4 ? 4 : wgs;
+    while (cu_waves % wgs) --wgs;
+    return cu_waves / wgs;
 }
 
 int tq_decode_fast_launch(const FastDecodeParams& prm, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream) {
     const void* kern = tq_decode_fast_kernel_ptr(kb, kq, vb, !prm.sparse ? 0 : prm.skip_stats ? 2 : 1, prm.addr);
     if (!kern) return TQ_ERR_BITS;
+    const int arc = tq_decode_fast_lds_attr(kern);
+    if (arc) return arc;
     FastDecodeParams p = prm;
     void* args[] = {&p};
-    hipError_t le = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(256), args, lds_bytes, stream);
+    const unsigned threads = 64u * (unsigned)tq_decode_fast_wg_waves(kb, kq, vb, lds_bytes);
+    hipError_t le = hipLaunchKernel(kern, dim3((unsigned)grid), dim3(threads), args, lds_bytes, stream);
     if (le != hipSuccess) return (int)le;
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TQ_OK : (int)e;

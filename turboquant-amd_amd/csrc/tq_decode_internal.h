@@ -51,7 +51,8 @@ struct FastDecodeParams {
     const float* v_cent;
     float k_cscale, v_cscale, v_cinv;
     uint32_t lds_sign, lds_k, lds_v;  // byte offsets of the LDS tables
-    uint32_t lds_scratch;             // 512-byte scratch after the tables
+    uint32_t rep_s, rep_k, rep_v;     // row tables: replicas - 1 (a power of two minus one)
+    uint32_t lds_scratch;             // 512 bytes of scratch (3-bit quad tables' build)
     int block_size, tile_shift;       // block_size = 16 << tile_shift
     int64_t num_blocks;
     const int32_t* bt;
@@ -103,12 +104,28 @@ constexpr int64_t kTqStreamBytes = 256ll << 20;
 // (0), on (1), on with skip statistics (2).
 const void* tq_decode_fast_kernel_ptr(int kb, bool kq, int vb, int spv = 0, int addr = TQ_ADDR_CACHED);
 
-// LDS byte offsets of the fp4 sign table, the K and the V tables, a 512-byte scratch, and the
-// total.
-void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, uint32_t* lds_sign, uint32_t* lds_k,
-                               uint32_t* lds_v, uint32_t* lds_scratch, size_t* total);
+// LDS layout of decode_fast_kernel / decode_contig_kernel: byte offsets of the fp4 sign table,
+// the K and the V tables and a 512-byte scratch, the replica counts - 1 of the row tables (2-bit
+// quads, 4-bit pairs, signs; 0 for a 3-bit quad table), and the total (at most kTqFastLdsMax).
+struct FastLdsLayout {
+    uint32_t sign, k, v, scratch;
+    uint32_t rep_s, rep_k, rep_v;
+    size_t total;
+};
+constexpr size_t kTqFastLdsMax = 131584;  // 128 KB of tables + the scratch
+void tq_decode_fast_lds_layout(int kb, bool kq, int vb, bool share, FastLdsLayout* l);
 
-// Launch decode_fast_kernel (grid of 256-thread workgroups, 4 work units each).
+// Waves per workgroup of the fast kernels for tables of lds_bytes: the compute unit's resident
+// waves (4 x waves per SIMD) split over as many workgroups as the LDS (kTqLdsPerCu) holds.
+constexpr size_t kTqLdsPerCu = 163840;
+int tq_decode_fast_wg_waves(int kb, bool kq, int vb, size_t lds_bytes);
+
+// Raise a fast kernel instance's dynamic-LDS limit to kTqFastLdsMax on the current device (once
+// per instance and device).
+int tq_decode_fast_lds_attr(const void* kern);
+
+// Launch decode_fast_kernel (grid of workgroups of tq_decode_fast_wg_waves(..., lds_bytes)
+// waves, one work unit or worker each).
 int tq_decode_fast_launch(const FastDecodeParams& p, int kb, bool kq, int vb, int64_t grid, size_t lds_bytes,
                           hipStream_t stream);
 
