@@ -235,7 +235,11 @@ void packed_compress_mfma_kernel(PackedParams p) {
             for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float xn = (float)((double)xv[ks][e] * inv);
+                    // x_n rounded to fp32 first (the hi part is then one fp32 -> fp16 conversion;
+                    // left to itself the compiler turns fp64 -> fp32 -> fp16 into a software
+                    // fp64 -> fp16 rounding of ~25 instructions per element)
+                    float xn = (float)((double)xv[ks][e] * inv);
+                    asm("" : "+v"(xn));
                     const _Float16 h = (_Float16)xn;
                     bh[rt][ks][e] = h;
                     bl[rt][ks][e] = (_Float16)(xn - (float)h);
