@@ -78,6 +78,14 @@ __device__ __forceinline__ uint32_t or_over_groups(uint32_t x) {
     auto b = __builtin_amdgcn_permlane16_swap(y, y, false, false);
     return b[0] | b[1];
 }
+// Element 2g + h of the 8 (lane group g = 0..3, h = 0, 1) by selects: an array indexed by the
+// lane's group would be kept in scratch memory.
+template <typename T>
+__device__ __forceinline__ T pick_group(const T (&a)[8], int g, int h) {
+    const T x01 = g == 1 ? a[2 + h] : a[h];
+    const T x23 = g == 3 ? a[6 + h] : a[4 + h];
+    return g >= 2 ? x23 : x01;
+}
 __device__ __forceinline__ float sum_over_groups(float x) {
     auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
@@ -364,10 +372,12 @@ void packed_compress_mfma_kernel(PackedParams p) {
             if (row < p.n_rows) {
                 // lane group g stores column blocks 2g and 2g + 1: 4 BITS bytes at byte 4 g BITS
                 uint32_t w[BITS];
-                const uint64_t s0 = BITS > 2 ? ((uint64_t)seg[2 * g][0] | ((uint64_t)seg[2 * g][BITS > 2 ? 1 : 0] << 32))
-                                             : seg[2 * g][0];
-                const uint64_t s1 = BITS > 2 ? ((uint64_t)seg[2 * g + 1][0] | ((uint64_t)seg[2 * g + 1][BITS > 2 ? 1 : 0] << 32))
-                                             : seg[2 * g + 1][0];
+                uint64_t sg64[8];
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb)
+                    sg64[cb] = BITS > 2 ? ((uint64_t)seg[cb][0] | ((uint64_t)seg[cb][BITS > 2 ? 1 : 0] << 32)) : seg[cb][0];
+                const uint64_t s0 = pick_group(sg64, g, 0);
+                const uint64_t s1 = pick_group(sg64, g, 1);
                 // two 16 BITS-bit segments -> 32 BITS bits
                 if (BITS == 1) {
                     w[0] = (uint32_t)(s0 & 0xffffu) | ((uint32_t)(s1 & 0xffffu) << 16);
@@ -434,7 +444,7 @@ void packed_compress_mfma_kernel(PackedParams p) {
                     seg[cb] = or_over_groups(f << (4 * g));
                 }
                 if (row < p.n_rows) {
-                    reinterpret_cast<uint32_t*>(p.signs_out + row * 16)[g] = seg[2 * g] | (seg[2 * g + 1] << 16);
+                    reinterpret_cast<uint32_t*>(p.signs_out + row * 16)[g] = pick_group(seg, g, 0) | (pick_group(seg, g, 1) << 16);
                     if (g == 0) p.rnorm_out[row] = (uint16_t)tq_f32_to_f16_bits(rnorm[rt]);
                 }
             }
