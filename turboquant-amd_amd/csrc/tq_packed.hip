@@ -183,7 +183,8 @@ void packed_compress_mfma_kernel(PackedParams p) {
     // idx = #{b <= v} and whether some boundary lies within the threshold of v, from the signs
     // and magnitudes of v - b (integer arithmetic: no compare-and-select chains)
     const float near_thr = __uint_as_float(near_bits);
-    auto quantize = [&](float v, uint32_t& k, bool& nb) {
+    // near: (nearest boundary distance) - threshold, negative within the band
+    auto quantize = [&](float v, uint32_t& k, float& near) {
         uint32_t neg = 0;
         float m = __builtin_huge_valf();
 #pragma unroll
@@ -193,7 +194,7 @@ void packed_compress_mfma_kernel(PackedParams p) {
             m = __builtin_fminf(m, __builtin_fabsf(d));
         }
         k = NB - neg;
-        nb = m <= near_thr;
+        near = m - near_thr;
     };
 
     const int lane = tid & 63;
@@ -299,12 +300,15 @@ void packed_compress_mfma_kernel(PackedParams p) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     uint32_t k;
-                    bool nb;
-                    quantize(acc[rt][cb][r], k, nb);
+                    float nr;
+                    quantize(acc[rt][cb][r], k, nr);
                     kf[8 * rt + cb] |= k << (BITS * r);
-                    nearw[rt] |= nb ? (1u << (4 * cb + r)) : 0u;
+                    // shift the sign bit of nr in at bit 0 (one funnel shift): after the 32
+                    // elements, element 4 cb + r of the tile sits at bit 31 - (4 cb + r)
+                    nearw[rt] = __builtin_amdgcn_alignbit(nearw[rt], __float_as_uint(nr), 31);
                 }
             }
+            nearw[rt] = __builtin_bitreverse32(nearw[rt]);  // element e at bit e
             if (row0 + 16 * rt + n >= p.n_rows) nearw[rt] = 0;
         }
         uint64_t near = nearw[0] | (kRT > 1 ? ((uint64_t)nearw[kRT > 1 ? 1 : 0] << 32) : 0ull);
