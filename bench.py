@@ -530,9 +530,11 @@ def profiled_traffic():
     """HBM bytes per launch of the headline decode kernel (two rocprofv3 --pmc runs of this script
     with --copy-calibration, FETCH_SIZE and WRITE_SIZE scaled by two kernels of known traffic)."""
     v = profile_value("decode_fast_kernel_config4_pmc.md", "traffic_bytes_per_launch")
-    return (int(v), "profiles/decode_fast_kernel_config4_pmc.md (FETCH_SIZE x1.91 + WRITE_SIZE x0.955, calibrated on "
-                    "a 256 MiB copy in the same profiled process)") \
-        if v is not None else (None, None)
+    fs = profile_value("decode_fast_kernel_config4_pmc.md", "fetch_scale")
+    ws = profile_value("decode_fast_kernel_config4_pmc.md", "write_scale")
+    return (int(v), f"profiles/decode_fast_kernel_config4_pmc.md (FETCH_SIZE x{fs:g} + WRITE_SIZE x{ws:g}, calibrated on "
+                    "a 256 MiB copy and multiply in the same profiled process)") \
+        if v is not None and fs is not None and ws is not None else (None, None)
 
 
 def cpu_info():
