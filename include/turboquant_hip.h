@@ -398,6 +398,16 @@ int tq_decode_noalloc(const void* q, int q_dtype, int64_t q_stride_seq, int64_t 
 int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int num_q_heads, int num_kv_heads,
                                int norm_row_bytes, int share_codebook, int* units);
 
+/* Waves per workgroup of the kernel tq_decode picks for this configuration: consecutive work
+ * units (fixed chunks: (sequence, chunk, KV head) order) share a workgroup, and the dispatcher
+ * deals workgroups to the XCDs and their shader engines in turn.  Callers that know the
+ * sequence lengths use it to keep every shader engine within one round of resident workgroups
+ * when they choose tokens_per_chunk.  No counterpart in the reference (its Triton launcher has
+ * fixed programs, kernels/attention.py:202-211).  Same arguments and checks as
+ * tq_decode_concurrent_units. */
+int tq_decode_workgroup_waves(int k_bits, int k_qjl, int v_bits, int num_q_heads, int num_kv_heads,
+                              int norm_row_bytes, int share_codebook, int* waves);
+
 /* ---- packing helpers ----------------------------------------------------------- */
 
 /* Reorder sign rows [n_rows, 16] natural -> stride-4 permuted (out bit 32c+k = in bit 4k+c).

@@ -276,6 +276,26 @@ def test_compute_entry_points_refuse_cpu_tensors():
         polarquant_compress(torch.randn(4, 128), c, b, PolarQuantConfig(), make_wht_matrix(128))
 
 
+def test_chunk_engine_load_matches_brute_force():
+    """chunk_engine_load (per-sequence ranges of workgroups, residues counted arithmetically)
+    against enumerating every busy unit."""
+    import random
+    from collections import Counter
+    from turboquant.kernels.paged import chunk_engine_load
+    rng = random.Random(7)
+    for _ in range(40):
+        S, hkv, wgw = rng.randint(1, 20), rng.choice([1, 2, 4, 8]), rng.choice([3, 4, 6, 8, 12, 16])
+        tiles = [rng.randint(0, 90) for _ in range(S)]
+        tmax = max(1, max(tiles))
+        ct = rng.randint(1, tmax)
+        n = -(-tmax // ct)
+        busy = {((s * n + ci) * hkv + kh) // wgw for s, t in enumerate(tiles) for ci in range(-(-t // ct))
+                for kh in range(hkv)}
+        want = max(Counter(b % 32 for b in busy).values()) if busy else 0
+        got = chunk_engine_load(tiles, tmax, ct, hkv, wgw) if busy else 0
+        assert got == want, (tiles, ct, hkv, wgw)
+
+
 def test_paged_format_geometry():
     from turboquant.kernels.paged import PagedKVFormat, choose_tokens_per_chunk
     f = PagedKVFormat(bits=3, qjl=True, block_size=16)
@@ -363,12 +383,14 @@ def test_chunk_planner_picks_balanced_beyond_one_round(monkeypatch):
     cpu = torch.device("cpu")
     assert plan_tokens_per_chunk(cpu, 64, 64, 8, 131072, kf2, vf2) == 0      # lengths unknown
     monkeypatch.setattr(paged, "concurrent_units", lambda dev, kb, *a: 3072 if kb != 4 else 4096)
+    monkeypatch.setattr(paged, "workgroup_waves", lambda dev, kb, kq, *a: 12 if kq else 8)
     r5 = random.Random(5)
     lens5 = [int(round(math.exp(r5.uniform(math.log(2048), math.log(131072))))) for _ in range(64)]
     assert plan_tokens_per_chunk(cpu, 64, 64, 8, max(lens5), kf2, vf2, seq_lens_host=lens5) == 0
     r3 = random.Random(3)
     lens3 = [r3.randint(1024, 8192) for _ in range(32)]
-    assert plan_tokens_per_chunk(cpu, 32, 32, 8, max(lens3), kf4, vf4, seq_lens_host=lens3) > 0
+    # config 3: the shortest chunk that leaves a slot free on every shader engine
+    assert plan_tokens_per_chunk(cpu, 32, 32, 8, max(lens3), kf4, vf4, seq_lens_host=lens3) == 384
     assert plan_tokens_per_chunk(cpu, 64, 48, 8, 32768, kf3, vf3, seq_lens_host=[32768] * 64) == 5472
 
 

@@ -6,7 +6,7 @@
 
 #include "turboquant_hip.h"
 
-#define TQ_ABI_VERSION 3
+#define TQ_ABI_VERSION 4
 #define TQ_HEAD_DIM 128
 #define TQ_WAVE 64
 

@@ -1132,6 +1132,23 @@ extern "C" int tq_decode_concurrent_units(int k_bits, int k_qjl, int v_bits, int
     return TQ_OK;
 }
 
+extern "C" int tq_decode_workgroup_waves(int k_bits, int k_qjl, int v_bits, int num_q_heads, int num_kv_heads,
+                                         int norm_row_bytes, int share_codebook, int* waves) {
+    if (!waves) return TQ_ERR_INVALID_ARGUMENT;
+    if (k_bits < 2 || k_bits > 4 || v_bits < 2 || v_bits > 4) return TQ_ERR_BITS;
+    if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return TQ_ERR_GQA;
+    const int group = num_q_heads / num_kv_heads;
+    if (group > 16) return TQ_ERR_GQA;
+    *waves = 4;  // decode_kernel: 256-thread workgroups
+    if (norm_row_bytes == 2 && group <= 8) {
+        const int share = (share_codebook && k_bits == v_bits) ? 1 : 0;
+        FastLdsLayout lay;
+        tq_decode_fast_lds_layout(k_bits, k_qjl != 0, v_bits, share != 0, &lay);
+        *waves = tq_decode_fast_wg_waves(k_bits, k_qjl != 0, v_bits, lay.total);
+    }
+    return TQ_OK;
+}
+
 // rotate: q (and q_proj when it is q) enter as q x H, the output leaves as out x H.
 // Shared by tq_decode, tq_decode_rotated and the fixed-scratch variant (tq_decode_internal.h).
 int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,

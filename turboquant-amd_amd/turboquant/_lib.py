@@ -18,7 +18,7 @@ import torch
 
 LIB_NAME = "libturboquant_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / "lib" / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 HEAD_DIM = 128
 
 TQ_F32, TQ_F16, TQ_BF16, TQ_I32, TQ_I64 = 0, 1, 2, 3, 4
@@ -142,6 +142,7 @@ SIGNATURES = {
          _f32, _f32, _f32, _i32, _vp, _i32, _i64, _i64, _vp, _vp],
     ),
     "tq_decode_concurrent_units": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
+    "tq_decode_workgroup_waves": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
     "tq_polarquant_compress_matrix": (
         _i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_compress_packed": (

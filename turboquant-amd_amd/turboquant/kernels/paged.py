@@ -31,6 +31,9 @@ from turboquant import _lib
 from turboquant.core.rotation import wht_scale
 
 MI355X_CUS = 256
+# The dispatcher deals workgroups to the 8 XCDs in turn and, within an XCD, to its 4 shader
+# engines in turn: workgroup b runs on shader engine (b % 8, (b // 8) % 4), i.e. b % 32.
+MI355X_SE_SLOTS = 32
 
 
 _LAYOUTS = {"rows": 0, "keys": 1, "values": 2}
@@ -339,10 +342,77 @@ def plan_tokens_per_chunk(device: torch.device, num_seqs: int, num_q_heads: int,
     overhead = 14.0 + group * 1024.0 / tile_bytes
     slots = concurrent_units(device, k_fmt.bits, k_fmt.qjl, v_fmt.bits, num_q_heads, num_kv_heads,
                              norm_row_bytes, share_codebook)
-    chunk = choose_tokens_per_chunk(num_seqs, num_kv_heads, max_seq_len, slots, seq_lens_host, overhead)
     msl = max(1, max_seq_len)
+    tiles = [-(-min(max(int(x), 0), msl) // 16) for x in seq_lens_host]
+    if len(set(tiles)) > 1:
+        # Variable lengths: the shortest chunk (at least 4 tiles) whose busy workgroups leave a
+        # slot free on every shader engine, so that all units run in one round (a unit's time is
+        # its chunk plus its start-up), if that round is not much longer than the balanced
+        # schedule's share per wave (which also pays its pieces' extra start-ups and a longer
+        # merge).  Measured on MI355X, config 3 (8-wave workgroups, 16 slots per engine):
+        # chunks of 384 tokens (15 busy on the fullest engine) 43.3 us, 400 (15) 45.4,
+        # 336 / 352 / 368 (20 / 21 / 17, over) 52.9 / 53.6 / 53.6 us, balanced 47.9 us;
+        # config 5 (one round only with 905-tile chunks against 369-tile shares) balanced.
+        wgw = workgroup_waves(device, k_fmt.bits, k_fmt.qjl, v_fmt.bits, num_q_heads, num_kv_heads,
+                              norm_row_bytes, share_codebook)
+        cap = max(1, slots // max(1, wgw) // MI355X_SE_SLOTS)
+        limit = cap - 1 if cap > 1 else cap
+        tmax = max(1, -(-msl // 16))
+        share = num_kv_heads * sum(tiles) / max(1, slots)
+        for ct in range(min(4, tmax), tmax + 1):
+            if ct + overhead > 1.3 * (share + overhead):
+                break
+            if chunk_engine_load(tiles, tmax, ct, num_kv_heads, wgw) <= limit:
+                return ct * 16
+        return 0
+    chunk = choose_tokens_per_chunk(num_seqs, num_kv_heads, max_seq_len, slots, seq_lens_host, overhead)
     units = num_kv_heads * sum(-(-min(max(int(x), 0), msl) // chunk) for x in seq_lens_host)
     return chunk if units <= slots else 0
+
+
+@functools.lru_cache(maxsize=256)
+def _workgroup_waves(device: int, k_bits: int, k_qjl: bool, v_bits: int, hq: int, hkv: int, norm_row: int,
+                     share: bool) -> int:
+    out = ctypes.c_int(0)
+    with torch.cuda.device(device):
+        _lib.check(_lib.lib().tq_decode_workgroup_waves(k_bits, int(k_qjl), v_bits, hq, hkv, norm_row, int(share),
+                                                        ctypes.byref(out)), "tq_decode_workgroup_waves")
+    return int(out.value)
+
+
+def workgroup_waves(device: torch.device, k_bits: int, k_qjl: bool, v_bits: int, num_q_heads: int,
+                    num_kv_heads: int, norm_row_bytes: int = 2, share_codebook: bool = False) -> int:
+    """Waves (work units) per workgroup of the decode kernel for this configuration."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _workgroup_waves(idx, k_bits, bool(k_qjl), v_bits, num_q_heads, num_kv_heads, norm_row_bytes,
+                            bool(share_codebook))
+
+
+def chunk_engine_load(tiles, tiles_max: int, ct: int, num_kv_heads: int, wg_waves: int,
+                      engines: int = MI355X_SE_SLOTS) -> int:
+    """Busy workgroups on the most loaded shader engine with chunks of ct tiles.
+
+    Units in (sequence, chunk, KV head) order over ceil(tiles_max / ct) chunks per sequence,
+    wg_waves units per workgroup, workgroup b on engine b % engines; a workgroup is busy when
+    one of its units holds tokens (a sequence's busy units are one contiguous range)."""
+    n = -(-tiles_max // ct)
+    cnt = [0] * engines
+    last = -1
+    for s, t in enumerate(tiles):
+        k = -(-t // ct)
+        if k <= 0:
+            continue
+        b0 = max((s * n * num_kv_heads) // wg_waves, last + 1)
+        b1 = ((s * n + k) * num_kv_heads - 1) // wg_waves
+        if b1 < b0:
+            continue
+        full, rem = divmod(b1 - b0 + 1, engines)
+        if full:
+            cnt = [c + full for c in cnt]
+        for j in range(rem):
+            cnt[(b0 + j) % engines] += 1
+        last = b1
+    return max(cnt)
 
 
 def concurrent_units(device: torch.device, k_bits: int, k_qjl: bool, v_bits: int, num_q_heads: int,
