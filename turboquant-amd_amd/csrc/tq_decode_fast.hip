@@ -461,21 +461,28 @@ __device__ __forceinline__ bool chunk_group_busy(const FastDecodeParams& p, int 
 // of fields as half2; 2-bit: the 16 pairs; 4-bit: the 16 values), then every entry is read from
 // there.  Row tables are written with 16-byte stores, consecutive threads along a row (a wave
 // writes 1 KB of consecutive bytes).  Ends with a workgroup barrier.
+// Thread tid's dword of the staging area (K in dwords 0-63, V's own table in 64-127; 0 where
+// unused), loaded at kernel entry so that its round trip overlaps the first length reads.
+template <int KB, int VB>
+__device__ __forceinline__ uint32_t stage_value(const FastDecodeParams& p, int tid) {
+    auto val = [&](auto bits_c, const float* cent, float cs, int x) -> uint32_t {
+        constexpr int bits = decltype(bits_c)::value;
+        if (bits == 3) return tq_pack_half2(cent[x & 7] * cs, cent[x >> 3] * cs);
+        if (x >= 16) return 0u;
+        return bits == 2 ? tq_pack_half2(cent[x & 3] * cs, cent[x >> 2] * cs) : tq_pack_half2(cent[x] * cs, 0.f);
+    };
+    if (tid < 64) return val(std::integral_constant<int, KB>{}, p.k_cent, p.k_cscale, tid);
+    if (tid < 128 && p.lds_v != p.lds_k) return val(std::integral_constant<int, VB>{}, p.v_cent, p.v_cscale, tid - 64);
+    return 0u;
+}
+
 template <int KB, bool KQJL, int VB>
-__device__ __forceinline__ void build_tables(const FastDecodeParams& p, uint32_t* s_lds, int tid) {
+__device__ __forceinline__ void build_tables(const FastDecodeParams& p, uint32_t* s_lds, int tid, uint32_t staged) {
     const int NT = (int)__builtin_amdgcn_workgroup_size_x();
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(s_lds);
     uint32_t* st = s_lds + p.lds_scratch / 4;
     const bool vown = p.lds_v != p.lds_k;
-    auto stage = [&](auto bits_c, const float* cent, float cs, int t) {
-        constexpr int bits = decltype(bits_c)::value;
-        const int x = t & 63;  // entry of this table's staging area
-        if (bits == 3) st[t] = tq_pack_half2(cent[x & 7] * cs, cent[x >> 3] * cs);
-        if (bits == 2 && x < 16) st[t] = tq_pack_half2(cent[x & 3] * cs, cent[x >> 2] * cs);
-        if (bits == 4 && x < 16) st[t] = tq_pack_half2(cent[x] * cs, 0.f);
-    };
-    if (tid < 64) stage(std::integral_constant<int, KB>{}, p.k_cent, p.k_cscale, tid);
-    if (vown && tid >= 64 && tid < 128) stage(std::integral_constant<int, VB>{}, p.v_cent, p.v_cscale, tid);
+    if (tid < 128) st[tid] = staged;
     // row table at base with es-byte entries, rep + 1 replicas; value(e): 16 bytes of entry e
     auto fill_row = [&](uint32_t base, uint32_t es, uint32_t rep, auto value) {
         const int S = (int)(es * (rep + 1) / 16);  // 16-byte stores per row: 8 or 16
@@ -613,6 +620,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     constexpr int AUX = ADDR == TQ_ADDR_CACHED ? 0 : 2;  // buffer-load cache policy: 2 = non-temporal
     extern __shared__ uint32_t s_lds[];
     const int tid = threadIdx.x;
+    const uint32_t staged = stage_value<KB, VB>(p, tid);
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wpg = (int)(__builtin_amdgcn_workgroup_size_x() >> 6);  // waves per workgroup
@@ -672,7 +680,7 @@ void decode_fast_kernel(FastDecodeParams p) {
     } else if (!chunk_group_busy(p, cap, wpg)) {
         return;
     }
-    build_tables<KB, KQJL, VB>(p, s_lds, tid);
+    build_tables<KB, KQJL, VB>(p, s_lds, tid, staged);
 
     const int g = lane >> 4;
     const int n = lane & 15;
@@ -1060,13 +1068,14 @@ void decode_contig_kernel(FastDecodeParams p) {
     static_assert(KB == 2 && KQJL && VB == 2, "row-major decode: 2-bit keys with QJL, 2-bit values");
     extern __shared__ uint32_t s_lds[];
     const int tid = threadIdx.x;
+    const uint32_t staged = stage_value<KB, VB>(p, tid);
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wpg = (int)(__builtin_amdgcn_workgroup_size_x() >> 6);  // waves per workgroup
     const int wv = (int)blockIdx.x * wpg + wave;  // this wave's unit
     const int cap = p.max_blocks * 16;          // rows per sequence in the arrays
     if (!chunk_group_busy(p, cap, wpg)) return;
-    build_tables<KB, KQJL, VB>(p, s_lds, tid);
+    build_tables<KB, KQJL, VB>(p, s_lds, tid, staged);
     const int g = lane >> 4;
     const int n = lane & 15;
     const int hcol = n & 7;
