@@ -398,26 +398,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         tq_half4v bop[kRT];
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) {
-            // tokens 4g + r below lim are usable and visible to the row (lim: one compare per token)
+            // tokens 4g + r below lim are usable and visible to the row (lim: one compare per
+            // token, in the tiles where some lane has one that is not: the diagonal and the
+            // last tile)
             int lim = qposR[rt] - ti * 16 + 1 - 4 * g;
             lim = lim < nv - 4 * g ? lim : nv - 4 * g;
             float sv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float v = __builtin_fmaf(kn1[r], sc[rt][r], kr2[r] * tj[rt][r]);
-                sv[r] = r < lim ? v : kNegInf;
+            for (int r = 0; r < 4; ++r) sv[r] = __builtin_fmaf(kn1[r], sc[rt][r], kr2[r] * tj[rt][r]);
+            if (__builtin_amdgcn_ballot_w64(lim < 4)) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv[r] = r < lim ? sv[r] : kNegInf;
             }
             float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
             mt = max_over_groups(mt);
-            const float m_new = fmaxf(m[rt], mt);
-            if (__builtin_amdgcn_ballot_w64(m_new > m[rt])) {
-                const float alpha = m_new > m[rt] ? __builtin_amdgcn_exp2f(m[rt] - m_new) : 1.f;  // 0 while m = -inf
+            // The exponent base m (per row) moves only when some row's max passes it by more
+            // than one log2 unit; p = exp2(s - m - 1) <= 1, and acc and lsum carry the same
+            // factor, so most tiles skip the rescale.
+            if (__builtin_amdgcn_ballot_w64(mt > m[rt] + 1.0f)) {
+                const float mb = fmaxf(m[rt], mt);
+                // 0 while m = -inf; 1 for a row whose max did not move (also a row that has seen
+                // no visible token yet: -inf - -inf would be NaN)
+                const float alpha = mb == m[rt] ? 1.0f : __builtin_amdgcn_exp2f(m[rt] - mb);
                 lsum[rt] *= alpha;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc[rt][j] *= alpha;
+                m[rt] = mb;
             }
-            m[rt] = m_new;
-            const float nb = m_new == kNegInf ? 0.f : -m_new;
+            const float nb = m[rt] == kNegInf ? 0.f : -m[rt] - 1.0f;
             float pr[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(sv[r] + nb);  // 0 for masked tokens
