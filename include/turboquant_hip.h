@@ -267,6 +267,7 @@ int tq_compress_regions(const void* x, int x_dtype, int64_t x_stride_token, int6
  * denominator.
  * q, q_proj: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
  * out: [num_seqs, num_q_heads, 128] (f32/f16/bf16) at the given element strides.
+ * seq_lens: device int32 [num_seqs], or NULL: every sequence holds max_seq_len tokens.
  * block_tables: int32 [num_seqs, block_table_stride]; entries outside [0, num_blocks) are skipped.
  * max_seq_len: an upper bound of seq_lens (sizes the grid); longer sequences are truncated
  *   (the balanced schedule: to max_seq_len tokens).
@@ -290,6 +291,29 @@ int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride
               void* out, int out_dtype, int64_t out_stride_seq, int64_t out_stride_head,
               unsigned long long* skip_stats,
               tq_stream_t stream);
+
+/*
+ * packed_attention of the reference (kernels/packed_attention.py:290-344) on its own arrays:
+ * split-K decode of one query per head over 2-bit keys with QJL signs and 2-bit values, every
+ * head a sequence of sk rows.  q, q_proj: [bh, 128] rows of q_dtype (f32/f16/bf16; the scores
+ * are not scaled, the caller pre-scales q); k_idx, v_idx: [bh][sk][32] packed 2-bit indices;
+ * k_signs: [bh][sk][16] sign bits (signs_permuted: the stride-4 order of
+ * permute_signs_for_chunked); k_rnorm, k_norm, v_norm: [bh][sk] fp16; centroids: 4 fp32 (K and
+ * V share them) with the table scale of tq_kv_view.centroid_scale (0 means 1); corr_scale the QJL
+ * factor (sqrt(pi/2)/128 in the reference); tokens_per_chunk as for tq_decode (0: the library's
+ * choice; the reference's num_splits corresponds to ceil(sk / num_splits) rounded up to 16);
+ * out: [bh, 128] of out_dtype.  The split combine is the exact (m, l, acc) merge.  Returns
+ * tq_decode's status codes.  Same kernels and results as tq_decode on contiguous regions with
+ * seq_lens = NULL; workspace >= tq_packed_attention_workspace_bytes(bh, sk, tokens_per_chunk),
+ * 256-byte aligned.
+ */
+int tq_packed_attention(const void* q, const void* q_proj, int q_dtype, const uint8_t* k_idx,
+                        const uint8_t* k_signs, int signs_permuted, const uint16_t* k_rnorm,
+                        const uint16_t* k_norm, const uint8_t* v_idx, const uint16_t* v_norm,
+                        const float* centroids, float centroid_scale, float corr_scale, int bh, int sk,
+                        int tokens_per_chunk, void* workspace, size_t workspace_bytes, void* out,
+                        int out_dtype, tq_stream_t stream);
+size_t tq_packed_attention_workspace_bytes(int bh, int sk, int tokens_per_chunk);
 
 /*
  * tq_decode with the query and the output in the original (unrotated) basis: the kernels use

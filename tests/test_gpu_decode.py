@@ -312,7 +312,7 @@ def test_packed_attention_v7_api(dev):
     rng = np.random.default_rng(3)
     cb = _cb(2)
     cs = math.sqrt(math.pi / 2) / math.sqrt(128)
-    for BH, Sk in [(8, 1), (4, 100), (3, 4097)]:
+    for BH, Sk, splits in [(8, 1, None), (4, 100, None), (3, 4097, None), (2, 4096, None), (5, 2048, 7)]:
         ki = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
         ks = rng.integers(0, 256, (BH, Sk, 16), dtype=np.uint8)
         vi = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
@@ -323,7 +323,8 @@ def test_packed_attention_v7_api(dev):
         Qp = (rng.standard_normal((BH, 128)) * 0.1).astype(np.float16)
         t = lambda a: torch.from_numpy(a).to(dev)
         ks_perm = permute_signs_for_chunked(t(ks), 128)
-        out = packed_attention(t(Q), t(Qp), t(ki), ks_perm, t(kr), t(kn), t(vi), t(vn), cb.to(dev), cs)
+        out = packed_attention(t(Q), t(Qp), t(ki), ks_perm, t(kr), t(kn), t(vi), t(vn), cb.to(dev), cs,
+                               num_splits=splits)
         assert out.dtype == torch.float16 and out.shape == (BH, 128)
         got = out.float().cpu().numpy()
         for h in range(BH):
@@ -404,6 +405,37 @@ def test_decode_row_major_arrays(dev, perm, S, Sk, hkv, G, chunk):
                                     cb.double().numpy(), 2)
             want = odec.decode_dense(q[s, hs].astype(np.float64), qp[s, hs].astype(np.float64), k, sg, rn, v, sm, cs)
             np.testing.assert_allclose(got[s, hs], want, rtol=RTOL, atol=ATOL, err_msg=f"seq {s} head {kh}")
+
+
+@pytest.mark.parametrize("layouts,kb,kq,vb,chunk", [(("keys", "values"), 3, True, 3, 64),
+                                                    (("keys", "values"), 2, True, 2, 0),
+                                                    (("rows", "rows"), 4, False, 4, 48)])
+def test_decode_null_seq_lens(dev, layouts, kb, kq, vb, chunk):
+    """seq_lens NULL means every sequence is max_seq_len tokens long: the same bits as a length
+    array of max_seq_len for every sequence, in the lane-grouped fast kernel, the general kernel
+    (row-major tiles) and the split-K merge; and the oracle's answer."""
+    from turboquant.kernels.paged import PagedKVFormat, paged_view, run_decode
+    S, Hq, Hkv, bs, L = 3, 8, 2, 16, 300
+    case = build_case(90 + kb, S, Hq, Hkv, [L] * S, kb, kq, vb, bs, layouts=layouts)
+    sm, cs = 1 / math.sqrt(128), math.sqrt(math.pi / 2) / 128
+    kf = PagedKVFormat(bits=kb, qjl=kq, block_size=bs, layout=layouts[0])
+    vf = PagedKVFormat(bits=vb, qjl=False, block_size=bs, layout=layouts[1])
+    kc, vc = _cb(kb).to(dev), _cb(vb).to(dev)
+    kcache, vcache = torch.from_numpy(case["k_cache"]).to(dev), torch.from_numpy(case["v_cache"]).to(dev)
+    bt = torch.from_numpy(case["bt"]).to(dev)
+    q = torch.from_numpy(case["q"]).to(torch.bfloat16).to(dev)
+    outs = []
+    for lens in (torch.from_numpy(case["seq_lens"]).to(dev), None):
+        out = torch.full((S, Hq, 128), float("nan"), dtype=torch.bfloat16, device=dev)
+        run_decode(q, paged_view(kcache, kf, kc), paged_view(vcache, vf, vc), num_kv_heads=Hkv, block_size=bs,
+                   num_blocks=kcache.shape[0], block_tables=bt, max_blocks_per_seq=bt.shape[1], seq_lens=lens,
+                   max_seq_len=L, sm_scale=sm, corr_scale=cs, q_proj=None, sparse_threshold=0.0,
+                   tokens_per_chunk=chunk, out=out, workspace=None, skip_stats=None, keep_alive=(kc, vc))
+        torch.cuda.synchronize()
+        outs.append(out.float().cpu().numpy())
+    assert np.array_equal(outs[0], outs[1])
+    want, _, _ = oracle_out(case, Hq, Hkv, kb, kq, vb, sm, cs, q_round=q.float().cpu().numpy().astype(np.float64))
+    np.testing.assert_allclose(outs[1], want, rtol=RTOL, atol=ATOL)
 
 
 def _skip_allowance(margins, thresh, delta=2e-3):

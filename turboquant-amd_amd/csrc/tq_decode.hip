@@ -64,7 +64,8 @@ struct DecodeParams {
     const int32_t* bt;
     int64_t bt_stride;
     int max_blocks;
-    const int32_t* seq_lens;
+    const int32_t* seq_lens;  // null: every sequence holds uniform_len tokens
+    int uniform_len;
     float q_scale;     // sm_scale * log2(e) / k_cscale  (MSE operand)
     float qp_scale;    // sm_scale * log2(e)             (QJL operand)
     float corr_scale;
@@ -488,7 +489,7 @@ void decode_kernel(DecodeParams p) {
     const int64_t s = sc / p.n_chunks;
     if (s >= p.num_seqs) return;
 
-    int L = p.seq_lens[s];
+    int L = tq_seq_len(p.seq_lens, s, p.uniform_len);
     const int cap = p.max_blocks * p.block_size;
     L = L < cap ? L : cap;
     const int t_begin = c * p.chunk;
@@ -768,7 +769,8 @@ struct ReduceParams {
     const float* ws_m;
     const float* ws_l;
     int num_seqs, hq, n_chunks, chunk, cap;
-    const int32_t* seq_lens;
+    const int32_t* seq_lens;  // null: every sequence holds uniform_len tokens
+    int uniform_len;
     void* out;
     int out_dtype;
     int64_t out_ss, out_sh;
@@ -809,7 +811,7 @@ __global__ __launch_bounds__(64 * W) void decode_reduce_kernel(ReduceParams p) {
     int nch;
     int64_t base, stride;  // partial row of the first piece, rows between pieces
     if (!p.balanced) {
-        int L = p.seq_lens[s];
+        int L = tq_seq_len(p.seq_lens, s, p.uniform_len);
         L = L < p.cap ? L : p.cap;
         nch = L > 0 ? (L + p.chunk - 1) / p.chunk : 0;
         nch = nch < p.n_chunks ? nch : p.n_chunks;  // tokens past max_seq_len were not processed
@@ -819,7 +821,7 @@ __global__ __launch_bounds__(64 * W) void decode_reduce_kernel(ReduceParams p) {
     } else {
         // the workers w0..w1 that hold segment (s, kh): partial slots w0 + g .. w1 + g
         const int kh = h / p.group;
-        const int np = tq_bal_pairs(p.seq_lens[s], p.len_cap);
+        const int np = tq_bal_pairs(tq_seq_len(p.seq_lens, s, p.uniform_len), p.len_cap);
         nch = 0;
         base = 0;
         stride = p.group;
@@ -949,8 +951,8 @@ bool q_vector_ok(const void* q, int dtype, int64_t ss, int64_t sh) {
 }
 
 int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num_q_heads, int n_chunks, int chunk,
-                  int cap, const int32_t* seq_lens, void* out, int out_dtype, int64_t out_ss, int64_t out_sh,
-                  int rot_out, hipStream_t st, const FastDecodeParams* bal = nullptr) {
+                  int cap, const int32_t* seq_lens, int uniform_len, void* out, int out_dtype, int64_t out_ss,
+                  int64_t out_sh, int rot_out, hipStream_t st, const FastDecodeParams* bal = nullptr) {
     ReduceParams rp = {};
     if (bal) {
         rp.balanced = 1;
@@ -971,6 +973,7 @@ int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num
     rp.chunk = chunk;
     rp.cap = cap;
     rp.seq_lens = seq_lens;
+    rp.uniform_len = uniform_len;
     rp.out = out;
     rp.out_dtype = out_dtype;
     rp.out_ss = out_ss;
@@ -1178,7 +1181,8 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     if (out_dtype != TQ_F32 && out_dtype != TQ_F16 && out_dtype != TQ_BF16) return TQ_ERR_DTYPE;
     if (max_blocks_per_seq < 0 || num_blocks < 0) return TQ_ERR_INVALID_ARGUMENT;
     if (num_seqs == 0) return TQ_OK;
-    if (!q || !seq_lens || !out || !k->centroids || !v->centroids) return TQ_ERR_INVALID_ARGUMENT;
+    if (!q || !out || !k->centroids || !v->centroids) return TQ_ERR_INVALID_ARGUMENT;
+    if (!seq_lens && max_seq_len <= 0) return TQ_ERR_INVALID_ARGUMENT;  // null lengths: max_seq_len each
     if (block_tables && block_table_stride < max_blocks_per_seq) return TQ_ERR_INVALID_ARGUMENT;
     // lane-grouped tiles: keys as TQ_TILE_KEYS, values as TQ_TILE_VALUES, paged, natural sign
     // order, the payload region's row stride = payload bytes per token
@@ -1320,6 +1324,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         f.bt_stride = block_table_stride;
         f.max_blocks = contig ? max_seq_len / 16 : max_blocks_per_seq;  // contiguous: whole tiles up to max_seq_len
         f.seq_lens = seq_lens;
+        f.uniform_len = max_seq_len;
         f.c_exp = sm_scale * kLog2e / k_cscale;
         f.sparse = sparse_threshold > 0.f ? 1 : 0;
         f.sparse_pair = sparse_pair ? 1 : 0;
@@ -1365,7 +1370,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         int frc = tq_decode_fast_launch(f, k->bits, k->qjl != 0, v->bits, grid, lds_total, (hipStream_t)stream);
         if (frc) return frc;
         return launch_reduce(f.ws_acc, f.ws_m, f.ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
-                             max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq,
+                             max_blocks_per_seq * block_size, seq_lens, max_seq_len, out, out_dtype, out_stride_seq,
                              out_stride_head, rotate, (hipStream_t)stream, balanced ? &f : nullptr);
     }
     float* ws_acc = reinterpret_cast<float*>(ws);
@@ -1406,6 +1411,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     p.bt_stride = block_table_stride;
     p.max_blocks = max_blocks_per_seq;
     p.seq_lens = seq_lens;
+    p.uniform_len = max_seq_len;
     p.qp_scale = sm_scale * kLog2e;
     p.q_scale = p.qp_scale / p.k_cscale;
     p.corr_scale = corr_scale;
@@ -1446,8 +1452,54 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     if (e != hipSuccess) return (int)e;
 
     return launch_reduce(ws_acc, ws_m, ws_l, num_seqs, num_q_heads, n_chunks, tokens_per_chunk,
-                         max_blocks_per_seq * block_size, seq_lens, out, out_dtype, out_stride_seq, out_stride_head,
+                         max_blocks_per_seq * block_size, seq_lens, max_seq_len, out, out_dtype, out_stride_seq, out_stride_head,
                          rotate, st);
+}
+
+extern "C" size_t tq_packed_attention_workspace_bytes(int bh, int sk, int tokens_per_chunk) {
+    if (bh <= 0 || sk <= 0 || tokens_per_chunk < 0) return 0;
+    return tq_decode_workspace_bytes(bh, 1, sk, tokens_per_chunk);
+}
+
+extern "C" int tq_packed_attention(const void* q, const void* q_proj, int q_dtype, const uint8_t* k_idx,
+                                   const uint8_t* k_signs, int signs_permuted, const uint16_t* k_rnorm,
+                                   const uint16_t* k_norm, const uint8_t* v_idx, const uint16_t* v_norm,
+                                   const float* centroids, float centroid_scale, float corr_scale, int bh, int sk,
+                                   int tokens_per_chunk, void* workspace, size_t workspace_bytes, void* out,
+                                   int out_dtype, tq_stream_t stream) {
+    if (bh < 0 || sk < 0) return TQ_ERR_INVALID_ARGUMENT;
+    if (bh == 0) return TQ_OK;
+    if (sk == 0 || !q || !q_proj || !k_idx || !k_signs || !k_rnorm || !k_norm || !v_idx || !v_norm || !centroids)
+        return TQ_ERR_INVALID_ARGUMENT;
+    // every head is a sequence of sk rows of its own (one query head per KV head), its rows
+    // following each other: 16-row tiles addressed by stride, no block table
+    const int64_t nblk = ((int64_t)sk + 15) / 16;
+    if (nblk > 0x7fffffff) return TQ_ERR_INVALID_ARGUMENT;
+    auto region = [&](const void* ptr, int64_t row) {
+        return tq_region{ptr, 16 * row, 0, (int64_t)sk * row, row};
+    };
+    tq_kv_view k = {};
+    k.idx = region(k_idx, 32);
+    k.signs = region(k_signs, 16);
+    k.norm = region(k_norm, 2);
+    k.rnorm = region(k_rnorm, 2);
+    k.centroids = centroids;
+    k.bits = 2;
+    k.qjl = 1;
+    k.signs_permuted = signs_permuted ? 1 : 0;
+    k.centroid_scale = centroid_scale;
+    k.layout = TQ_TILE_ROWS;
+    tq_kv_view v = {};
+    v.idx = region(v_idx, 32);
+    v.norm = region(v_norm, 2);
+    v.centroids = centroids;
+    v.bits = 2;
+    v.centroid_scale = centroid_scale;
+    v.layout = TQ_TILE_ROWS;
+    return tq_decode_impl(0, q, q_dtype, TQ_HEAD_DIM, TQ_HEAD_DIM, q_proj, TQ_HEAD_DIM, TQ_HEAD_DIM, bh, 1, 1,
+                          TQ_HEAD_DIM, &k, &v, 16, nblk, nullptr, 0, (int)nblk, nullptr, sk, 1.0f, corr_scale, 0.0f,
+                          tokens_per_chunk, workspace, workspace_bytes, out, out_dtype, TQ_HEAD_DIM, TQ_HEAD_DIM,
+                          nullptr, stream);
 }
 
 extern "C" int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride_head,

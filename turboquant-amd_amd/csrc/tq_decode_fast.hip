@@ -437,7 +437,7 @@ __device__ __forceinline__ bool chunk_unit(int u, const FastDecodeParams& p, int
     ci = t % p.n_chunks;
     s = t / p.n_chunks;
     if (s >= p.num_seqs) return false;
-    L = p.seq_lens[s];
+    L = tq_seq_len(p.seq_lens, s, p.uniform_len);
     L = L < cap ? L : cap;
     return ci * p.chunk < L;
 }
@@ -634,12 +634,12 @@ void decode_fast_kernel(FastDecodeParams p) {
     int bal_s = 0, bal_np = 0;
     if (p.balanced) {
         // the first 64 sequences' pairs and prefix sums are kept for the second pass
-        const uint32_t np0 = lane < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[lane], p.len_cap) : 0u;
+        const uint32_t np0 = lane < p.num_seqs ? (uint32_t)tq_bal_pairs(tq_seq_len(p.seq_lens, lane, p.uniform_len), p.len_cap) : 0u;
         const uint32_t incl0 = wave_incl_scan_u32(np0);
         int64_t tot = (int64_t)__builtin_amdgcn_readlane(incl0, 63);
         for (int b = 64; b < p.num_seqs; b += 64) {
             const int sl = b + lane;
-            const uint32_t np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
+            const uint32_t np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(tq_seq_len(p.seq_lens, sl, p.uniform_len), p.len_cap) : 0u;
             tot += (int64_t)__builtin_amdgcn_readlane(wave_incl_scan_u32(np), 63);
         }
         const int64_t P = tot * p.hkv;
@@ -656,7 +656,7 @@ void decode_fast_kernel(FastDecodeParams p) {
                 const int sl = b + lane;
                 uint32_t np = np0, incl = incl0;
                 if (b > 0) {
-                    np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(p.seq_lens[sl], p.len_cap) : 0u;
+                    np = sl < p.num_seqs ? (uint32_t)tq_bal_pairs(tq_seq_len(p.seq_lens, sl, p.uniform_len), p.len_cap) : 0u;
                     incl = wave_incl_scan_u32(np);
                 }
                 if (planner && sl < p.num_seqs) p.plan[1 + sl] = carry + (int64_t)(incl - np);
@@ -731,7 +731,7 @@ void decode_fast_kernel(FastDecodeParams p) {
         if (bal_pos >= bal_end) break;
         s = bal_s;
         kh = kh_b;
-        L = p.seq_lens[s];
+        L = tq_seq_len(p.seq_lens, s, p.uniform_len);
         L = L < p.len_cap ? L : p.len_cap;
         take = bal_np - pp;
         take = take < bal_end - bal_pos ? take : bal_end - bal_pos;
@@ -1013,7 +1013,7 @@ void decode_fast_kernel(FastDecodeParams p) {
                     bal_pos = bal_end;  // unreachable with the lengths the range was cut from
                     break;
                 }
-                bal_np = tq_bal_pairs(p.seq_lens[bal_s], p.len_cap);
+                bal_np = tq_bal_pairs(tq_seq_len(p.seq_lens, bal_s, p.uniform_len), p.len_cap);
                 if (bal_np > 0) break;
             }
         }

@@ -29,6 +29,12 @@ __host__ __device__ inline int tq_bal_pairs(int len, int len_cap) {
 // kTqBalRowsPerCu * CUs + num_seqs * num_q_heads (sequence, query head) partials.
 constexpr int kTqBalRowsPerCu = 128;  // 16 resident waves per CU x 8 query heads per group
 
+// Length of sequence s: seq_lens[s], or `uniform` when the caller gave no lengths (every sequence
+// holds max_seq_len tokens).
+__device__ __forceinline__ int tq_seq_len(const int32_t* seq_lens, int64_t s, int uniform) {
+    return seq_lens ? seq_lens[s] : uniform;
+}
+
 struct FastDecodeParams {
     const void* q;
     int64_t q_ss, q_sh;
@@ -58,7 +64,8 @@ struct FastDecodeParams {
     const int32_t* bt;
     int64_t bt_stride;
     int max_blocks;
-    const int32_t* seq_lens;
+    const int32_t* seq_lens;  // null: every sequence holds uniform_len tokens
+    int uniform_len;
     float c_exp;     // sm_scale * log2(e) / k_cscale: raw score units -> log2 units
     float thr_log;   // log2(threshold) / c_exp
     int sparse;

@@ -143,6 +143,9 @@ SIGNATURES = {
     ),
     "tq_decode_concurrent_units": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
     "tq_decode_workgroup_waves": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(ctypes.c_int)]),
+    "tq_packed_attention": (_i32, [_vp, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                   ctypes.c_float, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp, _i32, _vp]),
+    "tq_packed_attention_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32]),
     "tq_polarquant_compress_matrix": (
         _i32, [_vp, _i32, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tq_compress_packed": (

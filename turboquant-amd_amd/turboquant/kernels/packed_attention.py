@@ -2,11 +2,11 @@
 
 packed_attention keeps the signature of kernels/packed_attention.py:290-344 and reads the
 same arrays: 2-bit K/V indices [BH, Sk, 32], stride-4 permuted QJL sign rows [BH, Sk, 16],
-fp16 norms / residual norms [BH, Sk].  It calls tq_decode with a "contiguous" view: each of
-the BH query heads is a sequence with its own KV (no GQA), 16-token tiles addressed by stride
-instead of a block table.  For Sk a multiple of 16 the library runs its row-major kernel
-(decode_contig_kernel: the fast kernel's pair loop with loads for these arrays); other Sk go
-through the general decode kernel.
+fp16 norms / residual norms [BH, Sk].  It is one call of the C entry tq_packed_attention, whose
+argument list is the reference function's: each of the BH query heads is a sequence with its
+own KV (no GQA), 16-token tiles addressed by stride instead of a block table.  For Sk a
+multiple of 16 the library runs its row-major kernel (decode_contig_kernel: the fast kernel's
+pair loop with loads for these arrays); other Sk go through the general decode kernel.
 
 Differences from the reference, by design:
   - the split combine is the correct (m, l, acc) merge (kernels/attention.py:121-140), not
@@ -24,7 +24,7 @@ import torch.nn.functional as F
 
 from turboquant import _lib
 from turboquant.kernels.packed_compress import unpack_1bit, unpack_2bit  # noqa: F401  (API parity)
-from turboquant.kernels.paged import MI355X_CUS, run_decode
+from turboquant.kernels.paged import MI355X_CUS, decode_workspace
 
 BLOCK = 16
 
@@ -48,25 +48,6 @@ def _get_config(BH: int, Sk: int):
     return BLOCK, max(1, math.ceil(Sk / chunk)), 4, 1
 
 
-# Read-only [BH] int32 tensors of Sk, one per (device, BH, Sk): a per-call fill would cost a kernel
-# launch and several microseconds of host time on every call.
-_SEQ_LENS: dict = {}
-
-
-def _seq_lens(dev: torch.device, BH: int, Sk: int) -> torch.Tensor:
-    key = (dev.index, BH, Sk)
-    t = _SEQ_LENS.get(key)
-    if t is None:
-        if len(_SEQ_LENS) > 64:
-            _SEQ_LENS.clear()
-        t = _SEQ_LENS[key] = torch.full((BH,), Sk, dtype=torch.int32, device=dev)
-    return t
-
-
-def _contig_region(t: torch.Tensor, row_bytes: int, Sk: int) -> _lib.TQRegion:
-    return _lib.TQRegion(t.data_ptr(), BLOCK * row_bytes, 0, Sk * row_bytes, row_bytes)
-
-
 def packed_attention(Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
                      v_idx_packed, v_norm, centroids, corr_scale,
                      num_splits=None, block_sk=None, num_warps=None, num_stages=None):
@@ -75,13 +56,16 @@ def packed_attention(Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
     Q, Q_proj: [BH, D] (any float dtype; scores are not scaled, the caller pre-scales Q).
     k_signs_packed must be in the permuted order (permute_signs_for_chunked).
     num_splits selects the split count; block_sk / num_warps / num_stages are Triton tuning
-    knobs of the reference and are accepted and ignored.
+    knobs of the reference and are accepted and ignored.  One call of the C entry
+    tq_packed_attention, which takes the reference's argument list.
     """
     dev = _lib.require_gpu("packed_attention", Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
                            v_idx_packed, v_norm, centroids)
     BH, D = Q.shape
     if D != 128:
         raise ValueError("head_dim must be 128")
+    if tuple(Q_proj.shape) != (BH, D):
+        raise ValueError(f"Q_proj must be {(BH, D)}, got {tuple(Q_proj.shape)}")
     Sk = k_r_norm.shape[1]
     shapes = {
         "k_idx_packed": (k_idx_packed, (BH, Sk, D // 4), torch.uint8),
@@ -99,43 +83,30 @@ def packed_attention(Q, Q_proj, k_idx_packed, k_signs_packed, k_r_norm, k_norm,
             t = t.view(torch.uint8)
         if t.dtype != dt:
             raise TypeError(f"{name} must be {dt}")
-        ts[name] = t.contiguous()
+        ts[name] = t if t.is_contiguous() else t.contiguous()
     if centroids.numel() != 4:
         raise ValueError("packed_attention uses a 2-bit codebook (4 centroids)")
-    cb = centroids.to(device=dev, dtype=torch.float32).contiguous()
-    q = Q.reshape(BH, 1, D)
-    if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
-        q = q.float()
-    qp = Q_proj.reshape(BH, 1, D).to(q.dtype)
-    q = q.contiguous()
-    qp = qp.contiguous()
-
-    kv = _lib.TQKVView()
-    kv.idx = _contig_region(ts["k_idx_packed"], D // 4, Sk)
-    kv.signs = _contig_region(ts["k_signs_packed"], D // 8, Sk)
-    kv.norm = _contig_region(ts["k_norm"], 2, Sk)
-    kv.rnorm = _contig_region(ts["k_r_norm"], 2, Sk)
-    kv.centroids = cb.data_ptr()
-    kv.bits, kv.qjl, kv.signs_permuted = 2, 1, 1
-    kv.centroid_scale = _lib.centroid_scale(cb)
-    vv = _lib.TQKVView()
-    vv.idx = _contig_region(ts["v_idx_packed"], D // 4, Sk)
-    vv.norm = _contig_region(ts["v_norm"], 2, Sk)
-    vv.centroids = cb.data_ptr()
-    vv.bits, vv.qjl, vv.signs_permuted = 2, 0, 0
-    vv.centroid_scale = kv.centroid_scale
-
-    seq_lens = _seq_lens(dev, BH, Sk)
-    out = torch.empty((BH, 1, D), dtype=torch.float16, device=dev)
+    cb = centroids
+    if cb.dtype != torch.float32 or cb.device != dev or not cb.is_contiguous():
+        cb = cb.to(device=dev, dtype=torch.float32).contiguous()
+    q = Q if Q.dtype in (torch.float32, torch.float16, torch.bfloat16) else Q.float()
+    qp = Q_proj if Q_proj.dtype == q.dtype else Q_proj.to(q.dtype)
+    q = q if q.is_contiguous() else q.contiguous()
+    qp = qp if qp.is_contiguous() else qp.contiguous()
+    out = torch.empty((BH, D), dtype=torch.float16, device=dev)
     # num_splits given: that many chunks; otherwise the library's choice (for Sk a multiple of 16,
     # the row-major kernel with one round of the resident waves)
     chunk = _chunk_for(BH, Sk, num_splits) if num_splits else 0
-    nblk = math.ceil(Sk / BLOCK)
-    run_decode(q, kv, vv, num_kv_heads=1, block_size=BLOCK, num_blocks=nblk, block_tables=None,
-               max_blocks_per_seq=nblk, seq_lens=seq_lens, max_seq_len=Sk, sm_scale=1.0,
-               corr_scale=float(corr_scale), q_proj=qp, sparse_threshold=0.0, tokens_per_chunk=chunk,
-               out=out, workspace=None, skip_stats=None, keep_alive=(cb, ts))
-    return out.reshape(BH, D)
+    L = _lib.lib()
+    stream = _lib.stream_handle(dev)
+    ws = decode_workspace(dev, L.tq_packed_attention_workspace_bytes(BH, Sk, chunk))
+    rc = L.tq_packed_attention(q.data_ptr(), qp.data_ptr(), _lib.dtype_code(q), ts["k_idx_packed"].data_ptr(),
+                               ts["k_signs_packed"].data_ptr(), 1, ts["k_r_norm"].data_ptr(), ts["k_norm"].data_ptr(),
+                               ts["v_idx_packed"].data_ptr(), ts["v_norm"].data_ptr(), cb.data_ptr(),
+                               _lib.centroid_scale(cb), float(corr_scale), BH, Sk, chunk, ws.data_ptr(), ws.numel(),
+                               out.data_ptr(), _lib.TQ_F16, stream)
+    _lib.check(rc, "tq_packed_attention")
+    return out
 
 
 def attention_unpacked_ref(Q, Q_proj, K_mse_rot, signs_float, k_r_norm, V_mse_rot, corr_scale):

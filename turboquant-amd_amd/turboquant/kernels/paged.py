@@ -497,7 +497,7 @@ def run_decode(
     num_blocks: int,
     block_tables: Optional[torch.Tensor],
     max_blocks_per_seq: int,
-    seq_lens: torch.Tensor,
+    seq_lens: Optional[torch.Tensor],
     max_seq_len: int,
     sm_scale: float,
     corr_scale: float,
@@ -512,7 +512,8 @@ def run_decode(
 ) -> torch.Tensor:
     """Launch tq_decode for q [S, Hq, 128] given ready KV views (shared by all wrappers).
 
-    rotate=True launches tq_decode_rotated: q in the original basis, out returned in it."""
+    rotate=True launches tq_decode_rotated: q in the original basis, out returned in it.
+    seq_lens None: every sequence is max_seq_len tokens long (no length array is read)."""
     dev = q.device
     S, Hq, D = q.shape
     L = _lib.lib()
@@ -531,7 +532,7 @@ def run_decode(
         ctypes.byref(k_view), ctypes.byref(v_view),
         block_size, num_blocks,
         bt_ptr, bt_stride, max_blocks_per_seq,
-        seq_lens.data_ptr(), max_seq_len,
+        _lib.ptr(seq_lens), max_seq_len,
         float(sm_scale), float(corr_scale), float(sparse_threshold),
         tokens_per_chunk,
         workspace.data_ptr(), workspace.numel(),
