@@ -245,6 +245,116 @@ __device__ __forceinline__ void rotate_unscaled(const RawRow<DT>& r, int q, floa
     fmac_dpp32<kDppXor2>(v, (q & 2) ? 1.f : -1.f);
 }
 
+// ---- 16-bit paged rows on the matrix cores ----
+// A wave holds 16 rows; lane l works on row l & 15 with lane group G = l >> 4.  The rotation
+// z^T = H x^T runs as 32 v_mfma_f32_16x16x32 (bf16 / f16 products are exact, fp32 accumulation)
+// with the +-1 matrix as the A operand and the rows as B: lane l's B operand of K step kk is the
+// 16-byte load of row l & 15 at dims 32 kk + 8 G + (0..7), and its output tile t = 2 s + u
+// (s = 0..3, u = 0..1) holds dims 32 s + 8 G + 4 u + (0..3) of that row, in v[4 t .. 4 t + 3].
+// So a lane holds 8 consecutive dims of each 32-dim quarter s: group s of the lane is dims
+// 32 s + 8 G .. + 7.  A[o][in] = (-1)^popcount(o & in) with o = 32 s + 8 (m >> 2) + 4 u + (m & 3)
+// (m = l & 15, A's row) and in = 32 kk + 8 G + j: the sign factors into a per-lane pattern that
+// depends on u only and the lane-uniform (-1)^popcount(s & kk), so four fragments serve all 32
+// products.  Packed bits leave the kernel per quarter: a 4 x 4 transpose across the row's lanes
+// (two permlane32 and two permlane16 swaps per four words) gives lane G the words of dims
+// 32 G .. 32 G + 31, which the tile stores expect.
+typedef __bf16 tq_bf16x8 __attribute__((ext_vector_type(8)));
+template <int DT>
+struct HadamardFrags {
+    tq_u32x4 f[2][2];  // [u][negated]
+};
+template <int DT>
+__device__ __forceinline__ HadamardFrags<DT> hadamard_frags(int lane) {
+    const uint32_t one = DT == TQ_BF16 ? 0x3F80u : 0x3C00u;
+    const int m = lane & 15, g = lane >> 4;
+    const int e0 = __builtin_popcount((m >> 2) & g);
+    HadamardFrags<DT> h;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int pw = 0; pw < 4; ++pw) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int j = 2 * pw + hh;
+                const int e = e0 + __builtin_popcount((m & 3) & (j & 3)) + (u & (j >> 2));
+                w |= (one | ((e & 1) ? 0x8000u : 0u)) << (16 * hh);
+            }
+            h.f[u][0][pw] = w;
+            h.f[u][1][pw] = w ^ 0x80008000u;
+        }
+    return h;
+}
+template <int DT>
+__device__ __forceinline__ tq_floatx4 mfma_rows(const tq_u32x4& a, const tq_u32x4& b, const tq_floatx4& c) {
+    if constexpr (DT == TQ_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(tq_bf16x8, a), __builtin_bit_cast(tq_bf16x8, b),
+                                                       c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(tq_half8, a), __builtin_bit_cast(tq_half8, b), c,
+                                                      0, 0, 0);
+}
+// v <- x H (unscaled) of the lane's row, in the group order above; r.w[kk] = the K step kk operand
+template <int DT>
+__device__ __forceinline__ void rotate_mfma(const RawRow<DT>& r, const HadamardFrags<DT>& h, float (&v)[32]) {
+    tq_floatx4 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] = mfma_rows<DT>(h.f[t & 1][__builtin_popcount((t >> 1) & kk) & 1], r.w[kk], acc[t]);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[4 * t + i] = acc[t][i];
+}
+// A lane's four K-step operands: 16 bytes at dims 32 kk + 8 G of its row (off includes 8 G)
+template <int DT>
+__device__ __forceinline__ void load_raw_groups(const void* base, int64_t off, RawRow<DT>& r) {
+    const tq_u32x4* p = reinterpret_cast<const tq_u32x4*>(static_cast<const uint16_t*>(base) + off);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) r.w[kk] = p[4 * kk];
+}
+// g[s] of lane G (the row's lane groups G = 0..3, 16 lanes apart) becomes g[s] of lane s's
+// slot G: after the two stages lane G slot w holds what lane w held in slot G.
+__device__ __forceinline__ void transpose_groups(uint32_t (&g)[4]) {
+    auto a = __builtin_amdgcn_permlane32_swap(g[0], g[2], false, false);  // lanes 32 apart: slots 0 <-> 2
+    auto b = __builtin_amdgcn_permlane32_swap(g[1], g[3], false, false);
+    g[0] = a[0];
+    g[2] = a[1];
+    g[1] = b[0];
+    g[3] = b[1];
+    auto c = __builtin_amdgcn_permlane16_swap(g[0], g[1], false, false);  // lanes 16 apart: slots 0 <-> 1
+    auto d = __builtin_amdgcn_permlane16_swap(g[2], g[3], false, false);
+    g[0] = c[0];
+    g[1] = c[1];
+    g[2] = d[0];
+    g[3] = d[1];
+}
+// Sum of squares of the row held by the four lanes l, l ^ 16, l ^ 32, l ^ 48 (8-term fma chain
+// per group, then (s0 + s1) + (s2 + s3), then the two cross-lane sums: every lane of the row
+// gets the same bits).
+__device__ __forceinline__ float row_sumsq_groups(const float (&x)[32]) {
+    float s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        s[j] = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s[j] = __builtin_fmaf(x[8 * j + k], x[8 * j + k], s[j]);
+    }
+    const float t = (s[0] + s[1]) + (s[2] + s[3]);
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+template <bool GROUPS>
+__device__ __forceinline__ float row_sumsq_of(const float (&x)[32]) {
+    if constexpr (GROUPS) return row_sumsq_groups(x);
+    else return row_sumsq(x);
+}
+
 // Left searchsorted over NB sorted boundaries (count of boundaries < x) for |x| <= 1 through a
 // table of 256 cells of width 1/128 over [-1, 1] (plus one cell for x = 1): cell k holds
 // c0 = #{b < edge_k - eps} and the one boundary inside [edge_k - eps, edge_k+1 + eps] (or +inf),
@@ -348,6 +458,43 @@ __device__ __forceinline__ void pack_stream(const int (&idx)[32], uint32_t (&w)[
         }
     }
 }
+// The same bytes from the group order of the matrix-core rows: each group's 8 fields packed
+// (8 BITS bits), the groups transposed across the row's lanes, then joined into the stream.
+template <int BITS>
+__device__ __forceinline__ void pack_stream_groups(const int (&idx)[32], uint32_t (&w)[BITS]) {
+    uint32_t g[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        uint32_t t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = (uint32_t)idx[8 * s + k];
+#pragma unroll
+        for (int span = 1, sh = BITS; span < 8; span *= 2, sh *= 2)
+#pragma unroll
+            for (int k = 0; k < 8; k += 2 * span) t[k] = lshl_or(t[k + span], sh, t[k]);
+        g[s] = t[0];
+    }
+    transpose_groups(g);
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w[j] = g[j];
+    } else if constexpr (BITS == 2) {
+        w[0] = lshl_or(g[1], 16, g[0]);
+        w[1] = lshl_or(g[3], 16, g[2]);
+    } else if constexpr (BITS == 1) {
+        w[0] = lshl_or(g[3], 24, lshl_or(g[2], 16, lshl_or(g[1], 8, g[0])));
+    } else {
+        w[0] = lshl_or(g[1], 24, g[0]);
+        w[1] = lshl_or(g[2], 16, g[1] >> 8);
+        w[2] = lshl_or(g[3], 8, g[2] >> 16);
+    }
+}
+// 32 sign bits (bit k of the lane's element k, group order) -> the bits of dims 32 G .. 32 G + 31
+__device__ __forceinline__ uint32_t sign_bits_groups(uint32_t sb) {
+    uint32_t g[4] = {sb & 0xffu, (sb >> 8) & 0xffu, (sb >> 16) & 0xffu, sb >> 24};
+    transpose_groups(g);
+    return lshl_or(g[3], 24, lshl_or(g[2], 16, lshl_or(g[1], 8, g[0])));
+}
 
 // ---- values tile layout ----
 // Chunk 16g + n of a 16-row sub-tile (4 * BITS bytes) holds, at field 4j + r (BITS bits each,
@@ -393,28 +540,33 @@ __device__ __forceinline__ void shl_words(const uint32_t (&a)[BITS], uint32_t s,
     }
 }
 
-// Writes this lane's fields into the values layout.  Rows 4a..4a+3 of a workgroup (lanes
-// 16a'..16a'+15 of one wave) that land on slots 4k..4k+3 fill whole chunks: their slices are
-// exchanged through this wave's part of xchg and each lane stores one chunk.  Any other row
-// sets its own fields with atomic and / or on the chunk words (other rows of the chunk, written
-// by other launches or workgroups, are untouched).
-template <int BITS>
+// Writes this lane's fields into the values layout.  Rows 4a..4a+3 of a workgroup that land on
+// slots 4k..4k+3 fill whole chunks: their slices are exchanged through this group's part of
+// xchg and each lane stores one chunk.  Any other row sets its own fields with atomic and / or on
+// the chunk words (other rows of the chunk, written by other launches or workgroups, are
+// untouched).  Lane layouts: 4 consecutive lanes per row (a group of 4 rows is lanes
+// 16a'..16a'+15 of one wave, slice i of lane q is chunk 4q + i), or GROUPS, the matrix-core
+// rows (row l & 15, lane group q = l >> 4: a group of 4 rows is lanes 4a' + {0..3} + 16 {0..3},
+// slice i of lane q is chunk 4i + q).
+template <int BITS, bool GROUPS>
 __device__ __forceinline__ void store_values(const ValueSlices<BITS>& vs, bool write, int64_t slot, uint8_t* tile,
                                              int64_t r_in_blk, int q, uint32_t* xchg) {
     constexpr int VS = BITS == 3 ? 4 : BITS;  // words per slice in the exchange (b64 / b128 access)
     const int lane = threadIdx.x & 63;
-    const int rr = (threadIdx.x >> 2) & 3;    // row of the lane within its group of 4 rows
-    const int64_t s0 = __shfl(slot, lane & ~12);
+    const int rr = GROUPS ? (lane & 3) : ((threadIdx.x >> 2) & 3);  // row of the lane within its group of 4 rows
+    const int64_t s0 = __shfl(slot, GROUPS ? (lane & 12) : (lane & ~12));
     const bool ok = write && (s0 & 3) == 0 && slot == s0 + rr;
     const uint64_t bal = __builtin_amdgcn_ballot_w64(ok);
-    const bool full = ((bal >> (lane & 48)) & 0xffffull) == 0xffffull;
+    const bool full = GROUPS ? ((bal >> (lane & 12)) & 0x000F000F000F000Full) == 0x000F000F000F000Full
+                             : ((bal >> (lane & 48)) & 0xffffull) == 0xffffull;
     uint8_t* sub = tile + (r_in_blk & ~(int64_t)15) * (16 * BITS);
     const int g = (int)((r_in_blk & 15) >> 2);
     if (full) {
-        uint32_t* gx = xchg + (threadIdx.x >> 4) * (64 * VS);  // this group: [q][i][row][VS]
+        const int grp = GROUPS ? ((threadIdx.x >> 6) * 4 + ((lane & 15) >> 2)) : (threadIdx.x >> 4);
+        uint32_t* gx = xchg + grp * (64 * VS);  // this group: [chunk][row][VS]
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t* d = gx + ((q * 4 + i) * 4 + rr) * VS;
+            uint32_t* d = gx + ((GROUPS ? 4 * i + q : q * 4 + i) * 4 + rr) * VS;
             if (VS == 2) {
                 *reinterpret_cast<tq_u32x2*>(d) = tq_u32x2{vs.w[i][0], vs.w[i][1 % BITS]};
             } else {
@@ -459,7 +611,7 @@ __device__ __forceinline__ void store_values(const ValueSlices<BITS>& vs, bool w
         for (int i = 0; i < 4; ++i) {
             uint32_t b[BITS];
             shl_words<BITS>(vs.w[i], sh, b);
-            uint32_t* ch = reinterpret_cast<uint32_t*>(sub + (16 * g + 4 * q + i) * (4 * BITS));
+            uint32_t* ch = reinterpret_cast<uint32_t*>(sub + (16 * g + (GROUPS ? 4 * i + q : 4 * q + i)) * (4 * BITS));
 #pragma unroll
             for (int k = 0; k < BITS; ++k) {
                 __hip_atomic_fetch_and(ch + k, ~m[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -493,8 +645,15 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
     // 1e-8 in the units of the unscaled rotation (paged mode)
     const float den_eps = (MODE == MODE_PAGED && p.rotate) ? 1e-8f / p.wht_scale : 1e-8f;
 
-    const int q = threadIdx.x & 3;              // dims 32q..32q+31
-    const int row_in_wg = threadIdx.x >> 2;     // 0..63
+    // 16-bit paged rows run on the matrix cores (row l & 15 of the wave, lane group q = l >> 4);
+    // the others keep 4 consecutive lanes per row.  Either way the row's words leave lane q for
+    // dims 32q..32q+31.
+    constexpr bool GR = MODE == MODE_PAGED && DT != TQ_F32;
+    const int lane = threadIdx.x & 63;
+    const int q = GR ? (lane >> 4) : (threadIdx.x & 3);
+    const int row_in_wg = GR ? ((threadIdx.x >> 6) * 16 + (lane & 15)) : (threadIdx.x >> 2);  // 0..63
+    HadamardFrags<DT> hf;
+    if constexpr (GR) hf = hadamard_frags<DT>(lane);
 
     for (int64_t row0 = (int64_t)wg * kRowsPerWG; row0 < p.n_rows; row0 += (int64_t)nwg * kRowsPerWG) {
         const int64_t row = row0 + row_in_wg;
@@ -524,10 +683,12 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
         // Rows that are not written (padding, past the end) read token 0 of head 0, a row of the
         // same launch, and their results are dropped: no separate zero fill.
         int64_t off;
-        if (p.idx32) off = (uint32_t)tok * (uint32_t)p.x_stride_token + (uint32_t)head * (uint32_t)p.x_stride_head + 32u * q;
-        else off = tok * p.x_stride_token + head * p.x_stride_head + 32 * q;
+        const uint32_t lane_off = GR ? 8u * q : 32u * q;
+        if (p.idx32) off = (uint32_t)tok * (uint32_t)p.x_stride_token + (uint32_t)head * (uint32_t)p.x_stride_head + lane_off;
+        else off = tok * p.x_stride_token + head * p.x_stride_head + lane_off;
         RawRow<DT> raw;
-        load_raw<DT>(p.x, off, raw);
+        if constexpr (GR) load_raw_groups<DT>(p.x, off, raw);
+        else load_raw<DT>(p.x, off, raw);
         // the slot goes out with the row (token 0's for rows that are not written, whose result
         // is dropped): its round trip overlaps the row's instead of following the quantisation
         uint32_t slo = 0, shi = 0;
@@ -542,10 +703,14 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
         bool fast;
         if (MODE == MODE_PAGED) {
             // v = z, y = scale z (the rotation's scale h, or 1 without rotation)
-            if (p.rotate) rotate_unscaled<DT>(raw, q, v);
-            else raw_to_float<DT>(raw, v);
+            if (p.rotate) {
+                if constexpr (GR) rotate_mfma<DT>(raw, hf, v);
+                else rotate_unscaled<DT>(raw, q, v);
+            } else {
+                raw_to_float<DT>(raw, v);
+            }
             const float scale = p.rotate ? p.wht_scale : 1.f;
-            const float nz = __builtin_sqrtf(row_sumsq(v));
+            const float nz = __builtin_sqrtf(row_sumsq_of<GR>(v));
             fast = cells && !__builtin_amdgcn_ballot_w64(!(nz < __builtin_huge_valf()));
             if (fast) {
                 // x_n = y / (|y| + 1e-8) = z / (|z| + 1e-8 / scale): decisions on z and this
@@ -557,7 +722,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
             } else {
 #pragma unroll
                 for (int k = 0; k < 32; ++k) v[k] *= scale;
-                norm = __builtin_sqrtf(row_sumsq(v));
+                norm = __builtin_sqrtf(row_sumsq_of<GR>(v));
                 den = norm + 1e-8f;
                 rcp = 1.0f / den;
             }
@@ -587,7 +752,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                     r[k] = __builtin_fmaf(-s_cent[idx[k]], den, v[k]);
                     sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
                 }
-                rn = __builtin_sqrtf(row_sumsq(r)) * (norm / den);
+                rn = __builtin_sqrtf(row_sumsq_of<GR>(r)) * (norm / den);
                 if (norm == 0.f) sbits = 0xffffffffu;  // r = (0 - c) 0 = +-0: sign(0) counts as +1
             }
         } else {
@@ -607,7 +772,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
                     r[k] = (v[k] - s_cent[idx[k]]) * norm;
                     sbits |= (r[k] >= 0.f ? 1u : 0u) << k;
                 }
-                rn = __builtin_sqrtf(row_sumsq(r));
+                rn = __builtin_sqrtf(row_sumsq_of<GR>(r));
             }
         }
 
@@ -646,15 +811,21 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
             }
             uint8_t* tile = p.cache + blk * p.stride_block + head * p.stride_head;
             if (p.tile_layout == TQ_TILE_VALUES) {
-                if (BITS >= 2) store_values<BITS < 2 ? 2 : BITS>(value_slices<BITS < 2 ? 2 : BITS>(idx), write, slot, tile,
-                                                                  r_in_blk, q, s_xchg);
+                if (BITS >= 2)
+                    store_values<BITS < 2 ? 2 : BITS, GR>(value_slices<BITS < 2 ? 2 : BITS>(idx), write, slot, tile,
+                                                          r_in_blk, q, s_xchg);
                 if (write && q == 0)
                     *reinterpret_cast<uint16_t*>(tile + p.off_norm + r_in_blk * p.rs_norm) = (uint16_t)tq_f32_to_f16_bits(norm);
                 continue;
             }
             // this lane's 32 indices: 4 * BITS bytes of the row's little-endian bit stream
             uint32_t w[BITS];
-            pack_stream<BITS>(idx, w);
+            if constexpr (GR) {
+                pack_stream_groups<BITS>(idx, w);
+                if (QJL) sbits = sign_bits_groups(sbits);
+            } else {
+                pack_stream<BITS>(idx, w);
+            }
             if (write) {
                 if (p.tile_layout == TQ_TILE_KEYS) {
                     // chunk (4n + q) of the row's 16-row sub-tile: index bytes, then sign bytes
@@ -697,15 +868,25 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
     }
 }
 
+// Resident waves per SIMD the kernel is compiled for: the matrix-core rows (16-bit paged input)
+// without QJL fit 4 (128 registers: the Hadamard fragments, the accumulators and the row), the
+// others keep the compiler's own choice.
+template <int MODE, int DT, bool QJL>
+constexpr int compress_min_waves() {
+    return (MODE == MODE_PAGED && DT != TQ_F32 && !QJL) ? 4 : 1;
+}
+
 template <int BITS, bool QJL, int MODE, int DT>
-__global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(compress_min_waves<MODE, DT, QJL>(), 8)))
+void compress_kernel(CompressParams p) {
     compress_rows<BITS, QJL, MODE, DT>(p, blockIdx.x, gridDim.x);
 }
 
 // K and V of one layer in one launch (same bits; V without QJL): workgroups [0, gk) take K, the
 // rest V.  One launch instead of two halves the fixed cost of a K + V cache update.
 template <int BITS, bool QJL_K, int DT>
-__global__ __launch_bounds__(256) void compress_kv_kernel(CompressParams pk, CompressParams pv, int gk) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(compress_min_waves<MODE_PAGED, DT, QJL_K>(), 8)))
+void compress_kv_kernel(CompressParams pk, CompressParams pv, int gk) {
     if ((int)blockIdx.x < gk) compress_rows<BITS, QJL_K, MODE_PAGED, DT>(pk, blockIdx.x, gk);
     else compress_rows<BITS, false, MODE_PAGED, DT>(pv, blockIdx.x - gk, gridDim.x - gk);
 }
