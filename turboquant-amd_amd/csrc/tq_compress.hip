@@ -534,7 +534,9 @@ __device__ __forceinline__ void shl_words(const uint32_t (&a)[BITS], uint32_t s,
 #pragma unroll
     for (int k = 0; k < BITS; ++k) {
         if (BITS == 3 && k > 0)
-            o[k] = (uint32_t)(((((uint64_t)a[k]) << 32) | a[k - 1]) >> (32 - s));
+            // (a[k]:a[k-1]) >> (32 - s), one funnel shift (a 64-bit shift of the pair kept the
+            // slices in scratch memory)
+            o[k] = s == 0 ? a[k] : __builtin_amdgcn_alignbit(a[k], a[k - 1], 32 - s);
         else
             o[k] = a[k] << s;
     }

@@ -208,7 +208,8 @@ def dtype_code(t: torch.Tensor | torch.dtype) -> int:
 
 def require_gpu(what: str, *tensors: torch.Tensor) -> torch.device:
     """All tensors must live on one HIP device; returns it."""
-    dev = None
+    first = None
+    idx = -1
     for t in tensors:
         if t is None:
             continue
@@ -217,17 +218,19 @@ def require_gpu(what: str, *tensors: torch.Tensor) -> torch.device:
                 f"{what}: tensors must be on a GPU (turboquant computes with HIP kernels only); "
                 f"got a {t.device} tensor"
             )
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"{what}: tensors on different devices ({dev}, {t.device})")
-    if dev is None:
+        if first is None:
+            first, idx = t, t.get_device()
+        elif t.get_device() != idx:
+            raise ValueError(f"{what}: tensors on different devices ({first.device}, {t.device})")
+    if first is None:
         raise ValueError(f"{what}: no tensor arguments")
-    return dev
+    return first.device
 
 
 def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw hipStream_t of the device's current stream."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -183,9 +183,15 @@ def compress_paged(
     return cache
 
 
+def _f32_on(t: torch.Tensor, dev) -> torch.Tensor:
+    if t.dtype == torch.float32 and t.is_cuda and t.get_device() == dev.index and t.is_contiguous():
+        return t
+    return t.to(device=dev, dtype=torch.float32).contiguous()
+
+
 def _target(x: torch.Tensor, cache: torch.Tensor, fmt: PagedKVFormat, cb, dev, keep: list):
-    cent = cb[0].to(device=dev, dtype=torch.float32).contiguous()
-    bnd = cb[1].to(device=dev, dtype=torch.float32).contiguous()
+    cent = _f32_on(cb[0], dev)
+    bnd = _f32_on(cb[1], dev)
     if cent.numel() != 2 ** fmt.bits or bnd.numel() != 2 ** fmt.bits - 1:
         raise ValueError(f"need {2 ** fmt.bits} centroids and {2 ** fmt.bits - 1} boundaries for bits={fmt.bits}")
     keep += [x, cent, bnd]
