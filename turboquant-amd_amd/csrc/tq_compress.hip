@@ -1,11 +1,12 @@
 // PolarQuant compression kernels for gfx950.
 //
-// One 128-dim row per 4 lanes (32 dims each), so a wave64 works on 16 rows and a 256-thread
-// workgroup on 64 rows.  The Walsh-Hadamard rotation is 5 in-register butterfly stages (dim
-// bits 0-4; for 16-bit inputs the first one is a v_dot2 that also converts to fp32) plus 2
-// cross-lane stages (DPP, no LDS); indices come from an LDS cell table of the boundaries (129
-// cells in the paged kernels, 257 for polarquant_compress; one compare per value); each lane
-// stores its 4 * bits packed bytes at once.
+// A wave64 works on 16 rows and a 256-thread workgroup on 64 rows, 32 dims of a row per lane.
+// 16-bit rows of the paged kernels are rotated on the matrix cores (one row per lane and lane
+// group, rotate_mfma); fp32 rows and polarquant_compress keep 4 consecutive lanes per row and a
+// Walsh-Hadamard rotation of 5 in-register butterfly stages (dim bits 0-4) plus 2 cross-lane
+// stages (DPP, no LDS).  Indices come from an LDS cell table of the boundaries (129 cells in the
+// paged kernels, 257 for polarquant_compress; one compare per value); each lane stores its
+// 4 * bits packed bytes at once.
 // Row math follows turboquant/core/quantizer.py:141-174:
 //   x_rot = x @ H; norm = |x_rot|; x_n = x_rot / (norm + 1e-8); idx = #{b < x_n};
 //   r = (x_n - c[idx]) * norm; rnorm = |r|; sign = r >= 0.
@@ -184,54 +185,20 @@ __device__ __forceinline__ void raw_to_float(const RawRow<DT>& r, float (&v)[32]
         }
 }
 
-// The paged kernels' rotation without its scale: v <- x H (H the +-1 Sylvester matrix), so that
-// y = h v.  The lane's inputs enter multiplied by sigma = (-1)^(q bit 0 + q bit 1); the cross-lane
-// stages then compute own - partner in the lower lane and own + partner in the upper, and each
-// leaves the right sign (a lower lane's partner arrives negated relative to it, stage by stage),
-// so no final negation or scale pass is needed.  16-bit inputs: the first stage (dims bit 0, the
-// two halves of a loaded dword) is one v_dot2_f32 per output with weights sigma (1, 1) and
-// sigma (1, -1), which also does the conversion to fp32.
-template <int DT>
-__device__ __forceinline__ void rotate_unscaled(const RawRow<DT>& r, int q, float (&v)[32]) {
+// The paged kernels' rotation of fp32 rows without its scale: v <- x H (H the +-1 Sylvester
+// matrix), so that y = h v.  The lane's inputs enter multiplied by sigma = (-1)^(q bit 0 + q bit 1);
+// the cross-lane stages then compute own - partner in the lower lane and own + partner in the
+// upper, and each leaves the right sign (a lower lane's partner arrives negated relative to it,
+// stage by stage), so no final negation or scale pass is needed.  (16-bit rows take the
+// matrix-core rotation below.)
+__device__ __forceinline__ void rotate_unscaled_f32(const RawRow<TQ_F32>& r, int q, float (&v)[32]) {
     const bool neg = ((q ^ (q >> 1)) & 1) != 0;
-    if (DT == TQ_F32) {
-        raw_to_float<DT>(r, v);
-        const float sg = neg ? -1.f : 1.f;
+    raw_to_float<TQ_F32>(r, v);
+    const float sg = neg ? -1.f : 1.f;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) v[k] *= sg;
+    for (int k = 0; k < 32; ++k) v[k] *= sg;
 #pragma unroll
-        for (int k = 0; k < 32; k += 2) {
-            const float u = v[k], w = v[k + 1];
-            v[k] = u + w;
-            v[k + 1] = u - w;
-        }
-    } else {
-        // weights (lo, hi) as 16-bit pairs: +1 = 0x3F80 (bf16) / 0x3C00 (f16), sign bit 0x8000
-        const uint32_t one = DT == TQ_BF16 ? 0x3F803F80u : 0x3C003C00u;
-        const uint32_t wp = neg ? (one | 0x80008000u) : one;   // sigma ( 1,  1)
-        const uint32_t wm = wp ^ 0x80000000u;                  // sigma ( 1, -1)
-        // The eight products of one 16-byte word group sit in one asm block that ends in wait
-        // states: a dot2 result read by the next VALU instruction or the one after it was read
-        // stale (measured: a compiler-scheduled read one instruction later gave wrong rotations).
-#define TQ_DOT2_8(OP)                                                                                      \
-    asm(OP " %0, %8, %12, 0\n\t" OP " %1, %8, %13, 0\n\t" OP " %2, %9, %12, 0\n\t" OP " %3, %9, %13, 0\n\t" \
-        OP " %4, %10, %12, 0\n\t" OP " %5, %10, %13, 0\n\t" OP " %6, %11, %12, 0\n\t" OP " %7, %11, %13, 0\n\t" \
-        "s_nop 3"                                                                                          \
-        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7]) \
-        : "v"(w[0]), "v"(w[1]), "v"(w[2]), "v"(w[3]), "v"(wp), "v"(wm))
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const tq_u32x4 w = r.w[i];
-            float o[8];
-            if (DT == TQ_BF16) TQ_DOT2_8("v_dot2_f32_bf16");
-            else TQ_DOT2_8("v_dot2_f32_f16");
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v[8 * i + k] = o[k];
-        }
-#undef TQ_DOT2_8
-    }
-#pragma unroll
-    for (int b = 2; b < 32; b <<= 1) {
+    for (int b = 1; b < 32; b <<= 1) {
 #pragma unroll
         for (int k = 0; k < 32; ++k) {
             if (!(k & b)) {
@@ -707,7 +674,7 @@ __device__ __forceinline__ void compress_rows(const CompressParams& p, int wg, i
             // v = z, y = scale z (the rotation's scale h, or 1 without rotation)
             if (p.rotate) {
                 if constexpr (GR) rotate_mfma<DT>(raw, hf, v);
-                else rotate_unscaled<DT>(raw, q, v);
+                else if constexpr (DT == TQ_F32) rotate_unscaled_f32(raw, q, v);
             } else {
                 raw_to_float<DT>(raw, v);
             }
