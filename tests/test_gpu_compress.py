@@ -365,6 +365,33 @@ def test_compress_paged_16bit(dev, dtype, rotate, bits, qjl, layout, parity_log)
                   parity_log)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("layout", ["keys", "values"])
+def test_compress_paged_16bit_subnormal_rows(dev, dtype, layout):
+    """Rows of subnormal bf16 / fp16 values (all of them, or beside one normal element) and rows
+    near the bottom of the normal range, through the matrix-core rotation: the products keep the
+    subnormal inputs (a flush to zero would zero the row, and every positive element would then
+    fall on the other side of the middle boundary), under the same parity rule."""
+    from turboquant.kernels.paged import PagedKVFormat, allocate_cache, compress_paged
+    T, H, bs, nb = 64, 2, 16, 8
+    g = torch.Generator().manual_seed(21)
+    tiny = torch.finfo(dtype).tiny  # smallest normal
+    x = torch.randn(T, H, 128, generator=g)
+    x[0:16] *= tiny * 0.25          # every element subnormal
+    x[16:32] *= tiny * 0.25
+    x[16:32, :, 5] = 1.0            # one normal element beside subnormals
+    x[32:48] *= tiny * 4.0          # just above the normal range
+    x = x.to(dtype)
+    qjl = layout == "keys"
+    slots = block_order_slots(T, nb, bs, 9)
+    fmt = PagedKVFormat(bits=4 if layout == "values" else 3, qjl=qjl, block_size=bs, layout=layout)
+    cent, bnd = _codebook(fmt.bits)
+    cache = allocate_cache(nb, H, fmt, device=dev)
+    compress_paged(x.to(dev), torch.from_numpy(slots).to(dev), cache, fmt, cent.to(dev), bnd.to(dev), rotate=True)
+    torch.cuda.synchronize()
+    compare_paged(cache, x, slots, fmt, cent, bnd, True)
+
+
 @pytest.mark.parametrize("rotate", [True, False])
 @pytest.mark.parametrize("layout", ["keys", "values"])
 def test_compress_paged_16bit_edge_rows(dev, rotate, layout):
