@@ -44,7 +44,8 @@ constexpr int kOffV = 2 * 16 * kKRow;            // VhatT: 128 rows
 constexpr int kOffN = kOffV + 128 * kVRow;       // kn1[16], kr2[16], vn[16]
 constexpr int kBuf = kOffN + 3 * 16 * 4;         // one tile buffer
 constexpr int kOffTab = 2 * kBuf;                // pair tables: K then V, 256 x 4 bytes each
-constexpr int kLdsBytes = kOffTab + 2 * 1024;
+constexpr int kOffSgn = kOffTab + 2 * 1024;      // sign table: byte b -> 8 fp16 +-1 (16 bytes)
+constexpr int kLdsBytes = kOffSgn + 256 * 16;
 
 struct PrefillParams {
     const void* q;
@@ -127,6 +128,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             tk[tid] = tq_pack_half2(p.k_cent[tid & ((1 << KB) - 1)] * p.k_cs, p.k_cent[tid >> KB] * p.k_cs);
         if (tid < (1 << (2 * VB)))
             tv[tid] = tq_pack_half2(p.v_cent[tid & ((1 << VB) - 1)] * p.v_cs, p.v_cent[tid >> VB] * p.v_cs);
+        if (KQJL) {
+            // sign byte b -> halves j = 0..7: bit j set -> +1 (0x3c00), clear -> -1 (0xbc00)
+            tq_u32x4 h;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                h[k] = (((tid >> (2 * k)) & 1) ? 0x3c00u : 0xbc00u) | ((((tid >> (2 * k + 1)) & 1) ? 0x3c00u : 0xbc00u) << 16);
+            reinterpret_cast<tq_u32x4*>(s_lds + kOffSgn)[tid] = h;
+        }
     }
 
     // ---- this lane's rows: (token i, head gh) of MFMA tile rt, rows 32 wave + 16 rt + n ----
@@ -288,16 +297,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             *reinterpret_cast<tq_u32x4*>(b + tk * kKRow + 16 * pk) = h;
         }
         if (KQJL) {
-            // sign of dim 8pk + j: bit j of byte pk & 3 of the dword (natural bit order)
+            // sign of dim 8pk + j: bit j of byte pk & 3 of the dword (natural bit order); the
+            // byte's 8 fp16 +-1 come from the sign table
             const uint32_t bitsj = (w.sg0 >> (8 * (pk & 3))) & 0xffu;
-            tq_u32x4 h;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                // bit 1 -> +1 (0x3c00), bit 0 -> -1 (0xbc00)
-                const uint32_t lo = ((bitsj >> (2 * k)) & 1u) ? 0x3c00u : 0xbc00u;
-                const uint32_t hi = ((bitsj >> (2 * k + 1)) & 1u) ? 0x3c00u : 0xbc00u;
-                h[k] = lo | (hi << 16);
-            }
+            const tq_u32x4 h = *reinterpret_cast<const tq_u32x4*>(s_lds + kOffSgn + 16 * bitsj);
             *reinterpret_cast<tq_u32x4*>(b + kOffS + tk * kKRow + 16 * pk) = h;
         }
         {
