@@ -8,22 +8,25 @@
 // Workgroup (256 threads, 4 waves) = (sequence s, KV head kh, block of 128 rows); a row is one
 // (new token i, query head of the GQA group) pair, rows ordered token-major, so a workgroup
 // serves 128 / G tokens with all G heads of the group and each K/V tile is dequantised once for
-// all of them.  A wave owns two 16-row MFMA tiles: every LDS fragment it reads feeds two MFMAs.  The cache is walked in 16-token tiles (a tile never spans two blocks).  Per
-// tile the 256 threads dequantise into one of two LDS buffers (8 dims of one token per thread,
-// for the keys and for the values; mappings in the kernel) while the waves compute on the other:
+// all of them.  A wave owns two 16-row MFMA tiles: every LDS fragment it reads feeds two MFMAs.
+// The cache is walked in steps of two 16-token tiles (a tile never spans two blocks).  Per step
+// the 256 threads dequantise the next two tiles into the other of two LDS buffers (each two tile
+// sub-buffers; 8 dims of one token per thread, for the keys and for the values; mappings in the
+// kernel) while the waves compute on this step's:
 //   Khat [16 tok][128] fp16 = c[idx] * cscale       row stride 272 B (16 B pad: no bank clash)
-//   Shat [16 tok][128] fp16 = +-1                    QJL keys only
+//   Shat [16 tok][128] fp16 = +-1                    QJL keys only (sign byte -> LDS table)
 //   VhatT [128 dim][16 tok] fp16 = c[vidx] * cscale  transposed: the PV A operand; row stride
 //                                                    40 B, so the 4 dim rows a wave writes at
 //                                                    once start 16 banks apart
 //   kn1, kr2, vn [16] f32 = norm * c1, rnorm * c2, vnorm (c1, c2 below)
 // Each wave computes for each of its two 16-row tiles (MFMA layout: lane l, n = l % 16, g = l / 16):
-//   S^T [16 tok x 16 rows] = Khat . Q^T     4 x mfma_f32_16x16x32_f16 (B: q row n in registers)
-//   T^T = Shat . QP^T                        4 x mfma_f32_16x16x32_f16 (QJL keys)
-//   lane (n, g) holds tokens 4g + r of row n: s = kn1 * S + kr2 * T (log2 units), masked;
-//   online softmax per row (column) with the maxima and sums reduced over the lane groups;
-//   fp16(p * vnorm) of tokens 4g..4g+3 is exactly the B operand of
-//   O^T [128 x 16 rows] += VhatT . P^T        8 x mfma_f32_16x16x16_f16
+//   S^T [16 tok x 16 rows] = Khat . Q^T     4 x mfma_f32_16x16x32_f16 per tile (B: q row n in registers)
+//   T^T = Shat . QP^T                        4 x mfma_f32_16x16x32_f16 per tile (QJL keys)
+//   lane (n, g) holds tokens 4g + r of row n in each tile: s = kn1 * S + kr2 * T (log2 units),
+//   masked; online softmax per row (column) over the step's 32 keys, the maxima and sums reduced
+//   over the lane groups once per step; fp16(p * vnorm) of tokens 4g..4g+3 of both tiles is
+//   exactly the B operand (k = 8g + i: tile A token 4g + i, i < 4, tile B token 4g + i - 4) of
+//   O^T [128 x 16 rows] += VhatT . P^T        8 x mfma_f32_16x16x32_f16 per step
 // Output: lane (n, g) holds dims 16j + 4g + r of row n, divided by the row's denominator.
 #include "tq_common.h"
 
@@ -43,7 +46,7 @@ constexpr int kVRow = 40;                        // bytes per dim row of VhatT (
 constexpr int kOffV = 2 * 16 * kKRow;            // VhatT: 128 rows
 constexpr int kOffN = kOffV + 128 * kVRow;       // kn1[16], kr2[16], vn[16]
 constexpr int kBuf = kOffN + 3 * 16 * 4;         // one tile buffer
-constexpr int kOffTab = 2 * kBuf;                // pair tables: K then V, 256 x 4 bytes each
+constexpr int kOffTab = 4 * kBuf;                // pair tables: K then V, 256 x 4 bytes each
 constexpr int kOffSgn = kOffTab + 2 * 1024;      // sign table: byte b -> 8 fp16 +-1 (16 bytes)
 constexpr int kLdsBytes = kOffSgn + 256 * 16;
 
@@ -340,14 +343,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
 
     __syncthreads();  // pair tables
-    // Raw data runs two tiles ahead of the compute (two register sets; tile t + 2 is loaded
-    // while tile t is computed and tile t + 1 is dequantised).
+    // Steps of 32 keys (tiles 2j, 2j + 1, in the two sub-buffers of buffer j & 1).  The raw data
+    // of the next step's two tiles is requested at the start of a step and dequantised into the
+    // other buffer at its end.  A tile past the last is staged as an empty one (no loads; zero
+    // norms, finite table values), so a step's second tile never holds stale bits.
     Raw rawA, rawB;
-    if (ntiles > 0) {
-        load_raw(0, rawA);
+    auto load_or_empty = [&](int ti, Raw& w) {
+        if (ti < ntiles) {
+            load_raw(ti, w);
+        } else {
+            w.kw[0] = w.kw[1] = w.vw[0] = w.vw[1] = 0u;
+            w.sg0 = 0u;
+            w.nrm = 0u;
+            w.nv = 0;
+        }
+    };
+    const int nsteps = (ntiles + 1) >> 1;
+    int nvA = 0, nvB = 0;  // usable rows of the current step's tiles
+    if (nsteps > 0) {
+        load_or_empty(0, rawA);
+        load_or_empty(1, rawB);
         store_tile(0, rawA, 0);
+        store_tile(1, rawB, 1);
+        nvA = rawA.nv;
+        nvB = rawB.nv;
     }
-    if (ntiles > 1) load_raw(1, rawB);
     __syncthreads();
 
     float m[kRT], lsum[kRT];
@@ -360,64 +380,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int j = 0; j < 8; ++j) acc[rt][j] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // One tile: ld holds tile ti's raw data (already in LDS) and receives tile ti + 2's; nx holds
-    // tile ti + 1's, dequantised into the other buffer at the end.  Every LDS fragment feeds the
-    // MFMAs of both row tiles.
-    auto step = [&](int ti, Raw& ld, const Raw& nx) {
-        const int buf = ti & 1;
-        const int nv = ld.nv;  // tile ti
-        if (ti + 2 < ntiles) load_raw(ti + 2, ld);
-        const uint8_t* b = s_lds + buf * kBuf;
-        // scores^T: tokens 4g + r of row n
-        tq_floatx4 sc[kRT], tj[kRT];
-#pragma unroll
-        for (int rt = 0; rt < kRT; ++rt) {
-            sc[rt] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
-            tj[rt] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int js = 0; js < nsteps; ++js) {
+        const int cur = 2 * (js & 1);
+        const bool more = js + 1 < nsteps;
+        if (more) {
+            load_or_empty(2 * js + 2, rawA);
+            load_or_empty(2 * js + 3, rawB);
         }
+        const uint8_t* bA = s_lds + cur * kBuf;
+        const uint8_t* bB = bA + kBuf;
+        // scores^T of both tiles: tokens 4g + r of row n, tile A then tile B
+        float sv[kRT][8];
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const tq_half8 a = *reinterpret_cast<const tq_half8*>(
-                b + n * kKRow + 2 * (32 * cc + 8 * g));
+        for (int tt2 = 0; tt2 < 2; ++tt2) {
+            const uint8_t* b = tt2 ? bB : bA;
+            tq_floatx4 sc[kRT], tj[kRT];
 #pragma unroll
-            for (int rt = 0; rt < kRT; ++rt)
-                sc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[rt][cc], sc[rt], 0, 0, 0);
-        }
-        if (KQJL) {
+            for (int rt = 0; rt < kRT; ++rt) {
+                sc[rt] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+                tj[rt] = tq_floatx4{0.f, 0.f, 0.f, 0.f};
+            }
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
-                const tq_half8 a = *reinterpret_cast<const tq_half8*>(
-                    b + kOffS + n * kKRow + 2 * (32 * cc + 8 * g));
+                const tq_half8 a = *reinterpret_cast<const tq_half8*>(b + n * kKRow + 2 * (32 * cc + 8 * g));
 #pragma unroll
                 for (int rt = 0; rt < kRT; ++rt)
-                    tj[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qpop[rt][cc], tj[rt], 0, 0, 0);
+                    sc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qop[rt][cc], sc[rt], 0, 0, 0);
+            }
+            if (KQJL) {
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    const tq_half8 a =
+                        *reinterpret_cast<const tq_half8*>(b + kOffS + n * kKRow + 2 * (32 * cc + 8 * g));
+#pragma unroll
+                    for (int rt = 0; rt < kRT; ++rt)
+                        tj[rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qpop[rt][cc], tj[rt], 0, 0, 0);
+                }
+            }
+            const tq_floatx4 kn1 = *reinterpret_cast<const tq_floatx4*>(b + kOffN + 16 * g);
+            const tq_floatx4 kr2 = *reinterpret_cast<const tq_floatx4*>(b + kOffN + 64 + 16 * g);
+            const int nvt = tt2 ? nvB : nvA;
+#pragma unroll
+            for (int rt = 0; rt < kRT; ++rt) {
+                // tokens 4g + r below lim are usable and visible to the row (one compare per
+                // token, in the tiles where some lane has one that is not: the diagonal and the
+                // last tiles)
+                int lim = qposR[rt] - (2 * js + tt2) * 16 + 1 - 4 * g;
+                lim = lim < nvt - 4 * g ? lim : nvt - 4 * g;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv[rt][4 * tt2 + r] = __builtin_fmaf(kn1[r], sc[rt][r], kr2[r] * tj[rt][r]);
+                if (__builtin_amdgcn_ballot_w64(lim < 4)) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sv[rt][4 * tt2 + r] = r < lim ? sv[rt][4 * tt2 + r] : kNegInf;
+                }
             }
         }
-        const tq_floatx4 kn1 = *reinterpret_cast<const tq_floatx4*>(b + kOffN + 16 * g);
-        const tq_floatx4 kr2 =
-            *reinterpret_cast<const tq_floatx4*>(b + kOffN + 64 + 16 * g);
-        const tq_floatx4 vn =
-            *reinterpret_cast<const tq_floatx4*>(b + kOffN + 128 + 16 * g);
-        tq_half4v bop[kRT];
+        const tq_floatx4 vnA = *reinterpret_cast<const tq_floatx4*>(bA + kOffN + 128 + 16 * g);
+        const tq_floatx4 vnB = *reinterpret_cast<const tq_floatx4*>(bB + kOffN + 128 + 16 * g);
+        tq_half8 bop[kRT];
 #pragma unroll
         for (int rt = 0; rt < kRT; ++rt) {
-            // tokens 4g + r below lim are usable and visible to the row (lim: one compare per
-            // token, in the tiles where some lane has one that is not: the diagonal and the
-            // last tile)
-            int lim = qposR[rt] - ti * 16 + 1 - 4 * g;
-            lim = lim < nv - 4 * g ? lim : nv - 4 * g;
-            float sv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sv[r] = __builtin_fmaf(kn1[r], sc[rt][r], kr2[r] * tj[rt][r]);
-            if (__builtin_amdgcn_ballot_w64(lim < 4)) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) sv[r] = r < lim ? sv[r] : kNegInf;
-            }
-            float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            float mt = fmaxf(fmaxf(fmaxf(sv[rt][0], sv[rt][1]), fmaxf(sv[rt][2], sv[rt][3])),
+                             fmaxf(fmaxf(sv[rt][4], sv[rt][5]), fmaxf(sv[rt][6], sv[rt][7])));
             mt = max_over_groups(mt);
             // The exponent base m (per row) moves only when some row's max passes it by more
             // than one log2 unit; p = exp2(s - m - 1) <= 1, and acc and lsum carry the same
-            // factor, so most tiles skip the rescale.
+            // factor, so most steps skip the rescale.
             if (__builtin_amdgcn_ballot_w64(mt > m[rt] + 1.0f)) {
                 const float mb = fmaxf(m[rt], mt);
                 // 0 while m = -inf; 1 for a row whose max did not move (also a row that has seen
@@ -429,28 +457,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 m[rt] = mb;
             }
             const float nb = m[rt] == kNegInf ? 0.f : -m[rt] - 1.0f;
-            float pr[4];
+            float pr[8];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(sv[r] + nb);  // 0 for masked tokens
-            lsum[rt] += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+            for (int r = 0; r < 8; ++r) pr[r] = __builtin_amdgcn_exp2f(sv[rt][r] + nb);  // 0 for masked tokens
+            lsum[rt] += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 #pragma unroll
-            for (int r = 0; r < 4; ++r) bop[rt][r] = (_Float16)(pr[r] * vn[r]);
+            for (int r = 0; r < 4; ++r) {
+                bop[rt][r] = (_Float16)(pr[r] * vnA[r]);
+                bop[rt][4 + r] = (_Float16)(pr[4 + r] * vnB[r]);
+            }
         }
+        // O^T += VhatT . P^T over the step's 32 keys: k = 8g + i is token 4g + i of tile A
+        // (i < 4) or of tile B (i >= 4), the order of the B operand above
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const tq_half4v a = *reinterpret_cast<const tq_half4v*>(
-                b + kOffV + (16 * j + n) * kVRow + 8 * g);
+            const tq_half4v va = *reinterpret_cast<const tq_half4v*>(bA + kOffV + (16 * j + n) * kVRow + 8 * g);
+            const tq_half4v vb = *reinterpret_cast<const tq_half4v*>(bB + kOffV + (16 * j + n) * kVRow + 8 * g);
+            const tq_half8 a = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
 #pragma unroll
             for (int rt = 0; rt < kRT; ++rt)
-                acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop[rt], acc[rt][j], 0, 0, 0);
+                acc[rt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bop[rt], acc[rt][j], 0, 0, 0);
         }
-        if (ti + 1 < ntiles) store_tile(ti + 1, nx, buf ^ 1);
+        if (more) {
+            store_tile(2 * js + 2, rawA, 2 - cur);
+            store_tile(2 * js + 3, rawB, 3 - cur);
+            nvA = rawA.nv;
+            nvB = rawB.nv;
+        }
         __syncthreads();
-    };
-    for (int ti = 0; ti < ntiles; ti += 2) {
-        step(ti, rawA, rawB);
-        if (ti + 1 >= ntiles) break;
-        step(ti + 1, rawB, rawA);
     }
 
     // ---- normalise, rotate, write ----
