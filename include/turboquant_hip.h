@@ -300,7 +300,8 @@ int tq_decode(const void* q, int q_dtype, int64_t q_stride_seq, int64_t q_stride
  * k_signs: [bh][sk][16] sign bits (signs_permuted: the stride-4 order of
  * permute_signs_for_chunked); k_rnorm, k_norm, v_norm: [bh][sk] fp16; centroids: 4 fp32 (K and
  * V share them) with the table scale of tq_kv_view.centroid_scale (0 means 1); corr_scale the QJL
- * factor (sqrt(pi/2)/128 in the reference); tokens_per_chunk as for tq_decode (0: the library's
+ * factor as the caller passes it to the reference (the estimator's sqrt(pi/2)/m for m = 128
+ * projections, reference/pytorch_reference.py:153-154); tokens_per_chunk as for tq_decode (0: the library's
  * choice; the reference's num_splits corresponds to ceil(sk / num_splits) rounded up to 16);
  * out: [bh, 128] of out_dtype.  The split combine is the exact (m, l, acc) merge.  Returns
  * tq_decode's status codes.  Same kernels and results as tq_decode on contiguous regions with
