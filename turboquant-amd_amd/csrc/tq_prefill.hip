@@ -110,7 +110,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int n = lane & 15;
     const int g = lane >> 4;
 
-    const int rb = (int)(blockIdx.x % (unsigned)p.n_rb);
+    // row blocks of one (sequence, KV head) in decreasing order: under a causal mask the last
+    // rows see the most keys, and dispatching the longest workgroups first leaves short ones
+    // for the end of the launch
+    const int rb = p.n_rb - 1 - (int)(blockIdx.x % (unsigned)p.n_rb);
     const int skh = (int)(blockIdx.x / (unsigned)p.n_rb);
     const int kh = skh % p.hkv;
     const int s = skh / p.hkv;
