@@ -264,8 +264,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint32_t o_v0 = ov & ~3u, o_v1 = second(ov, p.v_lg, (uint32_t)(tt * p.vidx.stride_row), 4 * VB);
     const uint32_t sh_k = (ok & 3u) * 8u, sh_v = (ov & 3u) * 8u;
     const int ntok = tid & 15;  // token of the norm threads (0-47)
-    const tq_region& nreg = tid < 16 ? p.knorm : (tid < 32 ? p.krnorm : p.vnorm);
-    const uint32_t o_nm = (uint32_t)(ntok * nreg.stride_row);
+    // (the row strides are selected as values: a per-thread reference into the parameters would
+    // make every tile read the region fields with vector loads)
+    const int64_t nm_stride = tid < 16 ? p.knorm.stride_row : (tid < 32 ? p.krnorm.stride_row : p.vnorm.stride_row);
+    const uint32_t o_nm = (uint32_t)(ntok * nm_stride);
     auto load_raw = [&](int ti, Raw& w) {
         const int64_t blk = tile_block(ti, w.nv);
         const int row0 = (ti * 16) % p.block_size;
@@ -284,9 +286,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             w.sg0 = ld32(base(p.ksig), o_sg);
         }
         w.nrm = 0;
-        if (tid < 16) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.knorm) + (uint64_t)o_nm);
-        else if (tid < 32 && KQJL) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.krnorm) + (uint64_t)o_nm);
-        else if (tid >= 32 && tid < 48) w.nrm = *reinterpret_cast<const uint16_t*>(base(p.vnorm) + (uint64_t)o_nm);
+        if (tid < 48 && (KQJL || tid < 16 || tid >= 32)) {
+            // wave-uniform bases of the three norm regions, one picked per thread
+            const uint8_t* nk = base(p.knorm);
+            const uint8_t* nr = KQJL ? base(p.krnorm) : nk;
+            const uint8_t* nvb = base(p.vnorm);
+            const uint8_t* nb = tid < 16 ? nk : (tid < 32 ? nr : nvb);
+            w.nrm = *reinterpret_cast<const uint16_t*>(nb + (uint64_t)o_nm);
+        }
     };
     auto store_tile = [&](int ti, const Raw& w, int buf) {
         const int nv = w.nv;
