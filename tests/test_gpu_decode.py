@@ -340,6 +340,52 @@ def test_packed_attention_v7_api(dev):
             np.testing.assert_allclose(got[h], ref[0].cpu().numpy(), rtol=RTOL, atol=ATOL)
 
 
+def test_packed_attention_c_entry_dtypes(dev):
+    """tq_packed_attention called through the C-ABI with bf16 / fp32 queries and fp32 / bf16
+    output, natural or permuted sign rows, fixed and library-chosen chunks, against the fp64
+    oracle (the Python packed_attention always passes fp16 in and out)."""
+    from turboquant import _lib
+    from turboquant.kernels.paged import decode_workspace
+    rng = np.random.default_rng(17)
+    cb = _cb(2).to(dev)
+    cs = math.sqrt(math.pi / 2) / math.sqrt(128)
+    L = _lib.lib()
+    for BH, Sk, qdt, odt, perm, chunk in [(6, 1000, torch.bfloat16, torch.float32, True, 0),
+                                          (3, 2048, torch.float32, torch.bfloat16, False, 256),
+                                          (5, 37, torch.float16, torch.float32, True, 16)]:
+        ki = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
+        ks = rng.integers(0, 256, (BH, Sk, 16), dtype=np.uint8)
+        vi = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
+        kr = (rng.random((BH, Sk)) * 0.1).astype(np.float16)
+        kn = (rng.random((BH, Sk)) + 0.5).astype(np.float16)
+        vn = (rng.random((BH, Sk)) + 0.5).astype(np.float16)
+        Q = (rng.standard_normal((BH, 128)) * 0.1).astype(np.float32)
+        Qp = (rng.standard_normal((BH, 128)) * 0.1).astype(np.float32)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        ks_dev = opack.permute_signs(ks.reshape(-1, 16)).reshape(ks.shape) if perm else ks
+        q, qp = t(Q).to(qdt), t(Qp).to(qdt)
+        arrs = [t(ki), t(ks_dev), t(kr), t(kn), t(vi), t(vn)]
+        out = torch.full((BH, 128), float("nan"), dtype=odt, device=dev)
+        ws = decode_workspace(dev, L.tq_packed_attention_workspace_bytes(BH, Sk, chunk))
+        rc = L.tq_packed_attention(q.data_ptr(), qp.data_ptr(), _lib.dtype_code(q), arrs[0].data_ptr(), arrs[1].data_ptr(),
+                                   1 if perm else 0, arrs[2].data_ptr(), arrs[3].data_ptr(), arrs[4].data_ptr(),
+                                   arrs[5].data_ptr(), cb.data_ptr(), _lib.centroid_scale(cb), cs, BH, Sk, chunk,
+                                   ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.dtype_code(out), _lib.stream_handle(dev))
+        assert rc == 0, _lib.status_string(rc)
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        qr = q.float().cpu().numpy().astype(np.float64)
+        qpr = qp.float().cpu().numpy().astype(np.float64)
+        # bf16 output: the contract tolerance plus the output's own rounding (2^-9 relative)
+        tol = dict(rtol=RTOL, atol=ATOL) if odt == torch.float32 else dict(rtol=RTOL + 2.0 ** -8, atol=ATOL)
+        for h in range(BH):
+            k, sg, rn = odec.dequant_keys({"idx": ki[h], "norm": kn[h].view(np.uint16), "signs": ks[h],
+                                           "rnorm": kr[h].view(np.uint16)}, cb.double().cpu().numpy(), 2, True)
+            v = odec.dequant_values({"idx": vi[h], "norm": vn[h].view(np.uint16)}, cb.double().cpu().numpy(), 2)
+            want = odec.decode_dense(qr[h:h + 1], qpr[h:h + 1], k, sg, rn, v, 1.0, cs)
+            np.testing.assert_allclose(got[h], want[0], err_msg=f"BH {BH} Sk {Sk} head {h}", **tol)
+
+
 @pytest.mark.parametrize("perm", [True, False])
 @pytest.mark.parametrize("S,Sk,hkv,G,chunk", [(8, 256, 1, 1, 0), (3, 4096, 2, 6, 0), (2, 16, 1, 1, 0),
                                               (5, 1024, 1, 3, 512), (4, 2048, 2, 8, 96), (3, 1024, 1, 2, 16)])

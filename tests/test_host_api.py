@@ -432,6 +432,28 @@ def test_status_strings():
     assert _lib.status_string(-999) == "unknown status"
 
 
+def test_packed_attention_entry_rejections():
+    """tq_packed_attention (the v7 argument list): bad sizes, missing arrays, a chunk that is not a
+    multiple of 16 and unknown dtypes return their status before any HIP call (no GPU here);
+    bh = 0 is an empty call; the workspace size is tq_decode's for bh sequences of one head."""
+    from turboquant import _lib
+    L = _lib.lib()
+    f = ctypes.c_void_p(0x1000)  # never dereferenced: every call below returns before a launch
+
+    def call(bh=4, sk=64, chunk=0, q=f, q_dtype=1, out_dtype=1, k_idx=f):
+        return L.tq_packed_attention(q, f, q_dtype, k_idx, f, 1, f, f, f, f, f, 1.0, 0.01, bh, sk, chunk, f, 1 << 20,
+                                     f, out_dtype, None)
+
+    assert call(bh=-1) == -1
+    assert call(bh=0) == 0
+    assert call(sk=0) == -1 and call(sk=-5) == -1
+    assert call(q=None) == -1 and call(k_idx=None) == -1
+    assert call(chunk=8) == -9 and call(chunk=-16) == -9
+    assert call(q_dtype=9) == -7 and call(out_dtype=4) == -7
+    assert L.tq_packed_attention_workspace_bytes(8, 32768, 256) == L.tq_decode_workspace_bytes(8, 1, 32768, 256)
+    assert L.tq_packed_attention_workspace_bytes(-1, 10, 0) == 0
+
+
 def test_host_side_argument_rejection():
     """Invalid arguments return a negative status before any HIP call (runs without a GPU)."""
     from turboquant import _lib
