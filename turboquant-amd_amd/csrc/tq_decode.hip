@@ -978,11 +978,16 @@ int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num
     rp.out_dtype = out_dtype;
     rp.out_ss = out_ss;
     rp.out_sh = out_sh;
-    // four waves per (sequence, query head) when a sequence can span more than 32 chunks
+    // one wave per batch of 16 chunks, up to four, so a sequence's batches load in one round:
+    // four waves per (sequence, query head) when a sequence can span more than 32 chunks, two
+    // beyond 16
+    const unsigned nsh = (unsigned)((int64_t)num_seqs * num_q_heads);
     if (!bal && n_chunks > 32)
-        hipLaunchKernelGGL(decode_reduce_kernel<4>, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(256), 0, st, rp);
+        hipLaunchKernelGGL(decode_reduce_kernel<4>, dim3(nsh), dim3(256), 0, st, rp);
+    else if (!bal && n_chunks > 16)
+        hipLaunchKernelGGL(decode_reduce_kernel<2>, dim3(nsh), dim3(128), 0, st, rp);
     else
-        hipLaunchKernelGGL(decode_reduce_kernel<1>, dim3((unsigned)((int64_t)num_seqs * num_q_heads)), dim3(64), 0, st, rp);
+        hipLaunchKernelGGL(decode_reduce_kernel<1>, dim3(nsh), dim3(64), 0, st, rp);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? TQ_OK : (int)e;
 }
