@@ -312,7 +312,9 @@ def test_packed_attention_v7_api(dev):
     rng = np.random.default_rng(3)
     cb = _cb(2)
     cs = math.sqrt(math.pi / 2) / math.sqrt(128)
-    for BH, Sk, splits in [(8, 1, None), (4, 100, None), (3, 4097, None), (2, 4096, None), (5, 2048, 7)]:
+    # num_splits 100 and 256 give 94 and 256 chunks per head: the merge's 8- and 16-wave forms
+    for BH, Sk, splits in [(8, 1, None), (4, 100, None), (3, 4097, None), (2, 4096, None), (5, 2048, 7),
+                           (3, 3000, 100), (2, 4096, 256)]:
         ki = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)
         ks = rng.integers(0, 256, (BH, Sk, 16), dtype=np.uint8)
         vi = rng.integers(0, 256, (BH, Sk, 32), dtype=np.uint8)

@@ -978,11 +978,14 @@ int launch_reduce(float* ws_acc, float* ws_m, float* ws_l, int num_seqs, int num
     rp.out_dtype = out_dtype;
     rp.out_ss = out_ss;
     rp.out_sh = out_sh;
-    // one wave per batch of 16 chunks, up to four, so a sequence's batches load in one round:
-    // four waves per (sequence, query head) when a sequence can span more than 32 chunks, two
-    // beyond 16
+    // one wave per batch of 16 chunks, up to sixteen, so a sequence's batches load in one round
+    // (2, 4, 8 or 16 waves per (sequence, query head) beyond 16, 32, 64 or 128 chunks)
     const unsigned nsh = (unsigned)((int64_t)num_seqs * num_q_heads);
-    if (!bal && n_chunks > 32)
+    if (!bal && n_chunks > 128)
+        hipLaunchKernelGGL(decode_reduce_kernel<16>, dim3(nsh), dim3(1024), 0, st, rp);
+    else if (!bal && n_chunks > 64)
+        hipLaunchKernelGGL(decode_reduce_kernel<8>, dim3(nsh), dim3(512), 0, st, rp);
+    else if (!bal && n_chunks > 32)
         hipLaunchKernelGGL(decode_reduce_kernel<4>, dim3(nsh), dim3(256), 0, st, rp);
     else if (!bal && n_chunks > 16)
         hipLaunchKernelGGL(decode_reduce_kernel<2>, dim3(nsh), dim3(128), 0, st, rp);
