@@ -1242,8 +1242,9 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
     const bool contig = !fast && contig_path_ok(k, v, group, block_tables, block_size, max_seq_len, max_blocks_per_seq,
                                                 sparse_threshold, rotate);
     if (contig && tokens_per_chunk == 0) {
-        // one round of the resident waves, at least 8 tiles per unit (a unit's start-up is worth
-        // several tiles), and no more units than the workspace of tokens_per_chunk = 0 holds
+        // one round of the resident waves, at least 6 tiles per unit (a unit's start-up is worth
+        // several tiles; 6 measured faster than 8 at BH 8 x 32768), and no more units than the
+        // workspace of tokens_per_chunk = 0 holds
         FastLdsLayout lay;
         tq_decode_fast_lds_layout(2, true, 2, share, &lay);
         int waves = 0;
@@ -1252,7 +1253,7 @@ int tq_decode_impl(int rotate, const void* q, int q_dtype, int64_t q_stride_seq,
         if (orc) return orc;
         const int64_t tiles = (int64_t)num_seqs * num_kv_heads * (max_seq_len / 16);
         int64_t per = (tiles + waves - 1) / (waves > 0 ? waves : 1);
-        per = per < 8 ? 8 : per;
+        per = per < 6 ? 6 : per;
         int64_t chunk = 16 * per;
         const int64_t fit = general_chunk(num_seqs, num_q_heads, max_seq_len, false);
         chunk = chunk > fit ? chunk : fit;
