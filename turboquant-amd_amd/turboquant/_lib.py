@@ -227,10 +227,16 @@ def require_gpu(what: str, *tensors: torch.Tensor) -> torch.device:
     return first.device
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
-    """The raw hipStream_t of the device's current stream."""
+    """The raw hipStream_t of the device's current stream (torch's direct accessor where the
+    build has it: a fraction of the cost of building a Stream object per call)."""
+    if _RAW_STREAM is None:
+        return torch.cuda.current_stream(device).cuda_stream
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(idx)
+    return _RAW_STREAM(idx)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
