@@ -40,6 +40,7 @@ HBM_PEAK_GBS = 8000.0
 FP16_MFMA_TFLOPS = 2500.0
 D = 128
 SETTLE_S = 0.25
+BRACKETS = 5
 
 
 def outlier_kv(T, H, gen, device, dtype):
@@ -186,14 +187,30 @@ def settle(fn, seconds=SETTLE_S):
     return round((time.perf_counter() - t0) * 1e3, 1), n
 
 
-def timed(fn, steps, warmup, settle_s=SETTLE_S):
-    """Settle, W warmup steps, then K steps each bracketed by HIP events on the current stream.
-    Returns dict(median_ms, mean_ms, steps_ms, settle_ms)."""
+def timed(fn, steps, warmup, settle_s=SETTLE_S, brackets=BRACKETS):
+    """Step time of fn: after a settle phase (untimed) and W warmup steps, K steps enqueued back
+    to back between one pair of HIP events on the current stream, with a synchronize on both
+    sides; `brackets` such runs, ms = the median of their total / K.
+
+    A further run of K steps with an event recorded after every step gives the per-step
+    distribution (event_median_ms, steps_ms).  Each of those events is a completion signal in
+    the queue that the next launch waits behind (about 3 us per step on MI355X), so that figure
+    carries the instrumentation and is reported beside the step time, not as it.
+    Returns dict(ms, brackets_ms, event_median_ms, steps_ms, settle_ms, settle_steps)."""
     import torch
     settle_ms, settle_n = settle(fn, settle_s) if settle_s > 0 else (0.0, 0)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    brk = []
+    for _ in range(brackets):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        brk.append(e0.elapsed_time(e1) / steps)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record()
     for i in range(steps):
@@ -201,7 +218,7 @@ def timed(fn, steps, warmup, settle_s=SETTLE_S):
         ev[i + 1].record()
     torch.cuda.synchronize()
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
-    return {"median_ms": statistics.median(per), "mean_ms": ev[0].elapsed_time(ev[-1]) / steps,
+    return {"ms": statistics.median(brk), "brackets_ms": brk, "event_median_ms": statistics.median(per),
             "steps_ms": per, "settle_ms": settle_ms, "settle_steps": settle_n}
 
 
@@ -209,12 +226,12 @@ def decode_case(key, dev, steps, warmup, time_rotated=False):
     import torch
     st = build_decode_workload(key, dev)
     t = timed(decode_step(st), steps, warmup)
-    ms = t["median_ms"]
-    res = {"workload": st["name"], "us_per_layer": ms * 1e3, "mean_us": t["mean_ms"] * 1e3,
-           "settle_ms": t["settle_ms"]}
+    ms = t["ms"]
+    res = {"workload": st["name"], "us_per_layer": ms * 1e3,
+           "event_median_us": t["event_median_ms"] * 1e3, "settle_ms": t["settle_ms"]}
     if time_rotated:
         # the same decode with q and the output in the model basis (rotations fused)
-        res["rotated_us_per_layer"] = timed(decode_step(st, rotate=True), steps, warmup, settle_s=0.05)["median_ms"] * 1e3
+        res["rotated_us_per_layer"] = timed(decode_step(st, rotate=True), steps, warmup, settle_s=0.05)["ms"] * 1e3
         # the same tiles in a K cache spanning more than 2 GiB (a serving pool), the blocks moved
         # past 2 GiB: the kernel's 64-bit per-tile addressing
         kc = st["k_cache"]
@@ -225,7 +242,7 @@ def decode_case(key, dev, steps, warmup, time_rotated=False):
         vbig = torch.zeros((big.shape[0],) + tuple(st["v_cache"].shape[1:]), dtype=torch.uint8, device=dev)
         vbig[shift:] = st["v_cache"]
         stb = dict(st, k_cache=big, v_cache=vbig, bt=bt_big, out=torch.empty_like(st["q"]))
-        res["k_cache_beyond_2gib_us_per_layer"] = timed(decode_step(stb), steps, warmup, settle_s=0.05)["median_ms"] * 1e3
+        res["k_cache_beyond_2gib_us_per_layer"] = timed(decode_step(stb), steps, warmup, settle_s=0.05)["ms"] * 1e3
         del big, vbig, stb
     tokens = sum(st["lens_host"])
     kf, vf, Hkv = st["kf"], st["vf"], st["Hkv"]
@@ -280,7 +297,7 @@ def prefill_case(dev, steps, warmup, B=4, n=4096, Hq=48, Hkv=8, kb=3, kq=True, v
     def step():
         prefill_paged(q, cu, k_cache, kf, kc, v_cache, vf, vc, bt, lens, causal=True, max_q_len=n, out=out)
 
-    ms = timed(step, steps, warmup, settle_s=0.1)["median_ms"]
+    ms = timed(step, steps, warmup, settle_s=0.1)["ms"]
     # (query row, visible key) pairs x 3 products (q.k, qp.signs, p.v) x 2 x 128 flops
     pairs = B * Hq * n * (n + 1) // 2
     flops = pairs * (3 if kq else 2) * 2 * D
@@ -324,11 +341,11 @@ def compress_case(dev, steps, warmup):
                           (w["c"], w["b"]))
 
     t = timed(step, steps, warmup, settle_s=0.1)
-    ms = t["median_ms"]
+    ms = t["ms"]
     T, H = COMPRESS_T, COMPRESS_H
     alg = 2 * (T * H * D * 2 + T * H * w["fmt"].token_bytes) + T * 4
     return {"workload": "config2: turbo4 paged compress K+V, 16384 tok x 8 heads bf16, bs 16",
-            "us_per_layer": ms * 1e3, "mean_us": t["mean_ms"] * 1e3, "algorithmic_bytes": alg,
+            "us_per_layer": ms * 1e3, "event_median_us": t["event_median_ms"] * 1e3, "algorithmic_bytes": alg,
             "compress_gbs": alg / (ms * 1e-3) / 1e9, "frac_of_8tbs": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}, w
 
 
@@ -347,7 +364,7 @@ def config1_case(dev, steps, warmup):
     t = timed(lambda: polarquant_compress(Kd, cd, bd, cfg, Hd), steps, warmup, settle_s=0.05)
     out = polarquant_compress(Kd, cd, bd, cfg, Hd)
     torch.cuda.synchronize()
-    us = t["median_ms"] * 1e3
+    us = t["ms"] * 1e3
     return {"workload": "config1: polarquant_compress K [1024,128] fp32 N(0,1) seed 0, turbo3 + QJL, WHT",
             "us": us, "us_per_layer": us}, (K, cent, bnd, H, out)
 
@@ -441,8 +458,8 @@ def stream_reference(dev):
     import torch
     x = torch.ones(1 << 28, dtype=torch.int64, device=dev)
     y = torch.empty(1 << 27, dtype=torch.int64, device=dev)
-    r = timed(lambda: torch.amax(x), 20, 3, settle_s=0.05)["median_ms"]
-    c = timed(lambda: y.copy_(x[: 1 << 27]), 20, 3, settle_s=0.05)["median_ms"]
+    r = timed(lambda: torch.amax(x), 20, 3, settle_s=0.05)["ms"]
+    c = timed(lambda: y.copy_(x[: 1 << 27]), 20, 3, settle_s=0.05)["ms"]
     del x, y
     torch.cuda.empty_cache()
     return {"read_2gib_gbs": round((2 << 30) / (r * 1e-3) / 1e9, 1), "copy_1gib_gbs": round((2 << 30) / (c * 1e-3) / 1e9, 1)}
@@ -482,7 +499,7 @@ def published_shapes(dev, steps, warmup):
         def attend():
             return packed_attention(Q, Qp, ki, ks, kr, kn, vi, vn, cb, cs)
 
-        ms = timed(attend, steps, warmup, settle_s=0.05)["median_ms"]
+        ms = timed(attend, steps, warmup, settle_s=0.05)["ms"]
         nbytes = BH * Sk * (32 + 16 + 2 + 2 + 32 + 2) + 2 * BH * D * 2
         out["attention"].append({"BH": BH, "Sk": Sk, "us": ms * 1e3, "hbm_gbs": nbytes / (ms * 1e-3) / 1e9})
 
@@ -492,13 +509,13 @@ def published_shapes(dev, steps, warmup):
             return packed_attention(Q, Qp, a[0].view(BH, Sk, -1), a[1].view(BH, Sk, -1), a[2].view(BH, Sk),
                                     a[3].view(BH, Sk), b[0].view(BH, Sk, -1), b[1].view(BH, Sk), cb, cs)
 
-        ms = timed(pipeline, max(3, steps // 4), 2, settle_s=0.05)["median_ms"]
+        ms = timed(pipeline, max(3, steps // 4), 2, settle_s=0.05)["ms"]
         out["pipeline"].append({"BH": BH, "Sk": Sk, "us": ms * 1e3, "reference_published_us": pub[BH] * 1e3})
         del K, V, ki, ks, kr, kn, vi, vn
     pubk = {2048: 50, 32768: 59, 131072: 98, 524288: 271}
     for N in (2048, 32768, 131072, 524288):
         K = torch.randn(N, D, generator=gen, device=dev)
-        ms = timed(lambda: compress_k(K, PiT, PiST, cb, bnd), steps, warmup, settle_s=0.05)["median_ms"]
+        ms = timed(lambda: compress_k(K, PiT, PiST, cb, bnd), steps, warmup, settle_s=0.05)["ms"]
         # two 128 x 128 fp32 products per row (rotation, sign projection)
         out["compress_k"].append({"N": N, "us": ms * 1e3, "reference_published_us": pubk[N],
                                   "fp32_tflops": N * 2 * 2 * D * D / (ms * 1e-3) / 1e12})
@@ -657,7 +674,8 @@ def main():
     cpu = None
     if want("config4"):
         head, state4 = decode_case("config4", dev, steps, warmup, time_rotated=True)
-        print(f"# config4 {head['us_per_layer']:.1f} us/layer (mean {head['mean_us']:.1f}), {head['hbm_gbs']:.0f} GB/s",
+        print(f"# config4 {head['us_per_layer']:.1f} us/layer (per-step events {head['event_median_us']:.1f}), "
+              f"{head['hbm_gbs']:.0f} GB/s",
               file=sys.stderr, flush=True)
         if args.only is None:
             extra["stream_reference"] = stream_reference(dev)
@@ -671,7 +689,8 @@ def main():
         if want(key):
             r, _ = decode_case(key, dev, steps, warmup)
             extra[key] = r
-            print(f"# {key} {r['us_per_layer']:.1f} us (mean {r['mean_us']:.1f})", file=sys.stderr, flush=True)
+            print(f"# {key} {r['us_per_layer']:.1f} us (per-step events {r['event_median_us']:.1f})", file=sys.stderr,
+                  flush=True)
             torch.cuda.empty_cache()
     if want("prefill"):
         rp = prefill_case(dev, min(steps, 20), min(warmup, 5))
@@ -681,7 +700,8 @@ def main():
     if want("config2"):
         r2, w2 = compress_case(dev, steps, warmup)
         extra["config2"] = r2
-        print(f"# config2 {r2['us_per_layer']:.1f} us, {r2['compress_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+        print(f"# config2 {r2['us_per_layer']:.1f} us (per-step events {r2['event_median_us']:.1f}), "
+              f"{r2['compress_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
     if want("config2") or args.only == "config1":
         r1, c1 = config1_case(dev, steps, warmup)
         extra["config1"] = r1
@@ -709,8 +729,10 @@ def main():
     traffic, traffic_src = profiled_traffic() if head["workload"].startswith("config4") else (None, None)
     mfma = profile_value("decode_fast_kernel_config4_pmc.md", "mfma_busy_fraction")
     details = {"headline": head, **extra,
-               "timing": "median of K per-step HIP-event intervals after a settle phase (settle_ms, untimed) "
-                         "and W warmup steps; mean_us = total of the K steps / K",
+               "timing": "after a settle phase (settle_ms, untimed) and W warmup steps: K steps back to back "
+                         "between one pair of HIP events, synchronize on both sides, total / K; median of "
+                         f"{BRACKETS} such brackets.  event_median_us: median of a further K steps with an "
+                         "event recorded after each (the events' own queue signals included)",
                "reference_published_us_per_layer": {"turbo3_v12_sparse_v": 843, "turbo4": 797,
                                                     "note": "MI355X Triton, shape unstated (README.md:102-103)"}}
     if mfma is not None:
