@@ -92,40 +92,14 @@ __device__ __forceinline__ float row_sumsq(const float (&x)[32]) {
 }
 
 // v[k] += s * (v[k] of lane L ^ 1 (CTRL = quad_perm [1,0,3,2]) or L ^ 2 ([2,3,0,1])), 32 values:
-// one v_fmac_f32_dpp each (the compiler does not fold a DPP move into an fmac).  s_nop 1 first:
-// a DPP source written by the instruction just before needs two wait states.
+// one fma per value on the DPP-moved partner (s = +-1, so the product is exact and the fma rounds
+// once, as a v_fmac_f32_dpp would).  The moves are compiler builtins, so the wait states between
+// a VALU write and a DPP read of the same register are the compiler's to place.
 template <int CTRL>
 __device__ __forceinline__ void fmac_dpp32(float (&v)[32], float s) {
-#define TQ_FD(K) "v_fmac_f32_dpp %" #K ", %" #K ", %32 quad_perm:" CTRL_STR " row_mask:0xf bank_mask:0xf\n\t"
-#define TQ_FD8(B) TQ_FD(B) TQ_FD(B##1) TQ_FD(B##2) TQ_FD(B##3) TQ_FD(B##4) TQ_FD(B##5) TQ_FD(B##6) TQ_FD(B##7)
-    static_assert(CTRL == 0xB1 || CTRL == 0x4E, "quad_perm xor 1 or xor 2");
-    if constexpr (CTRL == 0xB1) {
-#define CTRL_STR "[1,0,3,2]"
-        asm volatile("s_nop 1\n\t" TQ_FD(0) TQ_FD(1) TQ_FD(2) TQ_FD(3) TQ_FD(4) TQ_FD(5) TQ_FD(6) TQ_FD(7)
-                     TQ_FD(8) TQ_FD(9) TQ_FD(10) TQ_FD(11) TQ_FD(12) TQ_FD(13) TQ_FD(14) TQ_FD(15)
-                     TQ_FD(16) TQ_FD(17) TQ_FD(18) TQ_FD(19) TQ_FD(20) TQ_FD(21) TQ_FD(22) TQ_FD(23)
-                     TQ_FD(24) TQ_FD(25) TQ_FD(26) TQ_FD(27) TQ_FD(28) TQ_FD(29) TQ_FD(30) TQ_FD(31)
-                     : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
-                       "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]),
-                       "+v"(v[16]), "+v"(v[17]), "+v"(v[18]), "+v"(v[19]), "+v"(v[20]), "+v"(v[21]), "+v"(v[22]), "+v"(v[23]),
-                       "+v"(v[24]), "+v"(v[25]), "+v"(v[26]), "+v"(v[27]), "+v"(v[28]), "+v"(v[29]), "+v"(v[30]), "+v"(v[31])
-                     : "v"(s));
-#undef CTRL_STR
-    } else {
-#define CTRL_STR "[2,3,0,1]"
-        asm volatile("s_nop 1\n\t" TQ_FD(0) TQ_FD(1) TQ_FD(2) TQ_FD(3) TQ_FD(4) TQ_FD(5) TQ_FD(6) TQ_FD(7)
-                     TQ_FD(8) TQ_FD(9) TQ_FD(10) TQ_FD(11) TQ_FD(12) TQ_FD(13) TQ_FD(14) TQ_FD(15)
-                     TQ_FD(16) TQ_FD(17) TQ_FD(18) TQ_FD(19) TQ_FD(20) TQ_FD(21) TQ_FD(22) TQ_FD(23)
-                     TQ_FD(24) TQ_FD(25) TQ_FD(26) TQ_FD(27) TQ_FD(28) TQ_FD(29) TQ_FD(30) TQ_FD(31)
-                     : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
-                       "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]),
-                       "+v"(v[16]), "+v"(v[17]), "+v"(v[18]), "+v"(v[19]), "+v"(v[20]), "+v"(v[21]), "+v"(v[22]), "+v"(v[23]),
-                       "+v"(v[24]), "+v"(v[25]), "+v"(v[26]), "+v"(v[27]), "+v"(v[28]), "+v"(v[29]), "+v"(v[30]), "+v"(v[31])
-                     : "v"(s));
-#undef CTRL_STR
-    }
-#undef TQ_FD8
-#undef TQ_FD
+    static_assert(CTRL == kDppXor1 || CTRL == kDppXor2, "quad_perm xor 1 or xor 2");
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = __builtin_fmaf(dppf<CTRL>(v[k]), s, v[k]);
 }
 
 // Normalised Hadamard transform of the row (dims 32q + k in v[k]): butterflies
