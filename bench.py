@@ -194,7 +194,7 @@ def timed(fn, steps, warmup, settle_s=SETTLE_S, brackets=BRACKETS):
 
     A further run of K steps with an event recorded after every step gives the per-step
     distribution (event_median_ms, steps_ms).  Each of those events is a completion signal in
-    the queue that the next launch waits behind (about 3 us per step on MI355X), so that figure
+    the queue that the next launch waits behind (1.5-3 us per step measured on MI355X), so that figure
     carries the instrumentation and is reported beside the step time, not as it.
     Returns dict(ms, brackets_ms, event_median_ms, steps_ms, settle_ms, settle_steps)."""
     import torch
